@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark of the LATENT fused low-rank expert FFN on one MI355X.
+
+Workload (DeepSeek-V3-shaped LATENT MoE layer): 256 experts, d=7168,
+ff=2048, uniform rank 256, NF4 group 32 + fp16 scales, top-8 softmax routing,
+bf16 activations.  A step is one `latent_moe_ffn_forward` call (token->expert
+grouping + the fused factor chain + router-weighted combine) on one batch;
+inputs are resident in HBM before the timed region.
+
+Cache honesty: the 256 MB MALL would hold a small batch's experts, so the
+timed loop rotates over `--layers` independently generated layers (1 GB of
+packed factors each) and several routings; consecutive steps never touch the
+same layer.
+
+The headline `value` is tokens/s at batch 64; batches 1, 8 and 32 and the
+4096-token prefill are reported under "sweep" / "prefill".  HBM GB/s counts
+the packed factor bytes of the distinct experts each step routes to.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "MoE-layer tokens/sec + HBM GB/s (% roofline), decode b=1..64 & prefill 4096"
+HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+E, D, FF, R, K = 256, 7168, 2048, 256, 8
+EXPERT_BYTES = (2 * D * R + 2 * R * FF + FF * R + R * D) // 2 + (2 * D * R + 2 * R * FF + FF * R + R * D) // 32 * 2
+PAIR_FLOPS = 2 * (2 * D * R + 2 * R * FF + FF * R + R * D)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--batch", type=int, default=64, help="headline decode batch")
+    p.add_argument("--sweep", type=str, default="1,8,32", help="other decode batches ('' to skip)")
+    p.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 to skip)")
+    p.add_argument("--prefill-steps", type=int, default=5)
+    p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
+    p.add_argument("--routings", type=int, default=8, help="distinct routings per batch size")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-batch", type=int, default=64)
+    return p.parse_args()
+
+
+def realized_bytes(ids_list):
+    """Packed factor bytes of the distinct experts each routing touches."""
+    out = []
+    for ids in ids_list:
+        v = ids[(ids >= 0) & (ids < E)]
+        out.append(np.unique(v).size * EXPERT_BYTES)
+    return out
+
+
+def time_loop(fn, n_steps, warmup, torch):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(n_steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / n_steps  # ms per step
+
+
+def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings):
+    routes = [gsynth.route(seed=10_000 + 97 * batch + r, n_tokens=batch, n_expert=E, k=K) for r in range(n_routings)]
+    xs = [gsynth.bf16_input(seed=20_000 + 89 * batch + r, n_tokens=batch, d=D) for r in range(n_routings)]
+    outs = [torch.empty((batch, D), dtype=torch.float32, device="cuda") for _ in range(n_routings)]
+    for L in layers:
+        L.workspace(batch, K)
+    ws = layers[0].workspace(batch, K)
+
+    def step(i):
+        r = i % n_routings
+        ids, w = routes[r]
+        latent.moe_forward(xs[r], ids, w, layers[i % len(layers)], out=outs[r], workspace=ws)
+
+    ms = time_loop(step, steps, warmup, torch)
+    ids_host = [routes[i % n_routings][0].cpu().numpy() for i in range(steps)]
+    bytes_per_step = float(np.mean(realized_bytes(ids_host)))
+    gbps = bytes_per_step / (ms * 1e-3) / 1e9
+    return {
+        "batch": batch,
+        "ms_per_step": ms,
+        "tokens_per_s": batch / (ms * 1e-3),
+        "hbm_gbps": gbps,
+        "roofline_frac": gbps / HBM_PEAK_GBPS,
+        "bytes_per_step": bytes_per_step,
+        "distinct_experts_mean": bytes_per_step / EXPERT_BYTES,
+    }, routes, xs
+
+
+def prefill_point(torch, latent, gsynth, layers, tokens, steps):
+    ids, w = gsynth.route(seed=30_000, n_tokens=tokens, n_expert=E, k=K, zipf_gamma=1.0)
+    x = gsynth.bf16_input(seed=30_001, n_tokens=tokens, d=D)
+    out = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
+    ws = layers[0].workspace(tokens, K)
+
+    def step(i):
+        latent.moe_forward(x, ids, w, layers[i % len(layers)], out=out, workspace=ws)
+
+    ms = time_loop(step, steps, 1, torch)
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
+    flops = float(PAIR_FLOPS) * int((ids >= 0).sum().item())
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "tokens": tokens,
+        "ms_per_step": ms,
+        "tokens_per_s": tokens / (ms * 1e-3),
+        "tflops": tflops,
+        "mfma_frac_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
+        "tokens_per_expert_max": int(counts.max()),
+        "tokens_per_expert_min": int(counts.min()),
+        "path": "wave64 GEMV chain (fp32)",
+    }
+
+
+def cpu_baseline(torch, layer, routes, xs, batch):
+    """The oracle (numpy port of loader/latent_runtime.py) on one decode step, 1 thread."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from threadpoolctl import threadpool_limits
+
+    from oracle import latent_ref as ref
+
+    ids = routes[0][0].cpu().numpy()
+    w = routes[0][1].cpu().numpy()
+    x = xs[0].float().cpu().numpy()
+    experts = np.unique(ids[(ids >= 0) & (ids < E)])
+    lut = -np.ones(E, np.int64)
+    lut[experts] = np.arange(experts.size)
+    local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
+    sel = torch.as_tensor(experts, device="cuda")
+    facs = {}
+    for name, f in layer.factors().items():
+        facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
+                                       f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
+    host = ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R)
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        ref.moe_forward(x, local, w, host)
+        dt = time.perf_counter() - t0
+    return {
+        "value": batch / dt,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"one decode step at batch {batch} ({experts.size} distinct experts dequantized once each, "
+                  f"numpy fp32, 1 BLAS thread) on {os.cpu_count()} visible host cores; {dt:.1f} s",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the expert-parallel "
+              "multi-GPU path is not built", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import latent_amd as latent
+    from latent_amd import synth as gsynth
+
+    t0 = time.time()
+    layers = [gsynth.make_layer(seed=1 + 1000 * i, n_expert=E, d=D, ff=FF, max_rank=R) for i in range(args.layers)]
+    torch.cuda.synchronize()
+    print(f"# generated {args.layers} layers ({layers[0].nbytes() / 1e9:.3f} GB packed each) in {time.time() - t0:.1f} s",
+          file=sys.stderr, flush=True)
+
+    head, routes, xs = decode_point(torch, latent, gsynth, layers, args.batch, args.steps, args.warmup, args.routings)
+    print(f"# decode B={args.batch}: {head['ms_per_step'] * 1e3:.1f} us/step, {head['hbm_gbps']:.0f} GB/s",
+          file=sys.stderr, flush=True)
+    sweep = []
+    for b in [int(v) for v in args.sweep.split(",") if v.strip()]:
+        pt, _, _ = decode_point(torch, latent, gsynth, layers, b, args.steps, args.warmup, args.routings)
+        sweep.append(pt)
+        print(f"# decode B={b}: {pt['ms_per_step'] * 1e3:.1f} us/step, {pt['hbm_gbps']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    prefill = None
+    if args.prefill:
+        prefill = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps)
+        print(f"# prefill T={args.prefill}: {prefill['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch)
+        print(f"# cpu baseline: {cpu['value']:.2f} tokens/s", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded closed-form low-rank factors packed NF4 g32 on the GPU; bf16 N(0,1) tokens; "
+                "softmax top-8 routing)",
+        "config": {
+            "workload": "deepseek-v3-shaped LATENT MoE layer decode",
+            "n_expert": E, "n_embd": D, "n_ff": FF, "rank": R, "top_k": K, "batch": args.batch,
+            "layers_rotated": args.layers, "routings": args.routings,
+        },
+        "hbm_gbps": head["hbm_gbps"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": head["hbm_gbps"],
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": head["roofline_frac"],
+            "traffic": None,
+            "kernel": "latent_moe_ffn_forward (all kernels of one call)",
+            "bytes_per_launch": head["bytes_per_step"],
+        },
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+        "prefill": prefill,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,166 @@
+/*
+ * latent_ffn.h -- C ABI of the MI355X (gfx950) LATENT fused low-rank expert FFN.
+ *
+ * For every routed (token, slot) pair with expert e = ids[t][slot]:
+ *
+ *     y[t][slot] = ( SiLU(x[t] . A_g[e] . B_g[e]) * (x[t] . A_u[e] . B_u[e]) ) . A_d[e] . B_d[e]
+ *
+ * with the six factors dequantized on the fly from packed NF4 (per-32-group
+ * fp16 scales) and optional per-group INT8 fallback, then either the
+ * router-weighted sum over slots (LATENT_OUT_REDUCED) or the per-slot,
+ * unweighted outputs of the ggml op (LATENT_OUT_PER_SLOT).
+ *
+ * Replaces, at the same boundary:
+ *   - void ggml_cuda_latent_expert_ffn(ggml_backend_cuda_context&, ggml_tensor* dst)
+ *       kernels/latent_fused_expert_ffn.h:64, implemented at
+ *       kernels/latent_fused_expert_ffn.cu:134-292 (15 srcs, order at :135-149)
+ *   - extern "C" __global__ latent_fused_expert_dispatch / latent_expert_reduce
+ *       kernels/latent_fused_expert_ffn.h:61-62
+ *   - swiglu_expert / load_pair of loader/latent_runtime.py:31-59 (Python side,
+ *       bound through ctypes by latent_amd.runtime)
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  All pointers are device pointers unless a
+ *     comment says otherwise; the caller owns every buffer.
+ *   - No call allocates device memory or synchronises the stream: scratch comes
+ *     from the caller's workspace (size from latent_moe_workspace_size).
+ *   - Errors are returned as LATENT_E_* status codes; nothing aborts.
+ *   - Calls are stream ordered.  Concurrent calls on different streams must use
+ *     different workspaces.
+ *
+ * Stacked operand layout (loader/write_latent_gguf.py:101-123, 227-257;
+ * shapes of patches/002-latent-gguf-tensors.patch:135-148 with the packed code
+ * axis asserted by tests/test_write_latent_gguf.py:112-154):
+ *   gate_a, up_a : codes u8 [E][d ][R/2],  scales f16 [E][d ][R/32]
+ *   gate_b, up_b : codes u8 [E][R ][ff/2], scales f16 [E][R ][ff/32]
+ *   down_a       : codes u8 [E][ff][R/2],  scales f16 [E][ff][R/32]
+ *   down_b       : codes u8 [E][R ][d/2],  scales f16 [E][R ][d/32]
+ * Row-major, expert-major.  Low nibble = even column.  A group is 32
+ * consecutive columns of one row.  Padding beyond an expert's true rank holds
+ * zeros (code 7, scale 1.0), so computing over the padding changes nothing.
+ */
+#ifndef LATENT_FFN_H
+#define LATENT_FFN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers. */
+typedef struct ihipStream_t* latent_stream_t;
+
+/* ---- status codes ------------------------------------------------------- */
+#define LATENT_OK 0
+#define LATENT_E_INVALID (-1)     /* null pointer / inconsistent dims / bad enum */
+#define LATENT_E_UNSUPPORTED (-2) /* valid request this build does not implement */
+#define LATENT_E_WORKSPACE (-3)   /* workspace missing or smaller than required */
+#define LATENT_E_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+
+/* ---- element types ------------------------------------------------------ */
+#define LATENT_F32 0
+#define LATENT_F16 1
+#define LATENT_BF16 2
+
+/* ---- output modes ------------------------------------------------------- */
+/* f32 [T][d]: sum over slots of w*y (y when weight_before_down). */
+#define LATENT_OUT_REDUCED 0
+/* f32 [T][k][d]: per slot, unweighted unless weight_before_down, zero for a
+ * dropped slot -- the dst of kernels/latent_fused_expert_ffn.cu:255-286. */
+#define LATENT_OUT_PER_SLOT 1
+
+/*
+ * One stacked factor (codes + scales for all E experts).
+ *   rows, cols      per-expert logical shape; cols % 32 == 0.
+ *   expert stride   rows*cols/2 code bytes and rows*cols/32 scales.
+ * Optional per-group INT8 fallback (no reference counterpart; the reference
+ * only has whole-factor INT8 at group 64, loader/latent_loader.py:229-249):
+ *   int8_bitmap     u32 [E][rows][ceil(cols/32/32)]; bit g => group g is INT8
+ *   int8_row_offset i32 [E][rows]; index of the row's first INT8 group in data
+ *   int8_data       i8  [n][32]; the flagged groups in (e,row,group) order
+ * A flagged group's scale (absmax/127, fp16) sits in `scales`; its NF4 bytes
+ * are ignored.  All three NULL => pure NF4.
+ */
+typedef struct latent_factor {
+  const uint8_t* codes;
+  const uint16_t* scales; /* IEEE binary16 bit patterns */
+  const uint32_t* int8_bitmap;
+  const int32_t* int8_row_offset;
+  const int8_t* int8_data;
+  int64_t rows;
+  int64_t cols;
+} latent_factor;
+
+/*
+ * Arguments of one MoE-layer expert FFN call: the 15 operands of
+ * GGML_OP_LATENT_EXPERT_FFN (kernels/latent_fused_expert_ffn.cu:135-149) in
+ * their order -- x, ids, weights, then gate_a..down_b with their scales --
+ * plus the dimensions, per-expert ranks, output mode and workspace.
+ */
+typedef struct latent_moe_args {
+  const void* x;            /* [T][d] of x_dtype (src0) */
+  int32_t x_dtype;          /* LATENT_F32 | LATENT_F16 | LATENT_BF16 */
+  const int32_t* ids;       /* [T][k] expert ids; id < 0 => dropped slot (src1) */
+  const void* weights;      /* [T][k] router weights of weights_dtype (src2) */
+  int32_t weights_dtype;    /* LATENT_F32 | LATENT_F16 */
+  latent_factor gate_a, gate_b, up_a, up_b, down_a, down_b; /* src3..src14 */
+  const int32_t* ranks;     /* [E][3] true (gate, up, down) ranks, or NULL => max_rank */
+  int64_t n_tokens;         /* T */
+  int64_t n_embd;           /* d */
+  int64_t n_ff;             /* ff (per expert) */
+  int64_t n_expert;         /* E */
+  int64_t n_expert_used;    /* k */
+  int64_t max_rank;         /* R, a multiple of 32 */
+  int32_t weight_before_down;
+  int32_t out_mode;         /* LATENT_OUT_REDUCED | LATENT_OUT_PER_SLOT */
+  void* out;                /* f32, shape per out_mode */
+  void* workspace;          /* device scratch, >= latent_moe_workspace_size() */
+  size_t workspace_bytes;
+} latent_moe_args;
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int latent_version(void);
+
+/* Static text for a status code. */
+const char* latent_status_string(int status);
+
+/* Workspace bytes required by latent_moe_ffn_forward for these dims. */
+int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes);
+
+/*
+ * The MoE-layer expert FFN (decode and prefill).  Stream ordered; ids outside
+ * [0, E) are treated as dropped slots.  Replaces ggml_cuda_latent_expert_ffn
+ * (kernels/latent_fused_expert_ffn.h:64).
+ */
+int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
+
+/*
+ * Dequantize expert `expert` of one stacked factor into f32 [rows][cols]
+ * (out, device).  Bit-exact restatement of dequantize_nf4 / dequantize_int8
+ * (loader/latent_loader.py:133-145, 161-170): one fp32 multiply per element.
+ */
+int latent_unpack(const latent_factor* factor, int64_t expert, float* out, latent_stream_t stream);
+
+/*
+ * Per-row NF4 pack of f32 [rows][cols] (device) into codes u8 [rows][cols/2]
+ * and fp16 scales [rows][cols/32]; cols % 32 == 0.  Byte-identical to
+ * quantize_nf4 per row (loader/latent_loader.py:111-130,
+ * loader/write_latent_gguf.py:227-257).
+ */
+int latent_pack_nf4(const float* values, int64_t rows, int64_t cols, uint8_t* codes, uint16_t* scales,
+                    latent_stream_t stream);
+
+/*
+ * INT8 pack of `n_groups` groups of 32 f32 values (device): q i8 [n][32] and
+ * fp16 scales [n].  Byte-identical to quantize_int8(group_size=32)
+ * (loader/latent_loader.py:148-158).
+ */
+int latent_pack_int8(const float* values, int64_t n_groups, int8_t* q, uint16_t* scales, latent_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LATENT_FFN_H */

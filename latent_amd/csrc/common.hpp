@@ -1,0 +1,100 @@
+// Shared device helpers for the gfx950 LATENT kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/latent_ffn.h"
+
+namespace latent {
+
+constexpr int kGroup = 32;     // elements per quantization group (one row segment)
+constexpr int kGroupBytes = 16; // NF4 bytes of a group: one 128-bit load
+constexpr int kWave = 64;
+
+// The 16 NF4 levels, loader/latent_loader.py:28-48.  Identical float literals,
+// so each rounds to the same binary32 value as np.float32(literal).
+__host__ __device__ constexpr float nf4_level(int c) {
+  constexpr float t[16] = {
+      -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
+      -0.09105004f, 0.0f,         0.0795803f,   0.1609302f,  0.2461123f,   0.33791524f,
+      0.44070983f,  0.562617f,    0.72295684f,  1.0f,
+  };
+  return t[c & 15];
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ float load_act(const void* p, int dtype, int64_t i) {
+  if (dtype == LATENT_F32) return static_cast<const float*>(p)[i];
+  uint16_t b = static_cast<const uint16_t*>(p)[i];
+  if (dtype == LATENT_F16) return half_bits_to_float(b);
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);  // bf16
+}
+
+// Lookup of an expert's per-group INT8 extension (see latent_factor).
+struct Int8Ext {
+  const uint32_t* bitmap;     // [E][rows][words]
+  const int32_t* row_offset;  // [E][rows]
+  const int8_t* data;         // [n][32]
+};
+
+// One stacked factor with the expert strides resolved.
+struct Factor {
+  const uint8_t* codes;
+  const uint16_t* scales;
+  Int8Ext ext;
+  int64_t rows, cols;
+  __host__ __device__ int64_t code_stride() const { return cols / 2; }      // bytes per row
+  __host__ __device__ int64_t scale_stride() const { return cols / kGroup; } // groups per row
+  __host__ __device__ int words() const { return static_cast<int>((cols / kGroup + 31) / 32); }
+};
+
+__device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
+
+// Decode one 32-element group of row `row` of expert `e` into fp32 codebook
+// values (not yet scaled).  NF4: 16 bytes, low nibble first.  INT8: 32 bytes
+// of the side buffer.  The group's scale is returned separately by the caller.
+template <bool kHasInt8>
+__device__ __forceinline__ void decode_group(const Factor& f, int64_t e, int64_t row, int g, const float* lut,
+                                             float v[kGroup]) {
+  const int64_t erow = e * f.rows + row;
+  if (kHasInt8) {
+    const uint32_t* bm = f.ext.bitmap + erow * f.words();
+    const uint32_t word = bm[g >> 5];
+    if ((word >> (g & 31)) & 1u) {
+      int before = popc(word & ((1u << (g & 31)) - 1u));
+      for (int w = 0; w < (g >> 5); ++w) before += popc(bm[w]);
+      const int64_t idx = static_cast<int64_t>(f.ext.row_offset[erow]) + before;
+      const uint4* q = reinterpret_cast<const uint4*>(f.ext.data + idx * kGroup);
+      const uint4 q0 = q[0], q1 = q[1];
+      const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) v[i * 4 + b] = static_cast<float>(static_cast<int8_t>((qw[i] >> (8 * b)) & 0xFF));
+      }
+      return;
+    }
+  }
+  const uint4 c = *reinterpret_cast<const uint4*>(f.codes + erow * f.code_stride() + static_cast<int64_t>(g) * kGroupBytes);
+  const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) v[i * 8 + n] = lut[(cw[i] >> (4 * n)) & 15u];
+  }
+}
+
+__device__ __forceinline__ float group_scale(const Factor& f, int64_t e, int64_t row, int g) {
+  return half_bits_to_float(f.scales[(e * f.rows + row) * f.scale_stride() + g]);
+}
+
+__device__ __forceinline__ void atomic_add_f32(float* p, float v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace latent

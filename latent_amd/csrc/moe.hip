@@ -1,0 +1,651 @@
+// MoE-layer LATENT expert FFN on gfx950: routed-token gather + wave64 NF4 GEMV chain.
+//
+// Replaces kernels/latent_fused_expert_ffn.cu:27-132 (dispatch / per-slot copy /
+// reduce kernels) and its host launcher :134-292.  The reference launches one
+// 128-thread block per (token, slot) and re-reads every factor per token; here
+// tokens are grouped by expert on the device so each routed expert's packed
+// factors stream from HBM once per call, split over many workgroups:
+//
+//   prep     group (token, slot) pairs by expert (histogram, scan, scatter) and
+//            clear the fp32 accumulators.
+//   phase A  [x]           . A_g | A_u  -> g_lat, u_lat   (split over rows of A)
+//   phase BC [g_lat,u_lat] . B_g , B_u  -> h = SiLU(g)*u  (split over ff columns)
+//            h[cols]       . A_d[cols]  -> d_lat           (same ff slice)
+//   phase D  d_lat         . B_d        -> y, weighted into out (split over d)
+//
+// Every phase is a GEMV over a row-major [K][N] factor whose 32-column groups
+// are one 128-bit load of NF4 codes + one fp16 scale.  A lane owns one group
+// (32 output columns) and walks rows; the activation for the row is multiplied
+// by the group scale once and then by 32 codebook levels read from a 16-entry
+// LDS table.  Lanes sharing a group are combined with wave shuffles, waves
+// through LDS, workgroups with fp32 atomics.  All arithmetic is fp32.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace latent {
+
+Factor make_factor(const latent_factor& f);
+int check_factor(const latent_factor& f);
+
+namespace {
+
+__constant__ float kLevelsMoe[16] = {
+    nf4_level(0),  nf4_level(1),  nf4_level(2),  nf4_level(3),  nf4_level(4),  nf4_level(5),
+    nf4_level(6),  nf4_level(7),  nf4_level(8),  nf4_level(9),  nf4_level(10), nf4_level(11),
+    nf4_level(12), nf4_level(13), nf4_level(14), nf4_level(15),
+};
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kMaxExperts = 4096;  // LDS histogram of the prep kernel
+constexpr int kMaxRank = 512;
+constexpr int kRouteThreads = 1024;
+enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
+
+struct MoeParams {
+  Factor fac[6];
+  const void* x;
+  const int32_t* ids;
+  const void* weights;
+  const int32_t* ranks;
+  float* out;
+  int* meta;  // [0] active experts, [1] invalid ids seen
+  int* act_expert;
+  int* act_start;
+  int* act_count;
+  int* pair_tok;
+  int* pair_slot;
+  float* pair_w;
+  float* gu;  // [P][2R]
+  float* dl;  // [P][R]
+  int x_dtype, w_dtype;
+  int T, d, ff, E, K, R;
+  int wbd, out_mode;
+  int a_max;             // upper bound of active experts (grid sizing)
+  int ra, n_a;           // phase A: rows per item, items per expert (2 * ceil(d/ra))
+  int cb, n_bc;          // phase BC: ff columns per item, items per expert
+  int cd, n_d;           // phase D: d columns per item, items per expert
+  int64_t zero_floats;   // accumulator floats cleared by prep
+};
+
+__device__ __forceinline__ int ilog2(int v) { return 31 - __builtin_clz(v); }
+__device__ __forceinline__ int next_pow2(int v) { return v <= 1 ? 1 : 1 << (32 - __builtin_clz(v - 1)); }
+
+__device__ __forceinline__ int rank_of(const MoeParams& p, int e, int kind) {
+  if (!p.ranks) return p.R;
+  const int r = p.ranks[e * 3 + kind];
+  return r < 0 ? 0 : (r > p.R ? p.R : r);
+}
+
+// Workgroup b -> (active expert a, item i) so that all items of one expert land
+// on the same XCD (workgroups are dispatched to the 8 XCDs round-robin): their
+// shared activations and atomics then stay in one L2.
+__device__ __forceinline__ bool map_item(int b, int n_items, int n_active, int& a, int& i) {
+  const int x = b & 7;
+  const int j = b >> 3;
+  a = x + 8 * (j / n_items);
+  i = j - (j / n_items) * n_items;
+  return a < n_active;
+}
+
+// ---------------------------------------------------------------------------
+// prep: workgroup 0 groups pairs by expert; the others clear accumulators.
+// ---------------------------------------------------------------------------
+__device__ void route_block(const MoeParams& p) {
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int fill[kMaxExperts];
+  __shared__ int scan_c[kRouteThreads];
+  __shared__ int scan_a[kRouteThreads];
+  __shared__ int bad;
+  const int tid = threadIdx.x;
+  const int P = p.T * p.K;
+  for (int e = tid; e < p.E; e += kRouteThreads) {
+    cnt[e] = 0;
+    fill[e] = 0;
+  }
+  if (tid == 0) bad = 0;
+  __syncthreads();
+  for (int i = tid; i < P; i += kRouteThreads) {
+    const int e = p.ids[i];
+    if (e >= 0 && e < p.E)
+      atomicAdd(&cnt[e], 1);
+    else if (e >= p.E)
+      atomicAdd(&bad, 1);
+  }
+  __syncthreads();
+  // Block scan over experts: each thread owns a contiguous run of experts.
+  const int per = (p.E + kRouteThreads - 1) / kRouteThreads;
+  const int e0 = min(p.E, tid * per), e1 = min(p.E, e0 + per);
+  int sc = 0, sa = 0;
+  for (int e = e0; e < e1; ++e) {
+    sc += cnt[e];
+    sa += cnt[e] > 0;
+  }
+  scan_c[tid] = sc;
+  scan_a[tid] = sa;
+  __syncthreads();
+  for (int off = 1; off < kRouteThreads; off <<= 1) {
+    const int vc = tid >= off ? scan_c[tid - off] : 0;
+    const int va = tid >= off ? scan_a[tid - off] : 0;
+    __syncthreads();
+    scan_c[tid] += vc;
+    scan_a[tid] += va;
+    __syncthreads();
+  }
+  int start = scan_c[tid] - sc;
+  int act = scan_a[tid] - sa;
+  for (int e = e0; e < e1; ++e) {
+    const int c = cnt[e];
+    fill[e] = start;  // reuse as the running insert position
+    if (c > 0) {
+      p.act_expert[act] = e;
+      p.act_start[act] = start;
+      p.act_count[act] = c;
+      ++act;
+    }
+    start += c;
+  }
+  if (tid == kRouteThreads - 1) {
+    p.meta[0] = scan_a[kRouteThreads - 1];
+    p.meta[1] = bad;
+  }
+  __syncthreads();
+  for (int i = tid; i < P; i += kRouteThreads) {
+    const int e = p.ids[i];
+    if (e >= 0 && e < p.E) {
+      const int pos = atomicAdd(&fill[e], 1);
+      p.pair_tok[pos] = i / p.K;
+      p.pair_slot[pos] = i - (i / p.K) * p.K;
+      p.pair_w[pos] = load_act(p.weights, p.w_dtype, i);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
+  if (blockIdx.x == 0) {
+    route_block(p);
+    return;
+  }
+  const int64_t nblk = gridDim.x - 1;
+  const int64_t t0 = (blockIdx.x - 1) * static_cast<int64_t>(kRouteThreads) + threadIdx.x;
+  const int64_t stride = nblk * kRouteThreads;
+  // Accumulators gu and dl are contiguous: zero_floats covers both.
+  float4* acc4 = reinterpret_cast<float4*>(p.gu);
+  const int64_t n4 = p.zero_floats / 4;
+  for (int64_t i = t0; i < n4; i += stride) acc4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (p.out_mode == LATENT_OUT_REDUCED) {
+    float4* o4 = reinterpret_cast<float4*>(p.out);
+    const int64_t no = static_cast<int64_t>(p.T) * p.d / 4;
+    for (int64_t i = t0; i < no; i += stride) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    // Per-slot output: only dropped slots are never written by phase D.
+    const int64_t rows = static_cast<int64_t>(p.T) * p.K;
+    const int64_t d4 = p.d / 4;
+    for (int64_t i = t0; i < rows * d4; i += stride) {
+      const int64_t r = i / d4;
+      const int e = p.ids[r];
+      if (e < 0 || e >= p.E) reinterpret_cast<float4*>(p.out)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV building blocks
+// ---------------------------------------------------------------------------
+// acc[t][j] += sum over this lane's rows of vin[t][row] * scale(row, g) * level(code(row, g*32+j))
+// Rows: row_begin, row_begin + step, ... < row_end.  vin[t][row] = vin[t*vstride + row - vbase].
+template <int MB, bool kInt8>
+__device__ __forceinline__ void accumulate_rows(const Factor& f, int64_t e, int row_begin, int row_end, int step, int g,
+                                                const float* lut, const float* vin, int vstride, int vbase, int m,
+                                                float (&acc)[MB][kGroup]) {
+  if constexpr (kInt8) {
+    for (int row = row_begin; row < row_end; row += step) {
+      float v[kGroup];
+      decode_group<true>(f, e, row, g, lut, v);
+      const float s = group_scale(f, e, row, g);
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        if (t < m) {
+          const float xs = vin[t * vstride + row - vbase] * s;
+#pragma unroll
+          for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+        }
+      }
+    }
+  } else {
+    constexpr int U = MB == 1 ? 4 : 2;
+    const int64_t cstride = f.code_stride();
+    const int64_t sstride = f.scale_stride();
+    const uint8_t* cbase = f.codes + e * f.rows * cstride + static_cast<int64_t>(g) * kGroupBytes;
+    const uint16_t* sbase = f.scales + e * f.rows * sstride + g;
+    int row = row_begin;
+    for (; row + (U - 1) * step < row_end; row += U * step) {
+      uint4 c[U];
+      float s[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        c[u] = *reinterpret_cast<const uint4*>(cbase + static_cast<int64_t>(row + u * step) * cstride);
+        s[u] = half_bits_to_float(sbase[static_cast<int64_t>(row + u * step) * sstride]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float v[kGroup];
+        const uint32_t cw[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+          for (int n = 0; n < 8; ++n) v[i * 8 + n] = lut[(cw[i] >> (4 * n)) & 15u];
+        }
+#pragma unroll
+        for (int t = 0; t < MB; ++t) {
+          if (t < m) {
+            const float xs = vin[t * vstride + row + u * step - vbase] * s[u];
+#pragma unroll
+            for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+          }
+        }
+      }
+    }
+    for (; row < row_end; row += step) {
+      const uint4 c = *reinterpret_cast<const uint4*>(cbase + static_cast<int64_t>(row) * cstride);
+      const float s = half_bits_to_float(sbase[static_cast<int64_t>(row) * sstride]);
+      float v[kGroup];
+      const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) v[i * 8 + n] = lut[(cw[i] >> (4 * n)) & 15u];
+      }
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        if (t < m) {
+          const float xs = vin[t * vstride + row - vbase] * s;
+#pragma unroll
+          for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+        }
+      }
+    }
+  }
+}
+
+// Sum acc over the lanes of a wave that share group g (lanes differing in the
+// bits at and above log2(lpr)), then the first lpr lanes store the wave's
+// partial to red[wave][t][g*32 + j] (red row length ncols).
+template <int MB>
+__device__ __forceinline__ void wave_reduce_store(float (&acc)[MB][kGroup], int lpr, int lane, int wave, int ngroups,
+                                                  int m, float* red, int ncols) {
+#pragma unroll
+  for (int t = 0; t < MB; ++t) {
+    if (t < m) {
+      for (int off = lpr; off < kWave; off <<= 1) {
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
+      }
+    }
+  }
+  if (lane < lpr && lane < ngroups) {
+#pragma unroll
+    for (int t = 0; t < MB; ++t) {
+      if (t < m) {
+        float* dst = red + (wave * MB + t) * ncols + lane * kGroup;
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) dst[j] = acc[t][j];
+      }
+    }
+  }
+}
+
+template <int MB>
+__device__ __forceinline__ void zero_acc(float (&acc)[MB][kGroup]) {
+#pragma unroll
+  for (int t = 0; t < MB; ++t)
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) acc[t][j] = 0.f;
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// ---------------------------------------------------------------------------
+// phase A: x . A_g and x . A_u over a slice of rows of A
+// ---------------------------------------------------------------------------
+template <int MB, bool kInt8>
+__global__ void __launch_bounds__(kThreads) phase_a_kernel(MoeParams p) {
+  extern __shared__ float smem[];
+  float* lut = smem;                 // 16
+  float* xin = smem + 16;            // [MB][ra]
+  float* red = xin + MB * p.ra;      // [kWaves][MB][R]
+  int a, item;
+  if (!map_item(blockIdx.x, p.n_a, p.meta[0], a, item)) return;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  if (tid < 16) lut[tid] = kLevelsMoe[tid];
+  const int kind = item & 1;  // 0 gate, 1 up
+  const int chunk = item >> 1;
+  const Factor f = kind == 0 ? p.fac[F_GATE_A] : p.fac[F_UP_A];
+  const int e = p.act_expert[a], s0 = p.act_start[a], mtot = p.act_count[a];
+  const int ng = (rank_of(p, e, kind) + kGroup - 1) / kGroup;
+  if (ng == 0) return;
+  const int lpr = next_pow2(ng), rpw = kWave / lpr;
+  const int g = lane & (lpr - 1), ro = lane >> ilog2(lpr);
+  const int r0 = chunk * p.ra, r1 = min(p.d, r0 + p.ra), nrows = r1 - r0;
+  const int ncols = ng * kGroup;
+  for (int tb = 0; tb < mtot; tb += MB) {
+    const int m = min(MB, mtot - tb);
+    for (int i = tid; i < m * nrows; i += kThreads) {
+      const int t = i / nrows, rr = i - t * nrows;
+      const int tok = p.pair_tok[s0 + tb + t];
+      xin[t * p.ra + rr] = load_act(p.x, p.x_dtype, static_cast<int64_t>(tok) * p.d + r0 + rr);
+    }
+    __syncthreads();
+    float acc[MB][kGroup];
+    zero_acc(acc);
+    if (g < ng)
+      accumulate_rows<MB, kInt8>(f, e, r0 + wave * rpw + ro, r1, kWaves * rpw, g, lut, xin, p.ra, r0, m, acc);
+    wave_reduce_store<MB>(acc, lpr, lane, wave, ng, m, red, p.R);
+    __syncthreads();
+    for (int i = tid; i < m * ncols; i += kThreads) {
+      const int t = i / ncols, col = i - t * ncols;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v += red[(w * MB + t) * p.R + col];
+      atomic_add_f32(p.gu + static_cast<int64_t>(s0 + tb + t) * (2 * p.R) + kind * p.R + col, v);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// phase BC: g,u over a slice of ff columns, h = SiLU(g)*u, then h . A_d[slice]
+// ---------------------------------------------------------------------------
+template <int MB, bool kInt8>
+__global__ void __launch_bounds__(kThreads) phase_bc_kernel(MoeParams p) {
+  extern __shared__ float smem[];
+  float* lut = smem;                      // 16
+  float* lat = smem + 16;                 // [MB][2R]
+  float* hs = lat + MB * 2 * p.R;         // [2][MB][cb]
+  float* red = hs + 2 * MB * p.cb;        // [kWaves][MB][max(cb, R)]
+  const int redw = max(p.cb, p.R);
+  int a, item;
+  if (!map_item(blockIdx.x, p.n_bc, p.meta[0], a, item)) return;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  if (tid < 16) lut[tid] = kLevelsMoe[tid];
+  const int e = p.act_expert[a], s0 = p.act_start[a], mtot = p.act_count[a];
+  const int c0 = item * p.cb, ncol = min(p.cb, p.ff - c0), gpc = ncol / kGroup;
+  const int lpr_b = next_pow2(p.cb / kGroup), rpw_b = kWave / lpr_b;
+  const int gb = lane & (lpr_b - 1), rob = lane >> ilog2(lpr_b);
+  const int rank_d = rank_of(p, e, 2);
+  const int ngd = (rank_d + kGroup - 1) / kGroup;
+  const int lpr_d = next_pow2(max(ngd, 1)), rpw_d = kWave / lpr_d;
+  const int gd = lane & (lpr_d - 1), rod = lane >> ilog2(lpr_d);
+  for (int tb = 0; tb < mtot; tb += MB) {
+    const int m = min(MB, mtot - tb);
+    for (int i = tid; i < m * 2 * p.R; i += kThreads) {
+      const int t = i / (2 * p.R), col = i - t * 2 * p.R;
+      lat[t * 2 * p.R + col] = p.gu[static_cast<int64_t>(s0 + tb + t) * 2 * p.R + col];
+    }
+    __syncthreads();
+    for (int kind = 0; kind < 2; ++kind) {
+      const Factor f = kind == 0 ? p.fac[F_GATE_B] : p.fac[F_UP_B];
+      const int rk = rank_of(p, e, kind);
+      float acc[MB][kGroup];
+      zero_acc(acc);
+      if (gb < gpc)
+        accumulate_rows<MB, kInt8>(f, e, wave * rpw_b + rob, rk, kWaves * rpw_b, c0 / kGroup + gb, lut,
+                                   lat + kind * p.R, 2 * p.R, 0, m, acc);
+      wave_reduce_store<MB>(acc, lpr_b, lane, wave, gpc, m, red, redw);
+      __syncthreads();
+      for (int i = tid; i < m * ncol; i += kThreads) {
+        const int t = i / ncol, col = i - t * ncol;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += red[(w * MB + t) * redw + col];
+        hs[(kind * MB + t) * p.cb + col] = v;
+      }
+      __syncthreads();
+    }
+    // h = SiLU(g) * u  (x router weight when weighting before down), in hs[0]
+    for (int i = tid; i < m * ncol; i += kThreads) {
+      const int t = i / ncol, col = i - t * ncol;
+      float h = silu_f32(hs[t * p.cb + col]) * hs[(MB + t) * p.cb + col];
+      if (p.wbd) h *= p.pair_w[s0 + tb + t];
+      hs[t * p.cb + col] = h;
+    }
+    __syncthreads();
+    if (ngd > 0) {
+      float acc[MB][kGroup];
+      zero_acc(acc);
+      if (gd < ngd)
+        accumulate_rows<MB, kInt8>(p.fac[F_DOWN_A], e, c0 + wave * rpw_d + rod, c0 + ncol, kWaves * rpw_d, gd, lut, hs,
+                                   p.cb, c0, m, acc);
+      wave_reduce_store<MB>(acc, lpr_d, lane, wave, ngd, m, red, redw);
+      __syncthreads();
+      const int ncols_d = ngd * kGroup;
+      for (int i = tid; i < m * ncols_d; i += kThreads) {
+        const int t = i / ncols_d, col = i - t * ncols_d;
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += red[(w * MB + t) * redw + col];
+        atomic_add_f32(p.dl + static_cast<int64_t>(s0 + tb + t) * p.R + col, v);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// phase D: y = d_lat . B_d over a slice of d columns, then the combine
+// ---------------------------------------------------------------------------
+template <int MB, bool kInt8>
+__global__ void __launch_bounds__(kThreads) phase_d_kernel(MoeParams p) {
+  extern __shared__ float smem[];
+  float* lut = smem;             // 16
+  float* lat = smem + 16;        // [MB][R]
+  float* red = lat + MB * p.R;   // [kWaves][MB][cd]
+  int a, item;
+  if (!map_item(blockIdx.x, p.n_d, p.meta[0], a, item)) return;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  if (tid < 16) lut[tid] = kLevelsMoe[tid];
+  const int e = p.act_expert[a], s0 = p.act_start[a], mtot = p.act_count[a];
+  const int c0 = item * p.cd, ncol = min(p.cd, p.d - c0), gpc = ncol / kGroup;
+  const int lpr = next_pow2(p.cd / kGroup), rpw = kWave / lpr;
+  const int g = lane & (lpr - 1), ro = lane >> ilog2(lpr);
+  const int rk = rank_of(p, e, 2);
+  for (int tb = 0; tb < mtot; tb += MB) {
+    const int m = min(MB, mtot - tb);
+    for (int i = tid; i < m * p.R; i += kThreads) {
+      const int t = i / p.R, col = i - t * p.R;
+      lat[t * p.R + col] = p.dl[static_cast<int64_t>(s0 + tb + t) * p.R + col];
+    }
+    __syncthreads();
+    float acc[MB][kGroup];
+    zero_acc(acc);
+    if (g < gpc)
+      accumulate_rows<MB, kInt8>(p.fac[F_DOWN_B], e, wave * rpw + ro, rk, kWaves * rpw, c0 / kGroup + g, lut, lat, p.R,
+                                 0, m, acc);
+    wave_reduce_store<MB>(acc, lpr, lane, wave, gpc, m, red, p.cd);
+    __syncthreads();
+    for (int i = tid; i < m * ncol; i += kThreads) {
+      const int t = i / ncol, col = i - t * ncol;
+      float y = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) y += red[(w * MB + t) * p.cd + col];
+      const int pair = s0 + tb + t;
+      const int tok = p.pair_tok[pair];
+      if (p.out_mode == LATENT_OUT_REDUCED) {
+        const float wgt = p.wbd ? 1.0f : p.pair_w[pair];
+        atomic_add_f32(p.out + static_cast<int64_t>(tok) * p.d + c0 + col, wgt * y);
+      } else {
+        p.out[(static_cast<int64_t>(tok) * p.K + p.pair_slot[pair]) * p.d + c0 + col] = y;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Layout {
+  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, gu, dl, total;
+};
+
+Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
+  Layout L{};
+  const int64_t P = T * K;
+  const int64_t amax = std::max<int64_t>(1, std::min(E, P));
+  size_t off = 0;
+  L.meta = off;       off = align_up(off + 64 * sizeof(int));
+  L.act_expert = off; off = align_up(off + amax * sizeof(int));
+  L.act_start = off;  off = align_up(off + amax * sizeof(int));
+  L.act_count = off;  off = align_up(off + amax * sizeof(int));
+  L.pair_tok = off;   off = align_up(off + P * sizeof(int));
+  L.pair_slot = off;  off = align_up(off + P * sizeof(int));
+  L.pair_w = off;     off = align_up(off + P * sizeof(float));
+  L.gu = off;         off += P * 2 * R * sizeof(float);  // gu and dl contiguous (one clear)
+  L.dl = off;         off = align_up(off + P * R * sizeof(float));
+  L.total = off;
+  return L;
+}
+
+int validate(const latent_moe_args& a) {
+  if (a.n_tokens < 0 || a.n_embd <= 0 || a.n_ff <= 0 || a.n_expert <= 0 || a.n_expert_used <= 0 || a.max_rank <= 0)
+    return LATENT_E_INVALID;
+  if (a.n_embd % kGroup || a.n_ff % kGroup || a.max_rank % kGroup) return LATENT_E_INVALID;
+  if (a.x_dtype < LATENT_F32 || a.x_dtype > LATENT_BF16) return LATENT_E_INVALID;
+  if (a.weights_dtype != LATENT_F32 && a.weights_dtype != LATENT_F16) return LATENT_E_INVALID;
+  if (a.out_mode != LATENT_OUT_REDUCED && a.out_mode != LATENT_OUT_PER_SLOT) return LATENT_E_INVALID;
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  const int64_t rows[6] = {a.n_embd, a.max_rank, a.n_embd, a.max_rank, a.n_ff, a.max_rank};
+  const int64_t cols[6] = {a.max_rank, a.n_ff, a.max_rank, a.n_ff, a.max_rank, a.n_embd};
+  for (int i = 0; i < 6; ++i) {
+    const int st = check_factor(*fs[i]);
+    if (st != LATENT_OK) return st;
+    if (fs[i]->rows != rows[i] || fs[i]->cols != cols[i]) return LATENT_E_INVALID;
+  }
+  if (a.n_expert > kMaxExperts || a.max_rank > kMaxRank) return LATENT_E_UNSUPPORTED;
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  if (a.n_tokens > (1 << 24) || P > (1 << 26) || a.n_embd > (1 << 20) || a.n_ff > (1 << 20)) return LATENT_E_UNSUPPORTED;
+  return LATENT_OK;
+}
+
+int pick_pow2_chunk(int64_t per_expert_extent, int64_t experts, int64_t target_items, int lo, int hi) {
+  int c = hi;
+  while (c > lo && experts * ((per_expert_extent + c - 1) / c) < target_items) c /= 2;
+  return c;
+}
+
+template <int MB, bool kInt8>
+int launch_phases(const MoeParams& p, hipStream_t s) {
+  const unsigned a_groups = static_cast<unsigned>((p.a_max + 7) / 8);
+  const size_t lds_a = (16 + MB * p.ra + kWaves * MB * p.R) * sizeof(float);
+  hipLaunchKernelGGL((phase_a_kernel<MB, kInt8>), dim3(8 * a_groups * p.n_a), dim3(kThreads), lds_a, s, p);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  const size_t lds_bc = (16 + MB * 2 * p.R + 2 * MB * p.cb + kWaves * MB * std::max(p.cb, p.R)) * sizeof(float);
+  hipLaunchKernelGGL((phase_bc_kernel<MB, kInt8>), dim3(8 * a_groups * p.n_bc), dim3(kThreads), lds_bc, s, p);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  const size_t lds_d = (16 + MB * p.R + kWaves * MB * p.cd) * sizeof(float);
+  hipLaunchKernelGGL((phase_d_kernel<MB, kInt8>), dim3(8 * a_groups * p.n_d), dim3(kThreads), lds_d, s, p);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  return LATENT_OK;
+}
+
+}  // namespace
+}  // namespace latent
+
+using namespace latent;
+
+extern "C" int latent_version(void) { return 100; }
+
+extern "C" const char* latent_status_string(int status) {
+  switch (status) {
+    case LATENT_OK: return "ok";
+    case LATENT_E_INVALID: return "invalid argument";
+    case LATENT_E_UNSUPPORTED: return "unsupported configuration";
+    case LATENT_E_WORKSPACE: return "workspace missing or too small";
+    case LATENT_E_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes) {
+  if (!args || !bytes) return LATENT_E_INVALID;
+  const int st = validate(*args);
+  if (st != LATENT_OK) return st;
+  *bytes = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank).total;
+  return LATENT_OK;
+}
+
+extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
+  if (!args) return LATENT_E_INVALID;
+  const latent_moe_args& a = *args;
+  int st = validate(a);
+  if (st != LATENT_OK) return st;
+  if (a.n_tokens == 0) return LATENT_OK;
+  if (!a.x || !a.ids || !a.weights || !a.out) return LATENT_E_INVALID;
+  if ((reinterpret_cast<uintptr_t>(a.out) & 15u) != 0) return LATENT_E_INVALID;
+  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
+  if (!a.workspace || a.workspace_bytes < L.total) return LATENT_E_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a.workspace) & (kAlign - 1)) != 0) return LATENT_E_WORKSPACE;
+
+  MoeParams p{};
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  bool any_int8 = false;
+  for (int i = 0; i < 6; ++i) {
+    p.fac[i] = make_factor(*fs[i]);
+    any_int8 = any_int8 || fs[i]->int8_bitmap != nullptr;
+  }
+  char* ws = static_cast<char*>(a.workspace);
+  p.x = a.x;
+  p.ids = a.ids;
+  p.weights = a.weights;
+  p.ranks = a.ranks;
+  p.out = static_cast<float*>(a.out);
+  p.meta = reinterpret_cast<int*>(ws + L.meta);
+  p.act_expert = reinterpret_cast<int*>(ws + L.act_expert);
+  p.act_start = reinterpret_cast<int*>(ws + L.act_start);
+  p.act_count = reinterpret_cast<int*>(ws + L.act_count);
+  p.pair_tok = reinterpret_cast<int*>(ws + L.pair_tok);
+  p.pair_slot = reinterpret_cast<int*>(ws + L.pair_slot);
+  p.pair_w = reinterpret_cast<float*>(ws + L.pair_w);
+  p.gu = reinterpret_cast<float*>(ws + L.gu);
+  p.dl = reinterpret_cast<float*>(ws + L.dl);
+  p.x_dtype = a.x_dtype;
+  p.w_dtype = a.weights_dtype;
+  p.T = static_cast<int>(a.n_tokens);
+  p.d = static_cast<int>(a.n_embd);
+  p.ff = static_cast<int>(a.n_ff);
+  p.E = static_cast<int>(a.n_expert);
+  p.K = static_cast<int>(a.n_expert_used);
+  p.R = static_cast<int>(a.max_rank);
+  p.wbd = a.weight_before_down ? 1 : 0;
+  p.out_mode = a.out_mode;
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  p.a_max = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P)));
+  p.zero_floats = P * 3 * a.max_rank;
+
+  // Work split: enough items to fill 256 CUs even when few experts are routed.
+  const int MB = a.n_tokens == 1 ? 1 : 4;
+  const int ra_hi = std::max(128, std::min(2048, static_cast<int>((48 * 1024 / 4 - 16 - 4 * MB * p.R) / MB) & ~127));
+  p.ra = pick_pow2_chunk(p.d, 2LL * p.a_max, 2048, 128, ra_hi);
+  p.n_a = 2 * ((p.d + p.ra - 1) / p.ra);
+  p.cb = pick_pow2_chunk(p.ff, p.a_max, 1024, 128, 256);
+  p.n_bc = (p.ff + p.cb - 1) / p.cb;
+  p.cd = pick_pow2_chunk(p.d, p.a_max, 2048, 128, 512);
+  p.n_d = (p.d + p.cd - 1) / p.cd;
+
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();  // clear a stale error so the checks below see only ours
+  const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? P / a.n_expert_used * a.n_embd / 4
+                                                                                  : P * a.n_embd / 4);
+  const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));
+  hipLaunchKernelGGL(prep_kernel, dim3(1 + zero_blocks), dim3(kRouteThreads), 0, s, p);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  if (MB == 1)
+    st = any_int8 ? launch_phases<1, true>(p, s) : launch_phases<1, false>(p, s);
+  else
+    st = any_int8 ? launch_phases<4, true>(p, s) : launch_phases<4, false>(p, s);
+  return st;
+}

@@ -1,0 +1,53 @@
+"""Test helpers that move layers between the oracle (host) and the product (GPU)."""
+
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+
+from oracle import latent_ref as ref
+
+
+def to_device(layer: ref.StackedLayer):
+    """Upload an oracle StackedLayer (incl. INT8 extension and ranks) to the GPU."""
+    import torch
+
+    from latent_amd import DeviceFactor, StackedLayer
+
+    facs = {}
+    for name in ref.FACTOR_NAMES:
+        f = layer.factors[name]
+        ext = None
+        if f.int8 is not None:
+            ext = (f.int8.bitmap, f.int8.row_offset, f.int8.data)
+        facs[name] = DeviceFactor.from_numpy(f.codes, f.scales, ext)
+    ranks = None if layer.ranks is None else torch.from_numpy(layer.ranks.astype(np.int32)).cuda()
+    return StackedLayer(**facs, ranks=ranks)
+
+
+def subset_to_host(dev_layer, experts: Sequence[int]) -> ref.StackedLayer:
+    """Oracle StackedLayer holding only `experts` (NF4 only) of a device layer."""
+    import torch
+
+    sel = torch.as_tensor(np.asarray(experts, dtype=np.int64), device=dev_layer.gate_a.codes.device)
+    facs = {}
+    for name, f in dev_layer.factors().items():
+        if f.has_int8:
+            raise NotImplementedError("subset copy of INT8 groups")
+        codes = f.codes.index_select(0, sel).cpu().numpy()
+        scales = f.scales.index_select(0, sel).cpu().numpy().view(np.float16)
+        facs[name] = ref.StackedFactor(codes, scales)
+    ranks = None if dev_layer.ranks is None else dev_layer.ranks.index_select(0, sel).cpu().numpy()
+    return ref.StackedLayer(factors=facs, d=dev_layer.d, ff=dev_layer.ff, max_rank=dev_layer.max_rank, ranks=ranks)
+
+
+def remap_ids(ids: np.ndarray, n_expert: int):
+    """(distinct valid experts, ids renumbered into that list; invalid -> -1)."""
+    ids = np.asarray(ids)
+    valid = (ids >= 0) & (ids < n_expert)
+    experts = np.unique(ids[valid])
+    lut = -np.ones(n_expert, np.int64)
+    lut[experts] = np.arange(experts.size)
+    out = np.where(valid, lut[np.clip(ids, 0, n_expert - 1)], -1).astype(np.int32)
+    return experts, out

@@ -1,0 +1,186 @@
+"""Pins the oracle's runtime, stacked layout and layer forward.
+
+loader/latent_runtime.py:13-73, loader/write_latent_gguf.py:101-123, 227-257.
+Checks: float64 dense algebra on the dequantized factors, the reference tests'
+own properties, literal per-row loops of the writer, and brute-force loops
+over (token, slot).
+"""
+
+import numpy as np
+import pytest
+from scipy.special import expit
+
+from oracle import latent_ref as ref
+from oracle import routing, synth
+
+
+def test_silu_closed_form():
+    x = np.array([-1e4, -100.0, -10.0, -1.0, -1e-6, 0.0, 1e-6, 0.5, 3.0, 80.0, 1e4], np.float32)
+    want = (x.astype(np.float64) * expit(x.astype(np.float64))).astype(np.float32)
+    np.testing.assert_allclose(ref.silu(x), want, rtol=1e-6, atol=1e-30)
+    assert ref.silu(np.array([np.float32(3e38)]))[0] == np.float32(1e30)  # clip at +-1e30
+
+
+def _pairs(rng, d, ff, r):
+    out = []
+    for n_in, n_out in ((d, ff), (d, ff), (ff, d)):
+        a, b = synth.closed_form_factors(rng, n_in, n_out, r)
+        out.append(ref.FactorPair(a, b))
+    return out
+
+
+def test_swiglu_expert_matches_float64_dense():
+    rng = np.random.default_rng(1)
+    gate, up, down = _pairs(rng, 96, 64, 32)
+    x = rng.standard_normal((5, 96)).astype(np.float32)
+    y = ref.swiglu_expert(x, gate, up, down)
+    x64 = x.astype(np.float64)
+    g = x64 @ (gate.a.astype(np.float64) @ gate.b)
+    u = x64 @ (up.a.astype(np.float64) @ up.b)
+    h = g / (1 + np.exp(-g)) * u
+    want = h @ (down.a.astype(np.float64) @ down.b)
+    assert ref.rel_l2(want, y) < 1e-5
+
+
+def test_weight_semantics():
+    # tests/test_latent_loader.py:130-141 (before == after * w) and the reference's
+    # behaviour of ignoring `weight` when it is applied after down.
+    rng = np.random.default_rng(2)
+    gate, up, down = _pairs(rng, 64, 32, 32)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    before = ref.swiglu_expert(x, gate, up, down, weight=0.25, weight_before_down=True)
+    plain = ref.swiglu_expert(x, gate, up, down)
+    np.testing.assert_allclose(before, plain * np.float32(0.25), rtol=1e-5, atol=1e-12)
+    np.testing.assert_array_equal(ref.swiglu_expert(x, gate, up, down, weight=7.0), plain)
+
+
+def test_load_pair_npz_keys_and_missing():
+    arrays, dense, x = synth.config0_expert(seed=3, d=128, ff=96, rank=32)
+    pair = ref.load_pair(arrays, "gate")
+    assert pair.a.shape == (128, 32) and pair.b.shape == (32, 96)
+    with pytest.raises(KeyError):
+        ref.load_pair(arrays, "missing")
+    # INT8 keys (group 64) are decoded too
+    q, s, shape = ref.quantize_int8(pair.a, group_size=64)
+    arrays2 = dict(arrays)
+    del arrays2["gate.a.nf4"]
+    arrays2["gate.a.int8"], arrays2["gate.a.scales"] = q, s
+    np.testing.assert_array_equal(ref.load_pair(arrays2, "gate").a, ref.dequantize_int8(q, s, shape, 64))
+
+
+def test_config0_latent_vs_dense_fidelity():
+    arrays, dense, x = synth.config0_expert(seed=0)
+    latent = ref.swiglu_expert(x, ref.load_pair(arrays, "gate"), ref.load_pair(arrays, "up"), ref.load_pair(arrays, "down"))
+    full = ref.dense_swiglu_expert(x, dense["gate"], dense["up"], dense["down"])
+    err = ref.relative_frobenius_error(full, latent)
+    assert np.isfinite(err) and err < 1.5  # noise norm exceeds the signal's at this config; report item
+
+
+def test_pack_rows_matches_writer_row_loop():
+    # loader/write_latent_gguf.py:227-257: quantize each row on its own, pad the
+    # last axis to a group multiple, pad bytes 0x77 and scales 1.0.
+    rng = np.random.default_rng(4)
+    st = rng.standard_normal((2, 5, 40)).astype(np.float32) * 1e-3
+    codes, scales = ref.pack_rows(st)
+    assert codes.shape == (2, 5, 32) and scales.shape == (2, 5, 2)
+    for e in range(2):
+        for r in range(5):
+            row = np.pad(st[e, r], (0, 24))
+            p, s, _ = ref.quantize_nf4(row, group_size=32)
+            np.testing.assert_array_equal(codes[e, r], p)
+            np.testing.assert_array_equal(scales[e, r].view(np.uint16), s.view(np.uint16))
+    np.testing.assert_array_equal(ref.unpack_rows(codes, scales)[..., :40].reshape(-1),
+                                  ref.dequantize_nf4(codes.reshape(-1), scales.reshape(-1), (2 * 5 * 64,))
+                                  .reshape(2, 5, 64)[..., :40].reshape(-1))
+
+
+def test_mixed_int8_groups_decode():
+    rng = np.random.default_rng(5)
+    st = rng.standard_normal((2, 3, 64)).astype(np.float32)
+    mask = np.zeros((2, 3, 2), bool)
+    mask[0, 1, 1] = mask[1, 0, 0] = mask[1, 2, 1] = True
+    codes, scales, ext = ref.pack_rows_mixed(st, mask)
+    plain_c, plain_s = ref.pack_rows(st)
+    for e in range(2):
+        out = ref.unpack_rows_mixed(codes, scales, ext, e)
+        for r in range(3):
+            for g in range(2):
+                seg = slice(32 * g, 32 * g + 32)
+                if mask[e, r, g]:
+                    q, s, _ = ref.quantize_int8(st[e, r, seg], group_size=32)
+                    np.testing.assert_array_equal(out[r, seg], ref.dequantize_int8(q, s, (32,), 32))
+                else:
+                    want = ref.dequantize_nf4(plain_c[e, r, 16 * g:16 * g + 16], plain_s[e, r, g:g + 1], (32,))
+                    np.testing.assert_array_equal(out[r, seg], want)
+    assert ext.row_offset.tolist() == [[0, 0, 1], [1, 2, 2]]
+
+
+def _brute_force_moe(x, ids, w, layer, wbd, mode):
+    T, K = ids.shape
+    per = np.zeros((T, K, layer.d), np.float32)
+    for t in range(T):
+        for k in range(K):
+            e = int(ids[t, k])
+            if 0 <= e < layer.n_expert:
+                gate, up, down = layer.pairs(e)
+                per[t, k] = ref.swiglu_expert(x[t:t + 1], gate, up, down, weight=w[t, k], weight_before_down=wbd)[0]
+    if mode == 1:
+        return per
+    scale = np.where((ids >= 0) & (ids < layer.n_expert), 1.0 if wbd else w, 0.0)
+    return (per.astype(np.float64) * scale[..., None]).sum(axis=1)
+
+
+@pytest.mark.parametrize("wbd", [False, True])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_moe_forward_matches_brute_force(wbd, mode):
+    layer = synth.make_layer(seed=10, n_expert=6, d=64, ff=96, max_rank=32, ranks=[32, 32, 17, 32, 9, 32])
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((5, 64)).astype(np.float32)
+    ids, w = routing.softmax_topk(rng.standard_normal((5, 6)), 3)
+    ids[1, 2] = -1
+    ids[3, 0] = 99  # out of range -> dropped
+    got = ref.moe_forward(x, ids, w, layer, weight_before_down=wbd, out_mode=mode)
+    want = _brute_force_moe(x, ids, w, layer, wbd, mode)
+    assert ref.rel_l2(want, got) < 1e-5
+    if mode == 1:
+        assert not got[1, 2].any() and not got[3, 0].any()
+
+
+def test_padding_beyond_rank_is_exact_zero():
+    layer = synth.make_layer(seed=11, n_expert=2, d=64, ff=64, max_rank=64, ranks=[32, 64])
+    gate_a = layer.factors["gate_a"].expert(0)
+    assert not gate_a[:, 32:].any() and not layer.factors["down_b"].expert(0)[32:].any()
+
+
+def test_expert_bytes_config1_shape():
+    # 3,981,312 packed bytes per expert at d=7168, ff=2048, r=256 (NF4 + fp16 scales)
+    d, ff, r = 7168, 2048, 256
+    elems = 2 * d * r + 2 * r * ff + ff * r + r * d
+    assert elems // 2 + elems // 32 * 2 == 3_981_312
+    layer = synth.make_layer(seed=12, n_expert=1, d=64, ff=32, max_rank=32)
+    elems = 2 * 64 * 32 + 2 * 32 * 32 + 32 * 32 + 32 * 64
+    assert layer.expert_bytes(0) == elems // 2 + elems // 32 * 2
+
+
+def test_softmax_topk_brute_force():
+    rng = np.random.default_rng(7)
+    logits = rng.standard_normal((9, 12)).astype(np.float32)
+    ids, w = routing.softmax_topk(logits, 4)
+    for t in range(9):
+        p = np.exp(logits[t].astype(np.float64))
+        p /= p.sum()
+        order = sorted(range(12), key=lambda e: (-p[e], e))[:4]
+        assert ids[t].tolist() == order
+        np.testing.assert_allclose(w[t], p[order] / p[order].sum(), rtol=1e-6)
+
+
+def test_adaptive_topk_reference_cases():
+    # tests/test_adaptive_topk.py:14-59
+    s = np.array([0.45, 0.22, 0.15, 0.08, 0.05, 0.03], np.float32)
+    assert routing.adaptive_topk_inclusive(s, 0.95) == 4
+    assert routing.adaptive_topk_inclusive(s, 1.0) == 6
+    assert routing.adaptive_topk_inclusive(s, 0.1) == 0
+    assert routing.adaptive_topk_inclusive(np.zeros(6, np.float32), 0.95) == 0
+    assert routing.adaptive_topk_inclusive(np.array([], np.float32), 0.95) == 0
+    ids, w = routing.adaptive_drop(np.array([[3, 1, 2]]), np.array([[0.7, 0.26, 0.04]], np.float32), 0.05)
+    assert ids.tolist() == [[3, 1, -1]] and w.tolist()[0][2] == 0.0
