@@ -62,7 +62,9 @@ template <bool kHasInt8>
 __device__ __forceinline__ void decode_group(const Factor& f, int64_t e, int64_t row, int g, const float* lut,
                                              float v[kGroup]) {
   const int64_t erow = e * f.rows + row;
-  if (kHasInt8) {
+  // kHasInt8 selects the code path for a layer in which some factor carries the
+  // extension; factors without it (bitmap == nullptr) are pure NF4.
+  if (kHasInt8 && f.ext.bitmap != nullptr) {
     const uint32_t* bm = f.ext.bitmap + erow * f.words();
     const uint32_t word = bm[g >> 5];
     if ((word >> (g & 31)) & 1u) {
