@@ -1,0 +1,29 @@
+// Host interface of the fused (persistent, one-launch) decode path.
+#pragma once
+
+#include <stddef.h>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/latent_ffn.h"
+
+namespace latent {
+namespace fused {
+
+// Workspace bytes at the start of every workspace that the fused path keeps
+// zero between calls (queue tickets, per-expert counters, combine counters).
+constexpr size_t kReserved = 256 * 1024;
+
+struct Plan {
+  int ra, nca, cb, ncb, cd, ncd, vmax, red_floats;
+  size_t lds;
+  size_t off_sync, off_ycnt;  // inside the reserved region
+  size_t off_partA, off_glat, off_partB, off_dlat, off_ybuf, scratch_bytes;  // after it
+};
+
+bool supported(const latent_moe_args& a);
+bool make_plan(const latent_moe_args& a, Plan& plan);
+int forward(const latent_moe_args& a, hipStream_t s, char* workspace, const Plan& plan);
+
+}  // namespace fused
+}  // namespace latent

@@ -20,6 +20,7 @@
 // LDS table.  Lanes sharing a group are combined with wave shuffles, waves
 // through LDS, workgroups with fp32 atomics.  All arithmetic is fp32.
 #include "common.hpp"
+#include "fused.hpp"
 
 #include <algorithm>
 
@@ -570,11 +571,15 @@ extern "C" const char* latent_status_string(int status) {
   }
 }
 
+// Workspace: [fused control block, zero between calls][scratch shared by both paths]
 extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes) {
   if (!args || !bytes) return LATENT_E_INVALID;
   const int st = validate(*args);
   if (st != LATENT_OK) return st;
-  *bytes = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank).total;
+  size_t scratch = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank).total;
+  fused::Plan pl;
+  if (fused::supported(*args) && fused::make_plan(*args, pl)) scratch = std::max(scratch, pl.scratch_bytes);
+  *bytes = fused::kReserved + scratch;
   return LATENT_OK;
 }
 
@@ -586,9 +591,16 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   if (a.n_tokens == 0) return LATENT_OK;
   if (!a.x || !a.ids || !a.weights || !a.out) return LATENT_E_INVALID;
   if ((reinterpret_cast<uintptr_t>(a.out) & 15u) != 0) return LATENT_E_INVALID;
-  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
-  if (!a.workspace || a.workspace_bytes < L.total) return LATENT_E_WORKSPACE;
+  size_t need = 0;
+  latent_moe_workspace_size(&a, &need);
+  if (!a.workspace || a.workspace_bytes < need) return LATENT_E_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a.workspace) & (kAlign - 1)) != 0) return LATENT_E_WORKSPACE;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();  // clear a stale error so the checks below see only ours
+  fused::Plan pl;
+  if (fused::supported(a) && fused::make_plan(a, pl))
+    return fused::forward(a, s, static_cast<char*>(a.workspace), pl);
+  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
 
   MoeParams p{};
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
@@ -597,7 +609,7 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.fac[i] = make_factor(*fs[i]);
     any_int8 = any_int8 || fs[i]->int8_bitmap != nullptr;
   }
-  char* ws = static_cast<char*>(a.workspace);
+  char* ws = static_cast<char*>(a.workspace) + fused::kReserved;
   p.x = a.x;
   p.ids = a.ids;
   p.weights = a.weights;
@@ -636,8 +648,6 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.cd = pick_pow2_chunk(p.d, p.a_max, 2048, 128, 512);
   p.n_d = (p.d + p.cd - 1) / p.cd;
 
-  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  (void)hipGetLastError();  // clear a stale error so the checks below see only ours
   const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? P / a.n_expert_used * a.n_embd / 4
                                                                                   : P * a.n_embd / 4);
   const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));

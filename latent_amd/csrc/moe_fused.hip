@@ -1,0 +1,878 @@
+// Fused decode path: the whole MoE-layer expert FFN in ONE persistent kernel.
+//
+// Replaces kernels/latent_fused_expert_ffn.cu:27-132 and its per-token launch
+// loop (:255-289) for decode-sized batches (T*k <= 512 routed pairs).
+//
+// Structure
+//   * Every workgroup (one per CU, 8 waves) builds a 64 KB codebook table in LDS
+//     and computes the token->expert grouping of all T*k pairs itself (cheap at
+//     decode sizes), so no grid-wide step precedes the work.
+//   * Work items, per active expert:  A  rows of A_g / A_u      -> g_lat, u_lat
+//                                      BC ff slice of B_g, B_u -> h -> h . A_d rows
+//                                      D  d slice of B_d       -> y -> output
+//     Experts are spread over 8 queues, one per XCD (workgroup b runs on XCD
+//     b % 8), so one expert's partial sums stay in one L2.  Workgroups take
+//     tickets from their queue; a queue lists all A items, then BC, then D, so a
+//     waiting item only ever waits on items already taken by running workgroups.
+//   * A and BC items write partial sums; the last item of an expert to finish
+//     (per-expert counter) adds them in a fixed order and publishes a ready
+//     flag (release / acquire at agent scope).  Results are deterministic.
+//   * Counters are reset by their last user, so the control block is zero again
+//     when the kernel ends; it must be zero before the first call.
+//
+// Dequant: a code byte b (two NF4 codes) indexes lut[b] = (level[b & 15],
+// level[b >> 4]) as a float2; the table is replicated for 32 lanes so reads are
+// bank-conflict free, and the address (b << 8 | lane*8) is one byte permute.
+// The group scale is folded into the activation: acc += (x * s) * level, fp32.
+#include "common.hpp"
+#include "fused.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace latent {
+
+Factor make_factor(const latent_factor& f);
+
+namespace fused {
+namespace {
+
+constexpr int kW = 8;            // waves per workgroup
+constexpr int kNT = kW * kWave;  // 512 threads
+constexpr int kMB = 4;           // tokens per pass
+constexpr int kLutEntries = 256 * 32;
+constexpr int64_t kSpinTicks = 100000000;  // 1 s of s_memrealtime (100 MHz)
+
+struct Ctrl {
+  int ticket[8];
+  int exit_count;
+  int error;
+  int pad[6];
+};
+
+struct ExpertSync {
+  int cA, rA, cB, rB, cD, pad[3];
+};
+
+struct Params {
+  Factor fac[6];
+  const void* x;
+  const int32_t* ids;
+  const void* weights;
+  const int32_t* ranks;
+  float* out;
+  Ctrl* ctrl;
+  ExpertSync* sync;  // [a_max]
+  int* ycnt;         // [T][ncd]
+  float* partA;      // [2][nca][P][R]
+  float* glat;       // [P][2R]
+  float* partB;      // [ncb][P][R]
+  float* dlat;       // [P][R]
+  float* ybuf;       // [P][d]
+  int x_dtype, w_dtype;
+  int T, d, ff, E, K, R, P;
+  int wbd, out_mode;
+  int ra, nca;  // phase A: rows per item, items per expert and factor
+  int cb, ncb;  // phase BC: ff columns per item, items per expert
+  int cd, ncd;  // phase D: d columns per item, items per expert
+  int vmax;     // floats per token in the activation staging buffer
+  int red_floats;
+};
+
+__device__ __forceinline__ int next_pow2(int v) { return v <= 1 ? 1 : 1 << (32 - __builtin_clz(v - 1)); }
+__device__ __forceinline__ int ilog2(int v) { return 31 - __builtin_clz(v); }
+
+__device__ __forceinline__ int rank_of(const Params& p, int e, int kind) {
+  if (!p.ranks) return p.R;
+  const int r = p.ranks[e * 3 + kind];
+  return r < 0 ? 0 : (r > p.R ? p.R : r);
+}
+
+// ---------------------------------------------------------------------------
+// LDS layout
+// ---------------------------------------------------------------------------
+struct Smem {
+  float2* lut;     // [256][32]
+  int* ids;        // [P]
+  float* w;        // [P]
+  int* cnt;        // [E]
+  int* start;      // [E]
+  int* act_e;      // [A]
+  int* act_s;      // [A]
+  int* act_c;      // [A]
+  int* pr_tok;     // [P] pairs grouped by expert
+  int* pr_slot;    // [P]
+  float* pr_w;     // [P]
+  int* pos_of;     // [P] position of pair t*K+slot, -1 if dropped
+  int* nvalid;     // [T]
+  int* misc;       // [16]: 0 n_active, 1 broadcast, 8..15 queue item counts
+  float* vin;      // [kMB][vmax]
+  float* hs;       // [kMB][cb]  (g of the BC slice, then h)
+  float* red;      // cross-wave partials
+};
+
+__device__ Smem carve(const Params& p, char* base) {
+  Smem s;
+  auto take = [&](size_t bytes) {
+    char* r = base;
+    base += (bytes + 15) / 16 * 16;
+    return r;
+  };
+  const int A = min(p.E, p.P);
+  s.lut = reinterpret_cast<float2*>(take(kLutEntries * sizeof(float2)));
+  s.ids = reinterpret_cast<int*>(take(p.P * 4));
+  s.w = reinterpret_cast<float*>(take(p.P * 4));
+  s.cnt = reinterpret_cast<int*>(take(p.E * 4));
+  s.start = reinterpret_cast<int*>(take(p.E * 4));
+  s.act_e = reinterpret_cast<int*>(take(A * 4));
+  s.act_s = reinterpret_cast<int*>(take(A * 4));
+  s.act_c = reinterpret_cast<int*>(take(A * 4));
+  s.pr_tok = reinterpret_cast<int*>(take(p.P * 4));
+  s.pr_slot = reinterpret_cast<int*>(take(p.P * 4));
+  s.pr_w = reinterpret_cast<float*>(take(p.P * 4));
+  s.pos_of = reinterpret_cast<int*>(take(p.P * 4));
+  s.nvalid = reinterpret_cast<int*>(take(p.T * 4));
+  s.misc = reinterpret_cast<int*>(take(16 * 4));
+  s.vin = reinterpret_cast<float*>(take(kMB * p.vmax * 4));
+  s.hs = reinterpret_cast<float*>(take(kMB * p.cb * 4));
+  s.red = reinterpret_cast<float*>(take(p.red_floats * 4));
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Routing, computed identically by every workgroup (deterministic order:
+// experts ascending, pairs of one expert in increasing t*K + slot).
+// ---------------------------------------------------------------------------
+__device__ void route(const Params& p, const Smem& s) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < p.P; i += kNT) {
+    s.ids[i] = p.ids[i];
+    s.w[i] = load_act(p.weights, p.w_dtype, i);
+    s.pos_of[i] = -1;
+  }
+  for (int e = tid; e < p.E; e += kNT) s.cnt[e] = 0;
+  for (int t = tid; t < p.T; t += kNT) s.nvalid[t] = 0;
+  __syncthreads();
+  for (int i = tid; i < p.P; i += kNT) {
+    const int e = s.ids[i];
+    if (e >= 0 && e < p.E) {
+      atomicAdd(&s.cnt[e], 1);
+      atomicAdd(&s.nvalid[i / p.K], 1);
+    }
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    // One wave scans the expert counts (E <= kMaxE).
+    int run = 0, act = 0;
+    for (int base = 0; base < p.E; base += kWave) {
+      const int e = base + tid;
+      const int c = e < p.E ? s.cnt[e] : 0;
+      int incl = c, ai = c > 0;
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        const int va = __shfl_up(ai, off);
+        if (tid >= off) {
+          incl += v;
+          ai += va;
+        }
+      }
+      if (e < p.E) {
+        s.start[e] = run + incl - c;
+        if (c > 0) {
+          const int a = act + ai - 1;
+          s.act_e[a] = e;
+          s.act_s[a] = run + incl - c;
+          s.act_c[a] = c;
+        }
+      }
+      run += __shfl(incl, kWave - 1);
+      act += __shfl(ai, kWave - 1);
+    }
+    if (tid == 0) s.misc[0] = act;
+  }
+  __syncthreads();
+  // Placement: thread j owns experts j, j+kNT, ... and scans the pairs in order.
+  for (int e = tid; e < p.E; e += kNT) {
+    if (s.cnt[e] == 0) continue;
+    int pos = s.start[e];
+    for (int i = 0; i < p.P; ++i) {
+      if (s.ids[i] == e) {
+        s.pr_tok[pos] = i / p.K;
+        s.pr_slot[pos] = i - (i / p.K) * p.K;
+        s.pr_w[pos] = s.w[i];
+        s.pos_of[i] = pos;
+        ++pos;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Item bookkeeping.  Queue q holds active experts a = q, q+8, q+16, ...
+// Items of a queue: [A: nq*2*nca][BC: nq*ncb][D: nq*ncd][Z: zero rows]
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int experts_in_queue(int n_active, int q) { return n_active > q ? (n_active - q + 7) / 8 : 0; }
+
+// Zero work for outputs no D item writes: tokens with no valid slot (reduced
+// mode) or dropped slots (per-slot mode); one item per (row, d slice).
+__device__ __forceinline__ int zero_rows(const Params& p, const Smem& s, int q, int idx, bool count_only) {
+  // Rows are enumerated in order; row r belongs to queue r % 8.
+  int n = 0;
+  const int rows = p.out_mode == LATENT_OUT_REDUCED ? p.T : p.P;
+  for (int r = q; r < rows; r += 8) {
+    const bool need = p.out_mode == LATENT_OUT_REDUCED ? (s.nvalid[r] == 0) : (s.pos_of[r] < 0);
+    if (need) {
+      if (!count_only && n == idx) return r;
+      ++n;
+    }
+  }
+  return count_only ? n : -1;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-workgroup signalling (agent scope).  A producer's waves each release
+// (write back their stores) before the barrier that precedes the counter
+// update; a consumer's waves each acquire after the barrier that follows the
+// flag read, so every wave observes the producer's data.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+// Bounded spin on a flag set with release semantics.  On timeout the error
+// word is set and the workgroup proceeds, so the kernel always terminates.
+__device__ void wait_flag(const Params& p, int* flag) {
+  if (threadIdx.x == 0) {
+    const int64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
+        __hip_atomic_store(&p.ctrl->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  acquire_agent();
+}
+
+// Arrive on a counter; true in every thread of the workgroup that is the last
+// of `total` arrivals (which then also observes all earlier arrivals' data).
+__device__ bool arrive_last(int* counter, int total, int* bcast) {
+  release_agent();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    *bcast = (old == total - 1);
+  }
+  __syncthreads();
+  const bool last = *bcast != 0;
+  if (last) acquire_agent();
+  return last;
+}
+
+__device__ void publish(int* flag) {
+  release_agent();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Tile GEMV.  y[t][j] = sum_{rows r} vin[t][r] * scale(r, g0 + j/32) * level(code(r, 32*g0 + j))
+// for rows [r0, r1), groups [g0, g0 + G) (G a power of two), t < M.
+// Lane layout: lpr lanes along groups x rpw lanes along rows in each wave;
+// wg waves along groups x wr waves along rows.  Every argument is a plain
+// value so the kernel-argument block never needs an address.
+// ---------------------------------------------------------------------------
+// Global-address-space pointers: keep loads as global_load_* across calls.
+#define LATENT_GLOBAL_AS __attribute__((address_space(1)))
+template <typename T>
+using gptr = const T LATENT_GLOBAL_AS*;
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global(const T* p) {
+  return (gptr<T>)(p);
+}
+#define LATENT_LDS_AS __attribute__((address_space(3)))
+template <typename T>
+using lptr = T LATENT_LDS_AS*;
+template <typename T>
+__device__ __forceinline__ lptr<T> as_lds(T* p) {
+  return (lptr<T>)(p);
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+struct FactorArgs {
+  gptr<uint8_t> codes;
+  gptr<uint16_t> scales;
+  gptr<uint32_t> bitmap;
+  gptr<int32_t> row_offset;
+  gptr<int8_t> data;
+  int64_t rows, cols;
+};
+
+__device__ __forceinline__ FactorArgs fargs(const Factor& f) {
+  return FactorArgs{as_global(f.codes), as_global(f.scales), as_global(f.ext.bitmap), as_global(f.ext.row_offset),
+                    as_global(f.ext.data), f.rows, f.cols};
+}
+
+// Where a tile's results go: dst[rowoff[t] + col] = v * scale[t], or with
+// swiglu set, dst[...] = SiLU(dst[...]) * v * scale[t] (dst holds the gate).
+struct Emit {
+  float* dst;
+  int64_t rowoff[kMB];
+  float scale[kMB];
+  int swiglu;
+};
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+__device__ __forceinline__ void emit_one(const Emit& em, int t, int col, float v) {
+  float* q = em.dst + em.rowoff[t] + col;
+  *q = em.swiglu ? silu_f32(*q) * v * em.scale[t] : v * em.scale[t];
+}
+
+template <int M, bool kInt8>
+__device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, int g0, int G, int g_valid,
+                                       lptr<const float> vin, int vstride, int vbase, lptr<const float2> lut2,
+                                       lptr<float> red, Emit em) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  int lpr, wg;
+  if (G <= 8) {
+    lpr = G;
+    wg = 1;
+  } else {
+    lpr = max(8, G / kW);
+    wg = G / lpr;
+  }
+  const int wr = kW / wg;
+  const int rpw = kWave / lpr;
+  const int gl = lane & (lpr - 1);             // group within the wave's slice
+  const int ro = lane >> ilog2(lpr);           // row lane
+  const int wgi = wave % wg, wri = wave / wg;  // wave's group slice / row slice
+  const int g = wgi * lpr + gl;                // group within the tile
+  const int rstep = wr * rpw;
+  const uint32_t lanebase = static_cast<uint32_t>(lane & 31) << 3;
+  const lptr<const char> lut = reinterpret_cast<lptr<const char>>(lut2);
+  const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
+  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
+
+  float acc[M][kGroup];
+#pragma unroll
+  for (int t = 0; t < M; ++t)
+#pragma unroll
+    for (int j = 0; j < kGroup; ++j) acc[t][j] = 0.f;
+
+  if (g < g_valid) {
+    const int gg = g0 + g;
+    const gptr<uint8_t> cbase = f.codes + e * f.rows * cstride + static_cast<int64_t>(gg) * kGroupBytes;
+    const gptr<uint16_t> sbase = f.scales + e * f.rows * sstride + gg;
+    constexpr int U = M <= 2 ? 4 : 2;
+    for (int row = r0 + wri * rpw + ro; row < r1; row += U * rstep) {
+      u32x4 c[U];
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int rr = row + u * rstep;
+        const int rc = rr < r1 ? rr : row;
+        c[u] = *reinterpret_cast<gptr<u32x4>>(cbase + static_cast<int64_t>(rc) * cstride);
+        sc[u] = half_bits_to_float(sbase[static_cast<int64_t>(rc) * sstride]);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int rr = row + u * rstep;
+        if (rr >= r1) break;
+        float xs[M];
+#pragma unroll
+        for (int t = 0; t < M; ++t) xs[t] = vin[t * vstride + rr - vbase] * sc[u];
+        bool is8 = false;
+        if constexpr (kInt8) {
+          if (f.bitmap != nullptr) {
+            const int64_t erow = e * f.rows + rr;
+            const gptr<uint32_t> bm = f.bitmap + erow * words;
+            const uint32_t word = bm[gg >> 5];
+            if ((word >> (gg & 31)) & 1u) {
+              is8 = true;
+              int before = popc(word & ((1u << (gg & 31)) - 1u));
+              for (int wi = 0; wi < (gg >> 5); ++wi) before += popc(bm[wi]);
+              const int64_t idx = static_cast<int64_t>(f.row_offset[erow]) + before;
+              const gptr<u32x4> qp = reinterpret_cast<gptr<u32x4>>(f.data + idx * kGroup);
+              const u32x4 q0 = qp[0], q1 = qp[1];
+              const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                  const float v = static_cast<float>(static_cast<int8_t>((qw[i] >> (8 * b)) & 0xFFu));
+#pragma unroll
+                  for (int t = 0; t < M; ++t) acc[t][i * 4 + b] = fmaf(xs[t], v, acc[t][i * 4 + b]);
+                }
+              }
+            }
+          }
+        }
+        if (!is8) {
+          const uint32_t cw[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              const uint32_t addr = (((cw[i] >> (8 * b)) & 0xFFu) << 8) | lanebase;
+              const f32x2 v = *reinterpret_cast<lptr<const f32x2>>(lut + addr);
+#pragma unroll
+              for (int t = 0; t < M; ++t) {
+                acc[t][i * 8 + 2 * b] = fmaf(xs[t], v.x, acc[t][i * 8 + 2 * b]);
+                acc[t][i * 8 + 2 * b + 1] = fmaf(xs[t], v.y, acc[t][i * 8 + 2 * b + 1]);
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+  // In-wave reduction over the rpw row lanes.
+  for (int off = lpr; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int t = 0; t < M; ++t)
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
+  }
+  const int ncols = G * kGroup;
+  if (wr == 1) {
+    if (ro == 0 && g < g_valid) {
+#pragma unroll
+      for (int t = 0; t < M; ++t)
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) emit_one(em, t, g * kGroup + j, acc[t][j]);
+    }
+    __syncthreads();
+    return;
+  }
+  // Cross-wave: row slices 0..wr-1 write partials, summed in slice order.
+  if (ro == 0 && g < g_valid) {
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      lptr<float> dst = red + (wri * M + t) * ncols + g * kGroup;
+#pragma unroll
+      for (int j = 0; j < kGroup; ++j) dst[j] = acc[t][j];
+    }
+  }
+  __syncthreads();
+  const int nvalid_cols = g_valid * kGroup;
+  for (int i = tid; i < M * nvalid_cols; i += kNT) {
+    const int t = i / nvalid_cols, col = i - t * nvalid_cols;
+    float v = 0.f;
+    for (int w = 0; w < wr; ++w) v += red[(w * M + t) * ncols + col];
+    emit_one(em, t, col, v);
+  }
+  __syncthreads();
+}
+
+template <bool kInt8>
+__device__ __forceinline__ void tile_gemv_m(int m, const Factor& fac, int64_t e, int r0, int r1, int g0, int G,
+                                            int g_valid, const float* vin, int vstride, int vbase, const Smem& s,
+                                            const Emit& em) {
+  const FactorArgs f = fargs(fac);
+  const lptr<const float> v = as_lds(vin);
+  const lptr<const float2> lut = as_lds(static_cast<const float2*>(s.lut));
+  const lptr<float> red = as_lds(s.red);
+  switch (m) {
+    case 1: tile_gemv<1, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
+    case 2: tile_gemv<2, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
+    case 3: tile_gemv<3, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
+    default: tile_gemv<4, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
+  }
+}
+
+__device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int swiglu = 0) {
+  Emit em;
+  em.dst = dst;
+#pragma unroll
+  for (int t = 0; t < kMB; ++t) {
+    em.rowoff[t] = row_stride * t;
+    em.scale[t] = 1.0f;
+  }
+  em.swiglu = swiglu;
+  return em;
+}
+
+
+// ---------------------------------------------------------------------------
+// Items
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ Factor pick(const Factor& a, const Factor& b, bool first) {
+  Factor f;
+  f.codes = first ? a.codes : b.codes;
+  f.scales = first ? a.scales : b.scales;
+  f.ext.bitmap = first ? a.ext.bitmap : b.ext.bitmap;
+  f.ext.row_offset = first ? a.ext.row_offset : b.ext.row_offset;
+  f.ext.data = first ? a.ext.data : b.ext.data;
+  f.rows = first ? a.rows : b.rows;
+  f.cols = first ? a.cols : b.cols;
+  return f;
+}
+
+template <bool kInt8>
+__device__ void item_a(const Params& p, const Smem& s, int a, int kind, int chunk) {
+  const Factor f = pick(p.fac[0], p.fac[2], kind == 0);
+  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
+  const int ng = (rank_of(p, e, kind) + kGroup - 1) / kGroup;
+  const int r0 = chunk * p.ra, r1 = min(p.d, r0 + p.ra), nrows = r1 - r0;
+  if (ng > 0 && nrows > 0) {
+    const int G = next_pow2(ng);
+    for (int tb = 0; tb < mtot; tb += kMB) {
+      const int m = min(kMB, mtot - tb);
+      for (int i = threadIdx.x; i < m * nrows; i += kNT) {
+        const int t = i / nrows, rr = i - t * nrows;
+        s.vin[t * p.vmax + rr] = load_act(p.x, p.x_dtype, static_cast<int64_t>(s.pr_tok[s0 + tb + t]) * p.d + r0 + rr);
+      }
+      __syncthreads();
+      float* dst = p.partA + ((static_cast<int64_t>(kind) * p.nca + chunk) * p.P + s0 + tb) * p.R;
+      tile_gemv_m<kInt8>(m, f, e, r0, r1, 0, G, ng, s.vin, p.vmax, r0, s, make_emit(dst, p.R));
+    }
+  }
+  // The last A item of the expert sums the partials into g_lat | u_lat.
+  if (arrive_last(&p.sync[a].cA, 2 * p.nca, &s.misc[1])) {
+    const int ng0 = (rank_of(p, e, 0) + kGroup - 1) / kGroup * kGroup;
+    const int ng1 = (rank_of(p, e, 1) + kGroup - 1) / kGroup * kGroup;
+    const int width = ng0 + ng1;
+    for (int i = threadIdx.x; i < mtot * width; i += kNT) {
+      const int t = i / width, cc = i - t * width;
+      const int k = cc < ng0 ? 0 : 1, col = cc < ng0 ? cc : cc - ng0;
+      const int nch = (p.d + p.ra - 1) / p.ra;
+      float v = 0.f;
+      for (int c = 0; c < nch; ++c) v += p.partA[((static_cast<int64_t>(k) * p.nca + c) * p.P + s0 + t) * p.R + col];
+      p.glat[static_cast<int64_t>(s0 + t) * 2 * p.R + k * p.R + col] = v;
+    }
+    publish(&p.sync[a].rA);
+  }
+}
+
+template <bool kInt8>
+__device__ void item_bc(const Params& p, const Smem& s, int a, int chunk) {
+  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
+  wait_flag(p, &p.sync[a].rA);
+  const int c0 = chunk * p.cb, ncol = min(p.cb, p.ff - c0);
+  const int gv = ncol / kGroup, G = next_pow2(p.cb / kGroup);
+  const int rk0 = rank_of(p, e, 0), rk1 = rank_of(p, e, 1), rkd = rank_of(p, e, 2);
+  const int ngd = (rkd + kGroup - 1) / kGroup;
+  float* dstB = p.partB + (static_cast<int64_t>(chunk) * p.P + s0) * p.R;
+  for (int tb = 0; tb < mtot; tb += kMB) {
+    const int m = min(kMB, mtot - tb);
+    for (int i = threadIdx.x; i < m * 2 * p.R; i += kNT) {
+      const int t = i / (2 * p.R), col = i - t * 2 * p.R;
+      s.vin[t * p.vmax + col] = p.glat[static_cast<int64_t>(s0 + tb + t) * 2 * p.R + col];
+    }
+    __syncthreads();
+    float* hs = s.hs;
+    const int cbw = p.cb;
+    if (ncol > 0) {
+      if (rk0 > 0)
+        tile_gemv_m<kInt8>(m, p.fac[1], e, 0, rk0, c0 / kGroup, G, gv, s.vin, p.vmax, 0, s, make_emit(hs, cbw));
+      else
+        for (int i = threadIdx.x; i < m * ncol; i += kNT) hs[(i / ncol) * cbw + i % ncol] = 0.f;
+      __syncthreads();
+      Emit em = make_emit(hs, cbw, 1);
+      if (p.wbd)
+        for (int t = 0; t < m; ++t) em.scale[t] = s.pr_w[s0 + tb + t];
+      if (rk1 > 0) {
+        tile_gemv_m<kInt8>(m, p.fac[3], e, 0, rk1, c0 / kGroup, G, gv, s.vin + p.R, p.vmax, 0, s, em);
+      } else {
+        for (int i = threadIdx.x; i < m * ncol; i += kNT) hs[(i / ncol) * cbw + i % ncol] = 0.f;
+        __syncthreads();
+      }
+    }
+    // h[cols] . A_d[cols] -> partial d_lat
+    if (ngd > 0 && ncol > 0)
+      tile_gemv_m<kInt8>(m, p.fac[4], e, c0, c0 + ncol, 0, next_pow2(ngd), ngd, hs, cbw, c0, s,
+                         make_emit(dstB + static_cast<int64_t>(tb) * p.R, p.R));
+  }
+  if (arrive_last(&p.sync[a].cB, p.ncb, &s.misc[1])) {
+    const int width = ngd * kGroup;
+    for (int i = threadIdx.x; i < mtot * width; i += kNT) {
+      const int t = i / width, col = i - t * width;
+      float v = 0.f;
+      for (int c = 0; c < p.ncb; ++c) v += p.partB[(static_cast<int64_t>(c) * p.P + s0 + t) * p.R + col];
+      p.dlat[static_cast<int64_t>(s0 + t) * p.R + col] = v;
+    }
+    publish(&p.sync[a].rB);
+  }
+}
+
+template <bool kInt8>
+__device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
+  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
+  wait_flag(p, &p.sync[a].rB);
+  const int c0 = chunk * p.cd, ncol = min(p.cd, p.d - c0);
+  const int gv = ncol / kGroup, G = next_pow2(p.cd / kGroup);
+  const int rkd = rank_of(p, e, 2);
+  for (int tb = 0; tb < mtot; tb += kMB) {
+    const int m = min(kMB, mtot - tb);
+    for (int i = threadIdx.x; i < m * p.R; i += kNT) {
+      const int t = i / p.R, col = i - t * p.R;
+      s.vin[t * p.vmax + col] = col < ((rkd + kGroup - 1) / kGroup) * kGroup ? p.dlat[static_cast<int64_t>(s0 + tb + t) * p.R + col] : 0.f;
+    }
+    __syncthreads();
+    if (ncol > 0) {
+      Emit em;
+      em.swiglu = 0;
+      for (int t = 0; t < kMB; ++t) {
+        const int tt = t < m ? t : 0;
+        const int pair = s0 + tb + tt;
+        if (p.out_mode == LATENT_OUT_PER_SLOT) {
+          em.rowoff[t] = (static_cast<int64_t>(s.pr_tok[pair]) * p.K + s.pr_slot[pair]) * p.d;
+          em.scale[t] = 1.0f;
+        } else {
+          em.rowoff[t] = static_cast<int64_t>(pair) * p.d;
+          em.scale[t] = p.wbd ? 1.0f : s.pr_w[pair];
+        }
+      }
+      em.dst = (p.out_mode == LATENT_OUT_PER_SLOT ? p.out : p.ybuf) + c0;
+      if (rkd > 0) {
+        tile_gemv_m<kInt8>(m, p.fac[5], e, 0, rkd, c0 / kGroup, G, gv, s.vin, p.vmax, 0, s, em);
+      } else {
+        for (int i = threadIdx.x; i < m * ncol; i += kNT) em.dst[em.rowoff[i / ncol] + i % ncol] = 0.f;
+      }
+    }
+    __syncthreads();
+  }
+  if (p.out_mode == LATENT_OUT_REDUCED && ncol > 0) {
+    // Combine: the last of a token's valid slots to finish this d slice sums
+    // them in slot order.
+    release_agent();
+    __syncthreads();
+    for (int t = 0; t < mtot; ++t) {
+      const int tok = s.pr_tok[s0 + t];
+      if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(&p.ycnt[tok * p.ncd + chunk], 1, __ATOMIC_ACQ_REL,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        s.misc[1] = (old == s.nvalid[tok] - 1);
+        if (old == s.nvalid[tok] - 1) p.ycnt[tok * p.ncd + chunk] = 0;
+      }
+      __syncthreads();
+      if (s.misc[1]) {
+        acquire_agent();
+        for (int col = threadIdx.x; col < ncol; col += kNT) {
+          float v = 0.f;
+          for (int k = 0; k < p.K; ++k) {
+            const int pos = s.pos_of[tok * p.K + k];
+            if (pos >= 0) v += p.ybuf[static_cast<int64_t>(pos) * p.d + c0 + col];
+          }
+          p.out[static_cast<int64_t>(tok) * p.d + c0 + col] = v;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  // The last D item of the expert resets the expert's counters for the next call.
+  if (arrive_last(&p.sync[a].cD, p.ncd, &s.misc[1])) {
+    if (threadIdx.x == 0) {
+      ExpertSync* es = &p.sync[a];
+      es->cA = 0;
+      es->rA = 0;
+      es->cB = 0;
+      es->rB = 0;
+      __hip_atomic_store(&es->cD, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+__device__ void item_zero(const Params& p, const Smem& s, int row, int chunk) {
+  const int c0 = chunk * p.cd, ncol = min(p.cd, p.d - c0);
+  float* dst = p.out + static_cast<int64_t>(row) * p.d + c0;
+  for (int col = threadIdx.x; col < ncol; col += kNT) dst[col] = 0.f;
+}
+
+template <bool kInt8>
+__global__ void __launch_bounds__(kNT) fused_kernel(Params p) {
+  extern __shared__ __align__(16) char smem_raw[];
+  const Smem s = carve(p, smem_raw);
+  const int tid = threadIdx.x;
+  // Codebook table: entry b holds (level[b & 15], level[b >> 4]) for 32 lanes.
+  for (int i = tid; i < kLutEntries; i += kNT) {
+    const int b = i >> 5;
+    s.lut[i] = make_float2(nf4_level(b & 15), nf4_level(b >> 4));
+  }
+  route(p, s);
+  const int n_active = s.misc[0];
+  const int q = blockIdx.x & 7;
+  const int nq = experts_in_queue(n_active, q);
+  const int nA = nq * 2 * p.nca, nB = nq * p.ncb, nD = nq * p.ncd;
+  const int nZ = zero_rows(p, s, q, 0, true) * p.ncd;
+  const int total = nA + nB + nD + nZ;
+  for (;;) {
+    if (tid == 0) s.misc[1] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    int t = s.misc[1];
+    __syncthreads();
+    if (t >= total) break;
+    if (t < nA) {
+      const int per = 2 * p.nca;
+      const int a = q + 8 * (t / per), r = t % per;
+      item_a<kInt8>(p, s, a, r / p.nca, r % p.nca);
+    } else if ((t -= nA) < nB) {
+      item_bc<kInt8>(p, s, q + 8 * (t / p.ncb), t % p.ncb);
+    } else if ((t -= nB) < nD) {
+      item_d<kInt8>(p, s, q + 8 * (t / p.ncd), t % p.ncd);
+    } else {
+      t -= nD;
+      item_zero(p, s, zero_rows(p, s, q, t / p.ncd, false), t % p.ncd);
+    }
+    __syncthreads();
+  }
+  // The last workgroup out resets the queues.
+  __syncthreads();
+  if (tid == 0) {
+    const int old = __hip_atomic_fetch_add(&p.ctrl->exit_count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == static_cast<int>(gridDim.x) - 1) {
+      for (int i = 0; i < 8; ++i) p.ctrl->ticket[i] = 0;
+      __hip_atomic_store(&p.ctrl->exit_count, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace fused
+}  // namespace latent
+
+// ===========================================================================
+// Host side
+// ===========================================================================
+namespace latent {
+namespace fused {
+
+constexpr int kMaxPairs = 512;
+constexpr int kMaxE = 512;
+constexpr size_t kLdsLimit = 160 * 1024;
+
+static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+static size_t lds_bytes(const latent_moe_args& a, int vmax, int cb, int red) {
+  const size_t P = a.n_tokens * a.n_expert_used, E = a.n_expert, A = std::min<size_t>(E, P), T = a.n_tokens;
+  auto r16 = [](size_t b) { return (b + 15) / 16 * 16; };
+  return r16(kLutEntries * 8) + 6 * r16(P * 4) + 2 * r16(E * 4) + 3 * r16(A * 4) + r16(T * 4) + r16(64) +
+         r16(kMB * vmax * 4) + r16(kMB * cb * 4) + r16(red * 4);
+}
+
+bool supported(const latent_moe_args& a) {
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  return P >= 1 && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512;
+}
+
+static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi) {
+  int c = hi;
+  while (c > lo && static_cast<double>((extent + c - 1) / c) * per_xcd < target) c /= 2;
+  return c;
+}
+
+bool make_plan(const latent_moe_args& a, Plan& pl) {
+  const int64_t T = a.n_tokens, K = a.n_expert_used, E = a.n_expert, R = a.max_rank, d = a.n_embd, ff = a.n_ff;
+  const int64_t P = T * K, A = std::min(E, P);
+  const double est = static_cast<double>(E) * (1.0 - std::pow(1.0 - static_cast<double>(K) / E, static_cast<double>(T)));
+  const double per_xcd = std::max(1.0, std::ceil(est / 8.0));
+  pl.red_floats = kMB * 8 * 256;
+  pl.cb = pick_cols(ff, per_xcd, 48, 128, 512);
+  pl.ncb = static_cast<int>((ff + pl.cb - 1) / pl.cb);
+  pl.cd = pick_cols(d, per_xcd, 48, 128, 2048);
+  pl.ncd = static_cast<int>((d + pl.cd - 1) / pl.cd);
+  int nca = std::max<int>(1, static_cast<int>(std::ceil(32.0 / per_xcd)));
+  nca = std::max<int>(nca, static_cast<int>((d + 2047) / 2048));
+  for (;; ++nca) {
+    pl.nca = static_cast<int>(std::min<int64_t>(nca, d));
+    pl.ra = static_cast<int>((d + pl.nca - 1) / pl.nca);
+    pl.nca = static_cast<int>((d + pl.ra - 1) / pl.ra);
+    pl.vmax = static_cast<int>(std::max<int64_t>(pl.ra, 2 * R));
+    pl.lds = lds_bytes(a, pl.vmax, pl.cb, pl.red_floats);
+    if (pl.lds <= kLdsLimit) break;
+    if (pl.ra <= 2 * R) return false;  // activations of 2R per token do not fit either
+  }
+  size_t off = 256;
+  pl.off_sync = off;
+  off = align256(off + A * sizeof(ExpertSync));
+  pl.off_ycnt = off;
+  off = align256(off + T * pl.ncd * sizeof(int));
+  if (off > kReserved) return false;
+  off = 0;
+  pl.off_partA = off; off = align256(off + 2ull * pl.nca * P * R * 4);
+  pl.off_glat = off;  off = align256(off + P * 2 * R * 4);
+  pl.off_partB = off; off = align256(off + static_cast<size_t>(pl.ncb) * P * R * 4);
+  pl.off_dlat = off;  off = align256(off + P * R * 4);
+  pl.off_ybuf = off;  off = align256(off + P * d * 4);
+  pl.scratch_bytes = off;
+  return true;
+}
+
+static int grid_size() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = std::max(8, n / 8 * 8);
+  }
+  return cached[dev];
+}
+
+template <bool kInt8>
+static int launch(const Params& p, const Plan& pl, hipStream_t s) {
+  static size_t attr_bytes = 0;  // largest dynamic LDS size granted so far
+  if (pl.lds > attr_bytes) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&fused_kernel<kInt8>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(pl.lds)) != hipSuccess)
+      return LATENT_E_HIP;
+    attr_bytes = pl.lds;
+  }
+  const int grid = grid_size();
+  if (grid <= 0) return LATENT_E_HIP;
+  hipLaunchKernelGGL(fused_kernel<kInt8>, dim3(grid), dim3(kNT), pl.lds, s, p);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}
+
+int forward(const latent_moe_args& a, hipStream_t s, char* ws, const Plan& pl) {
+  Params p{};
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  bool any_int8 = false;
+  for (int i = 0; i < 6; ++i) {
+    p.fac[i] = make_factor(*fs[i]);
+    any_int8 = any_int8 || fs[i]->int8_bitmap != nullptr;
+  }
+  char* scratch = ws + kReserved;
+  p.x = a.x;
+  p.ids = a.ids;
+  p.weights = a.weights;
+  p.ranks = a.ranks;
+  p.out = static_cast<float*>(a.out);
+  p.ctrl = reinterpret_cast<Ctrl*>(ws);
+  p.sync = reinterpret_cast<ExpertSync*>(ws + pl.off_sync);
+  p.ycnt = reinterpret_cast<int*>(ws + pl.off_ycnt);
+  p.partA = reinterpret_cast<float*>(scratch + pl.off_partA);
+  p.glat = reinterpret_cast<float*>(scratch + pl.off_glat);
+  p.partB = reinterpret_cast<float*>(scratch + pl.off_partB);
+  p.dlat = reinterpret_cast<float*>(scratch + pl.off_dlat);
+  p.ybuf = reinterpret_cast<float*>(scratch + pl.off_ybuf);
+  p.x_dtype = a.x_dtype;
+  p.w_dtype = a.weights_dtype;
+  p.T = static_cast<int>(a.n_tokens);
+  p.d = static_cast<int>(a.n_embd);
+  p.ff = static_cast<int>(a.n_ff);
+  p.E = static_cast<int>(a.n_expert);
+  p.K = static_cast<int>(a.n_expert_used);
+  p.R = static_cast<int>(a.max_rank);
+  p.P = p.T * p.K;
+  p.wbd = a.weight_before_down ? 1 : 0;
+  p.out_mode = a.out_mode;
+  p.ra = pl.ra;
+  p.nca = pl.nca;
+  p.cb = pl.cb;
+  p.ncb = pl.ncb;
+  p.cd = pl.cd;
+  p.ncd = pl.ncd;
+  p.vmax = pl.vmax;
+  p.red_floats = pl.red_floats;
+  return any_int8 ? launch<true>(p, pl, s) : launch<false>(p, pl, s);
+}
+
+}  // namespace fused
+}  // namespace latent

@@ -216,9 +216,18 @@ class StackedLayer:
         key = dev.index or 0
         ws = self._workspace.get(key)
         if ws is None or ws.numel() < need:
-            ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            # Zero-filled: the library keeps its control block zero between calls.
+            ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=dev)
             self._workspace[key] = ws
         return ws
+
+
+CTRL_ERROR_OFFSET = 36  # int32 error word of the workspace control block
+
+
+def workspace_error(workspace: torch.Tensor) -> int:
+    """Error word the fused kernel sets when a bounded wait times out (0 = none)."""
+    return int(workspace[CTRL_ERROR_OFFSET:CTRL_ERROR_OFFSET + 4].view(torch.int32).item())
 
 
 def workspace_size(layer: StackedLayer, n_tokens: int, n_expert_used: int) -> int:
@@ -265,6 +274,7 @@ def moe_forward(
         raise ValueError(f"out must be contiguous f32 {shape}")
     if workspace is None:
         workspace = layer.workspace(T, k)
+    # A caller-provided workspace must be zero-filled before its first use.
     a = layer.args()
     a.x, a.x_dtype = x.data_ptr(), _DTYPE_CODE[x.dtype]
     a.ids = ids.data_ptr()
