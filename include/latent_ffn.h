@@ -137,6 +137,14 @@ int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes);
 int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 
 /*
+ * Which implementation latent_moe_ffn_forward uses for these arguments:
+ * 1 = single persistent decode kernel (up to 512 routed pairs, 512 experts,
+ * rank 512), 0 = multi-kernel general path; < 0 = LATENT_E_* for bad arguments.
+ * Diagnostic only; no counterpart in the reference.
+ */
+int latent_moe_path(const latent_moe_args* args);
+
+/*
  * Dequantize expert `expert` of one stacked factor into f32 [rows][cols]
  * (out, device).  Bit-exact restatement of dequantize_nf4 / dequantize_int8
  * (loader/latent_loader.py:133-145, 161-170): one fp32 multiply per element.

@@ -9,11 +9,13 @@ this module raises.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the CDLL load; see module docstring)
 
-LIB_PATH = Path(__file__).resolve().parent / "liblatent_hip.so"
+# LATENT_HIP_LIB points at another build of the same library (e.g. a debug build).
+LIB_PATH = Path(os.environ.get("LATENT_HIP_LIB", Path(__file__).resolve().parent / "liblatent_hip.so"))
 
 LATENT_OK = 0
 LATENT_E_INVALID = -1
@@ -33,6 +35,7 @@ EXPORTED = (
     "latent_status_string",
     "latent_moe_workspace_size",
     "latent_moe_ffn_forward",
+    "latent_moe_path",
     "latent_unpack",
     "latent_pack_nf4",
     "latent_pack_int8",
@@ -100,6 +103,8 @@ def _load() -> ctypes.CDLL:
     lib.latent_moe_workspace_size.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.latent_moe_ffn_forward.restype = ctypes.c_int
     lib.latent_moe_ffn_forward.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p]
+    lib.latent_moe_path.restype = ctypes.c_int
+    lib.latent_moe_path.argtypes = [ctypes.POINTER(LatentMoeArgs)]
     lib.latent_unpack.restype = ctypes.c_int
     lib.latent_unpack.argtypes = [ctypes.POINTER(LatentFactor), ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
     lib.latent_pack_nf4.restype = ctypes.c_int

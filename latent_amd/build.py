@@ -1,6 +1,8 @@
 """Build liblatent_hip.so (gfx950) in-tree with hipcc.
 
-    python -m latent_amd.build
+    python latent_amd/build.py
+
+(Run as a script: importing the package would load the library being rebuilt.)
 
 The library links only against the HIP runtime; no torch headers.  When the
 Python binding loads it after `import torch`, the dynamic linker binds it to

@@ -583,6 +583,14 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   return LATENT_OK;
 }
 
+extern "C" int latent_moe_path(const latent_moe_args* args) {
+  if (!args) return LATENT_E_INVALID;
+  const int st = validate(*args);
+  if (st != LATENT_OK) return st;
+  fused::Plan pl;
+  return (fused::supported(*args) && fused::make_plan(*args, pl)) ? 1 : 0;
+}
+
 extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
   if (!args) return LATENT_E_INVALID;
   const latent_moe_args& a = *args;

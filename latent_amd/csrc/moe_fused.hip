@@ -4,7 +4,7 @@
 // loop (:255-289) for decode-sized batches (T*k <= 512 routed pairs).
 //
 // Structure
-//   * Every workgroup (one per CU, 8 waves) builds a 64 KB codebook table in LDS
+//   * Every workgroup (two per CU, 8 waves each) builds a 16 KB codebook table in LDS
 //     and computes the token->expert grouping of all T*k pairs itself (cheap at
 //     decode sizes), so no grid-wide step precedes the work.
 //   * Work items, per active expert:  A  rows of A_g / A_u      -> g_lat, u_lat
@@ -16,13 +16,14 @@
 //     waiting item only ever waits on items already taken by running workgroups.
 //   * A and BC items write partial sums; the last item of an expert to finish
 //     (per-expert counter) adds them in a fixed order and publishes a ready
-//     flag (release / acquire at agent scope).  Results are deterministic.
+//     flag; cross-workgroup data moves through coherent (sc1) loads and stores.
+//     Results are deterministic.
 //   * Counters are reset by their last user, so the control block is zero again
 //     when the kernel ends; it must be zero before the first call.
 //
 // Dequant: a code byte b (two NF4 codes) indexes lut[b] = (level[b & 15],
-// level[b >> 4]) as a float2; the table is replicated for 32 lanes so reads are
-// bank-conflict free, and the address (b << 8 | lane*8) is one byte permute.
+// level[b >> 4]) as a float2; the table is replicated for 8 lanes to spread
+// LDS banks, and the address is (b << 6) | (lane % 8) * 8.
 // The group scale is folded into the activation: acc += (x * s) * level, fp32.
 #include "common.hpp"
 #include "fused.hpp"
@@ -37,10 +38,11 @@ Factor make_factor(const latent_factor& f);
 namespace fused {
 namespace {
 
-constexpr int kW = 8;            // waves per workgroup
+constexpr int kW = 8;            // waves per workgroup (two workgroups per CU)
 constexpr int kNT = kW * kWave;  // 512 threads
 constexpr int kMB = 4;           // tokens per pass
-constexpr int kLutEntries = 256 * 32;
+constexpr int kLutCopies = 8;
+constexpr int kLutEntries = 256 * kLutCopies;
 constexpr int64_t kSpinTicks = 100000000;  // 1 s of s_memrealtime (100 MHz)
 
 struct Ctrl {
@@ -231,21 +233,28 @@ __device__ __forceinline__ int zero_rows(const Params& p, const Smem& s, int q, 
 }
 
 // ---------------------------------------------------------------------------
-// Cross-workgroup signalling (agent scope).  A producer's waves each release
-// (write back their stores) before the barrier that precedes the counter
-// update; a consumer's waves each acquire after the barrier that follows the
-// flag read, so every wave observes the producer's data.
+// Cross-workgroup signalling.  Data that another workgroup reads is written and
+// read with agent-scope relaxed atomics (single sc1 loads / stores, coherent
+// across XCDs without L2 write-back or invalidate).  A producer's waves drain
+// their stores (s_waitcnt) before the barrier that precedes the counter
+// update; counters and flags are relaxed agent-scope atomics.  No release or
+// acquire fences: on gfx950 those write back / invalidate the whole L2.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void drain_stores() { __builtin_amdgcn_s_waitcnt(0); }
 
-// Bounded spin on a flag set with release semantics.  On timeout the error
-// word is set and the workgroup proceeds, so the kernel always terminates.
+// Bounded spin on a flag.  On timeout the error word is set and the workgroup
+// proceeds, so the kernel always terminates.
 __device__ void wait_flag(const Params& p, int* flag) {
   if (threadIdx.x == 0) {
     const int64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-      __builtin_amdgcn_s_sleep(2);
+    while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      __builtin_amdgcn_s_sleep(1);
       if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
         __hip_atomic_store(&p.ctrl->error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -253,28 +262,25 @@ __device__ void wait_flag(const Params& p, int* flag) {
     }
   }
   __syncthreads();
-  acquire_agent();
 }
 
 // Arrive on a counter; true in every thread of the workgroup that is the last
-// of `total` arrivals (which then also observes all earlier arrivals' data).
+// of `total` arrivals.
 __device__ bool arrive_last(int* counter, int total, int* bcast) {
-  release_agent();
+  drain_stores();
   __syncthreads();
   if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *bcast = (old == total - 1);
   }
   __syncthreads();
-  const bool last = *bcast != 0;
-  if (last) acquire_agent();
-  return last;
+  return *bcast != 0;
 }
 
 __device__ void publish(int* flag) {
-  release_agent();
+  drain_stores();
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -324,146 +330,205 @@ struct Emit {
   int64_t rowoff[kMB];
   float scale[kMB];
   int swiglu;
+  int coherent;  // dst is read by another workgroup: store with st_coh
 };
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 __device__ __forceinline__ void emit_one(const Emit& em, int t, int col, float v) {
   float* q = em.dst + em.rowoff[t] + col;
-  *q = em.swiglu ? silu_f32(*q) * v * em.scale[t] : v * em.scale[t];
+  if (em.coherent)
+    st_coh(q, v * em.scale[t]);
+  else
+    *q = em.swiglu ? silu_f32(*q) * v * em.scale[t] : v * em.scale[t];
 }
 
+// A lane owns half a group: 16 columns (8 code bytes) of one row per step.
+constexpr int kHalf = kGroup / 2;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// acc[t][j] += xs[t] * level(code j) for the 16 columns of one half group.
+template <int M>
+__device__ __forceinline__ void fma_half_nf4(const u32x2& c, const float (&xs)[M], lptr<const char> lut,
+                                             uint32_t lanebase, float (&acc)[M][kHalf]) {
+  f32x2 v[8];
+  const uint32_t cw[2] = {c.x, c.y};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t addr = (((cw[i] >> (8 * b)) & 0xFFu) << 6) | lanebase;  // entry stride kLutCopies x 8 B
+      v[i * 4 + b] = *reinterpret_cast<lptr<const f32x2>>(lut + addr);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      acc[t][2 * k] = fmaf(xs[t], v[k].x, acc[t][2 * k]);
+      acc[t][2 * k + 1] = fmaf(xs[t], v[k].y, acc[t][2 * k + 1]);
+    }
+  }
+}
+
+// Same for a half group stored as INT8 in the side buffer.
+template <int M>
+__device__ __forceinline__ void fma_half_int8(const FactorArgs& f, int64_t e, int row, int gg, int half,
+                                              const float (&xs)[M], float (&acc)[M][kHalf]) {
+  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
+  const int64_t erow = e * f.rows + row;
+  const gptr<uint32_t> bm = f.bitmap + erow * words;
+  const uint32_t word = bm[gg >> 5];
+  int before = popc(word & ((1u << (gg & 31)) - 1u));
+  for (int wi = 0; wi < (gg >> 5); ++wi) before += popc(bm[wi]);
+  const int64_t idx = static_cast<int64_t>(f.row_offset[erow]) + before;
+  const u32x4 q = *reinterpret_cast<gptr<u32x4>>(f.data + idx * kGroup + half * kHalf);
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float v = static_cast<float>(static_cast<int8_t>((qw[i] >> (8 * b)) & 0xFFu));
+#pragma unroll
+      for (int t = 0; t < M; ++t) acc[t][i * 4 + b] = fmaf(xs[t], v, acc[t][i * 4 + b]);
+    }
+  }
+}
+
+__device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, int row, int gg) {
+  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
+  const gptr<uint32_t> bm = f.bitmap + (e * f.rows + row) * words;
+  return (bm[gg >> 5] >> (gg & 31)) & 1u;
+}
+
+// Tile GEMV over half groups: H = 2G half groups, lanes along half groups (lph
+// per row; 16 lanes = one 128-byte row segment) x rows; waves along half
+// groups (wg) x rows (wr).  The in-wave sum runs over the row lanes; the
+// cross-wave sum folds the upper half of the row slices onto the lower half,
+// then adds the lower slices in order (fixed order, deterministic).
 template <int M, bool kInt8>
 __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, int g0, int G, int g_valid,
                                        lptr<const float> vin, int vstride, int vbase, lptr<const float2> lut2,
                                        lptr<float> red, Emit em) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  int lpr, wg;
-  if (G <= 8) {
-    lpr = G;
+  const int H = 2 * G, h_valid = 2 * g_valid;
+  int lph, wg;
+  if (H <= 16) {
+    lph = H;
     wg = 1;
   } else {
-    lpr = max(8, G / kW);
-    wg = G / lpr;
+    lph = max(16, H / kW);
+    wg = H / lph;
   }
   const int wr = kW / wg;
-  const int rpw = kWave / lpr;
-  const int gl = lane & (lpr - 1);             // group within the wave's slice
-  const int ro = lane >> ilog2(lpr);           // row lane
-  const int wgi = wave % wg, wri = wave / wg;  // wave's group slice / row slice
-  const int g = wgi * lpr + gl;                // group within the tile
+  const int rpw = kWave / lph;
+  const int hl = lane & (lph - 1);             // half group within the wave's slice
+  const int ro = lane >> ilog2(lph);           // row lane
+  const int wgi = wave % wg, wri = wave / wg;  // wave's half-group slice / row slice
+  const int h = wgi * lph + hl;                // half group within the tile
   const int rstep = wr * rpw;
-  const uint32_t lanebase = static_cast<uint32_t>(lane & 31) << 3;
+  const uint32_t lanebase = static_cast<uint32_t>(lane & (kLutCopies - 1)) << 3;
   const lptr<const char> lut = reinterpret_cast<lptr<const char>>(lut2);
   const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
-  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
 
-  float acc[M][kGroup];
+  float acc[M][kHalf];
 #pragma unroll
   for (int t = 0; t < M; ++t)
 #pragma unroll
-    for (int j = 0; j < kGroup; ++j) acc[t][j] = 0.f;
+    for (int j = 0; j < kHalf; ++j) acc[t][j] = 0.f;
 
-  if (g < g_valid) {
-    const int gg = g0 + g;
-    const gptr<uint8_t> cbase = f.codes + e * f.rows * cstride + static_cast<int64_t>(gg) * kGroupBytes;
-    const gptr<uint16_t> sbase = f.scales + e * f.rows * sstride + gg;
-    constexpr int U = M <= 2 ? 4 : 2;
-    for (int row = r0 + wri * rpw + ro; row < r1; row += U * rstep) {
-      u32x4 c[U];
-      float sc[U];
+  // Rows of this lane: row_w + ro + k*rstep for k < nsteps (uniform across the
+  // wave); rows past r1 read a valid row and are masked by a zero scale.
+  const int row_w = r0 + wri * rpw;
+  const int nsteps = row_w < r1 ? (r1 - 1 - row_w) / rstep + 1 : 0;
+  const int row0 = min(row_w + ro, r1 - 1);
+  const bool hvalid = h < h_valid;
+  const int hh = hvalid ? h : 0;
+  const int gg = g0 + (hh >> 1), half = hh & 1;
+  const gptr<uint8_t> cbase =
+      f.codes + (e * f.rows + row0) * cstride + static_cast<int64_t>(gg) * kGroupBytes + half * (kGroupBytes / 2);
+  const gptr<uint16_t> sbase = f.scales + (e * f.rows + row0) * sstride + gg;
+  const int64_t cstep = static_cast<int64_t>(rstep) * cstride, sstep = static_cast<int64_t>(rstep) * sstride;
+  // Ring of kRing rows in flight per lane; slot u is refilled with the row
+  // kRing steps ahead right after it is consumed.
+  constexpr int kRing = 8;
+  u32x2 ring[kRing];
+  float sring[kRing];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int rr = row + u * rstep;
-        const int rc = rr < r1 ? rr : row;
-        c[u] = *reinterpret_cast<gptr<u32x4>>(cbase + static_cast<int64_t>(rc) * cstride);
-        sc[u] = half_bits_to_float(sbase[static_cast<int64_t>(rc) * sstride]);
-      }
+  for (int u = 0; u < kRing; ++u) {
+    const int k = u < nsteps ? u : 0;
+    ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + k * cstep);
+    sring[u] = half_bits_to_float(sbase[k * sstep]);
+  }
+  for (int k0 = 0; k0 < nsteps; k0 += kRing) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int rr = row + u * rstep;
-        if (rr >= r1) break;
-        float xs[M];
+    for (int u = 0; u < kRing; ++u) {
+      const int k = k0 + u;
+      const int row = row_w + ro + k * rstep;
+      const bool ok = hvalid && k < nsteps && row < r1;
+      const int vr = (ok ? row : r0) - vbase;
+      const float sm = ok ? sring[u] : 0.f;
+      float xs[M];
 #pragma unroll
-        for (int t = 0; t < M; ++t) xs[t] = vin[t * vstride + rr - vbase] * sc[u];
-        bool is8 = false;
-        if constexpr (kInt8) {
-          if (f.bitmap != nullptr) {
-            const int64_t erow = e * f.rows + rr;
-            const gptr<uint32_t> bm = f.bitmap + erow * words;
-            const uint32_t word = bm[gg >> 5];
-            if ((word >> (gg & 31)) & 1u) {
-              is8 = true;
-              int before = popc(word & ((1u << (gg & 31)) - 1u));
-              for (int wi = 0; wi < (gg >> 5); ++wi) before += popc(bm[wi]);
-              const int64_t idx = static_cast<int64_t>(f.row_offset[erow]) + before;
-              const gptr<u32x4> qp = reinterpret_cast<gptr<u32x4>>(f.data + idx * kGroup);
-              const u32x4 q0 = qp[0], q1 = qp[1];
-              const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-              for (int i = 0; i < 8; ++i) {
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                  const float v = static_cast<float>(static_cast<int8_t>((qw[i] >> (8 * b)) & 0xFFu));
-#pragma unroll
-                  for (int t = 0; t < M; ++t) acc[t][i * 4 + b] = fmaf(xs[t], v, acc[t][i * 4 + b]);
-                }
-              }
-            }
-          }
-        }
-        if (!is8) {
-          const uint32_t cw[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-              const uint32_t addr = (((cw[i] >> (8 * b)) & 0xFFu) << 8) | lanebase;
-              const f32x2 v = *reinterpret_cast<lptr<const f32x2>>(lut + addr);
-#pragma unroll
-              for (int t = 0; t < M; ++t) {
-                acc[t][i * 8 + 2 * b] = fmaf(xs[t], v.x, acc[t][i * 8 + 2 * b]);
-                acc[t][i * 8 + 2 * b + 1] = fmaf(xs[t], v.y, acc[t][i * 8 + 2 * b + 1]);
-              }
-            }
-          }
+      for (int t = 0; t < M; ++t) xs[t] = vin[t * vstride + vr] * sm;
+      bool done = false;
+      if constexpr (kInt8) {
+        if (f.bitmap != nullptr && ok && is_int8_group(f, e, row, gg)) {
+          fma_half_int8<M>(f, e, row, gg, half, xs, acc);
+          done = true;
         }
       }
+      if (!done) fma_half_nf4<M>(ring[u], xs, lut, lanebase, acc);
+      const int kn = k + kRing < nsteps ? k + kRing : 0;
+      ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + kn * cstep);
+      sring[u] = half_bits_to_float(sbase[kn * sstep]);
     }
   }
   // In-wave reduction over the rpw row lanes.
-  for (int off = lpr; off < kWave; off <<= 1) {
+  for (int off = lph; off < kWave; off <<= 1) {
 #pragma unroll
     for (int t = 0; t < M; ++t)
 #pragma unroll
-      for (int j = 0; j < kGroup; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
+      for (int j = 0; j < kHalf; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
   }
-  const int ncols = G * kGroup;
+  const int ncols = H * kHalf;
+  const bool writer = ro == 0 && hvalid;
   if (wr == 1) {
-    if (ro == 0 && g < g_valid) {
+    if (writer) {
 #pragma unroll
       for (int t = 0; t < M; ++t)
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) emit_one(em, t, g * kGroup + j, acc[t][j]);
+        for (int j = 0; j < kHalf; ++j) emit_one(em, t, h * kHalf + j, acc[t][j]);
     }
     __syncthreads();
     return;
   }
-  // Cross-wave: row slices 0..wr-1 write partials, summed in slice order.
-  if (ro == 0 && g < g_valid) {
+  // Cross-wave: slices wri < wr/2 store, slices wri >= wr/2 add into slot
+  // wri - wr/2, then the wr/2 slots are summed in order.
+  const int slots = wr / 2;
+  if (writer && wri < slots) {
 #pragma unroll
     for (int t = 0; t < M; ++t) {
-      lptr<float> dst = red + (wri * M + t) * ncols + g * kGroup;
+      lptr<float> dst = red + (wri * M + t) * ncols + h * kHalf;
 #pragma unroll
-      for (int j = 0; j < kGroup; ++j) dst[j] = acc[t][j];
+      for (int j = 0; j < kHalf; ++j) dst[j] = acc[t][j];
     }
   }
   __syncthreads();
-  const int nvalid_cols = g_valid * kGroup;
+  if (writer && wri >= slots) {
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      lptr<float> dst = red + ((wri - slots) * M + t) * ncols + h * kHalf;
+#pragma unroll
+      for (int j = 0; j < kHalf; ++j) dst[j] += acc[t][j];
+    }
+  }
+  __syncthreads();
+  const int nvalid_cols = h_valid * kHalf;
   for (int i = tid; i < M * nvalid_cols; i += kNT) {
     const int t = i / nvalid_cols, col = i - t * nvalid_cols;
     float v = 0.f;
-    for (int w = 0; w < wr; ++w) v += red[(w * M + t) * ncols + col];
+    for (int w = 0; w < slots; ++w) v += red[(w * M + t) * ncols + col];
     emit_one(em, t, col, v);
   }
   __syncthreads();
@@ -485,9 +550,10 @@ __device__ __forceinline__ void tile_gemv_m(int m, const Factor& fac, int64_t e,
   }
 }
 
-__device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int swiglu = 0) {
+__device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int swiglu = 0, int coherent = 0) {
   Emit em;
   em.dst = dst;
+  em.coherent = coherent;
 #pragma unroll
   for (int t = 0; t < kMB; ++t) {
     em.rowoff[t] = row_stride * t;
@@ -497,6 +563,76 @@ __device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int sw
   return em;
 }
 
+
+// ---------------------------------------------------------------------------
+// Staging and reduction helpers.  Loads are issued in batches before any use
+// so one item pays one memory round trip per batch, not one per element.
+// ---------------------------------------------------------------------------
+// x rows of up to kMB tokens, columns [c0, c0 + n) (n % 8 == 0, c0 % 8 == 0),
+// converted to fp32 into dst[t * dstride + j].
+__device__ void stage_x(const Params& p, const int* toks, int m, int c0, int n, float* dst, int dstride) {
+  const int tid = threadIdx.x;
+  for (int j0 = tid * 8; j0 < n; j0 += kNT * 8) {
+    float v[kMB][8];
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) {
+      if (t < m) {
+        const int64_t base = static_cast<int64_t>(toks[t]) * p.d + c0 + j0;
+        if (p.x_dtype == LATENT_F32) {
+          const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p.x) + base);
+          const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p.x) + base + 4);
+          v[t][0] = a.x; v[t][1] = a.y; v[t][2] = a.z; v[t][3] = a.w;
+          v[t][4] = b.x; v[t][5] = b.y; v[t][6] = b.z; v[t][7] = b.w;
+        } else {
+          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + base);
+          const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (p.x_dtype == LATENT_BF16) {
+              v[t][2 * i] = __uint_as_float(w[i] << 16);
+              v[t][2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+            } else {
+              v[t][2 * i] = half_bits_to_float(static_cast<uint16_t>(w[i] & 0xFFFFu));
+              v[t][2 * i + 1] = half_bits_to_float(static_cast<uint16_t>(w[i] >> 16));
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) {
+      if (t < m) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dst[t * dstride + j0 + i] = v[t][i];
+      }
+    }
+  }
+}
+
+// Coherent rows src[t * sstride + j] (j < n) of up to kMB tokens into LDS.
+__device__ void stage_coh(const float* src, int64_t sstride, int m, int n, float* dst, int dstride) {
+  for (int j = threadIdx.x; j < n; j += kNT) {
+    float v[kMB];
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) v[t] = t < m ? ld_coh(src + t * sstride + j) : 0.f;
+#pragma unroll
+    for (int t = 0; t < kMB; ++t)
+      if (t < m) dst[t * dstride + j] = v[t];
+  }
+}
+
+// sum_{c < n} src[c * cstride], loads batched 8 at a time, summed in c order.
+__device__ __forceinline__ float sum_coh(const float* src, int64_t cstride, int n) {
+  float acc = 0.f;
+  for (int c0 = 0; c0 < n; c0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = c0 + i < n ? ld_coh(src + (c0 + i) * cstride) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += v[i];
+  }
+  return acc;
+}
 
 // ---------------------------------------------------------------------------
 // Items
@@ -523,13 +659,10 @@ __device__ void item_a(const Params& p, const Smem& s, int a, int kind, int chun
     const int G = next_pow2(ng);
     for (int tb = 0; tb < mtot; tb += kMB) {
       const int m = min(kMB, mtot - tb);
-      for (int i = threadIdx.x; i < m * nrows; i += kNT) {
-        const int t = i / nrows, rr = i - t * nrows;
-        s.vin[t * p.vmax + rr] = load_act(p.x, p.x_dtype, static_cast<int64_t>(s.pr_tok[s0 + tb + t]) * p.d + r0 + rr);
-      }
+      stage_x(p, s.pr_tok + s0 + tb, m, r0, nrows, s.vin, p.vmax);
       __syncthreads();
       float* dst = p.partA + ((static_cast<int64_t>(kind) * p.nca + chunk) * p.P + s0 + tb) * p.R;
-      tile_gemv_m<kInt8>(m, f, e, r0, r1, 0, G, ng, s.vin, p.vmax, r0, s, make_emit(dst, p.R));
+      tile_gemv_m<kInt8>(m, f, e, r0, r1, 0, G, ng, s.vin, p.vmax, r0, s, make_emit(dst, p.R, 0, 1));
     }
   }
   // The last A item of the expert sums the partials into g_lat | u_lat.
@@ -537,13 +670,13 @@ __device__ void item_a(const Params& p, const Smem& s, int a, int kind, int chun
     const int ng0 = (rank_of(p, e, 0) + kGroup - 1) / kGroup * kGroup;
     const int ng1 = (rank_of(p, e, 1) + kGroup - 1) / kGroup * kGroup;
     const int width = ng0 + ng1;
-    for (int i = threadIdx.x; i < mtot * width; i += kNT) {
-      const int t = i / width, cc = i - t * width;
-      const int k = cc < ng0 ? 0 : 1, col = cc < ng0 ? cc : cc - ng0;
-      const int nch = (p.d + p.ra - 1) / p.ra;
-      float v = 0.f;
-      for (int c = 0; c < nch; ++c) v += p.partA[((static_cast<int64_t>(k) * p.nca + c) * p.P + s0 + t) * p.R + col];
-      p.glat[static_cast<int64_t>(s0 + t) * 2 * p.R + k * p.R + col] = v;
+    for (int t = 0; t < mtot; ++t) {
+      for (int cc = threadIdx.x; cc < width; cc += kNT) {
+        const int k = cc < ng0 ? 0 : 1, col = cc < ng0 ? cc : cc - ng0;
+        const float v = sum_coh(p.partA + ((static_cast<int64_t>(k) * p.nca) * p.P + s0 + t) * p.R + col,
+                                static_cast<int64_t>(p.P) * p.R, p.nca);
+        st_coh(p.glat + static_cast<int64_t>(s0 + t) * 2 * p.R + k * p.R + col, v);
+      }
     }
     publish(&p.sync[a].rA);
   }
@@ -560,10 +693,7 @@ __device__ void item_bc(const Params& p, const Smem& s, int a, int chunk) {
   float* dstB = p.partB + (static_cast<int64_t>(chunk) * p.P + s0) * p.R;
   for (int tb = 0; tb < mtot; tb += kMB) {
     const int m = min(kMB, mtot - tb);
-    for (int i = threadIdx.x; i < m * 2 * p.R; i += kNT) {
-      const int t = i / (2 * p.R), col = i - t * 2 * p.R;
-      s.vin[t * p.vmax + col] = p.glat[static_cast<int64_t>(s0 + tb + t) * 2 * p.R + col];
-    }
+    stage_coh(p.glat + static_cast<int64_t>(s0 + tb) * 2 * p.R, 2 * p.R, m, 2 * p.R, s.vin, p.vmax);
     __syncthreads();
     float* hs = s.hs;
     const int cbw = p.cb;
@@ -586,15 +716,15 @@ __device__ void item_bc(const Params& p, const Smem& s, int a, int chunk) {
     // h[cols] . A_d[cols] -> partial d_lat
     if (ngd > 0 && ncol > 0)
       tile_gemv_m<kInt8>(m, p.fac[4], e, c0, c0 + ncol, 0, next_pow2(ngd), ngd, hs, cbw, c0, s,
-                         make_emit(dstB + static_cast<int64_t>(tb) * p.R, p.R));
+                         make_emit(dstB + static_cast<int64_t>(tb) * p.R, p.R, 0, 1));
   }
   if (arrive_last(&p.sync[a].cB, p.ncb, &s.misc[1])) {
     const int width = ngd * kGroup;
-    for (int i = threadIdx.x; i < mtot * width; i += kNT) {
-      const int t = i / width, col = i - t * width;
-      float v = 0.f;
-      for (int c = 0; c < p.ncb; ++c) v += p.partB[(static_cast<int64_t>(c) * p.P + s0 + t) * p.R + col];
-      p.dlat[static_cast<int64_t>(s0 + t) * p.R + col] = v;
+    for (int t = 0; t < mtot; ++t) {
+      for (int col = threadIdx.x; col < width; col += kNT) {
+        const float v = sum_coh(p.partB + static_cast<int64_t>(s0 + t) * p.R + col, static_cast<int64_t>(p.P) * p.R, p.ncb);
+        st_coh(p.dlat + static_cast<int64_t>(s0 + t) * p.R + col, v);
+      }
     }
     publish(&p.sync[a].rB);
   }
@@ -609,14 +739,12 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
   const int rkd = rank_of(p, e, 2);
   for (int tb = 0; tb < mtot; tb += kMB) {
     const int m = min(kMB, mtot - tb);
-    for (int i = threadIdx.x; i < m * p.R; i += kNT) {
-      const int t = i / p.R, col = i - t * p.R;
-      s.vin[t * p.vmax + col] = col < ((rkd + kGroup - 1) / kGroup) * kGroup ? p.dlat[static_cast<int64_t>(s0 + tb + t) * p.R + col] : 0.f;
-    }
+    stage_coh(p.dlat + static_cast<int64_t>(s0 + tb) * p.R, p.R, m, ((rkd + kGroup - 1) / kGroup) * kGroup, s.vin, p.vmax);
     __syncthreads();
     if (ncol > 0) {
       Emit em;
       em.swiglu = 0;
+      em.coherent = p.out_mode == LATENT_OUT_PER_SLOT ? 0 : 1;
       for (int t = 0; t < kMB; ++t) {
         const int tt = t < m ? t : 0;
         const int pair = s0 + tb + tt;
@@ -632,7 +760,7 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
       if (rkd > 0) {
         tile_gemv_m<kInt8>(m, p.fac[5], e, 0, rkd, c0 / kGroup, G, gv, s.vin, p.vmax, 0, s, em);
       } else {
-        for (int i = threadIdx.x; i < m * ncol; i += kNT) em.dst[em.rowoff[i / ncol] + i % ncol] = 0.f;
+        for (int i = threadIdx.x; i < m * ncol; i += kNT) st_coh(em.dst + em.rowoff[i / ncol] + i % ncol, 0.f);
       }
     }
     __syncthreads();
@@ -640,24 +768,29 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
   if (p.out_mode == LATENT_OUT_REDUCED && ncol > 0) {
     // Combine: the last of a token's valid slots to finish this d slice sums
     // them in slot order.
-    release_agent();
+    drain_stores();
     __syncthreads();
     for (int t = 0; t < mtot; ++t) {
       const int tok = s.pr_tok[s0 + t];
       if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(&p.ycnt[tok * p.ncd + chunk], 1, __ATOMIC_ACQ_REL,
-                                               __HIP_MEMORY_SCOPE_AGENT);
+        int* cnt = &p.ycnt[tok * p.ncd + chunk];
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s.misc[1] = (old == s.nvalid[tok] - 1);
-        if (old == s.nvalid[tok] - 1) p.ycnt[tok * p.ncd + chunk] = 0;
+        if (old == s.nvalid[tok] - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
       if (s.misc[1]) {
-        acquire_agent();
         for (int col = threadIdx.x; col < ncol; col += kNT) {
           float v = 0.f;
-          for (int k = 0; k < p.K; ++k) {
-            const int pos = s.pos_of[tok * p.K + k];
-            if (pos >= 0) v += p.ybuf[static_cast<int64_t>(pos) * p.d + c0 + col];
+          for (int k0 = 0; k0 < p.K; k0 += 8) {
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int pos = k0 + i < p.K ? s.pos_of[tok * p.K + k0 + i] : -1;
+              y[i] = pos >= 0 ? ld_coh(p.ybuf + static_cast<int64_t>(pos) * p.d + c0 + col) : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v += y[i];
           }
           p.out[static_cast<int64_t>(tok) * p.d + c0 + col] = v;
         }
@@ -669,11 +802,11 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
   if (arrive_last(&p.sync[a].cD, p.ncd, &s.misc[1])) {
     if (threadIdx.x == 0) {
       ExpertSync* es = &p.sync[a];
-      es->cA = 0;
-      es->rA = 0;
-      es->cB = 0;
-      es->rB = 0;
-      __hip_atomic_store(&es->cD, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&es->cA, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&es->rA, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&es->cB, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&es->rB, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&es->cD, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -685,13 +818,14 @@ __device__ void item_zero(const Params& p, const Smem& s, int row, int chunk) {
 }
 
 template <bool kInt8>
-__global__ void __launch_bounds__(kNT) fused_kernel(Params p) {
+__global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 waves per SIMD: two workgroups per CU
   extern __shared__ __align__(16) char smem_raw[];
   const Smem s = carve(p, smem_raw);
   const int tid = threadIdx.x;
-  // Codebook table: entry b holds (level[b & 15], level[b >> 4]) for 32 lanes.
+  // Codebook table: entry b holds (level[b & 15], level[b >> 4]), one copy per
+  // lane of a 16-lane LDS cycle.
   for (int i = tid; i < kLutEntries; i += kNT) {
-    const int b = i >> 5;
+    const int b = i / kLutCopies;
     s.lut[i] = make_float2(nf4_level(b & 15), nf4_level(b >> 4));
   }
   route(p, s);
@@ -701,12 +835,14 @@ __global__ void __launch_bounds__(kNT) fused_kernel(Params p) {
   const int nA = nq * 2 * p.nca, nB = nq * p.ncb, nD = nq * p.ncd;
   const int nZ = zero_rows(p, s, q, 0, true) * p.ncd;
   const int total = nA + nB + nD + nZ;
+  // The next ticket is taken while the current item runs (misc[2]).
+  if (tid == 0) s.misc[2] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (;;) {
-    if (tid == 0) s.misc[1] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    int t = s.misc[1];
+    int t = s.misc[2];
     __syncthreads();
     if (t >= total) break;
+    if (tid == 0) s.misc[2] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t < nA) {
       const int per = 2 * p.nca;
       const int a = q + 8 * (t / per), r = t % per;
@@ -724,10 +860,10 @@ __global__ void __launch_bounds__(kNT) fused_kernel(Params p) {
   // The last workgroup out resets the queues.
   __syncthreads();
   if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(&p.ctrl->exit_count, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(&p.ctrl->exit_count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == static_cast<int>(gridDim.x) - 1) {
-      for (int i = 0; i < 8; ++i) p.ctrl->ticket[i] = 0;
-      __hip_atomic_store(&p.ctrl->exit_count, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < 8; ++i) __hip_atomic_store(&p.ctrl->ticket[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&p.ctrl->exit_count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -744,7 +880,8 @@ namespace fused {
 
 constexpr int kMaxPairs = 512;
 constexpr int kMaxE = 512;
-constexpr size_t kLdsLimit = 160 * 1024;
+constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU
+constexpr int kWgPerCu = 2;
 
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
@@ -757,7 +894,8 @@ static size_t lds_bytes(const latent_moe_args& a, int vmax, int cb, int red) {
 
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
-  return P >= 1 && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512;
+  const bool x_aligned = (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0;  // 16-byte vector staging of x
+  return P >= 1 && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512 && x_aligned;
 }
 
 static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi) {
@@ -771,16 +909,17 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   const int64_t P = T * K, A = std::min(E, P);
   const double est = static_cast<double>(E) * (1.0 - std::pow(1.0 - static_cast<double>(K) / E, static_cast<double>(T)));
   const double per_xcd = std::max(1.0, std::ceil(est / 8.0));
-  pl.red_floats = kMB * 8 * 256;
-  pl.cb = pick_cols(ff, per_xcd, 48, 128, 512);
+  pl.red_floats = kMB * (kW / 2) * 256;  // cross-wave partial slots: (wr / 2) * M * ncols
+  const double wgs_per_xcd = 32.0 * kWgPerCu;
+  pl.cb = pick_cols(ff, per_xcd, 1.5 * wgs_per_xcd, 128, 512);
   pl.ncb = static_cast<int>((ff + pl.cb - 1) / pl.cb);
-  pl.cd = pick_cols(d, per_xcd, 48, 128, 2048);
+  pl.cd = pick_cols(d, per_xcd, 1.5 * wgs_per_xcd, 128, 2048);
   pl.ncd = static_cast<int>((d + pl.cd - 1) / pl.cd);
-  int nca = std::max<int>(1, static_cast<int>(std::ceil(32.0 / per_xcd)));
-  nca = std::max<int>(nca, static_cast<int>((d + 2047) / 2048));
+  int nca = std::max<int>(1, static_cast<int>(std::ceil(wgs_per_xcd / per_xcd)));
+  nca = std::max<int>(nca, static_cast<int>((d + 1023) / 1024));
   for (;; ++nca) {
-    pl.nca = static_cast<int>(std::min<int64_t>(nca, d));
-    pl.ra = static_cast<int>((d + pl.nca - 1) / pl.nca);
+    pl.nca = static_cast<int>(std::min<int64_t>(nca, d / kGroup));
+    pl.ra = static_cast<int>(((d + pl.nca - 1) / pl.nca + kGroup - 1) / kGroup * kGroup);  // whole groups of rows
     pl.nca = static_cast<int>((d + pl.ra - 1) / pl.ra);
     pl.vmax = static_cast<int>(std::max<int64_t>(pl.ra, 2 * R));
     pl.lds = lds_bytes(a, pl.vmax, pl.cb, pl.red_floats);
@@ -810,7 +949,7 @@ static int grid_size() {
   if (!cached[dev]) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = std::max(8, n / 8 * 8);
+    cached[dev] = std::max(8, n / 8 * 8) * kWgPerCu;
   }
   return cached[dev];
 }

@@ -239,6 +239,18 @@ def workspace_size(layer: StackedLayer, n_tokens: int, n_expert_used: int) -> in
     return int(n.value)
 
 
+def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
+    """'fused' (one persistent decode kernel) or 'general' (multi-kernel) for this call shape."""
+    a = layer.args()
+    a.x = x.data_ptr()
+    a.n_tokens, a.n_expert_used = int(x.shape[0]), int(n_expert_used)
+    a.x_dtype, a.weights_dtype, a.out_mode = _DTYPE_CODE[x.dtype], _lib.LATENT_F32, _lib.LATENT_OUT_REDUCED
+    r = lib.latent_moe_path(ctypes.byref(a))
+    if r < 0:
+        check(r, "latent_moe_path")
+    return "fused" if r == 1 else "general"
+
+
 def moe_forward(
     x: torch.Tensor,
     ids: torch.Tensor,

@@ -191,6 +191,14 @@ def test_dsv3_decode_parity(gpu, dsv3, B):
     x_t = gsynth.bf16_input(seed=2000 + B, n_tokens=B, d=7168)
     out = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
     torch.cuda.synchronize()
+    # A second call must reproduce the first bit for bit (the decode kernel is
+    # deterministic and leaves its control block as it found it).
+    again = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    from latent_amd.moe import workspace_error
+
+    assert workspace_error(dsv3.workspace(B, 8)) == 0
     ids, w, x = ids_t.cpu().numpy(), w_t.cpu().numpy(), x_t.float().cpu().numpy()
     experts, local = remap_ids(ids, 256)
     host = subset_to_host(dsv3, experts)
