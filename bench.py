@@ -47,7 +47,11 @@ def parse():
     p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
     p.add_argument("--routings", type=int, default=8, help="distinct routings per batch size")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-batch", type=int, default=64)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU-baseline sample time")
+    p.add_argument("--copy-probe-mb", type=int, default=0,
+                   help="run one device-to-device copy of this many MiB first (counter calibration)")
+    p.add_argument("--zipf-gamma", type=float, default=0.11,
+                   help="prefill router skew; 0.11 gives about 70..400 tokens per expert at 4096 tokens")
     return p.parse_args()
 
 
@@ -94,6 +98,7 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
     gbps = bytes_per_step / (ms * 1e-3) / 1e9
     return {
         "batch": batch,
+        "path": latent.moe_path(layers[0], xs[0], K),
         "ms_per_step": ms,
         "tokens_per_s": batch / (ms * 1e-3),
         "hbm_gbps": gbps,
@@ -103,8 +108,8 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
     }, routes, xs
 
 
-def prefill_point(torch, latent, gsynth, layers, tokens, steps):
-    ids, w = gsynth.route(seed=30_000, n_tokens=tokens, n_expert=E, k=K, zipf_gamma=1.0)
+def prefill_point(torch, latent, gsynth, layers, tokens, steps, zipf_gamma):
+    ids, w = gsynth.route(seed=30_000, n_tokens=tokens, n_expert=E, k=K, zipf_gamma=zipf_gamma)
     x = gsynth.bf16_input(seed=30_001, n_tokens=tokens, d=D)
     out = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
     ws = layers[0].workspace(tokens, K)
@@ -124,42 +129,67 @@ def prefill_point(torch, latent, gsynth, layers, tokens, steps):
         "mfma_frac_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
         "tokens_per_expert_max": int(counts.max()),
         "tokens_per_expert_min": int(counts.min()),
-        "path": "wave64 GEMV chain (fp32)",
+        "path": latent.moe_path(layers[0], x, K),
+        "zipf_gamma": zipf_gamma,
     }
 
 
-def cpu_baseline(torch, layer, routes, xs, batch):
-    """The oracle (numpy port of loader/latent_runtime.py) on one decode step, 1 thread."""
+def cpu_baseline(torch, layer, routes, xs, batch, min_seconds):
+    """The oracle (numpy port of loader/latent_runtime.py) on decode steps of the
+    same workload, 1 thread, repeated over the routings until min_seconds."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from threadpoolctl import threadpool_limits
 
     from oracle import latent_ref as ref
 
-    ids = routes[0][0].cpu().numpy()
-    w = routes[0][1].cpu().numpy()
-    x = xs[0].float().cpu().numpy()
-    experts = np.unique(ids[(ids >= 0) & (ids < E)])
-    lut = -np.ones(E, np.int64)
-    lut[experts] = np.arange(experts.size)
-    local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
-    sel = torch.as_tensor(experts, device="cuda")
-    facs = {}
-    for name, f in layer.factors().items():
-        facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
-                                       f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
-    host = ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R)
-    with threadpool_limits(limits=1):
-        t0 = time.perf_counter()
-        ref.moe_forward(x, local, w, host)
-        dt = time.perf_counter() - t0
+    total, steps, experts_seen = 0.0, 0, 0
+    while total < min_seconds and steps < len(routes):
+        ids = routes[steps][0].cpu().numpy()
+        w = routes[steps][1].cpu().numpy()
+        x = xs[steps].float().cpu().numpy()
+        experts = np.unique(ids[(ids >= 0) & (ids < E)])
+        lut = -np.ones(E, np.int64)
+        lut[experts] = np.arange(experts.size)
+        local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
+        sel = torch.as_tensor(experts, device="cuda")
+        facs = {}
+        for name, f in layer.factors().items():
+            facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
+                                           f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
+        host = ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R)
+        with threadpool_limits(limits=1):
+            t0 = time.perf_counter()
+            ref.moe_forward(x, local, w, host)
+            total += time.perf_counter() - t0
+        steps += 1
+        experts_seen += experts.size
     return {
-        "value": batch / dt,
+        "value": batch * steps / total,
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"one decode step at batch {batch} ({experts.size} distinct experts dequantized once each, "
-                  f"numpy fp32, 1 BLAS thread) on {os.cpu_count()} visible host cores; {dt:.1f} s",
+        "sample": f"{steps} decode steps at batch {batch} ({experts_seen / steps:.0f} distinct experts per step, "
+                  f"each dequantized once; numpy fp32, 1 BLAS thread; {os.cpu_count()} host cores visible), "
+                  f"{total:.1f} s of CPU time",
     }
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "fused_kernel_decode_b64_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per fused_kernel launch at batch 64 from the committed counter
+    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a
+    1 GiB copy), or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -173,6 +203,11 @@ def main():
     import latent_amd as latent
     from latent_amd import synth as gsynth
 
+    if args.copy_probe_mb:
+        src = torch.empty(args.copy_probe_mb << 20, dtype=torch.uint8, device="cuda")
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     t0 = time.time()
     layers = [gsynth.make_layer(seed=1 + 1000 * i, n_expert=E, d=D, ff=FF, max_rank=R) for i in range(args.layers)]
     torch.cuda.synchronize()
@@ -190,11 +225,11 @@ def main():
               file=sys.stderr, flush=True)
     prefill = None
     if args.prefill:
-        prefill = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps)
+        prefill = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps, args.zipf_gamma)
         print(f"# prefill T={args.prefill}: {prefill['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch)
+        cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch, args.cpu_seconds)
         print(f"# cpu baseline: {cpu['value']:.2f} tokens/s", file=sys.stderr, flush=True)
 
     result = {
@@ -223,8 +258,10 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": head["roofline_frac"],
-            "traffic": None,
-            "kernel": "latent_moe_ffn_forward (all kernels of one call)",
+            "traffic": measured_traffic() if head["path"] == "fused" and args.batch == 64 else None,
+            "traffic_source": "profiles/fused_kernel_decode_b64_hbm_traffic.md (rocprofv3 --pmc)",
+            "kernel": ("fused_kernel (one launch per step)" if head["path"] == "fused"
+                       else "latent_moe_ffn_forward (prep + 3 phase kernels per step)"),
             "bytes_per_launch": head["bytes_per_step"],
         },
         "cpu_baseline": cpu,

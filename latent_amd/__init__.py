@@ -17,7 +17,16 @@ from ._lib import (  # noqa: F401
     LatentError,
     lib,
 )
-from .moe import DeviceFactor, StackedLayer, moe_forward, pack_int8, pack_nf4, unpack, workspace_size  # noqa: F401
+from .moe import (  # noqa: F401
+    DeviceFactor,
+    StackedLayer,
+    moe_forward,
+    moe_path,
+    pack_int8,
+    pack_nf4,
+    unpack,
+    workspace_size,
+)
 
 __version__ = "0.1.0"
 

@@ -91,7 +91,7 @@ class LatentError(RuntimeError):
 def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
-            f"{LIB_PATH} is missing: build it with `python -m latent_amd.build` "
+            f"{LIB_PATH} is missing: build it with `python latent_amd/build.py` "
             "(there is no CPU fallback)"
         )
     lib = ctypes.CDLL(str(LIB_PATH))

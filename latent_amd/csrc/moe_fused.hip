@@ -318,14 +318,25 @@ struct FactorArgs {
   int64_t rows, cols;
 };
 
-__device__ __forceinline__ FactorArgs fargs(const Factor& f) {
+// One factor of the six, selected without indexing the kernel arguments at run
+// time (a runtime index would force them into private memory).
+__device__ __forceinline__ FactorArgs fargs(const Params& p, int i) {
+  const Factor& f = i == 0 ? p.fac[0] : i == 1 ? p.fac[1] : i == 2 ? p.fac[2] : i == 3 ? p.fac[3] : i == 4 ? p.fac[4] : p.fac[5];
   return FactorArgs{as_global(f.codes), as_global(f.scales), as_global(f.ext.bitmap), as_global(f.ext.row_offset),
                     as_global(f.ext.data), f.rows, f.cols};
 }
 
-// Where a tile's results go: dst[rowoff[t] + col] = v * scale[t], or with
-// swiglu set, dst[...] = SiLU(dst[...]) * v * scale[t] (dst holds the gate).
-struct Emit {
+// One tile GEMV of a workgroup:
+//   y[t][j] = sum_{r0 <= r < r1} vin[t][r - vbase] * scale(r, g0 + j/32) * level(code(r, 32*g0 + j))
+// for the g_valid groups starting at g0 (G = next power of two >= g_valid),
+// t < m, written as dst[rowoff[t] + j] = y * scale[t], or with swiglu set as
+// dst[...] = SiLU(dst[...]) * y * scale[t] (dst then holds the gate).
+struct Job {
+  FactorArgs f;
+  int64_t e;
+  int r0, r1, g0, G, g_valid;
+  lptr<const float> vin;
+  int vstride, vbase;
   float* dst;
   int64_t rowoff[kMB];
   float scale[kMB];
@@ -333,14 +344,19 @@ struct Emit {
   int coherent;  // dst is read by another workgroup: store with st_coh
 };
 
+template <typename T>
+__device__ __forceinline__ T pick_t(int t, const T (&a)[kMB]) {
+  return t == 0 ? a[0] : t == 1 ? a[1] : t == 2 ? a[2] : a[3];
+}
+
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
-__device__ __forceinline__ void emit_one(const Emit& em, int t, int col, float v) {
-  float* q = em.dst + em.rowoff[t] + col;
-  if (em.coherent)
-    st_coh(q, v * em.scale[t]);
+__device__ __forceinline__ void emit_one(const Job& j, int64_t rowoff, float scale, int col, float v) {
+  float* q = j.dst + rowoff + col;
+  if (j.coherent)
+    st_coh(q, v * scale);
   else
-    *q = em.swiglu ? silu_f32(*q) * v * em.scale[t] : v * em.scale[t];
+    *q = j.swiglu ? silu_f32(*q) * v * scale : v * scale;
 }
 
 // A lane owns half a group: 16 columns (8 code bytes) of one row per step.
@@ -405,13 +421,12 @@ __device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, in
 // per row; 16 lanes = one 128-byte row segment) x rows; waves along half
 // groups (wg) x rows (wr).  The in-wave sum runs over the row lanes; the
 // cross-wave sum folds the upper half of the row slices onto the lower half,
-// then adds the lower slices in order (fixed order, deterministic).
+// then adds the lower slices in order (fixed order, deterministic).  M is the
+// token capacity of the accumulators, m <= M the tokens present.
 template <int M, bool kInt8>
-__device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, int g0, int G, int g_valid,
-                                       lptr<const float> vin, int vstride, int vbase, lptr<const float2> lut2,
-                                       lptr<float> red, Emit em) {
+__device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> lut, lptr<float> red) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int H = 2 * G, h_valid = 2 * g_valid;
+  const int H = 2 * j.G, h_valid = 2 * j.g_valid;
   int lph, wg;
   if (H <= 16) {
     lph = H;
@@ -428,26 +443,28 @@ __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, 
   const int h = wgi * lph + hl;                // half group within the tile
   const int rstep = wr * rpw;
   const uint32_t lanebase = static_cast<uint32_t>(lane & (kLutCopies - 1)) << 3;
-  const lptr<const char> lut = reinterpret_cast<lptr<const char>>(lut2);
+  const FactorArgs& f = j.f;
   const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
 
   float acc[M][kHalf];
 #pragma unroll
   for (int t = 0; t < M; ++t)
 #pragma unroll
-    for (int j = 0; j < kHalf; ++j) acc[t][j] = 0.f;
+    for (int c = 0; c < kHalf; ++c) acc[t][c] = 0.f;
 
   // Rows of this lane: row_w + ro + k*rstep for k < nsteps (uniform across the
-  // wave); rows past r1 read a valid row and are masked by a zero scale.
+  // wave); rows past r1 read a valid row (clamped into [r0, r1), or r0 for an
+  // empty range) and are masked by a zero scale.
+  const int r0 = j.r0, r1 = j.r1;
   const int row_w = r0 + wri * rpw;
   const int nsteps = row_w < r1 ? (r1 - 1 - row_w) / rstep + 1 : 0;
-  const int row0 = min(row_w + ro, r1 - 1);
+  const int row0 = max(r0, min(row_w + ro, r1 - 1));
   const bool hvalid = h < h_valid;
   const int hh = hvalid ? h : 0;
-  const int gg = g0 + (hh >> 1), half = hh & 1;
+  const int gg = j.g0 + (hh >> 1), half = hh & 1;
   const gptr<uint8_t> cbase =
-      f.codes + (e * f.rows + row0) * cstride + static_cast<int64_t>(gg) * kGroupBytes + half * (kGroupBytes / 2);
-  const gptr<uint16_t> sbase = f.scales + (e * f.rows + row0) * sstride + gg;
+      f.codes + (j.e * f.rows + row0) * cstride + static_cast<int64_t>(gg) * kGroupBytes + half * (kGroupBytes / 2);
+  const gptr<uint16_t> sbase = f.scales + (j.e * f.rows + row0) * sstride + gg;
   const int64_t cstep = static_cast<int64_t>(rstep) * cstride, sstep = static_cast<int64_t>(rstep) * sstride;
   // Ring of kRing rows in flight per lane; slot u is refilled with the row
   // kRing steps ahead right after it is consumed.
@@ -466,15 +483,15 @@ __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, 
       const int k = k0 + u;
       const int row = row_w + ro + k * rstep;
       const bool ok = hvalid && k < nsteps && row < r1;
-      const int vr = (ok ? row : r0) - vbase;
+      const int vr = (ok ? row : r0) - j.vbase;
       const float sm = ok ? sring[u] : 0.f;
       float xs[M];
 #pragma unroll
-      for (int t = 0; t < M; ++t) xs[t] = vin[t * vstride + vr] * sm;
+      for (int t = 0; t < M; ++t) xs[t] = j.vin[t * j.vstride + vr] * sm;
       bool done = false;
       if constexpr (kInt8) {
-        if (f.bitmap != nullptr && ok && is_int8_group(f, e, row, gg)) {
-          fma_half_int8<M>(f, e, row, gg, half, xs, acc);
+        if (f.bitmap != nullptr && ok && is_int8_group(f, j.e, row, gg)) {
+          fma_half_int8<M>(f, j.e, row, gg, half, xs, acc);
           done = true;
         }
       }
@@ -489,16 +506,19 @@ __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, 
 #pragma unroll
     for (int t = 0; t < M; ++t)
 #pragma unroll
-      for (int j = 0; j < kHalf; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
+      for (int c = 0; c < kHalf; ++c) acc[t][c] += __shfl_xor(acc[t][c], off);
   }
   const int ncols = H * kHalf;
   const bool writer = ro == 0 && hvalid;
   if (wr == 1) {
     if (writer) {
 #pragma unroll
-      for (int t = 0; t < M; ++t)
+      for (int t = 0; t < M; ++t) {
+        if (t < m) {
 #pragma unroll
-        for (int j = 0; j < kHalf; ++j) emit_one(em, t, h * kHalf + j, acc[t][j]);
+          for (int c = 0; c < kHalf; ++c) emit_one(j, j.rowoff[t], j.scale[t], h * kHalf + c, acc[t][c]);
+        }
+      }
     }
     __syncthreads();
     return;
@@ -511,7 +531,7 @@ __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, 
     for (int t = 0; t < M; ++t) {
       lptr<float> dst = red + (wri * M + t) * ncols + h * kHalf;
 #pragma unroll
-      for (int j = 0; j < kHalf; ++j) dst[j] = acc[t][j];
+      for (int c = 0; c < kHalf; ++c) dst[c] = acc[t][c];
     }
   }
   __syncthreads();
@@ -520,49 +540,32 @@ __device__ __noinline__ void tile_gemv(FactorArgs f, int64_t e, int r0, int r1, 
     for (int t = 0; t < M; ++t) {
       lptr<float> dst = red + ((wri - slots) * M + t) * ncols + h * kHalf;
 #pragma unroll
-      for (int j = 0; j < kHalf; ++j) dst[j] += acc[t][j];
+      for (int c = 0; c < kHalf; ++c) dst[c] += acc[t][c];
     }
   }
   __syncthreads();
   const int nvalid_cols = h_valid * kHalf;
-  for (int i = tid; i < M * nvalid_cols; i += kNT) {
+  for (int i = tid; i < m * nvalid_cols; i += kNT) {
     const int t = i / nvalid_cols, col = i - t * nvalid_cols;
     float v = 0.f;
     for (int w = 0; w < slots; ++w) v += red[(w * M + t) * ncols + col];
-    emit_one(em, t, col, v);
+    emit_one(j, pick_t(t, j.rowoff), pick_t(t, j.scale), col, v);
   }
   __syncthreads();
 }
 
+// The one place the tile is expanded (accumulator capacities 1, 2 and 4 tokens).
 template <bool kInt8>
-__device__ __forceinline__ void tile_gemv_m(int m, const Factor& fac, int64_t e, int r0, int r1, int g0, int G,
-                                            int g_valid, const float* vin, int vstride, int vbase, const Smem& s,
-                                            const Emit& em) {
-  const FactorArgs f = fargs(fac);
-  const lptr<const float> v = as_lds(vin);
-  const lptr<const float2> lut = as_lds(static_cast<const float2*>(s.lut));
+__device__ __forceinline__ void run_tile(const Job& j, int m, const Smem& s) {
+  const lptr<const char> lut = reinterpret_cast<lptr<const char>>(as_lds(static_cast<const float2*>(s.lut)));
   const lptr<float> red = as_lds(s.red);
-  switch (m) {
-    case 1: tile_gemv<1, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
-    case 2: tile_gemv<2, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
-    case 3: tile_gemv<3, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
-    default: tile_gemv<4, kInt8>(f, e, r0, r1, g0, G, g_valid, v, vstride, vbase, lut, red, em); break;
-  }
+  if (m == 1)
+    tile_gemv<1, kInt8>(j, 1, lut, red);
+  else if (m == 2)
+    tile_gemv<2, kInt8>(j, 2, lut, red);
+  else
+    tile_gemv<4, kInt8>(j, m, lut, red);
 }
-
-__device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int swiglu = 0, int coherent = 0) {
-  Emit em;
-  em.dst = dst;
-  em.coherent = coherent;
-#pragma unroll
-  for (int t = 0; t < kMB; ++t) {
-    em.rowoff[t] = row_stride * t;
-    em.scale[t] = 1.0f;
-  }
-  em.swiglu = swiglu;
-  return em;
-}
-
 
 // ---------------------------------------------------------------------------
 // Staging and reduction helpers.  Loads are issued in batches before any use
@@ -570,7 +573,8 @@ __device__ __forceinline__ Emit make_emit(float* dst, int64_t row_stride, int sw
 // ---------------------------------------------------------------------------
 // x rows of up to kMB tokens, columns [c0, c0 + n) (n % 8 == 0, c0 % 8 == 0),
 // converted to fp32 into dst[t * dstride + j].
-__device__ void stage_x(const Params& p, const int* toks, int m, int c0, int n, float* dst, int dstride) {
+__device__ __forceinline__ void stage_x(const Params& p, const int* toks, int m, int c0, int n, float* dst,
+                                        int dstride) {
   const int tid = threadIdx.x;
   for (int j0 = tid * 8; j0 < n; j0 += kNT * 8) {
     float v[kMB][8];
@@ -584,8 +588,8 @@ __device__ void stage_x(const Params& p, const int* toks, int m, int c0, int n, 
           v[t][0] = a.x; v[t][1] = a.y; v[t][2] = a.z; v[t][3] = a.w;
           v[t][4] = b.x; v[t][5] = b.y; v[t][6] = b.z; v[t][7] = b.w;
         } else {
-          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + base);
-          const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+          const uint4 hv = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + base);
+          const uint32_t w[4] = {hv.x, hv.y, hv.z, hv.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             if (p.x_dtype == LATENT_BF16) {
@@ -610,7 +614,7 @@ __device__ void stage_x(const Params& p, const int* toks, int m, int c0, int n, 
 }
 
 // Coherent rows src[t * sstride + j] (j < n) of up to kMB tokens into LDS.
-__device__ void stage_coh(const float* src, int64_t sstride, int m, int n, float* dst, int dstride) {
+__device__ __forceinline__ void stage_coh(const float* src, int64_t sstride, int m, int n, float* dst, int dstride) {
   for (int j = threadIdx.x; j < n; j += kNT) {
     float v[kMB];
 #pragma unroll
@@ -635,145 +639,169 @@ __device__ __forceinline__ float sum_coh(const float* src, int64_t cstride, int 
 }
 
 // ---------------------------------------------------------------------------
-// Items
+// Items.  An item is a list of tile jobs per batch of up to kMB of the
+// expert's pairs, bracketed by a prologue (wait for its inputs) and an
+// epilogue (partial-sum reduction / output combine / counter reset):
+//   A  (kind, chunk): rows [chunk*ra, +ra) of A_g (kind 0) or A_u (kind 1)
+//                     x -> partA[kind][chunk]
+//   BC (chunk):       ff columns [chunk*cb, +cb):  g_lat . B_g -> hs,
+//                     hs = SiLU(hs) * (u_lat . B_u), hs . A_d rows -> partB[chunk]
+//   D  (chunk):       d columns [chunk*cd, +cd) of d_lat . B_d -> out / ybuf
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ Factor pick(const Factor& a, const Factor& b, bool first) {
-  Factor f;
-  f.codes = first ? a.codes : b.codes;
-  f.scales = first ? a.scales : b.scales;
-  f.ext.bitmap = first ? a.ext.bitmap : b.ext.bitmap;
-  f.ext.row_offset = first ? a.ext.row_offset : b.ext.row_offset;
-  f.ext.data = first ? a.ext.data : b.ext.data;
-  f.rows = first ? a.rows : b.rows;
-  f.cols = first ? a.cols : b.cols;
-  return f;
-}
+enum ItemType { kItemA = 0, kItemBC = 1, kItemD = 2, kItemZ = 3 };
 
-template <bool kInt8>
-__device__ void item_a(const Params& p, const Smem& s, int a, int kind, int chunk) {
-  const Factor f = pick(p.fac[0], p.fac[2], kind == 0);
-  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
-  const int ng = (rank_of(p, e, kind) + kGroup - 1) / kGroup;
-  const int r0 = chunk * p.ra, r1 = min(p.d, r0 + p.ra), nrows = r1 - r0;
-  if (ng > 0 && nrows > 0) {
-    const int G = next_pow2(ng);
-    for (int tb = 0; tb < mtot; tb += kMB) {
-      const int m = min(kMB, mtot - tb);
-      stage_x(p, s.pr_tok + s0 + tb, m, r0, nrows, s.vin, p.vmax);
-      __syncthreads();
-      float* dst = p.partA + ((static_cast<int64_t>(kind) * p.nca + chunk) * p.P + s0 + tb) * p.R;
-      tile_gemv_m<kInt8>(m, f, e, r0, r1, 0, G, ng, s.vin, p.vmax, r0, s, make_emit(dst, p.R, 0, 1));
-    }
-  }
-  // The last A item of the expert sums the partials into g_lat | u_lat.
-  if (arrive_last(&p.sync[a].cA, 2 * p.nca, &s.misc[1])) {
-    const int ng0 = (rank_of(p, e, 0) + kGroup - 1) / kGroup * kGroup;
-    const int ng1 = (rank_of(p, e, 1) + kGroup - 1) / kGroup * kGroup;
-    const int width = ng0 + ng1;
-    for (int t = 0; t < mtot; ++t) {
-      for (int cc = threadIdx.x; cc < width; cc += kNT) {
-        const int k = cc < ng0 ? 0 : 1, col = cc < ng0 ? cc : cc - ng0;
-        const float v = sum_coh(p.partA + ((static_cast<int64_t>(k) * p.nca) * p.P + s0 + t) * p.R + col,
-                                static_cast<int64_t>(p.P) * p.R, p.nca);
-        st_coh(p.glat + static_cast<int64_t>(s0 + t) * 2 * p.R + k * p.R + col, v);
-      }
-    }
-    publish(&p.sync[a].rA);
+struct Item {
+  int type, a, kind, chunk;
+  int e, s0, mtot;
+};
+
+__device__ __forceinline__ int groups_of(int rank) { return (rank + kGroup - 1) / kGroup; }
+
+// Stage the batch's activations (tokens tb.., m of them) into LDS.
+__device__ __forceinline__ void stage_batch(const Params& p, const Smem& s, const Item& it, int tb, int m) {
+  if (it.type == kItemA) {
+    const int r0 = it.chunk * p.ra, nrows = min(p.d, r0 + p.ra) - r0;
+    stage_x(p, s.pr_tok + it.s0 + tb, m, r0, nrows, s.vin, p.vmax);
+  } else if (it.type == kItemBC) {
+    stage_coh(p.glat + static_cast<int64_t>(it.s0 + tb) * 2 * p.R, 2 * p.R, m, 2 * p.R, s.vin, p.vmax);
+  } else {
+    const int n = groups_of(rank_of(p, it.e, 2)) * kGroup;
+    stage_coh(p.dlat + static_cast<int64_t>(it.s0 + tb) * p.R, p.R, m, n, s.vin, p.vmax);
   }
 }
 
-template <bool kInt8>
-__device__ void item_bc(const Params& p, const Smem& s, int a, int chunk) {
-  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
-  wait_flag(p, &p.sync[a].rA);
-  const int c0 = chunk * p.cb, ncol = min(p.cb, p.ff - c0);
-  const int gv = ncol / kGroup, G = next_pow2(p.cb / kGroup);
-  const int rk0 = rank_of(p, e, 0), rk1 = rank_of(p, e, 1), rkd = rank_of(p, e, 2);
-  const int ngd = (rkd + kGroup - 1) / kGroup;
-  float* dstB = p.partB + (static_cast<int64_t>(chunk) * p.P + s0) * p.R;
-  for (int tb = 0; tb < mtot; tb += kMB) {
-    const int m = min(kMB, mtot - tb);
-    stage_coh(p.glat + static_cast<int64_t>(s0 + tb) * 2 * p.R, 2 * p.R, m, 2 * p.R, s.vin, p.vmax);
-    __syncthreads();
-    float* hs = s.hs;
-    const int cbw = p.cb;
-    if (ncol > 0) {
-      if (rk0 > 0)
-        tile_gemv_m<kInt8>(m, p.fac[1], e, 0, rk0, c0 / kGroup, G, gv, s.vin, p.vmax, 0, s, make_emit(hs, cbw));
-      else
-        for (int i = threadIdx.x; i < m * ncol; i += kNT) hs[(i / ncol) * cbw + i % ncol] = 0.f;
-      __syncthreads();
-      Emit em = make_emit(hs, cbw, 1);
-      if (p.wbd)
-        for (int t = 0; t < m; ++t) em.scale[t] = s.pr_w[s0 + tb + t];
-      if (rk1 > 0) {
-        tile_gemv_m<kInt8>(m, p.fac[3], e, 0, rk1, c0 / kGroup, G, gv, s.vin + p.R, p.vmax, 0, s, em);
-      } else {
-        for (int i = threadIdx.x; i < m * ncol; i += kNT) hs[(i / ncol) * cbw + i % ncol] = 0.f;
-        __syncthreads();
-      }
-    }
-    // h[cols] . A_d[cols] -> partial d_lat
-    if (ngd > 0 && ncol > 0)
-      tile_gemv_m<kInt8>(m, p.fac[4], e, c0, c0 + ncol, 0, next_pow2(ngd), ngd, hs, cbw, c0, s,
-                         make_emit(dstB + static_cast<int64_t>(tb) * p.R, p.R, 0, 1));
+// Tile job `sub` of the batch at tb; false if there is nothing to compute.
+__device__ __forceinline__ bool make_job(const Params& p, const Smem& s, const Item& it, int sub, int tb, int m,
+                                         Job& j) {
+  j.e = it.e;
+  j.swiglu = 0;
+  j.coherent = 0;
+  j.vin = as_lds(static_cast<const float*>(s.vin));
+  j.vstride = p.vmax;
+  j.vbase = 0;
+  j.g0 = 0;
+#pragma unroll
+  for (int t = 0; t < kMB; ++t) j.scale[t] = 1.0f;
+  if (it.type == kItemA) {
+    const int ng = groups_of(rank_of(p, it.e, it.kind));
+    j.f = fargs(p, it.kind == 0 ? 0 : 2);
+    j.r0 = it.chunk * p.ra;
+    j.r1 = min(p.d, j.r0 + p.ra);
+    j.G = next_pow2(ng);
+    j.g_valid = ng;
+    j.vbase = j.r0;
+    j.dst = p.partA + ((static_cast<int64_t>(it.kind) * p.nca + it.chunk) * p.P + it.s0 + tb) * p.R;
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) j.rowoff[t] = static_cast<int64_t>(t) * p.R;
+    j.coherent = 1;
+    return ng > 0 && j.r1 > j.r0;
   }
-  if (arrive_last(&p.sync[a].cB, p.ncb, &s.misc[1])) {
-    const int width = ngd * kGroup;
-    for (int t = 0; t < mtot; ++t) {
-      for (int col = threadIdx.x; col < width; col += kNT) {
-        const float v = sum_coh(p.partB + static_cast<int64_t>(s0 + t) * p.R + col, static_cast<int64_t>(p.P) * p.R, p.ncb);
-        st_coh(p.dlat + static_cast<int64_t>(s0 + t) * p.R + col, v);
-      }
-    }
-    publish(&p.sync[a].rB);
-  }
-}
-
-template <bool kInt8>
-__device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
-  const int e = s.act_e[a], s0 = s.act_s[a], mtot = s.act_c[a];
-  wait_flag(p, &p.sync[a].rB);
-  const int c0 = chunk * p.cd, ncol = min(p.cd, p.d - c0);
-  const int gv = ncol / kGroup, G = next_pow2(p.cd / kGroup);
-  const int rkd = rank_of(p, e, 2);
-  for (int tb = 0; tb < mtot; tb += kMB) {
-    const int m = min(kMB, mtot - tb);
-    stage_coh(p.dlat + static_cast<int64_t>(s0 + tb) * p.R, p.R, m, ((rkd + kGroup - 1) / kGroup) * kGroup, s.vin, p.vmax);
-    __syncthreads();
-    if (ncol > 0) {
-      Emit em;
-      em.swiglu = 0;
-      em.coherent = p.out_mode == LATENT_OUT_PER_SLOT ? 0 : 1;
-      for (int t = 0; t < kMB; ++t) {
-        const int tt = t < m ? t : 0;
-        const int pair = s0 + tb + tt;
-        if (p.out_mode == LATENT_OUT_PER_SLOT) {
-          em.rowoff[t] = (static_cast<int64_t>(s.pr_tok[pair]) * p.K + s.pr_slot[pair]) * p.d;
-          em.scale[t] = 1.0f;
-        } else {
-          em.rowoff[t] = static_cast<int64_t>(pair) * p.d;
-          em.scale[t] = p.wbd ? 1.0f : s.pr_w[pair];
+  if (it.type == kItemBC) {
+    const int c0 = it.chunk * p.cb, ncol = min(p.cb, p.ff - c0);
+    if (ncol <= 0) return false;
+    if (sub < 2) {
+      // g = g_lat . B_g (sub 0) into hs, then hs = SiLU(hs) * (u_lat . B_u) (sub 1).
+      j.f = fargs(p, sub == 0 ? 1 : 3);
+      j.r0 = 0;
+      j.r1 = rank_of(p, it.e, sub);  // an empty row range yields zeros
+      j.g0 = c0 / kGroup;
+      j.G = next_pow2(p.cb / kGroup);
+      j.g_valid = ncol / kGroup;
+      j.vin = as_lds(static_cast<const float*>(s.vin + sub * p.R));
+      j.dst = s.hs;
+#pragma unroll
+      for (int t = 0; t < kMB; ++t) j.rowoff[t] = static_cast<int64_t>(t) * p.cb;
+      if (sub == 1) {
+        j.swiglu = 1;
+        if (p.wbd) {
+#pragma unroll
+          for (int t = 0; t < kMB; ++t) j.scale[t] = s.pr_w[it.s0 + tb + min(t, m - 1)];
         }
       }
-      em.dst = (p.out_mode == LATENT_OUT_PER_SLOT ? p.out : p.ybuf) + c0;
-      if (rkd > 0) {
-        tile_gemv_m<kInt8>(m, p.fac[5], e, 0, rkd, c0 / kGroup, G, gv, s.vin, p.vmax, 0, s, em);
-      } else {
-        for (int i = threadIdx.x; i < m * ncol; i += kNT) st_coh(em.dst + em.rowoff[i / ncol] + i % ncol, 0.f);
-      }
+      return true;
     }
-    __syncthreads();
+    // hs . A_d rows [c0, c0 + ncol) -> partial d_lat.
+    const int ngd = groups_of(rank_of(p, it.e, 2));
+    j.f = fargs(p, 4);
+    j.r0 = c0;
+    j.r1 = c0 + ncol;
+    j.G = next_pow2(ngd);
+    j.g_valid = ngd;
+    j.vin = as_lds(static_cast<const float*>(s.hs));
+    j.vstride = p.cb;
+    j.vbase = c0;
+    j.dst = p.partB + (static_cast<int64_t>(it.chunk) * p.P + it.s0 + tb) * p.R;
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) j.rowoff[t] = static_cast<int64_t>(t) * p.R;
+    j.coherent = 1;
+    return ngd > 0;
   }
+  // D: d_lat . B_d, columns [c0, c0 + ncol).
+  const int c0 = it.chunk * p.cd, ncol = min(p.cd, p.d - c0);
+  j.f = fargs(p, 5);
+  j.r0 = 0;
+  j.r1 = rank_of(p, it.e, 2);
+  j.g0 = c0 / kGroup;
+  j.G = next_pow2(p.cd / kGroup);
+  j.g_valid = ncol / kGroup;
+  const bool per_slot = p.out_mode == LATENT_OUT_PER_SLOT;
+  j.coherent = per_slot ? 0 : 1;
+  j.dst = (per_slot ? p.out : p.ybuf) + c0;
+#pragma unroll
+  for (int t = 0; t < kMB; ++t) {
+    const int pair = it.s0 + tb + min(t, m - 1);
+    if (per_slot) {
+      j.rowoff[t] = (static_cast<int64_t>(s.pr_tok[pair]) * p.K + s.pr_slot[pair]) * p.d;
+    } else {
+      j.rowoff[t] = static_cast<int64_t>(pair) * p.d;
+      j.scale[t] = p.wbd ? 1.0f : s.pr_w[pair];
+    }
+  }
+  return ncol > 0;
+}
+
+// A: the last A item of the expert sums the partials into g_lat | u_lat.
+__device__ __forceinline__ void finish_a(const Params& p, const Smem& s, const Item& it) {
+  if (!arrive_last(&p.sync[it.a].cA, 2 * p.nca, &s.misc[1])) return;
+  const int ng0 = groups_of(rank_of(p, it.e, 0)) * kGroup;
+  const int ng1 = groups_of(rank_of(p, it.e, 1)) * kGroup;
+  const int width = ng0 + ng1;
+  for (int t = 0; t < it.mtot; ++t) {
+    for (int cc = threadIdx.x; cc < width; cc += kNT) {
+      const int k = cc < ng0 ? 0 : 1, col = cc < ng0 ? cc : cc - ng0;
+      const float v = sum_coh(p.partA + ((static_cast<int64_t>(k) * p.nca) * p.P + it.s0 + t) * p.R + col,
+                              static_cast<int64_t>(p.P) * p.R, p.nca);
+      st_coh(p.glat + static_cast<int64_t>(it.s0 + t) * 2 * p.R + k * p.R + col, v);
+    }
+  }
+  publish(&p.sync[it.a].rA);
+}
+
+// BC: the last BC item of the expert sums the partials into d_lat.
+__device__ __forceinline__ void finish_bc(const Params& p, const Smem& s, const Item& it) {
+  if (!arrive_last(&p.sync[it.a].cB, p.ncb, &s.misc[1])) return;
+  const int width = groups_of(rank_of(p, it.e, 2)) * kGroup;
+  for (int t = 0; t < it.mtot; ++t) {
+    for (int col = threadIdx.x; col < width; col += kNT) {
+      const float v =
+          sum_coh(p.partB + static_cast<int64_t>(it.s0 + t) * p.R + col, static_cast<int64_t>(p.P) * p.R, p.ncb);
+      st_coh(p.dlat + static_cast<int64_t>(it.s0 + t) * p.R + col, v);
+    }
+  }
+  publish(&p.sync[it.a].rB);
+}
+
+// D: in reduced mode the last of a token's valid slots to finish this d slice
+// sums them in slot order; the last D item of the expert resets its counters.
+__device__ __forceinline__ void finish_d(const Params& p, const Smem& s, const Item& it) {
+  const int c0 = it.chunk * p.cd, ncol = min(p.cd, p.d - c0);
   if (p.out_mode == LATENT_OUT_REDUCED && ncol > 0) {
-    // Combine: the last of a token's valid slots to finish this d slice sums
-    // them in slot order.
     drain_stores();
     __syncthreads();
-    for (int t = 0; t < mtot; ++t) {
-      const int tok = s.pr_tok[s0 + t];
+    for (int t = 0; t < it.mtot; ++t) {
+      const int tok = s.pr_tok[it.s0 + t];
       if (threadIdx.x == 0) {
-        int* cnt = &p.ycnt[tok * p.ncd + chunk];
+        int* cnt = &p.ycnt[tok * p.ncd + it.chunk];
         const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s.misc[1] = (old == s.nvalid[tok] - 1);
         if (old == s.nvalid[tok] - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -798,10 +826,9 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
       __syncthreads();
     }
   }
-  // The last D item of the expert resets the expert's counters for the next call.
-  if (arrive_last(&p.sync[a].cD, p.ncd, &s.misc[1])) {
+  if (arrive_last(&p.sync[it.a].cD, p.ncd, &s.misc[1])) {
     if (threadIdx.x == 0) {
-      ExpertSync* es = &p.sync[a];
+      ExpertSync* es = &p.sync[it.a];
       __hip_atomic_store(&es->cA, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&es->rA, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&es->cB, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -811,7 +838,7 @@ __device__ void item_d(const Params& p, const Smem& s, int a, int chunk) {
   }
 }
 
-__device__ void item_zero(const Params& p, const Smem& s, int row, int chunk) {
+__device__ __forceinline__ void item_zero(const Params& p, int row, int chunk) {
   const int c0 = chunk * p.cd, ncol = min(p.cd, p.d - c0);
   float* dst = p.out + static_cast<int64_t>(row) * p.d + c0;
   for (int col = threadIdx.x; col < ncol; col += kNT) dst[col] = 0.f;
@@ -835,27 +862,59 @@ __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 wave
   const int nA = nq * 2 * p.nca, nB = nq * p.ncb, nD = nq * p.ncd;
   const int nZ = zero_rows(p, s, q, 0, true) * p.ncd;
   const int total = nA + nB + nD + nZ;
-  // The next ticket is taken while the current item runs (misc[2]).
-  if (tid == 0) s.misc[2] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The next ticket is fetched while the current item runs; thread 0 holds it
+  // in a register until the item is done, so no wave waits on the atomic.
+  int next_ticket = 0;
+  if (tid == 0) next_ticket = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (;;) {
+    if (tid == 0) s.misc[2] = next_ticket;
     __syncthreads();
     int t = s.misc[2];
     __syncthreads();
     if (t >= total) break;
-    if (tid == 0) s.misc[2] = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) next_ticket = __hip_atomic_fetch_add(&p.ctrl->ticket[q], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Item it;
+    it.kind = 0;
     if (t < nA) {
-      const int per = 2 * p.nca;
-      const int a = q + 8 * (t / per), r = t % per;
-      item_a<kInt8>(p, s, a, r / p.nca, r % p.nca);
+      const int per = 2 * p.nca, r = t % per;
+      it.type = kItemA;
+      it.a = q + 8 * (t / per);
+      it.kind = r / p.nca;
+      it.chunk = r % p.nca;
     } else if ((t -= nA) < nB) {
-      item_bc<kInt8>(p, s, q + 8 * (t / p.ncb), t % p.ncb);
+      it.type = kItemBC;
+      it.a = q + 8 * (t / p.ncb);
+      it.chunk = t % p.ncb;
     } else if ((t -= nB) < nD) {
-      item_d<kInt8>(p, s, q + 8 * (t / p.ncd), t % p.ncd);
+      it.type = kItemD;
+      it.a = q + 8 * (t / p.ncd);
+      it.chunk = t % p.ncd;
     } else {
       t -= nD;
-      item_zero(p, s, zero_rows(p, s, q, t / p.ncd, false), t % p.ncd);
+      item_zero(p, zero_rows(p, s, q, t / p.ncd, false), t % p.ncd);
+      continue;
     }
-    __syncthreads();
+    it.e = s.act_e[it.a];
+    it.s0 = s.act_s[it.a];
+    it.mtot = s.act_c[it.a];
+    if (it.type == kItemBC) wait_flag(p, &p.sync[it.a].rA);
+    if (it.type == kItemD) wait_flag(p, &p.sync[it.a].rB);
+    const int nsub = it.type == kItemBC ? 3 : 1;
+    for (int tb = 0; tb < it.mtot; tb += kMB) {
+      const int m = min(kMB, it.mtot - tb);
+      stage_batch(p, s, it, tb, m);
+      __syncthreads();
+      for (int sub = 0; sub < nsub; ++sub) {
+        Job j;
+        if (make_job(p, s, it, sub, tb, m, j)) run_tile<kInt8>(j, m, s);
+      }
+    }
+    if (it.type == kItemA)
+      finish_a(p, s, it);
+    else if (it.type == kItemBC)
+      finish_bc(p, s, it);
+    else
+      finish_d(p, s, it);
   }
   // The last workgroup out resets the queues.
   __syncthreads();
@@ -867,7 +926,6 @@ __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 wave
     }
   }
 }
-
 }  // namespace
 }  // namespace fused
 }  // namespace latent
@@ -878,6 +936,9 @@ __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 wave
 namespace latent {
 namespace fused {
 
+// Below kMinPairs routed pairs (one or two tokens at top-8) the multi-kernel
+// path is faster: its per-workgroup items are larger than this kernel's.
+constexpr int kMinPairs = 32;
 constexpr int kMaxPairs = 512;
 constexpr int kMaxE = 512;
 constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU
@@ -895,7 +956,7 @@ static size_t lds_bytes(const latent_moe_args& a, int vmax, int cb, int red) {
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
   const bool x_aligned = (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0;  // 16-byte vector staging of x
-  return P >= 1 && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512 && x_aligned;
+  return P >= kMinPairs && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512 && x_aligned;
 }
 
 static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi) {
@@ -911,11 +972,14 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   const double per_xcd = std::max(1.0, std::ceil(est / 8.0));
   pl.red_floats = kMB * (kW / 2) * 256;  // cross-wave partial slots: (wr / 2) * M * ncols
   const double wgs_per_xcd = 32.0 * kWgPerCu;
-  pl.cb = pick_cols(ff, per_xcd, 1.5 * wgs_per_xcd, 128, 512);
+  pl.cb = pick_cols(ff, per_xcd, 1.5 * wgs_per_xcd, 64, 512);
   pl.ncb = static_cast<int>((ff + pl.cb - 1) / pl.cb);
-  pl.cd = pick_cols(d, per_xcd, 1.5 * wgs_per_xcd, 128, 2048);
+  // At most 1024 columns (32 groups): the tile then folds its row slices
+  // through LDS and stores whole rows (coalesced), never 16-column lane runs.
+  pl.cd = pick_cols(d, per_xcd, 1.5 * wgs_per_xcd, 128, 1024);
   pl.ncd = static_cast<int>((d + pl.cd - 1) / pl.cd);
-  int nca = std::max<int>(1, static_cast<int>(std::ceil(wgs_per_xcd / per_xcd)));
+  // One round of A items per queue where the activations fit: 2 * nca items per expert.
+  int nca = std::max<int>(1, static_cast<int>(std::floor(wgs_per_xcd / (2.0 * per_xcd))));
   nca = std::max<int>(nca, static_cast<int>((d + 1023) / 1024));
   for (;; ++nca) {
     pl.nca = static_cast<int>(std::min<int64_t>(nca, d / kGroup));

@@ -191,12 +191,17 @@ def test_dsv3_decode_parity(gpu, dsv3, B):
     x_t = gsynth.bf16_input(seed=2000 + B, n_tokens=B, d=7168)
     out = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
     torch.cuda.synchronize()
-    # A second call must reproduce the first bit for bit (the decode kernel is
-    # deterministic and leaves its control block as it found it).
+    # A second call must reproduce the first: bit for bit on the persistent
+    # decode kernel (fixed summation order, control block left as found); the
+    # multi-kernel path accumulates with float atomics, so only to rounding.
     again = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
     torch.cuda.synchronize()
-    assert torch.equal(out, again)
-    from latent_amd.moe import workspace_error
+    from latent_amd.moe import moe_path, workspace_error
+
+    if moe_path(dsv3, x_t, 8) == "fused":
+        assert torch.equal(out, again)
+    else:
+        assert torch.allclose(out, again, rtol=1e-5, atol=1e-6 * out.abs().max().item())
 
     assert workspace_error(dsv3.workspace(B, 8)) == 0
     ids, w, x = ids_t.cpu().numpy(), w_t.cpu().numpy(), x_t.float().cpu().numpy()
