@@ -15,8 +15,7 @@ namespace fused {
 constexpr size_t kReserved = 256 * 1024;
 
 struct Plan {
-  int ra, nca, cb, ncb, cd, ncd, vmax, red_floats;
-  size_t lds;
+  int ra, nca, cb, ncb, cd, ncd;
   size_t off_sync, off_ycnt;  // inside the reserved region
   size_t off_partA, off_glat, off_partB, off_dlat, off_ybuf, scratch_bytes;  // after it
 };

@@ -44,6 +44,7 @@ constexpr int kMB = 4;           // tokens per pass
 constexpr int kLutCopies = 8;
 constexpr int kLutEntries = 256 * kLutCopies;
 constexpr int64_t kSpinTicks = 100000000;  // 1 s of s_memrealtime (100 MHz)
+constexpr int kFactorArgsBytes = 6 * 64;   // LDS table of the six factor descriptors
 
 struct Ctrl {
   int ticket[8];
@@ -77,8 +78,6 @@ struct Params {
   int ra, nca;  // phase A: rows per item, items per expert and factor
   int cb, ncb;  // phase BC: ff columns per item, items per expert
   int cd, ncd;  // phase D: d columns per item, items per expert
-  int vmax;     // floats per token in the activation staging buffer
-  int red_floats;
 };
 
 __device__ __forceinline__ int next_pow2(int v) { return v <= 1 ? 1 : 1 << (32 - __builtin_clz(v - 1)); }
@@ -93,8 +92,45 @@ __device__ __forceinline__ int rank_of(const Params& p, int e, int kind) {
 // ---------------------------------------------------------------------------
 // LDS layout
 // ---------------------------------------------------------------------------
+struct FactorArgs;
+
+// Fixed LDS layout (compile-time offsets: every LDS access uses an immediate
+// address, so no scalar registers hold array bases).  The routing scratch
+// (ids, w, cnt, start) is only live inside route() and shares its space with
+// the activation / slice / cross-wave buffers used afterwards.
+constexpr int kMaxP = 512;                    // routed pairs (T * k)
+constexpr int kMaxEx = 512;                   // experts
+constexpr int kVMax = 1024;                   // staged activation floats per token
+constexpr int kCbMax = 512;                   // ff columns of a BC slice
+constexpr int kRedFloats = kMB * (kW / 2) * 256;  // cross-wave partial slots: (wr / 2) * M * ncols
+
+struct SmemLayout {
+  alignas(16) char fac[kFactorArgsBytes];
+  float2 lut[kLutEntries];
+  int act_e[kMaxP], act_s[kMaxP], act_c[kMaxP];
+  int pr_tok[kMaxP], pr_slot[kMaxP];
+  float pr_w[kMaxP];
+  int pos_of[kMaxP];
+  int nvalid[kMaxP];
+  int misc[16];
+  union {
+    struct {
+      int ids[kMaxP];
+      float w[kMaxP];
+      int cnt[kMaxEx];
+      int start[kMaxEx];
+    } route;
+    struct {
+      float vin[kMB * kVMax];
+      float hs[kMB * kCbMax];
+      float red[kRedFloats];
+    } work;
+  } u;
+};
+
 struct Smem {
-  float2* lut;     // [256][32]
+  FactorArgs* fac; // [6] factor descriptors (kept in LDS, not in scalar registers)
+  float2* lut;     // [256][kLutCopies]
   int* ids;        // [P]
   float* w;        // [P]
   int* cnt;        // [E]
@@ -107,37 +143,32 @@ struct Smem {
   float* pr_w;     // [P]
   int* pos_of;     // [P] position of pair t*K+slot, -1 if dropped
   int* nvalid;     // [T]
-  int* misc;       // [16]: 0 n_active, 1 broadcast, 8..15 queue item counts
-  float* vin;      // [kMB][vmax]
+  int* misc;       // [16]: 0 n_active, 1 broadcast, 2 ticket
+  float* vin;      // [kMB][kVMax]
   float* hs;       // [kMB][cb]  (g of the BC slice, then h)
   float* red;      // cross-wave partials
 };
 
-__device__ Smem carve(const Params& p, char* base) {
+__device__ __forceinline__ Smem carve(SmemLayout& m) {
   Smem s;
-  auto take = [&](size_t bytes) {
-    char* r = base;
-    base += (bytes + 15) / 16 * 16;
-    return r;
-  };
-  const int A = min(p.E, p.P);
-  s.lut = reinterpret_cast<float2*>(take(kLutEntries * sizeof(float2)));
-  s.ids = reinterpret_cast<int*>(take(p.P * 4));
-  s.w = reinterpret_cast<float*>(take(p.P * 4));
-  s.cnt = reinterpret_cast<int*>(take(p.E * 4));
-  s.start = reinterpret_cast<int*>(take(p.E * 4));
-  s.act_e = reinterpret_cast<int*>(take(A * 4));
-  s.act_s = reinterpret_cast<int*>(take(A * 4));
-  s.act_c = reinterpret_cast<int*>(take(A * 4));
-  s.pr_tok = reinterpret_cast<int*>(take(p.P * 4));
-  s.pr_slot = reinterpret_cast<int*>(take(p.P * 4));
-  s.pr_w = reinterpret_cast<float*>(take(p.P * 4));
-  s.pos_of = reinterpret_cast<int*>(take(p.P * 4));
-  s.nvalid = reinterpret_cast<int*>(take(p.T * 4));
-  s.misc = reinterpret_cast<int*>(take(16 * 4));
-  s.vin = reinterpret_cast<float*>(take(kMB * p.vmax * 4));
-  s.hs = reinterpret_cast<float*>(take(kMB * p.cb * 4));
-  s.red = reinterpret_cast<float*>(take(p.red_floats * 4));
+  s.fac = reinterpret_cast<FactorArgs*>(m.fac);
+  s.lut = m.lut;
+  s.ids = m.u.route.ids;
+  s.w = m.u.route.w;
+  s.cnt = m.u.route.cnt;
+  s.start = m.u.route.start;
+  s.act_e = m.act_e;
+  s.act_s = m.act_s;
+  s.act_c = m.act_c;
+  s.pr_tok = m.pr_tok;
+  s.pr_slot = m.pr_slot;
+  s.pr_w = m.pr_w;
+  s.pos_of = m.pos_of;
+  s.nvalid = m.nvalid;
+  s.misc = m.misc;
+  s.vin = m.u.work.vin;
+  s.hs = m.u.work.hs;
+  s.red = m.u.work.red;
   return s;
 }
 
@@ -318,13 +349,22 @@ struct FactorArgs {
   int64_t rows, cols;
 };
 
-// One factor of the six, selected without indexing the kernel arguments at run
-// time (a runtime index would force them into private memory).
-__device__ __forceinline__ FactorArgs fargs(const Params& p, int i) {
-  const Factor& f = i == 0 ? p.fac[0] : i == 1 ? p.fac[1] : i == 2 ? p.fac[2] : i == 3 ? p.fac[3] : i == 4 ? p.fac[4] : p.fac[5];
-  return FactorArgs{as_global(f.codes), as_global(f.scales), as_global(f.ext.bitmap), as_global(f.ext.row_offset),
-                    as_global(f.ext.data), f.rows, f.cols};
+static_assert(sizeof(FactorArgs) <= kFactorArgsBytes / 6, "factor table slot");
+
+// The six factor descriptors are copied to LDS once per workgroup: held in
+// scalar registers for the whole kernel they would crowd out everything else.
+__device__ __forceinline__ void stage_factors(const Params& p, const Smem& s) {
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const Factor& f = p.fac[i];
+      s.fac[i] = FactorArgs{as_global(f.codes), as_global(f.scales), as_global(f.ext.bitmap),
+                            as_global(f.ext.row_offset), as_global(f.ext.data), f.rows, f.cols};
+    }
+  }
 }
+
+__device__ __forceinline__ FactorArgs fargs(const Smem& s, int i) { return s.fac[i]; }
 
 // One tile GEMV of a workgroup:
 //   y[t][j] = sum_{r0 <= r < r1} vin[t][r - vbase] * scale(r, g0 + j/32) * level(code(r, 32*g0 + j))
@@ -467,8 +507,10 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   const gptr<uint16_t> sbase = f.scales + (j.e * f.rows + row0) * sstride + gg;
   const int64_t cstep = static_cast<int64_t>(rstep) * cstride, sstep = static_cast<int64_t>(rstep) * sstride;
   // Ring of kRing rows in flight per lane; slot u is refilled with the row
-  // kRing steps ahead right after it is consumed.
-  constexpr int kRing = 8;
+  // kRing steps ahead right after it is consumed.  Four-token tiles spend
+  // their registers on accumulators and do 4x the arithmetic per row, so a
+  // shallower ring keeps them inside 128 VGPRs without starving the loads.
+  constexpr int kRing = M >= 4 ? 4 : 8;
   u32x2 ring[kRing];
   float sring[kRing];
 #pragma unroll
@@ -661,12 +703,12 @@ __device__ __forceinline__ int groups_of(int rank) { return (rank + kGroup - 1) 
 __device__ __forceinline__ void stage_batch(const Params& p, const Smem& s, const Item& it, int tb, int m) {
   if (it.type == kItemA) {
     const int r0 = it.chunk * p.ra, nrows = min(p.d, r0 + p.ra) - r0;
-    stage_x(p, s.pr_tok + it.s0 + tb, m, r0, nrows, s.vin, p.vmax);
+    stage_x(p, s.pr_tok + it.s0 + tb, m, r0, nrows, s.vin, kVMax);
   } else if (it.type == kItemBC) {
-    stage_coh(p.glat + static_cast<int64_t>(it.s0 + tb) * 2 * p.R, 2 * p.R, m, 2 * p.R, s.vin, p.vmax);
+    stage_coh(p.glat + static_cast<int64_t>(it.s0 + tb) * 2 * p.R, 2 * p.R, m, 2 * p.R, s.vin, kVMax);
   } else {
     const int n = groups_of(rank_of(p, it.e, 2)) * kGroup;
-    stage_coh(p.dlat + static_cast<int64_t>(it.s0 + tb) * p.R, p.R, m, n, s.vin, p.vmax);
+    stage_coh(p.dlat + static_cast<int64_t>(it.s0 + tb) * p.R, p.R, m, n, s.vin, kVMax);
   }
 }
 
@@ -677,14 +719,14 @@ __device__ __forceinline__ bool make_job(const Params& p, const Smem& s, const I
   j.swiglu = 0;
   j.coherent = 0;
   j.vin = as_lds(static_cast<const float*>(s.vin));
-  j.vstride = p.vmax;
+  j.vstride = kVMax;
   j.vbase = 0;
   j.g0 = 0;
 #pragma unroll
   for (int t = 0; t < kMB; ++t) j.scale[t] = 1.0f;
   if (it.type == kItemA) {
     const int ng = groups_of(rank_of(p, it.e, it.kind));
-    j.f = fargs(p, it.kind == 0 ? 0 : 2);
+    j.f = fargs(s, it.kind == 0 ? 0 : 2);
     j.r0 = it.chunk * p.ra;
     j.r1 = min(p.d, j.r0 + p.ra);
     j.G = next_pow2(ng);
@@ -701,7 +743,7 @@ __device__ __forceinline__ bool make_job(const Params& p, const Smem& s, const I
     if (ncol <= 0) return false;
     if (sub < 2) {
       // g = g_lat . B_g (sub 0) into hs, then hs = SiLU(hs) * (u_lat . B_u) (sub 1).
-      j.f = fargs(p, sub == 0 ? 1 : 3);
+      j.f = fargs(s, sub == 0 ? 1 : 3);
       j.r0 = 0;
       j.r1 = rank_of(p, it.e, sub);  // an empty row range yields zeros
       j.g0 = c0 / kGroup;
@@ -722,7 +764,7 @@ __device__ __forceinline__ bool make_job(const Params& p, const Smem& s, const I
     }
     // hs . A_d rows [c0, c0 + ncol) -> partial d_lat.
     const int ngd = groups_of(rank_of(p, it.e, 2));
-    j.f = fargs(p, 4);
+    j.f = fargs(s, 4);
     j.r0 = c0;
     j.r1 = c0 + ncol;
     j.G = next_pow2(ngd);
@@ -738,7 +780,7 @@ __device__ __forceinline__ bool make_job(const Params& p, const Smem& s, const I
   }
   // D: d_lat . B_d, columns [c0, c0 + ncol).
   const int c0 = it.chunk * p.cd, ncol = min(p.cd, p.d - c0);
-  j.f = fargs(p, 5);
+  j.f = fargs(s, 5);
   j.r0 = 0;
   j.r1 = rank_of(p, it.e, 2);
   j.g0 = c0 / kGroup;
@@ -846,8 +888,8 @@ __device__ __forceinline__ void item_zero(const Params& p, int row, int chunk) {
 
 template <bool kInt8>
 __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 waves per SIMD: two workgroups per CU
-  extern __shared__ __align__(16) char smem_raw[];
-  const Smem s = carve(p, smem_raw);
+  __shared__ SmemLayout smem;
+  const Smem s = carve(smem);
   const int tid = threadIdx.x;
   // Codebook table: entry b holds (level[b & 15], level[b >> 4]), one copy per
   // lane of a 16-lane LDS cycle.
@@ -855,6 +897,7 @@ __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 wave
     const int b = i / kLutCopies;
     s.lut[i] = make_float2(nf4_level(b & 15), nf4_level(b >> 4));
   }
+  stage_factors(p, s);
   route(p, s);
   const int n_active = s.misc[0];
   const int q = blockIdx.x & 7;
@@ -939,24 +982,17 @@ namespace fused {
 // Below kMinPairs routed pairs (one or two tokens at top-8) the multi-kernel
 // path is faster: its per-workgroup items are larger than this kernel's.
 constexpr int kMinPairs = 32;
-constexpr int kMaxPairs = 512;
-constexpr int kMaxE = 512;
-constexpr size_t kLdsLimit = 80 * 1024;  // two workgroups per CU
-constexpr int kWgPerCu = 2;
+constexpr int kMaxPairs = kMaxP;
+constexpr int kMaxE = kMaxEx;
+constexpr int kWgPerCu = 2;  // two 512-thread workgroups per CU (<= 80 KB of LDS each)
+static_assert(sizeof(SmemLayout) <= 80 * 1024, "two workgroups per CU");
 
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
-
-static size_t lds_bytes(const latent_moe_args& a, int vmax, int cb, int red) {
-  const size_t P = a.n_tokens * a.n_expert_used, E = a.n_expert, A = std::min<size_t>(E, P), T = a.n_tokens;
-  auto r16 = [](size_t b) { return (b + 15) / 16 * 16; };
-  return r16(kLutEntries * 8) + 6 * r16(P * 4) + 2 * r16(E * 4) + 3 * r16(A * 4) + r16(T * 4) + r16(64) +
-         r16(kMB * vmax * 4) + r16(kMB * cb * 4) + r16(red * 4);
-}
 
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
   const bool x_aligned = (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0;  // 16-byte vector staging of x
-  return P >= kMinPairs && P <= kMaxPairs && a.n_expert <= kMaxE && a.max_rank <= 512 && x_aligned;
+  return P >= kMinPairs && P <= kMaxPairs && a.n_expert <= kMaxE && 2 * a.max_rank <= kVMax && x_aligned;
 }
 
 static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi) {
@@ -970,9 +1006,8 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   const int64_t P = T * K, A = std::min(E, P);
   const double est = static_cast<double>(E) * (1.0 - std::pow(1.0 - static_cast<double>(K) / E, static_cast<double>(T)));
   const double per_xcd = std::max(1.0, std::ceil(est / 8.0));
-  pl.red_floats = kMB * (kW / 2) * 256;  // cross-wave partial slots: (wr / 2) * M * ncols
   const double wgs_per_xcd = 32.0 * kWgPerCu;
-  pl.cb = pick_cols(ff, per_xcd, 1.5 * wgs_per_xcd, 64, 512);
+  pl.cb = pick_cols(ff, per_xcd, 1.5 * wgs_per_xcd, 64, kCbMax);
   pl.ncb = static_cast<int>((ff + pl.cb - 1) / pl.cb);
   // At most 1024 columns (32 groups): the tile then folds its row slices
   // through LDS and stores whole rows (coalesced), never 16-column lane runs.
@@ -981,15 +1016,11 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   // One round of A items per queue where the activations fit: 2 * nca items per expert.
   int nca = std::max<int>(1, static_cast<int>(std::floor(wgs_per_xcd / (2.0 * per_xcd))));
   nca = std::max<int>(nca, static_cast<int>((d + 1023) / 1024));
-  for (;; ++nca) {
-    pl.nca = static_cast<int>(std::min<int64_t>(nca, d / kGroup));
-    pl.ra = static_cast<int>(((d + pl.nca - 1) / pl.nca + kGroup - 1) / kGroup * kGroup);  // whole groups of rows
-    pl.nca = static_cast<int>((d + pl.ra - 1) / pl.ra);
-    pl.vmax = static_cast<int>(std::max<int64_t>(pl.ra, 2 * R));
-    pl.lds = lds_bytes(a, pl.vmax, pl.cb, pl.red_floats);
-    if (pl.lds <= kLdsLimit) break;
-    if (pl.ra <= 2 * R) return false;  // activations of 2R per token do not fit either
-  }
+  // Rows per A item: whole groups of rows, at most kVMax (the staged x slice).
+  nca = std::min<int>(nca, static_cast<int>(std::max<int64_t>(1, d / kGroup)));
+  pl.ra = static_cast<int>(((d + nca - 1) / nca + kGroup - 1) / kGroup * kGroup);
+  pl.nca = static_cast<int>((d + pl.ra - 1) / pl.ra);
+  if (pl.ra > kVMax || 2 * R > kVMax || pl.cb > kCbMax) return false;
   size_t off = 256;
   pl.off_sync = off;
   off = align256(off + A * sizeof(ExpertSync));
@@ -1019,17 +1050,10 @@ static int grid_size() {
 }
 
 template <bool kInt8>
-static int launch(const Params& p, const Plan& pl, hipStream_t s) {
-  static size_t attr_bytes = 0;  // largest dynamic LDS size granted so far
-  if (pl.lds > attr_bytes) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&fused_kernel<kInt8>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(pl.lds)) != hipSuccess)
-      return LATENT_E_HIP;
-    attr_bytes = pl.lds;
-  }
+static int launch(const Params& p, hipStream_t s) {
   const int grid = grid_size();
   if (grid <= 0) return LATENT_E_HIP;
-  hipLaunchKernelGGL(fused_kernel<kInt8>, dim3(grid), dim3(kNT), pl.lds, s, p);
+  hipLaunchKernelGGL(fused_kernel<kInt8>, dim3(grid), dim3(kNT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
@@ -1072,9 +1096,7 @@ int forward(const latent_moe_args& a, hipStream_t s, char* ws, const Plan& pl) {
   p.ncb = pl.ncb;
   p.cd = pl.cd;
   p.ncd = pl.ncd;
-  p.vmax = pl.vmax;
-  p.red_floats = pl.red_floats;
-  return any_int8 ? launch<true>(p, pl, s) : launch<false>(p, pl, s);
+  return any_int8 ? launch<true>(p, s) : launch<false>(p, s);
 }
 
 }  // namespace fused
