@@ -511,13 +511,16 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   // their registers on accumulators and do 4x the arithmetic per row, so a
   // shallower ring keeps them inside 128 VGPRs without starving the loads.
   constexpr int kRing = M >= 4 ? 4 : 8;
+  // Scales stay raw fp16 bits in the ring: converting at load time would make
+  // the refill wait for its own load.
   u32x2 ring[kRing];
-  float sring[kRing];
+  uint32_t sring[kRing];  // one register per scale (16-bit packing would force a wait per refill)
 #pragma unroll
   for (int u = 0; u < kRing; ++u) {
     const int k = u < nsteps ? u : 0;
     ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + k * cstep);
-    sring[u] = half_bits_to_float(sbase[k * sstep]);
+    sring[u] = sbase[k * sstep];
+    __builtin_amdgcn_sched_barrier(0);  // issue in consumption order
   }
   for (int k0 = 0; k0 < nsteps; k0 += kRing) {
 #pragma unroll
@@ -526,7 +529,7 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
       const int row = row_w + ro + k * rstep;
       const bool ok = hvalid && k < nsteps && row < r1;
       const int vr = (ok ? row : r0) - j.vbase;
-      const float sm = ok ? sring[u] : 0.f;
+      const float sm = ok ? half_bits_to_float(sring[u]) : 0.f;
       float xs[M];
 #pragma unroll
       for (int t = 0; t < M; ++t) xs[t] = j.vin[t * j.vstride + vr] * sm;
@@ -538,9 +541,16 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
         }
       }
       if (!done) fma_half_nf4<M>(ring[u], xs, lut, lanebase, acc);
+      // Pin the refill between this step and the next.  Hoisted above the
+      // step, its load would need a fresh register and a copy at the loop
+      // latch, and that copy waits for every load in flight; sunk below, it
+      // loses the distance to its use.  Either way the ring stops hiding the
+      // memory latency.
+      __builtin_amdgcn_sched_barrier(0);
       const int kn = k + kRing < nsteps ? k + kRing : 0;
       ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + kn * cstep);
-      sring[u] = half_bits_to_float(sbase[kn * sstep]);
+      sring[u] = sbase[kn * sstep];
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // In-wave reduction over the rpw row lanes.
