@@ -139,8 +139,9 @@ int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 /*
  * Which implementation latent_moe_ffn_forward uses for these arguments:
  * 1 = single persistent decode kernel (32 to 512 routed pairs, up to 512
- * experts, rank 512), 0 = multi-kernel general path; < 0 = LATENT_E_* for bad
- * arguments.
+ * experts, rank 512), 2 = grouped fp16-MFMA prefill (at least 16 routed pairs
+ * per active expert, no INT8 groups), 0 = multi-kernel GEMV path; < 0 =
+ * LATENT_E_* for bad arguments.
  * Diagnostic only; no counterpart in the reference.
  */
 int latent_moe_path(const latent_moe_args* args);

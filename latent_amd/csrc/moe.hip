@@ -21,6 +21,7 @@
 // through LDS, workgroups with fp32 atomics.  All arithmetic is fp32.
 #include "common.hpp"
 #include "fused.hpp"
+#include "prefill.hpp"
 
 #include <algorithm>
 
@@ -576,7 +577,9 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   if (!args || !bytes) return LATENT_E_INVALID;
   const int st = validate(*args);
   if (st != LATENT_OK) return st;
-  size_t scratch = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank).total;
+  const Layout L = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank);
+  size_t scratch = L.total;
+  if (prefill::supported(*args)) scratch = std::max(scratch, L.gu + prefill::layout_for(*args).total);
   fused::Plan pl;
   if (fused::supported(*args) && fused::make_plan(*args, pl)) scratch = std::max(scratch, pl.scratch_bytes);
   *bytes = fused::kReserved + scratch;
@@ -588,7 +591,8 @@ extern "C" int latent_moe_path(const latent_moe_args* args) {
   const int st = validate(*args);
   if (st != LATENT_OK) return st;
   fused::Plan pl;
-  return (fused::supported(*args) && fused::make_plan(*args, pl)) ? 1 : 0;
+  if (fused::supported(*args) && fused::make_plan(*args, pl)) return 1;
+  return prefill::supported(*args) ? 2 : 0;
 }
 
 extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
@@ -644,7 +648,8 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.out_mode = a.out_mode;
   const int64_t P = a.n_tokens * a.n_expert_used;
   p.a_max = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P)));
-  p.zero_floats = P * 3 * a.max_rank;
+  const bool use_prefill = prefill::supported(a);
+  p.zero_floats = use_prefill ? 0 : P * 3 * a.max_rank;  // the MFMA path writes its intermediates whole
 
   // Work split: enough items to fill 256 CUs even when few experts are routed.
   const int MB = a.n_tokens == 1 ? 1 : 4;
@@ -661,6 +666,10 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));
   hipLaunchKernelGGL(prep_kernel, dim3(1 + zero_blocks), dim3(kRouteThreads), 0, s, p);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  if (use_prefill) {
+    const prefill::Grouping g{p.meta, p.act_expert, p.act_start, p.act_count, p.pair_tok, p.pair_slot, p.pair_w};
+    return prefill::forward(a, p.fac, g, ws + L.gu, s);
+  }
   if (MB == 1)
     st = any_int8 ? launch_phases<1, true>(p, s) : launch_phases<1, false>(p, s);
   else

@@ -1,0 +1,565 @@
+// Grouped-MFMA prefill path: the LATENT factor chain as four grouped GEMMs over
+// the expert-sorted (token, slot) pairs.
+//
+// Replaces, for prefill-sized batches, the per-token launch loop of
+// kernels/latent_fused_expert_ffn.cu:255-289; restates project /
+// swiglu_expert (loader/latent_runtime.py:35-59) per expert:
+//
+//   A    gu[p]  = x[tok(p)] . [A_g | A_u]                 K = d,  N = 2R
+//   BC1  h[p]   = SiLU(gu[p][:R] . B_g) * (gu[p][R:] . B_u)  K = R,  N = ff
+//   BC2  dl[p]  = h[p] . A_d                               K = ff, N = R
+//   D    out[tok(p)] += w(p) * dl[p] . B_d                 K = R,  N = d
+//
+// Each GEMM tile is 128 pairs x 128 columns on 4 waves (2 x 2 of 64 x 64,
+// v_mfma_f32_32x32x16_f16, fp32 accumulation).  Per 32-row K slice the NF4
+// factor slice is dequantized (level * scale in fp32, rounded to fp16) into
+// LDS transposed to [column][k], the activation slice is gathered and
+// converted to fp16 into LDS as [pair][k]; both are double-buffered and the
+// next slice's global loads are in flight while the current one multiplies.
+// Intermediates (gu, h, dl) are stored in fp16 per pair; the output combine
+// adds w * y into out with fp32 atomics (reduced mode) or stores per slot.
+//
+// fp16 range: the latents of a LATENT chain are small (about 1e-3 .. 1e-9 at
+// the DeepSeek-V3 shape), far below fp16's normal range.  Every fp16 operand
+// row therefore carries a power-of-two exponent: a producer tile stores
+// v * 2^e with e chosen per (row, 128-column block) so that the block's
+// largest |v| lands in [2^14, 2^15), and records e; a consumer rescales each
+// block of its row to the row's smallest exponent c (exact ldexp on fp16) and
+// multiplies its fp32 accumulators by 2^-c.  x rows get their exponent from a
+// max pass over x.  Scaling by powers of two adds no rounding.
+#include "prefill.hpp"
+
+#include <algorithm>
+
+namespace latent {
+namespace prefill {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;  // 4 waves
+constexpr int kMT = 128;       // pairs per tile
+constexpr int kNT = 128;       // output columns per tile
+constexpr int kKS = 32;        // K rows staged per slice
+constexpr int kLds = 40;       // halfs per LDS row: 32 + 8 pad keeps 16-byte fragment reads conflict-free
+constexpr int kTileThreads = 1024;
+constexpr int kExpMin = -120, kExpMax = 120;
+
+enum ASrc { kFromX = 0, kFromPairs = 1 };
+enum Epi { kStoreHalf = 0, kSwiGLU = 1, kToOutput = 2 };
+
+struct Params {
+  Grouping g;
+  const int* tile_a;
+  const int* tile_r0;
+  const void* x;  // kFromX: x [T][d] of x_dtype, row tok(p)
+  int x_dtype, d;
+  const _Float16* a;  // kFromPairs: a[p * lda + col], scaled by 2^a_exp[p][col / 128]
+  int64_t lda;
+  int a_col0, a_col1;  // A columns of the first / second product
+  const int* a_exp;    // kFromPairs: [P][a_exp_ld] block exponents; kFromX: [T] row exponents of x
+  int a_exp_ld;
+  int a_part, a_part_blocks;  // the A rows were written as parts of a_part columns, ceil(a_part / 128) blocks each
+  int K;
+  Factor f0, f1;  // second factor: the u side of SwiGLU, or the blockIdx.z == 1 factor
+  int ncols;      // output columns of one factor
+  _Float16* dst;  // kStoreHalf / kSwiGLU: dst[p * ldd + col]
+  int64_t ldd;
+  int dst_col1;   // column offset of the blockIdx.z == 1 product
+  int* dst_exp;   // [P][dst_exp_ld] exponents of the stored blocks
+  int dst_exp_ld;
+  float* out;     // kToOutput
+  int out_mode, wbd, n_expert_used;
+};
+
+struct Smem {
+  _Float16 a[2][kMT * kLds];
+  _Float16 b[2][kNT * kLds];
+  float lut[16];
+  int cexp[2][kMT];   // per-row exponent of the tile's operand rows (both products)
+  float rmax[2][kMT]; // row maxima of the two column halves of the output tile
+  int tok[kMT];
+  int slot[kMT];
+  float w[kMT];
+};
+
+// One thread's share of a K slice, held in registers between the global loads
+// and the LDS commit.
+struct Stage {
+  uint4 a[4];         // 16 activations: 16-bit types use a[0..1], f32 uses a[0..3]
+  int shift;          // exponent change applied to them (kFromPairs: row exponent - block exponent)
+  uint32_t c0, c1;    // NF4 codes: 8 columns of rows k and k + 1
+  uint32_t s0, s1;    // their fp16 scales
+};
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
+
+// Exponent block of column `col` of an intermediate row.
+__device__ __forceinline__ int a_block(const Params& p, int col) {
+  return (col / p.a_part) * p.a_part_blocks + (col % p.a_part) / kNT;
+}
+
+// Activation loads: row tid / 2, columns k0 + 16 * (tid % 2) .. + 15.
+template <int kA>
+__device__ __forceinline__ void load_a(const Params& p, const Smem& s, int p0, int rows, int k0, int acol, int q,
+                                       Stage& st) {
+  const int tid = threadIdx.x, r = tid >> 1, kh = (tid & 1) * 16;
+  st.a[0] = st.a[1] = st.a[2] = st.a[3] = zero4();
+  st.shift = 0;
+  if (r >= rows) return;
+  if constexpr (kA == kFromX) {
+    st.shift = s.cexp[q][r];
+    const int64_t off = static_cast<int64_t>(s.tok[r]) * p.d + k0 + kh;
+    if (p.x_dtype == LATENT_F32) {
+      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(p.x) + off);
+      st.a[0] = q[0]; st.a[1] = q[1]; st.a[2] = q[2]; st.a[3] = q[3];
+    } else {
+      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + off);
+      st.a[0] = q[0]; st.a[1] = q[1];
+    }
+  } else {
+    const uint4* v = reinterpret_cast<const uint4*>(p.a + static_cast<int64_t>(p0 + r) * p.lda + acol + k0 + kh);
+    st.a[0] = v[0]; st.a[1] = v[1];
+    st.shift = s.cexp[q][r] - p.a_exp[static_cast<int64_t>(p0 + r) * p.a_exp_ld + a_block(p, acol + k0)];
+  }
+}
+
+// Factor loads: rows k0 + 2 * (tid % 16) + {0, 1}, columns n0 + 8 * (tid / 16) .. + 7.
+__device__ __forceinline__ void load_b(const Factor& f, int64_t e, int k0, int n0, int ncols, Stage& st) {
+  const int tid = threadIdx.x, rp = tid & 15, cg = tid >> 4;
+  const int col = n0 + 8 * cg;
+  st.c0 = st.c1 = 0x77777777u;  // code 7 = 0.0
+  st.s0 = st.s1 = 0;
+  if (col >= ncols) return;
+  const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
+  const int64_t row = e * f.rows + k0 + 2 * rp;
+  st.c0 = *reinterpret_cast<const uint32_t*>(f.codes + row * cstride + col / 2);
+  st.c1 = *reinterpret_cast<const uint32_t*>(f.codes + (row + 1) * cstride + col / 2);
+  st.s0 = f.scales[row * sstride + col / kGroup];
+  st.s1 = f.scales[(row + 1) * sstride + col / kGroup];
+}
+
+template <int kA>
+__device__ __forceinline__ void commit(const Params& p, Smem& s, int buf, const Stage& st) {
+  const int tid = threadIdx.x;
+  {
+    const int r = tid >> 1, kh = (tid & 1) * 16;
+    half8 h[2];
+    if (kA == kFromX && p.x_dtype == LATENT_F32) {
+      const float* f = reinterpret_cast<const float*>(st.a);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = static_cast<_Float16>(__builtin_ldexpf(f[i], st.shift));
+    } else if (kA == kFromX && p.x_dtype == LATENT_BF16) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(st.a);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        h[i / 4][2 * (i % 4)] =
+            static_cast<_Float16>(__builtin_ldexpf(__uint_as_float((w[i] & 0xFFFFu) << 16), st.shift));
+        h[i / 4][2 * (i % 4) + 1] = static_cast<_Float16>(__builtin_ldexpf(__uint_as_float(w[i] & 0xFFFF0000u), st.shift));
+      }
+    } else if (kA == kFromX) {
+      const _Float16* f = reinterpret_cast<const _Float16*>(st.a);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        h[i / 8][i % 8] = static_cast<_Float16>(__builtin_ldexpf(static_cast<float>(f[i]), st.shift));
+    } else {
+      h[0] = *reinterpret_cast<const half8*>(&st.a[0]);
+      h[1] = *reinterpret_cast<const half8*>(&st.a[1]);
+      if (st.shift != 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = __builtin_ldexpf16(h[i / 8][i % 8], st.shift);
+      }
+    }
+    half8* dst = reinterpret_cast<half8*>(&s.a[buf][r * kLds + kh]);
+    dst[0] = h[0];
+    dst[1] = h[1];
+  }
+  {
+    const int rp = tid & 15, cg = tid >> 4;
+    const float s0 = __half2float(__ushort_as_half(static_cast<uint16_t>(st.s0)));
+    const float s1 = __half2float(__ushort_as_half(static_cast<uint16_t>(st.s1)));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      half2v v;
+      v[0] = static_cast<_Float16>(s.lut[(st.c0 >> (4 * j)) & 15u] * s0);
+      v[1] = static_cast<_Float16>(s.lut[(st.c1 >> (4 * j)) & 15u] * s1);
+      *reinterpret_cast<half2v*>(&s.b[buf][(8 * cg + j) * kLds + 2 * rp]) = v;
+    }
+  }
+}
+
+// acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
+// whole K of the tile, for factor f (expert e) and activation column acol.
+template <int kA>
+__device__ __forceinline__ void run_k(const Params& p, Smem& s, const Factor& f, int64_t e, int p0, int rows,
+                                      int n0, int acol, int q, f32x16 (&acc)[2][2]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w & 1, wn = w >> 1;
+  const int nslices = p.K / kKS;
+  Stage st;
+  load_a<kA>(p, s, p0, rows, 0, acol, q, st);
+  load_b(f, e, 0, n0, p.ncols, st);
+  commit<kA>(p, s, 0, st);
+  __syncthreads();
+  for (int sl = 0; sl < nslices; ++sl) {
+    const int buf = sl & 1;
+    const bool more = sl + 1 < nslices;
+    if (more) {
+      load_a<kA>(p, s, p0, rows, (sl + 1) * kKS, acol, q, st);
+      load_b(f, e, (sl + 1) * kKS, n0, p.ncols, st);
+    }
+#pragma unroll
+    for (int ks = 0; ks < kKS; ks += 16) {
+      half8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        af[i] = *reinterpret_cast<const half8*>(&s.a[buf][(64 * wm + 32 * i + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bf[j] = *reinterpret_cast<const half8*>(&s.b[buf][(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) commit<kA>(p, s, buf ^ 1, st);
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
+// Exponent e with m * 2^e in [2^14, 2^15) (0 for m == 0 or not finite).
+__device__ __forceinline__ int block_exponent(float m) {
+  if (!(m > 0.f) || !(m < 3.0e38f)) return 0;
+  const int ilog = static_cast<int>((__float_as_uint(m) >> 23) & 0xFFu) - 127;  // floor(log2 m), normal m
+  return min(kExpMax, max(kExpMin, 14 - ilog));
+}
+
+template <int kA, int kEpi>
+__global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two workgroups per CU
+  __shared__ Smem s;
+  const int tile = blockIdx.x;
+  if (tile >= p.g.meta[2]) return;
+  const int a = p.tile_a[tile], r0 = p.tile_r0[tile];
+  const int rows = min(kMT, p.g.act_count[a] - r0);
+  const int p0 = p.g.act_start[a] + r0;
+  const int64_t e = p.g.act_expert[a];
+  const int n0 = blockIdx.y * kNT;
+  const int z = blockIdx.z;
+  const int tid = threadIdx.x;
+  if (tid < 16) s.lut[tid] = nf4_level(tid);
+  if (tid < kMT) {
+    const bool ok = tid < rows;
+    s.tok[tid] = ok ? p.g.pair_tok[p0 + tid] : 0;
+    s.slot[tid] = ok ? p.g.pair_slot[p0 + tid] : 0;
+    s.w[tid] = ok ? p.g.pair_w[p0 + tid] : 0.f;
+  }
+  __syncthreads();
+  // Operand row exponents: x rows carry one; intermediate rows are rescaled to
+  // the smallest block exponent over the K range each product reads.
+  constexpr int kProducts = kEpi == kSwiGLU ? 2 : 1;
+  for (int i = tid; i < kProducts * kMT; i += kThreads) {
+    const int q = i / kMT, r = i % kMT;
+    int c = 0;
+    if (r < rows) {
+      if constexpr (kA == kFromX) {
+        c = p.a_exp[s.tok[r]];
+      } else {
+        const int acol = q ? p.a_col1 : p.a_col0;
+        const int* ex = p.a_exp + static_cast<int64_t>(p0 + r) * p.a_exp_ld;
+        c = kExpMax;
+        for (int b = a_block(p, acol); b <= a_block(p, acol + p.K - 1); ++b) c = min(c, ex[b]);
+      }
+    }
+    s.cexp[q][r] = c;
+  }
+  __syncthreads();
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  run_k<kA>(p, s, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
+
+  const int lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
+  if constexpr (kEpi == kSwiGLU) {
+    f32x16 acc_u[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_u[i][j][r] = 0.f;
+    run_k<kA>(p, s, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
+    // h = SiLU(g) * u (* w), in place of g.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          const float g = __builtin_ldexpf(acc[i][j][r], -s.cexp[0][row]);
+          const float u = __builtin_ldexpf(acc_u[i][j][r], -s.cexp[1][row]);
+          float h = silu_f32(g) * u;
+          if (p.wbd) h *= s.w[row];
+          acc[i][j][r] = h;
+        }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          acc[i][j][r] = __builtin_ldexpf(acc[i][j][r], -s.cexp[0][row]);
+        }
+  }
+
+  if constexpr (kEpi == kToOutput) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = n0 + 64 * wn + 32 * j + (lane & 31);
+        if (col >= p.ncols) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row >= rows) continue;
+          const float v = acc[i][j][r];
+          if (p.out_mode == LATENT_OUT_PER_SLOT)
+            p.out[(static_cast<int64_t>(s.tok[row]) * p.n_expert_used + s.slot[row]) * p.ncols + col] = v;
+          else
+            atomic_add_f32(p.out + static_cast<int64_t>(s.tok[row]) * p.ncols + col, p.wbd ? v : s.w[row] * v);
+        }
+      }
+    return;
+  }
+
+  // fp16 store with a per-(row, 128-column block) exponent.  Row maxima: over
+  // the lane's two column blocks, the 32 lanes of a row, then the two waves
+  // that share the rows.
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float m = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (n0 + 64 * wn + 32 * j + (lane & 31) < p.ncols) m = fmaxf(m, fabsf(acc[i][j][r]));
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+      if ((lane & 31) == 0) s.rmax[wn][64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = m;
+    }
+  __syncthreads();
+  const int blk = z * ((p.ncols + kNT - 1) / kNT) + blockIdx.y;
+  if (tid < rows) p.dst_exp[static_cast<int64_t>(p0 + tid) * p.dst_exp_ld + blk] = block_exponent(fmaxf(s.rmax[0][tid], s.rmax[1][tid]));
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + 64 * wn + 32 * j + (lane & 31);
+      if (col >= p.ncols) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row >= rows) continue;
+        const int ex = block_exponent(fmaxf(s.rmax[0][row], s.rmax[1][row]));
+        p.dst[static_cast<int64_t>(p0 + row) * p.ldd + (z ? p.dst_col1 : 0) + col] =
+            static_cast<_Float16>(__builtin_ldexpf(acc[i][j][r], ex));
+      }
+    }
+}
+
+// Row exponents of x: 2^e * max|x[t]| in [2^14, 2^15).
+__global__ void __launch_bounds__(kThreads) x_exponent_kernel(const void* x, int x_dtype, int d, int* xexp) {
+  __shared__ float red[kThreads / kWave];
+  const int t = blockIdx.x;
+  float m = 0.f;
+  for (int c = threadIdx.x; c < d; c += kThreads) m = fmaxf(m, fabsf(load_act(x, x_dtype, static_cast<int64_t>(t) * d + c)));
+  for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kThreads / kWave; ++i) m = fmaxf(m, red[i]);
+    xexp[t] = block_exponent(m);
+  }
+}
+
+// M tiles of kMT pairs for every active expert, in expert order.
+__global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int* tile_a, int* tile_r0) {
+  __shared__ int scan[kTileThreads];
+  const int tid = threadIdx.x;
+  const int n_active = g.meta[0];
+  const int per = (n_active + kTileThreads - 1) / kTileThreads;
+  const int a0 = min(n_active, tid * per), a1 = min(n_active, a0 + per);
+  int mine = 0;
+  for (int a = a0; a < a1; ++a) mine += (g.act_count[a] + kMT - 1) / kMT;
+  scan[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < kTileThreads; off <<= 1) {
+    const int v = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += v;
+    __syncthreads();
+  }
+  int t = scan[tid] - mine;
+  for (int a = a0; a < a1; ++a) {
+    for (int r = 0; r < g.act_count[a]; r += kMT) {
+      tile_a[t] = a;
+      tile_r0[t] = r;
+      ++t;
+    }
+  }
+  if (tid == kTileThreads - 1) g.meta[2] = scan[tid];
+}
+
+size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
+
+int64_t max_tiles(const latent_moe_args& a) {
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  return (P + kMT - 1) / kMT + std::min<int64_t>(a.n_expert, P);
+}
+
+template <int kA, int kEpi>
+int launch(const Params& p, int64_t tiles, int ncols, int zdim, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>((ncols + kNT - 1) / kNT), zdim);
+  hipLaunchKernelGGL((gemm_kernel<kA, kEpi>), grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}
+
+}  // namespace
+
+bool supported(const latent_moe_args& a) {
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  const int64_t active = std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P));
+  if (P < static_cast<int64_t>(kMinPairsPerExpert) * active) return false;
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  for (const latent_factor* f : fs)
+    if (f->int8_bitmap != nullptr) return false;  // per-group INT8 layers take the general path
+  if ((reinterpret_cast<uintptr_t>(a.x) & 15u) != 0) return false;
+  return true;
+}
+
+Layout layout_for(const latent_moe_args& a) {
+  const int64_t P = a.n_tokens * a.n_expert_used, R = a.max_rank, T = max_tiles(a);
+  Layout L{};
+  size_t off = 0;
+  L.tile_a = off;  off = align_up(off + T * sizeof(int));
+  L.tile_r0 = off; off = align_up(off + T * sizeof(int));
+  const int64_t rb = (R + kNT - 1) / kNT, fb = (a.n_ff + kNT - 1) / kNT;
+  L.xexp = off;    off = align_up(off + a.n_tokens * sizeof(int));
+  L.gu = off;      off = align_up(off + P * 2 * R * sizeof(_Float16));
+  L.gu_exp = off;  off = align_up(off + P * 2 * rb * sizeof(int));
+  L.h = off;       off = align_up(off + P * a.n_ff * sizeof(_Float16));
+  L.h_exp = off;   off = align_up(off + P * fb * sizeof(int));
+  L.dl = off;      off = align_up(off + P * R * sizeof(_Float16));
+  L.dl_exp = off;  off = align_up(off + P * rb * sizeof(int));
+  L.total = off;
+  return L;
+}
+
+int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char* scratch, hipStream_t s) {
+  const Layout L = layout_for(a);
+  const int64_t tiles = max_tiles(a);
+  int* tile_a = reinterpret_cast<int*>(scratch + L.tile_a);
+  int* tile_r0 = reinterpret_cast<int*>(scratch + L.tile_r0);
+  _Float16* gu = reinterpret_cast<_Float16*>(scratch + L.gu);
+  _Float16* h = reinterpret_cast<_Float16*>(scratch + L.h);
+  _Float16* dl = reinterpret_cast<_Float16*>(scratch + L.dl);
+  int* xexp = reinterpret_cast<int*>(scratch + L.xexp);
+  int* gu_exp = reinterpret_cast<int*>(scratch + L.gu_exp);
+  int* h_exp = reinterpret_cast<int*>(scratch + L.h_exp);
+  int* dl_exp = reinterpret_cast<int*>(scratch + L.dl_exp);
+  const int R = static_cast<int>(a.max_rank), d = static_cast<int>(a.n_embd), ff = static_cast<int>(a.n_ff);
+  const int rb = (R + kNT - 1) / kNT, fb = (ff + kNT - 1) / kNT;
+  hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, tile_a, tile_r0);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  hipLaunchKernelGGL(x_exponent_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype,
+                     d, xexp);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+
+  Params p{};
+  p.g = g;
+  p.tile_a = tile_a;
+  p.tile_r0 = tile_r0;
+  p.x = a.x;
+  p.x_dtype = a.x_dtype;
+  p.d = d;
+  p.out = static_cast<float*>(a.out);
+  p.out_mode = a.out_mode;
+  p.wbd = a.weight_before_down ? 1 : 0;
+  p.n_expert_used = static_cast<int>(a.n_expert_used);
+
+  // A: gu = x . [A_g | A_u]
+  p.K = d;
+  p.a_exp = xexp;
+  p.f0 = fac[0];
+  p.f1 = fac[2];
+  p.ncols = R;
+  p.dst = gu;
+  p.ldd = 2 * R;
+  p.dst_col1 = R;
+  p.dst_exp = gu_exp;
+  p.dst_exp_ld = 2 * rb;
+  int st = launch<kFromX, kStoreHalf>(p, tiles, R, 2, s);
+  if (st != LATENT_OK) return st;
+  // BC1: h = SiLU(g . B_g) * (u . B_u)
+  p.K = R;
+  p.a = gu;
+  p.lda = 2 * R;
+  p.a_col0 = 0;
+  p.a_col1 = R;
+  p.a_exp = gu_exp;
+  p.a_exp_ld = 2 * rb;
+  p.a_part = R;
+  p.a_part_blocks = rb;
+  p.f0 = fac[1];
+  p.f1 = fac[3];
+  p.ncols = ff;
+  p.dst = h;
+  p.ldd = ff;
+  p.dst_col1 = 0;
+  p.dst_exp = h_exp;
+  p.dst_exp_ld = fb;
+  st = launch<kFromPairs, kSwiGLU>(p, tiles, ff, 1, s);
+  if (st != LATENT_OK) return st;
+  // BC2: dl = h . A_d
+  p.K = ff;
+  p.a = h;
+  p.lda = ff;
+  p.a_col0 = p.a_col1 = 0;
+  p.a_exp = h_exp;
+  p.a_exp_ld = fb;
+  p.a_part = ff;
+  p.a_part_blocks = fb;
+  p.f0 = p.f1 = fac[4];
+  p.ncols = R;
+  p.dst = dl;
+  p.ldd = R;
+  p.dst_exp = dl_exp;
+  p.dst_exp_ld = rb;
+  st = launch<kFromPairs, kStoreHalf>(p, tiles, R, 1, s);
+  if (st != LATENT_OK) return st;
+  // D: out += w * (dl . B_d)
+  p.K = R;
+  p.a = dl;
+  p.lda = R;
+  p.a_exp = dl_exp;
+  p.a_exp_ld = rb;
+  p.a_part = R;
+  p.a_part_blocks = rb;
+  p.f0 = p.f1 = fac[5];
+  p.ncols = d;
+  return launch<kFromPairs, kToOutput>(p, tiles, d, 1, s);
+}
+
+}  // namespace prefill
+}  // namespace latent

@@ -211,3 +211,51 @@ def test_dsv3_decode_parity(gpu, dsv3, B):
     err = ref.rel_l2(want, out.cpu().numpy())
     print(f"dsv3 decode B={B} experts={experts.size} rel_l2={err:.3e}")
     assert err <= TOL
+
+
+# --------------------------------------------------------------------------------
+# prefill: grouped fp16 MFMA path (>= 16 routed pairs per active expert)
+# --------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def prefill_layer():
+    return synth.make_layer(seed=300, n_expert=32, d=1024, ff=512, max_rank=128)
+
+
+@pytest.fixture(scope="module")
+def prefill_dev(gpu, prefill_layer):
+    return to_device(prefill_layer)
+
+
+@pytest.mark.parametrize("x_dtype,wbd", [("bf16", False), ("f32", True), ("f16", False)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_prefill_mfma_parity(gpu, prefill_layer, prefill_dev, x_dtype, wbd, mode):
+    import torch
+
+    T, E, K = 256, 32, 4
+    rng = np.random.default_rng(31)
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
+    logits = routing.zipf_logits(rng, T, E, gamma=0.5)
+    ids, w = routing.softmax_topk(logits, K)
+    xt = torch.from_numpy(x).cuda().to({"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[x_dtype])
+    assert gpu.moe_path(prefill_dev, xt, K) == "prefill"
+    got, xq, wq = _run(gpu, prefill_dev, x, ids, w, wbd=wbd, mode=mode, x_dtype=x_dtype)
+    want = ref.moe_forward(xq, ids, wq, prefill_layer, weight_before_down=wbd, out_mode=mode)
+    err = ref.rel_l2(want, got)
+    print(f"prefill x={x_dtype} wbd={wbd} mode={mode} rel_l2={err:.3e}")
+    assert err <= TOL
+    if mode == 1:
+        assert not got[ids < 0].any()
+
+
+def test_prefill_mfma_ragged_tiles(gpu, prefill_layer, prefill_dev):
+    # Expert counts that are not multiples of the 128-pair tile, an expert with
+    # exactly one tile, dropped slots and an unrouted expert.
+    T, E, K = 300, 32, 4
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
+    ids, w = routing.softmax_topk(rng.standard_normal((T, E)), K)
+    ids[ids == 5] = -1
+    ids[:128, 0] = 7
+    got, xq, wq = _run(gpu, prefill_dev, x, ids, w, mode=0, x_dtype="bf16")
+    want = ref.moe_forward(xq, ids, wq, prefill_layer, out_mode=0)
+    assert ref.rel_l2(want, got) <= TOL
