@@ -69,6 +69,7 @@ struct MoeParams {
   int cb, n_bc;          // phase BC: ff columns per item, items per expert
   int cd, n_d;           // phase D: d columns per item, items per expert
   int64_t zero_floats;   // accumulator floats cleared by prep
+  int zero_out;          // reduced mode: prep clears out (the phase kernels accumulate into it)
 };
 
 __device__ __forceinline__ int ilog2(int v) { return 31 - __builtin_clz(v); }
@@ -151,6 +152,7 @@ __device__ void route_block(const MoeParams& p) {
   if (tid == kRouteThreads - 1) {
     p.meta[0] = scan_a[kRouteThreads - 1];
     p.meta[1] = bad;
+    p.meta[3] = scan_c[kRouteThreads - 1];  // routed pairs
   }
   __syncthreads();
   for (int i = tid; i < P; i += kRouteThreads) {
@@ -177,6 +179,7 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
   const int64_t n4 = p.zero_floats / 4;
   for (int64_t i = t0; i < n4; i += stride) acc4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   if (p.out_mode == LATENT_OUT_REDUCED) {
+    if (!p.zero_out) return;
     float4* o4 = reinterpret_cast<float4*>(p.out);
     const int64_t no = static_cast<int64_t>(p.T) * p.d / 4;
     for (int64_t i = t0; i < no; i += stride) o4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -650,6 +653,7 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.a_max = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P)));
   const bool use_prefill = prefill::supported(a);
   p.zero_floats = use_prefill ? 0 : P * 3 * a.max_rank;  // the MFMA path writes its intermediates whole
+  p.zero_out = use_prefill ? 0 : 1;                       // and every output row (per-token combine)
 
   // Work split: enough items to fill 256 CUs even when few experts are routed.
   const int MB = a.n_tokens == 1 ? 1 : 4;
@@ -661,7 +665,7 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.cd = pick_pow2_chunk(p.d, p.a_max, 2048, 128, 512);
   p.n_d = (p.d + p.cd - 1) / p.cd;
 
-  const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? P / a.n_expert_used * a.n_embd / 4
+  const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
                                                                                   : P * a.n_embd / 4);
   const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));
   hipLaunchKernelGGL(prep_kernel, dim3(1 + zero_blocks), dim3(kRouteThreads), 0, s, p);

@@ -8,7 +8,8 @@
 //   A    gu[p]  = x[tok(p)] . [A_g | A_u]                 K = d,  N = 2R
 //   BC1  h[p]   = SiLU(gu[p][:R] . B_g) * (gu[p][R:] . B_u)  K = R,  N = ff
 //   BC2  dl[p]  = h[p] . A_d                               K = ff, N = R
-//   D    out[tok(p)] += w(p) * dl[p] . B_d                 K = R,  N = d
+//   D    y[p]   = dl[p] . B_d                              K = R,  N = d
+//   out[t] = sum over the token's slots of w * y (reduced), or y per slot
 //
 // Each GEMM tile is 128 pairs x 128 columns on 4 waves (2 x 2 of 64 x 64,
 // v_mfma_f32_32x32x16_f16, fp32 accumulation).  Per 32-row K slice the NF4
@@ -16,8 +17,9 @@
 // LDS transposed to [column][k], the activation slice is gathered and
 // converted to fp16 into LDS as [pair][k]; both are double-buffered and the
 // next slice's global loads are in flight while the current one multiplies.
-// Intermediates (gu, h, dl) are stored in fp16 per pair; the output combine
-// adds w * y into out with fp32 atomics (reduced mode) or stores per slot.
+// Intermediates (gu, h, dl, y) are stored in fp16 per pair; a per-token
+// combine kernel sums the weighted slot rows in slot order (reduced mode), or
+// the last GEMM stores fp32 rows per slot.
 //
 // fp16 range: the latents of a LATENT chain are small (about 1e-3 .. 1e-9 at
 // the DeepSeek-V3 shape), far below fp16's normal range.  Every fp16 operand
@@ -25,8 +27,9 @@
 // v * 2^e with e chosen per (row, 128-column block) so that the block's
 // largest |v| lands in [2^14, 2^15), and records e; a consumer rescales each
 // block of its row to the row's smallest exponent c (exact ldexp on fp16) and
-// multiplies its fp32 accumulators by 2^-c.  x rows get their exponent from a
-// max pass over x.  Scaling by powers of two adds no rounding.
+// multiplies its fp32 accumulators by 2^-c.  x is converted once per call to
+// fp16 rows scaled the same way (one exponent per token).  Scaling by powers
+// of two adds no rounding.
 #include "prefill.hpp"
 
 #include <algorithm>
@@ -54,8 +57,8 @@ struct Params {
   Grouping g;
   const int* tile_a;
   const int* tile_r0;
-  const void* x;  // kFromX: x [T][d] of x_dtype, row tok(p)
-  int x_dtype, d;
+  const _Float16* xh;  // kFromX: scaled fp16 x [T][d], row tok(p)
+  int d;
   const _Float16* a;  // kFromPairs: a[p * lda + col], scaled by 2^a_exp[p][col / 128]
   int64_t lda;
   int a_col0, a_col1;  // A columns of the first / second product
@@ -70,8 +73,8 @@ struct Params {
   int dst_col1;   // column offset of the blockIdx.z == 1 product
   int* dst_exp;   // [P][dst_exp_ld] exponents of the stored blocks
   int dst_exp_ld;
-  float* out;     // kToOutput
-  int out_mode, wbd, n_expert_used;
+  float* out;     // kToOutput: per-slot rows out[(tok * k + slot) * ncols + col]
+  int wbd, n_expert_used;
 };
 
 struct Smem {
@@ -88,8 +91,8 @@ struct Smem {
 // One thread's share of a K slice, held in registers between the global loads
 // and the LDS commit.
 struct Stage {
-  uint4 a[4];         // 16 activations: 16-bit types use a[0..1], f32 uses a[0..3]
-  int shift;          // exponent change applied to them (kFromPairs: row exponent - block exponent)
+  uint4 a[2];         // 16 fp16 activations
+  int shift;          // exponent change applied to them (row exponent - block exponent)
   uint32_t c0, c1;    // NF4 codes: 8 columns of rows k and k + 1
   uint32_t s0, s1;    // their fp16 scales
 };
@@ -106,19 +109,12 @@ template <int kA>
 __device__ __forceinline__ void load_a(const Params& p, const Smem& s, int p0, int rows, int k0, int acol, int q,
                                        Stage& st) {
   const int tid = threadIdx.x, r = tid >> 1, kh = (tid & 1) * 16;
-  st.a[0] = st.a[1] = st.a[2] = st.a[3] = zero4();
+  st.a[0] = st.a[1] = zero4();
   st.shift = 0;
   if (r >= rows) return;
   if constexpr (kA == kFromX) {
-    st.shift = s.cexp[q][r];
-    const int64_t off = static_cast<int64_t>(s.tok[r]) * p.d + k0 + kh;
-    if (p.x_dtype == LATENT_F32) {
-      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(p.x) + off);
-      st.a[0] = q[0]; st.a[1] = q[1]; st.a[2] = q[2]; st.a[3] = q[3];
-    } else {
-      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + off);
-      st.a[0] = q[0]; st.a[1] = q[1];
-    }
+    const uint4* v = reinterpret_cast<const uint4*>(p.xh + static_cast<int64_t>(s.tok[r]) * p.d + k0 + kh);
+    st.a[0] = v[0]; st.a[1] = v[1];
   } else {
     const uint4* v = reinterpret_cast<const uint4*>(p.a + static_cast<int64_t>(p0 + r) * p.lda + acol + k0 + kh);
     st.a[0] = v[0]; st.a[1] = v[1];
@@ -147,30 +143,11 @@ __device__ __forceinline__ void commit(const Params& p, Smem& s, int buf, const 
   {
     const int r = tid >> 1, kh = (tid & 1) * 16;
     half8 h[2];
-    if (kA == kFromX && p.x_dtype == LATENT_F32) {
-      const float* f = reinterpret_cast<const float*>(st.a);
+    h[0] = *reinterpret_cast<const half8*>(&st.a[0]);
+    h[1] = *reinterpret_cast<const half8*>(&st.a[1]);
+    if (kA == kFromPairs && st.shift != 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = static_cast<_Float16>(__builtin_ldexpf(f[i], st.shift));
-    } else if (kA == kFromX && p.x_dtype == LATENT_BF16) {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(st.a);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        h[i / 4][2 * (i % 4)] =
-            static_cast<_Float16>(__builtin_ldexpf(__uint_as_float((w[i] & 0xFFFFu) << 16), st.shift));
-        h[i / 4][2 * (i % 4) + 1] = static_cast<_Float16>(__builtin_ldexpf(__uint_as_float(w[i] & 0xFFFF0000u), st.shift));
-      }
-    } else if (kA == kFromX) {
-      const _Float16* f = reinterpret_cast<const _Float16*>(st.a);
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        h[i / 8][i % 8] = static_cast<_Float16>(__builtin_ldexpf(static_cast<float>(f[i]), st.shift));
-    } else {
-      h[0] = *reinterpret_cast<const half8*>(&st.a[0]);
-      h[1] = *reinterpret_cast<const half8*>(&st.a[1]);
-      if (st.shift != 0) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = __builtin_ldexpf16(h[i / 8][i % 8], st.shift);
-      }
+      for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = __builtin_ldexpf16(h[i / 8][i % 8], st.shift);
     }
     half8* dst = reinterpret_cast<half8*>(&s.a[buf][r * kLds + kh]);
     dst[0] = h[0];
@@ -193,39 +170,81 @@ __device__ __forceinline__ void commit(const Params& p, Smem& s, int buf, const 
 // acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
 // whole K of the tile, for factor f (expert e) and activation column acol.
 template <int kA>
+__device__ __forceinline__ void mfma_slice(const Smem& s, int buf, f32x16 (&acc)[2][2]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w & 1, wn = w >> 1;
+#pragma unroll
+  for (int ks = 0; ks < kKS; ks += 16) {
+    half8 af[2], bf[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      af[i] = *reinterpret_cast<const half8*>(&s.a[buf][(64 * wm + 32 * i + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      bf[j] = *reinterpret_cast<const half8*>(&s.b[buf][(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+  }
+}
+
+// acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
+// whole K of the tile, for factor f (expert e) and activation column acol.
+// Slices s + 1 and s + 2 are in flight (registers) while slice s multiplies
+// out of LDS; the loop is unrolled by two so the two register stages swap
+// roles without copies.
+template <int kA, bool kDeep>
 __device__ __forceinline__ void run_k(const Params& p, Smem& s, const Factor& f, int64_t e, int p0, int rows,
                                       int n0, int acol, int q, f32x16 (&acc)[2][2]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w & 1, wn = w >> 1;
-  const int nslices = p.K / kKS;
-  Stage st;
-  load_a<kA>(p, s, p0, rows, 0, acol, q, st);
-  load_b(f, e, 0, n0, p.ncols, st);
-  commit<kA>(p, s, 0, st);
+  const int nslices = p.K / kKS;  // >= 1
+  if constexpr (!kDeep) {
+    // One slice in flight (fewer registers: the SwiGLU tile holds two accumulator sets).
+    Stage st;
+    load_a<kA>(p, s, p0, rows, 0, acol, q, st);
+    load_b(f, e, 0, n0, p.ncols, st);
+    commit<kA>(p, s, 0, st);
+    __syncthreads();
+    for (int sl = 0; sl < nslices; ++sl) {
+      const bool more = sl + 1 < nslices;
+      if (more) {
+        load_a<kA>(p, s, p0, rows, (sl + 1) * kKS, acol, q, st);
+        load_b(f, e, (sl + 1) * kKS, n0, p.ncols, st);
+      }
+      mfma_slice<kA>(s, sl & 1, acc);
+      if (more) commit<kA>(p, s, (sl & 1) ^ 1, st);
+      __syncthreads();
+    }
+    return;
+  }
+  Stage st0, st1;
+  load_a<kA>(p, s, p0, rows, 0, acol, q, st0);
+  load_b(f, e, 0, n0, p.ncols, st0);
+  if (nslices > 1) {
+    load_a<kA>(p, s, p0, rows, kKS, acol, q, st1);
+    load_b(f, e, kKS, n0, p.ncols, st1);
+  }
+  commit<kA>(p, s, 0, st0);
   __syncthreads();
-  for (int sl = 0; sl < nslices; ++sl) {
-    const int buf = sl & 1;
-    const bool more = sl + 1 < nslices;
-    if (more) {
-      load_a<kA>(p, s, p0, rows, (sl + 1) * kKS, acol, q, st);
-      load_b(f, e, (sl + 1) * kKS, n0, p.ncols, st);
+  for (int sl = 0; sl < nslices; sl += 2) {
+    // Even slice sl is in buffer 0; st1 holds slice sl + 1.
+    if (sl + 2 < nslices) {
+      load_a<kA>(p, s, p0, rows, (sl + 2) * kKS, acol, q, st0);
+      load_b(f, e, (sl + 2) * kKS, n0, p.ncols, st0);
     }
-#pragma unroll
-    for (int ks = 0; ks < kKS; ks += 16) {
-      half8 af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const half8*>(&s.a[buf][(64 * wm + 32 * i + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const half8*>(&s.b[buf][(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    mfma_slice<kA>(s, 0, acc);
+    if (sl + 1 >= nslices) break;
+    commit<kA>(p, s, 1, st1);
+    __syncthreads();
+    // Odd slice sl + 1 is in buffer 1; st0 holds slice sl + 2.
+    if (sl + 3 < nslices) {
+      load_a<kA>(p, s, p0, rows, (sl + 3) * kKS, acol, q, st1);
+      load_b(f, e, (sl + 3) * kKS, n0, p.ncols, st1);
     }
-    if (more) commit<kA>(p, s, buf ^ 1, st);
+    mfma_slice<kA>(s, 1, acc);
+    if (sl + 2 < nslices) commit<kA>(p, s, 0, st0);
     __syncthreads();
   }
+  __syncthreads();
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
@@ -284,7 +303,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  run_k<kA>(p, s, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
+  run_k<kA, kEpi != kSwiGLU>(p, s, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
 
   const int lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
   if constexpr (kEpi == kSwiGLU) {
@@ -295,7 +314,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_u[i][j][r] = 0.f;
-    run_k<kA>(p, s, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
+    run_k<kA, false>(p, s, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
     // h = SiLU(g) * u (* w), in place of g.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -333,11 +352,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
         for (int r = 0; r < 16; ++r) {
           const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
           if (row >= rows) continue;
-          const float v = acc[i][j][r];
-          if (p.out_mode == LATENT_OUT_PER_SLOT)
-            p.out[(static_cast<int64_t>(s.tok[row]) * p.n_expert_used + s.slot[row]) * p.ncols + col] = v;
-          else
-            atomic_add_f32(p.out + static_cast<int64_t>(s.tok[row]) * p.ncols + col, p.wbd ? v : s.w[row] * v);
+          p.out[(static_cast<int64_t>(s.tok[row]) * p.n_expert_used + s.slot[row]) * p.ncols + col] = acc[i][j][r];
         }
       }
     return;
@@ -378,18 +393,88 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
     }
 }
 
-// Row exponents of x: 2^e * max|x[t]| in [2^14, 2^15).
-__global__ void __launch_bounds__(kThreads) x_exponent_kernel(const void* x, int x_dtype, int d, int* xexp) {
+// x rows to fp16: xh[t] = fp16(x[t] * 2^e[t]) with 2^e * max|x[t]| in [2^14, 2^15).
+// One workgroup per token; d % 8 == 0 and x 16-byte aligned.
+// Also clears the token's slot entries of pos_of.
+__global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_dtype, int d, _Float16* xh, int* xexp,
+                                                          int* pos_of, int k) {
   __shared__ float red[kThreads / kWave];
-  const int t = blockIdx.x;
+  __shared__ int ex;
+  const int t = blockIdx.x, tid = threadIdx.x;
+  if (tid < k) pos_of[t * k + tid] = -1;
+  const int64_t base = static_cast<int64_t>(t) * d;
+  auto load8 = [&](int c, float (&v)[8]) {
+    if (x_dtype == LATENT_F32) {
+      const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + c);
+      const float4 a = q[0], b = q[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + c);
+      const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (x_dtype == LATENT_BF16) {
+          v[2 * i] = __uint_as_float(w[i] << 16);
+          v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+        } else {
+          v[2 * i] = half_bits_to_float(static_cast<uint16_t>(w[i] & 0xFFFFu));
+          v[2 * i + 1] = half_bits_to_float(static_cast<uint16_t>(w[i] >> 16));
+        }
+      }
+    }
+  };
   float m = 0.f;
-  for (int c = threadIdx.x; c < d; c += kThreads) m = fmaxf(m, fabsf(load_act(x, x_dtype, static_cast<int64_t>(t) * d + c)));
+  for (int c = tid * 8; c < d; c += kThreads * 8) {
+    float v[8];
+    load8(c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+  }
   for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = m;
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     for (int i = 1; i < kThreads / kWave; ++i) m = fmaxf(m, red[i]);
-    xexp[t] = block_exponent(m);
+    ex = block_exponent(m);
+    xexp[t] = ex;
+  }
+  __syncthreads();
+  const int e = ex;
+  for (int c = tid * 8; c < d; c += kThreads * 8) {
+    float v[8];
+    load8(c, v);
+    half8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(v[i], e));
+    *reinterpret_cast<half8*>(xh + base + c) = h;
+  }
+}
+
+// pos_of[tok * k + slot] = pair for the routed pairs (x_prep_kernel cleared it to -1).
+__global__ void __launch_bounds__(kThreads) slots_kernel(Grouping g, int* pos_of, int P, int k) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < P && i < g.meta[3]) pos_of[g.pair_tok[i] * k + g.pair_slot[i]] = i;
+}
+
+// out[t] = sum over slots (in slot order) of w * y[pos_of[t][slot]] * 2^-exp,
+// y rows in fp16 with one exponent per 128 columns.  One workgroup per token.
+__global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, const int* yexp, int yexp_ld,
+                                                           const int* pos_of, const float* pair_w, int k, int d, int wbd,
+                                                           float* out) {
+  const int t = blockIdx.x;
+  for (int c = threadIdx.x * 8; c < d; c += kThreads * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < k; ++sl) {
+      const int pos = pos_of[t * k + sl];
+      if (pos < 0) continue;
+      const half8 h = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
+      const float w = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kNT]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, static_cast<float>(h[i]), acc[i]);
+    }
+    float4* o = reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * d + c);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
 }
 
@@ -456,12 +541,17 @@ Layout layout_for(const latent_moe_args& a) {
   L.tile_r0 = off; off = align_up(off + T * sizeof(int));
   const int64_t rb = (R + kNT - 1) / kNT, fb = (a.n_ff + kNT - 1) / kNT;
   L.xexp = off;    off = align_up(off + a.n_tokens * sizeof(int));
+  L.xh = off;      off = align_up(off + a.n_tokens * a.n_embd * sizeof(_Float16));
   L.gu = off;      off = align_up(off + P * 2 * R * sizeof(_Float16));
   L.gu_exp = off;  off = align_up(off + P * 2 * rb * sizeof(int));
   L.h = off;       off = align_up(off + P * a.n_ff * sizeof(_Float16));
   L.h_exp = off;   off = align_up(off + P * fb * sizeof(int));
   L.dl = off;      off = align_up(off + P * R * sizeof(_Float16));
   L.dl_exp = off;  off = align_up(off + P * rb * sizeof(int));
+  const int64_t db = (a.n_embd + kNT - 1) / kNT;
+  L.pos_of = off;  off = align_up(off + P * sizeof(int));
+  L.y = off;       off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * a.n_embd * sizeof(_Float16) : 0));
+  L.y_exp = off;   off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * db * sizeof(int) : 0));
   L.total = off;
   return L;
 }
@@ -475,26 +565,33 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   _Float16* h = reinterpret_cast<_Float16*>(scratch + L.h);
   _Float16* dl = reinterpret_cast<_Float16*>(scratch + L.dl);
   int* xexp = reinterpret_cast<int*>(scratch + L.xexp);
+  _Float16* xh = reinterpret_cast<_Float16*>(scratch + L.xh);
   int* gu_exp = reinterpret_cast<int*>(scratch + L.gu_exp);
   int* h_exp = reinterpret_cast<int*>(scratch + L.h_exp);
   int* dl_exp = reinterpret_cast<int*>(scratch + L.dl_exp);
+  int* pos_of = reinterpret_cast<int*>(scratch + L.pos_of);
+  _Float16* y = reinterpret_cast<_Float16*>(scratch + L.y);
+  int* y_exp = reinterpret_cast<int*>(scratch + L.y_exp);
+  const int K = static_cast<int>(a.n_expert_used);
+  const int P = static_cast<int>(a.n_tokens * a.n_expert_used);
   const int R = static_cast<int>(a.max_rank), d = static_cast<int>(a.n_embd), ff = static_cast<int>(a.n_ff);
   const int rb = (R + kNT - 1) / kNT, fb = (ff + kNT - 1) / kNT;
+  hipLaunchKernelGGL(x_prep_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype, d,
+                     xh, xexp, pos_of, K);
+  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, tile_a, tile_r0);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
-  hipLaunchKernelGGL(x_exponent_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype,
-                     d, xexp);
+  hipLaunchKernelGGL(slots_kernel, dim3(static_cast<unsigned>((P + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g,
+                     pos_of, P, K);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
 
   Params p{};
   p.g = g;
   p.tile_a = tile_a;
   p.tile_r0 = tile_r0;
-  p.x = a.x;
-  p.x_dtype = a.x_dtype;
+  p.xh = xh;
   p.d = d;
   p.out = static_cast<float*>(a.out);
-  p.out_mode = a.out_mode;
   p.wbd = a.weight_before_down ? 1 : 0;
   p.n_expert_used = static_cast<int>(a.n_expert_used);
 
@@ -558,7 +655,19 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   p.a_part_blocks = rb;
   p.f0 = p.f1 = fac[5];
   p.ncols = d;
-  return launch<kFromPairs, kToOutput>(p, tiles, d, 1, s);
+  if (a.out_mode == LATENT_OUT_PER_SLOT) return launch<kFromPairs, kToOutput>(p, tiles, d, 1, s);
+  // Reduced: y rows in fp16, then the per-token weighted sum.
+  const int db = (d + kNT - 1) / kNT;
+  p.dst = y;
+  p.ldd = d;
+  p.dst_col1 = 0;
+  p.dst_exp = y_exp;
+  p.dst_exp_ld = db;
+  st = launch<kFromPairs, kStoreHalf>(p, tiles, d, 1, s);
+  if (st != LATENT_OK) return st;
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, y, y_exp, db, pos_of,
+                     g.pair_w, K, d, p.wbd, static_cast<float*>(a.out));
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
 }  // namespace prefill

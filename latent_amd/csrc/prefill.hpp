@@ -12,7 +12,7 @@ namespace prefill {
 
 // Token->expert grouping written by the general path's prep kernel.
 struct Grouping {
-  int* meta;              // [0] active experts, [2] M tiles (written by the tile kernel)
+  int* meta;              // [0] active experts, [3] routed pairs; [2] M tiles (written by the tile kernel)
   const int* act_expert;  // [A]
   const int* act_start;   // [A]
   const int* act_count;   // [A]
@@ -23,7 +23,7 @@ struct Grouping {
 
 // Scratch of the prefill path inside the caller's workspace.
 struct Layout {
-  size_t tile_a, tile_r0, xexp, gu, gu_exp, h, h_exp, dl, dl_exp, total;
+  size_t tile_a, tile_r0, xexp, xh, gu, gu_exp, h, h_exp, dl, dl_exp, pos_of, y, y_exp, total;
 };
 
 // Routed pairs per active expert needed before the MFMA path pays off.
