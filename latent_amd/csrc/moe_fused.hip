@@ -329,6 +329,15 @@ template <typename T>
 __device__ __forceinline__ gptr<T> as_global(const T* p) {
   return (gptr<T>)(p);
 }
+// The same global address in every lane, made visibly uniform so the compiler
+// keeps it in scalar registers (loads then use scalar base + 32-bit offset).
+template <typename T>
+__device__ __forceinline__ gptr<T> uniform(gptr<T> p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<gptr<T>>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 #define LATENT_LDS_AS __attribute__((address_space(3)))
 template <typename T>
 using lptr = T LATENT_LDS_AS*;
@@ -492,20 +501,33 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
 #pragma unroll
     for (int c = 0; c < kHalf; ++c) acc[t][c] = 0.f;
 
-  // Rows of this lane: row_w + ro + k*rstep for k < nsteps (uniform across the
-  // wave); rows past r1 read a valid row (clamped into [r0, r1), or r0 for an
-  // empty range) and are masked by a zero scale.
+  // Rows of this lane: row_l + k*rstep for k < nsteps (nsteps uniform across
+  // the wave); the lane's valid rows are those below r1 (nv of them).  Loads
+  // past them re-read the lane's last valid row (or r0 for none) and are
+  // masked by a zero scale, so every access stays inside the expert.
   const int r0 = j.r0, r1 = j.r1;
   const int row_w = r0 + wri * rpw;
   const int nsteps = row_w < r1 ? (r1 - 1 - row_w) / rstep + 1 : 0;
-  const int row0 = max(r0, min(row_w + ro, r1 - 1));
+  const int row_l = row_w + ro;
   const bool hvalid = h < h_valid;
+  const int nv = (hvalid && row_l < r1) ? (r1 - 1 - row_l) / rstep + 1 : 0;
+  const int row0 = max(r0, min(row_l, r1 - 1));
+  const int rowz = nv > 0 ? row_l + (nv - 1) * rstep : row0;
   const int hh = hvalid ? h : 0;
   const int gg = j.g0 + (hh >> 1), half = hh & 1;
-  const gptr<uint8_t> cbase =
-      f.codes + (j.e * f.rows + row0) * cstride + static_cast<int64_t>(gg) * kGroupBytes + half * (kGroupBytes / 2);
-  const gptr<uint16_t> sbase = f.scales + (j.e * f.rows + row0) * sstride + gg;
-  const int64_t cstep = static_cast<int64_t>(rstep) * cstride, sstep = static_cast<int64_t>(rstep) * sstride;
+  // Expert bases are uniform (scalar registers); lanes address with 32-bit
+  // offsets from them, clamped to the lane's last valid row.
+  const gptr<uint8_t> cexp = uniform(f.codes + j.e * f.rows * cstride);
+  const gptr<uint8_t> sexp = uniform(reinterpret_cast<gptr<uint8_t>>(f.scales + j.e * f.rows * sstride));
+  const uint32_t ccol = static_cast<uint32_t>(gg * kGroupBytes + half * (kGroupBytes / 2));
+  const uint32_t c_first = static_cast<uint32_t>(row0) * static_cast<uint32_t>(cstride) + ccol;
+  const uint32_t c_last = static_cast<uint32_t>(rowz) * static_cast<uint32_t>(cstride) + ccol;
+  // Scale offsets in bytes.
+  const uint32_t s_first = 2u * (static_cast<uint32_t>(row0) * static_cast<uint32_t>(sstride) + gg);
+  const uint32_t s_last = 2u * (static_cast<uint32_t>(rowz) * static_cast<uint32_t>(sstride) + gg);
+  const uint32_t cdelta = static_cast<uint32_t>(rstep) * static_cast<uint32_t>(cstride);
+  const uint32_t sdelta = 2u * static_cast<uint32_t>(rstep) * static_cast<uint32_t>(sstride);
+  const int v_first = row0 - j.vbase, v_last = rowz - j.vbase;
   // Ring of kRing rows in flight per lane; slot u is refilled with the row
   // kRing steps ahead right after it is consumed.  Four-token tiles spend
   // their registers on accumulators and do 4x the arithmetic per row, so a
@@ -517,25 +539,25 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   uint32_t sring[kRing];  // one register per scale (16-bit packing would force a wait per refill)
 #pragma unroll
   for (int u = 0; u < kRing; ++u) {
-    const int k = u < nsteps ? u : 0;
-    ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + k * cstep);
-    sring[u] = sbase[k * sstep];
+    ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(c_first + u * cdelta, c_last));
+    sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(s_first + u * sdelta, s_last));
     __builtin_amdgcn_sched_barrier(0);  // issue in consumption order
   }
+  uint32_t ck = c_first, sk = s_first;
+  int vk = v_first;
   for (int k0 = 0; k0 < nsteps; k0 += kRing) {
 #pragma unroll
     for (int u = 0; u < kRing; ++u) {
       const int k = k0 + u;
-      const int row = row_w + ro + k * rstep;
-      const bool ok = hvalid && k < nsteps && row < r1;
-      const int vr = (ok ? row : r0) - j.vbase;
-      const float sm = ok ? half_bits_to_float(sring[u]) : 0.f;
+      const float sm = k < nv ? half_bits_to_float(sring[u]) : 0.f;
+      const int vr = min(vk + u * rstep, v_last);
       float xs[M];
 #pragma unroll
       for (int t = 0; t < M; ++t) xs[t] = j.vin[t * j.vstride + vr] * sm;
       bool done = false;
       if constexpr (kInt8) {
-        if (f.bitmap != nullptr && ok && is_int8_group(f, j.e, row, gg)) {
+        const int row = row_l + k * rstep;
+        if (f.bitmap != nullptr && k < nv && is_int8_group(f, j.e, row, gg)) {
           fma_half_int8<M>(f, j.e, row, gg, half, xs, acc);
           done = true;
         }
@@ -547,11 +569,13 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
       // loses the distance to its use.  Either way the ring stops hiding the
       // memory latency.
       __builtin_amdgcn_sched_barrier(0);
-      const int kn = k + kRing < nsteps ? k + kRing : 0;
-      ring[u] = *reinterpret_cast<gptr<u32x2>>(cbase + kn * cstep);
-      sring[u] = sbase[kn * sstep];
+      ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(ck + (u + kRing) * cdelta, c_last));
+      sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(sk + (u + kRing) * sdelta, s_last));
       __builtin_amdgcn_sched_barrier(0);
     }
+    ck += kRing * cdelta;
+    sk += kRing * sdelta;
+    vk += kRing * rstep;
   }
   // In-wave reduction over the rpw row lanes.
   for (int off = lph; off < kWave; off <<= 1) {
