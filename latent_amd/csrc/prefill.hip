@@ -68,6 +68,7 @@ struct Params {
   int K;
   Factor f0, f1;  // second factor: the u side of SwiGLU, or the blockIdx.z == 1 factor
   int ncols;      // output columns of one factor
+  int zdim;       // products per tile: 2 for [A_g | A_u], else 1
   _Float16* dst;  // kStoreHalf / kSwiGLU: dst[p * ldd + col]
   int64_t ldd;
   int dst_col1;   // column offset of the blockIdx.z == 1 product
@@ -77,110 +78,181 @@ struct Params {
   int wbd, n_expert_used;
 };
 
+// LDS: a ring of kStages raw K slices filled by direct global->LDS loads
+// (activations as fp16 16-byte chunks, NF4 codes, fp16 scales), and the
+// decoded factor slice, double-buffered, as fp16 [column][k].  Every ring
+// stage and decode buffer is its own __shared__ variable and is indexed at
+// compile time, so the compiler can tell which direct loads an LDS read
+// depends on (one shared object would make every LDS read wait for all of
+// them).
+constexpr int kStages = 4;
+constexpr int kMaxBlocks = 16;  // 128-column exponent blocks per operand row (K <= 2048)
+
+// Bank-conflict-free placements (checked for 32 and 64 banks of 4 bytes):
+//   activation chunk c (8 halfs) of row r  -> 16-byte slot r*4 + (c ^ a_swz(r))
+//   code chunk c (16 bytes) of factor row r -> 16-byte slot code_row(r)*4 + (c ^ code_swz(r))
+__device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int code_row(int r) { return (r >> 1) + 16 * (r & 1); }
+__device__ __forceinline__ int code_swz(int r) { return (r >> 3) & 3; }
+
+struct Stage {
+  _Float16 a[kMT * kKS];       // activations [row][4 chunks of 8 halfs], swizzled
+  uint32_t bc[kKS * kNT / 8];  // NF4 codes [32 rows][4 chunks of 16 bytes], rows and chunks permuted
+  uint32_t bs[2 * 64];         // scales: [32 rows][4 fp16]; the second half takes a balancing load
+};
+
+struct Decoded {
+  _Float16 b[kNT * kLds];      // decoded factor slice [column][k]
+};
+
 struct Smem {
-  _Float16 a[2][kMT * kLds];
-  _Float16 b[2][kNT * kLds];
   float lut[16];
-  int cexp[2][kMT];   // per-row exponent of the tile's operand rows (both products)
-  float rmax[2][kMT]; // row maxima of the two column halves of the output tile
+  int cexp[2][kMT];                  // per-row exponent of the operand rows (both products)
+  int8_t shift[2][kMT][kMaxBlocks];  // per-row, per-block exponent change to reach cexp
+  float rmax[2][kMT];                // row maxima of the two column halves of the output tile
   int tok[kMT];
   int slot[kMT];
   float w[kMT];
 };
 
-// One thread's share of a K slice, held in registers between the global loads
-// and the LDS commit.
-struct Stage {
-  uint4 a[2];         // 16 fp16 activations
-  int shift;          // exponent change applied to them (row exponent - block exponent)
-  uint32_t c0, c1;    // NF4 codes: 8 columns of rows k and k + 1
-  uint32_t s0, s1;    // their fp16 scales
+struct Lds {
+  Smem& m;
+  Stage &s0, &s1, &s2, &s3;
+  Decoded &d0, &d1;
+  template <int I>
+  __device__ __forceinline__ Stage& stage() const {
+    if constexpr (I % kStages == 0) return s0;
+    else if constexpr (I % kStages == 1) return s1;
+    else if constexpr (I % kStages == 2) return s2;
+    else return s3;
+  }
+  template <int I>
+  __device__ __forceinline__ Decoded& dec() const {
+    if constexpr (I % 2 == 0) return d0;
+    else return d1;
+  }
 };
-
-__device__ __forceinline__ uint4 zero4() { return make_uint4(0, 0, 0, 0); }
 
 // Exponent block of column `col` of an intermediate row.
 __device__ __forceinline__ int a_block(const Params& p, int col) {
   return (col / p.a_part) * p.a_part_blocks + (col % p.a_part) / kNT;
 }
 
-// Activation loads: row tid / 2, columns k0 + 16 * (tid % 2) .. + 15.
-template <int kA>
-__device__ __forceinline__ void load_a(const Params& p, const Smem& s, int p0, int rows, int k0, int acol, int q,
-                                       Stage& st) {
-  const int tid = threadIdx.x, r = tid >> 1, kh = (tid & 1) * 16;
-  st.a[0] = st.a[1] = zero4();
-  st.shift = 0;
-  if (r >= rows) return;
-  if constexpr (kA == kFromX) {
-    const uint4* v = reinterpret_cast<const uint4*>(p.xh + static_cast<int64_t>(s.tok[r]) * p.d + k0 + kh);
-    st.a[0] = v[0]; st.a[1] = v[1];
-  } else {
-    const uint4* v = reinterpret_cast<const uint4*>(p.a + static_cast<int64_t>(p0 + r) * p.lda + acol + k0 + kh);
-    st.a[0] = v[0]; st.a[1] = v[1];
-    st.shift = s.cexp[q][r] - p.a_exp[static_cast<int64_t>(p0 + r) * p.a_exp_ld + a_block(p, acol + k0)];
-  }
+// Direct global -> LDS loads: lane l's 16 (4) bytes land at lds + 16 l (4 l).
+// Written as inline assembly so the compiler does not treat every later LDS
+// read as dependent on them (it would wait for all of them, vmcnt(0)); the
+// pipeline waits for them itself (slice_barrier).  lds must be wave-uniform.
+__device__ __forceinline__ uint32_t lds_u32(void* lds) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)(lds))));
+}
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_u32(lds))
+               : "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_u32(lds))
+               : "m0");
 }
 
-// Factor loads: rows k0 + 2 * (tid % 16) + {0, 1}, columns n0 + 8 * (tid / 16) .. + 7.
-__device__ __forceinline__ void load_b(const Factor& f, int64_t e, int k0, int n0, int ncols, Stage& st) {
-  const int tid = threadIdx.x, rp = tid & 15, cg = tid >> 4;
-  const int col = n0 + 8 * cg;
-  st.c0 = st.c1 = 0x77777777u;  // code 7 = 0.0
-  st.s0 = st.s1 = 0;
-  if (col >= ncols) return;
-  const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
-  const int64_t row = e * f.rows + k0 + 2 * rp;
-  st.c0 = *reinterpret_cast<const uint32_t*>(f.codes + row * cstride + col / 2);
-  st.c1 = *reinterpret_cast<const uint32_t*>(f.codes + (row + 1) * cstride + col / 2);
-  st.s0 = f.scales[row * sstride + col / kGroup];
-  st.s1 = f.scales[(row + 1) * sstride + col / kGroup];
-}
-
+// Issue K slice sl into ring stage st: every wave issues exactly three direct
+// loads (two groups of activation rows, then codes or scales), so one vmcnt
+// value covers a whole slice.
 template <int kA>
-__device__ __forceinline__ void commit(const Params& p, Smem& s, int buf, const Stage& st) {
-  const int tid = threadIdx.x;
-  {
-    const int r = tid >> 1, kh = (tid & 1) * 16;
-    half8 h[2];
-    h[0] = *reinterpret_cast<const half8*>(&st.a[0]);
-    h[1] = *reinterpret_cast<const half8*>(&st.a[1]);
-    if (kA == kFromPairs && st.shift != 0) {
+__device__ __forceinline__ void issue_slice(const Params& p, const Smem& m, Stage& st, const Factor& f, int64_t e,
+                                            int p0, int rows, int n0, int acol, int sl) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int k0 = sl * kKS;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) h[i / 8][i % 8] = __builtin_ldexpf16(h[i / 8][i % 8], st.shift);
-    }
-    half8* dst = reinterpret_cast<half8*>(&s.a[buf][r * kLds + kh]);
-    dst[0] = h[0];
-    dst[1] = h[1];
+  for (int i = 0; i < 2; ++i) {
+    const int q = (2 * w + i) * 64 + lane;  // LDS chunk position
+    const int r = q >> 2, c = (q & 3) ^ a_swz(r);  // holds chunk c of row r
+    const int rr = r < rows ? r : 0;                     // pad rows re-read row 0 (finite; never stored)
+    const _Float16* src = kA == kFromX ? p.xh + static_cast<int64_t>(m.tok[rr]) * p.d + k0 + 8 * c
+                                       : p.a + static_cast<int64_t>(p0 + rr) * p.lda + acol + k0 + 8 * c;
+    dma16(src, &st.a[(2 * w + i) * 512]);
   }
+  const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
+  if (w < 2) {
+    const int pr = 16 * w + (lane >> 2);                 // LDS row position
+    const int row = 2 * (pr & 15) + (pr >> 4);           // factor row held there
+    const int col = n0 + 32 * ((lane & 3) ^ code_swz(row));
+    const int colc = col < p.ncols ? col : n0;  // chunks past the factor's columns re-read chunk 0 (decoded as zero)
+    dma16(f.codes + (e * f.rows + k0 + row) * cstride + colc / 2, &st.bc[w * 256]);
+  } else {
+    const int row = lane >> 1, g0 = n0 / kGroup + 2 * (lane & 1);
+    const int g = g0 * kGroup < p.ncols ? g0 : n0 / kGroup;
+    dma4(f.scales + (e * f.rows + k0 + row) * sstride + g, &st.bs[(w - 2) * 64]);
+  }
+}
+
+// Workgroup barrier for the slice pipeline.  __syncthreads() would fence
+// every outstanding direct load (vmcnt(0)); instead each wave waits until at
+// most c slices (3 direct loads each) are in flight and its LDS writes are
+// done (s_waitcnt vmcnt(3c) lgkmcnt(0)), then meets the others at s_barrier.
+// The signal fences keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void slice_barrier(int c) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (c >= 2)
+    __builtin_amdgcn_s_waitcnt(0x0070 | 6);
+  else if (c == 1)
+    __builtin_amdgcn_s_waitcnt(0x0070 | 3);
+  else
+    __builtin_amdgcn_s_waitcnt(0x0070);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Decode a ring stage into a decode buffer (thread: rows 2rp, 2rp+1; columns
+// 8cg .. 8cg+7) and, for intermediate operands, bring each activation chunk of
+// the stage to its row exponent (multiply by 2^shift, exact).
+template <int kA>
+__device__ __forceinline__ void prepare_slice(const Params& p, const Smem& m, Stage& st, Decoded& d, int n0, int acol,
+                                              int q, int sl) {
+  const int tid = threadIdx.x, rp = tid & 15, cg = tid >> 4;
   {
-    const int rp = tid & 15, cg = tid >> 4;
-    const float s0 = __half2float(__ushort_as_half(static_cast<uint16_t>(st.s0)));
-    const float s1 = __half2float(__ushort_as_half(static_cast<uint16_t>(st.s1)));
+    const int r0 = 2 * rp, r1 = 2 * rp + 1;
+    const uint32_t c0 = st.bc[4 * (4 * code_row(r0) + ((cg >> 2) ^ code_swz(r0))) + (cg & 3)];
+    const uint32_t c1 = st.bc[4 * (4 * code_row(r1) + ((cg >> 2) ^ code_swz(r1))) + (cg & 3)];
+    const uint16_t* sh = reinterpret_cast<const uint16_t*>(st.bs);
+    const bool ok = n0 + 8 * cg < p.ncols;
+    const float s0 = ok ? half_bits_to_float(sh[(2 * rp) * 4 + (cg >> 2)]) : 0.f;
+    const float s1 = ok ? half_bits_to_float(sh[(2 * rp + 1) * 4 + (cg >> 2)]) : 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       half2v v;
-      v[0] = static_cast<_Float16>(s.lut[(st.c0 >> (4 * j)) & 15u] * s0);
-      v[1] = static_cast<_Float16>(s.lut[(st.c1 >> (4 * j)) & 15u] * s1);
-      *reinterpret_cast<half2v*>(&s.b[buf][(8 * cg + j) * kLds + 2 * rp]) = v;
+      v[0] = static_cast<_Float16>(m.lut[(c0 >> (4 * j)) & 15u] * s0);
+      v[1] = static_cast<_Float16>(m.lut[(c1 >> (4 * j)) & 15u] * s1);
+      *reinterpret_cast<half2v*>(&d.b[(8 * cg + j) * kLds + 2 * rp]) = v;
+    }
+  }
+  if constexpr (kA == kFromPairs) {
+    const int r = tid >> 1;
+    const int sft = m.shift[q][r][a_block(p, acol + sl * kKS) - a_block(p, acol)];
+    if (sft != 0) {
+      const _Float16 mul = sft < -24 ? static_cast<_Float16>(0.f) : static_cast<_Float16>(__builtin_ldexpf(1.f, sft));
+#pragma unroll
+      for (int c = 2 * (tid & 1); c < 2 * (tid & 1) + 2; ++c) {
+        half8* v = reinterpret_cast<half8*>(&st.a[(r * 4 + (c ^ a_swz(r))) * 8]);
+        *v = *v * mul;
+      }
     }
   }
 }
 
-// acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
-// whole K of the tile, for factor f (expert e) and activation column acol.
-template <int kA>
-__device__ __forceinline__ void mfma_slice(const Smem& s, int buf, f32x16 (&acc)[2][2]) {
+__device__ __forceinline__ void mfma_slice(const Stage& st, const Decoded& d, f32x16 (&acc)[2][2]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w & 1, wn = w >> 1;
 #pragma unroll
   for (int ks = 0; ks < kKS; ks += 16) {
     half8 af[2], bf[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      af[i] = *reinterpret_cast<const half8*>(&s.a[buf][(64 * wm + 32 * i + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+    for (int i = 0; i < 2; ++i) {
+      const int r = 64 * wm + 32 * i + (lane & 31), c = (ks >> 3) + (lane >> 5);
+      af[i] = *reinterpret_cast<const half8*>(&st.a[(r * 4 + (c ^ a_swz(r))) * 8]);
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-      bf[j] = *reinterpret_cast<const half8*>(&s.b[buf][(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
+      bf[j] = *reinterpret_cast<const half8*>(&d.b[(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -188,61 +260,39 @@ __device__ __forceinline__ void mfma_slice(const Smem& s, int buf, f32x16 (&acc)
   }
 }
 
+// One pipeline step for slice sl = sl0 + I (stage I % kStages, decode buffer
+// I % 2): wait for slice sl + 1, refill the stage slice sl - 1 used, prepare
+// slice sl + 1, multiply slice sl.
+template <int kA, int I>
+__device__ __forceinline__ void k_step(const Params& p, const Lds& L, const Factor& f, int64_t e, int p0, int rows,
+                                       int n0, int acol, int q, int sl0, int n, f32x16 (&acc)[2][2]) {
+  const int sl = sl0 + I;
+  if (sl >= n) return;
+  // Slices issued so far: 0 .. min(n - 1, sl + kStages - 2); slice sl + 1 must have landed.
+  slice_barrier(sl + 1 < n ? min(n - 1, sl + kStages - 2) - (sl + 1) : 0);
+  if (sl + kStages - 1 < n)
+    issue_slice<kA>(p, L.m, L.template stage<I + kStages - 1>(), f, e, p0, rows, n0, acol, sl + kStages - 1);
+  if (sl + 1 < n)
+    prepare_slice<kA>(p, L.m, L.template stage<I + 1>(), L.template dec<I + 1>(), n0, acol, q, sl + 1);
+  mfma_slice(L.template stage<I>(), L.template dec<I>(), acc);
+}
+
 // acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
 // whole K of the tile, for factor f (expert e) and activation column acol.
-// Slices s + 1 and s + 2 are in flight (registers) while slice s multiplies
-// out of LDS; the loop is unrolled by two so the two register stages swap
-// roles without copies.
-template <int kA, bool kDeep>
-__device__ __forceinline__ void run_k(const Params& p, Smem& s, const Factor& f, int64_t e, int p0, int rows,
+template <int kA>
+__device__ __forceinline__ void run_k(const Params& p, const Lds& L, const Factor& f, int64_t e, int p0, int rows,
                                       int n0, int acol, int q, f32x16 (&acc)[2][2]) {
-  const int nslices = p.K / kKS;  // >= 1
-  if constexpr (!kDeep) {
-    // One slice in flight (fewer registers: the SwiGLU tile holds two accumulator sets).
-    Stage st;
-    load_a<kA>(p, s, p0, rows, 0, acol, q, st);
-    load_b(f, e, 0, n0, p.ncols, st);
-    commit<kA>(p, s, 0, st);
-    __syncthreads();
-    for (int sl = 0; sl < nslices; ++sl) {
-      const bool more = sl + 1 < nslices;
-      if (more) {
-        load_a<kA>(p, s, p0, rows, (sl + 1) * kKS, acol, q, st);
-        load_b(f, e, (sl + 1) * kKS, n0, p.ncols, st);
-      }
-      mfma_slice<kA>(s, sl & 1, acc);
-      if (more) commit<kA>(p, s, (sl & 1) ^ 1, st);
-      __syncthreads();
-    }
-    return;
-  }
-  Stage st0, st1;
-  load_a<kA>(p, s, p0, rows, 0, acol, q, st0);
-  load_b(f, e, 0, n0, p.ncols, st0);
-  if (nslices > 1) {
-    load_a<kA>(p, s, p0, rows, kKS, acol, q, st1);
-    load_b(f, e, kKS, n0, p.ncols, st1);
-  }
-  commit<kA>(p, s, 0, st0);
-  __syncthreads();
-  for (int sl = 0; sl < nslices; sl += 2) {
-    // Even slice sl is in buffer 0; st1 holds slice sl + 1.
-    if (sl + 2 < nslices) {
-      load_a<kA>(p, s, p0, rows, (sl + 2) * kKS, acol, q, st0);
-      load_b(f, e, (sl + 2) * kKS, n0, p.ncols, st0);
-    }
-    mfma_slice<kA>(s, 0, acc);
-    if (sl + 1 >= nslices) break;
-    commit<kA>(p, s, 1, st1);
-    __syncthreads();
-    // Odd slice sl + 1 is in buffer 1; st0 holds slice sl + 2.
-    if (sl + 3 < nslices) {
-      load_a<kA>(p, s, p0, rows, (sl + 3) * kKS, acol, q, st1);
-      load_b(f, e, (sl + 3) * kKS, n0, p.ncols, st1);
-    }
-    mfma_slice<kA>(s, 1, acc);
-    if (sl + 2 < nslices) commit<kA>(p, s, 0, st0);
-    __syncthreads();
+  const int n = p.K / kKS;  // >= 1
+  issue_slice<kA>(p, L.m, L.s0, f, e, p0, rows, n0, acol, 0);
+  if (n > 1) issue_slice<kA>(p, L.m, L.s1, f, e, p0, rows, n0, acol, 1);
+  if (n > 2) issue_slice<kA>(p, L.m, L.s2, f, e, p0, rows, n0, acol, 2);
+  slice_barrier(min(n - 1, kStages - 2));  // slice 0 landed
+  prepare_slice<kA>(p, L.m, L.s0, L.d0, n0, acol, q, 0);
+  for (int sl0 = 0; sl0 < n; sl0 += kStages) {
+    k_step<kA, 0>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
+    k_step<kA, 1>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
+    k_step<kA, 2>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
+    k_step<kA, 3>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
   }
   __syncthreads();
 }
@@ -259,14 +309,25 @@ __device__ __forceinline__ int block_exponent(float m) {
 template <int kA, int kEpi>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two workgroups per CU
   __shared__ Smem s;
-  const int tile = blockIdx.x;
-  if (tile >= p.g.meta[2]) return;
+  __shared__ Stage st0, st1, st2, st3;
+  __shared__ Decoded dc0, dc1;
+  const Lds L{s, st0, st1, st2, st3, dc0, dc1};
+  // Work items (tile, product z, column tile) in expert order, cut into 8
+  // contiguous runs, one per XCD (workgroup b runs on XCD b % 8): a tile's
+  // column tiles share its activation rows, an expert's tiles share its factor
+  // slices, both in one L2.
+  const int nn = (p.ncols + kNT - 1) / kNT, per_tile = nn * p.zdim;
+  const int total = p.g.meta[2] * per_tile;
+  const int per_xcd = (total + 7) / 8;
+  const int j = blockIdx.x >> 3, item = (blockIdx.x & 7) * per_xcd + j;
+  if (j >= per_xcd || item >= total) return;
+  const int tile = item / per_tile, rem = item - tile * per_tile;
   const int a = p.tile_a[tile], r0 = p.tile_r0[tile];
   const int rows = min(kMT, p.g.act_count[a] - r0);
   const int p0 = p.g.act_start[a] + r0;
   const int64_t e = p.g.act_expert[a];
-  const int n0 = blockIdx.y * kNT;
-  const int z = blockIdx.z;
+  const int z = rem / nn;
+  const int n0 = (rem - z * nn) * kNT;
   const int tid = threadIdx.x;
   if (tid < 16) s.lut[tid] = nf4_level(tid);
   if (tid < kMT) {
@@ -287,10 +348,14 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
         c = p.a_exp[s.tok[r]];
       } else {
         const int acol = q ? p.a_col1 : p.a_col0;
+        const int b0 = a_block(p, acol), b1 = a_block(p, acol + p.K - 1);
         const int* ex = p.a_exp + static_cast<int64_t>(p0 + r) * p.a_exp_ld;
         c = kExpMax;
-        for (int b = a_block(p, acol); b <= a_block(p, acol + p.K - 1); ++b) c = min(c, ex[b]);
+        for (int b = b0; b <= b1; ++b) c = min(c, ex[b]);
+        for (int b = b0; b <= b1; ++b) s.shift[q][r][b - b0] = static_cast<int8_t>(max(-128, c - ex[b]));
       }
+    } else if constexpr (kA == kFromPairs) {
+      for (int b = 0; b < kMaxBlocks; ++b) s.shift[q][r][b] = 0;
     }
     s.cexp[q][r] = c;
   }
@@ -303,7 +368,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  run_k<kA, kEpi != kSwiGLU>(p, s, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
+  run_k<kA>(p, L, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
 
   const int lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
   if constexpr (kEpi == kSwiGLU) {
@@ -314,7 +379,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_u[i][j][r] = 0.f;
-    run_k<kA, false>(p, s, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
+    run_k<kA>(p, L, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
     // h = SiLU(g) * u (* w), in place of g.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -374,7 +439,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two w
       if ((lane & 31) == 0) s.rmax[wn][64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = m;
     }
   __syncthreads();
-  const int blk = z * ((p.ncols + kNT - 1) / kNT) + blockIdx.y;
+  const int blk = z * nn + n0 / kNT;
   if (tid < rows) p.dst_exp[static_cast<int64_t>(p0 + tid) * p.dst_exp_ld + blk] = block_exponent(fmaxf(s.rmax[0][tid], s.rmax[1][tid]));
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -514,8 +579,10 @@ int64_t max_tiles(const latent_moe_args& a) {
 }
 
 template <int kA, int kEpi>
-int launch(const Params& p, int64_t tiles, int ncols, int zdim, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>((ncols + kNT - 1) / kNT), zdim);
+int launch(Params p, int64_t tiles, int ncols, int zdim, hipStream_t s) {
+  p.zdim = zdim;
+  const int64_t items = tiles * ((ncols + kNT - 1) / kNT) * zdim;
+  const dim3 grid(static_cast<unsigned>(8 * ((items + 7) / 8)));
   hipLaunchKernelGGL((gemm_kernel<kA, kEpi>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
@@ -530,6 +597,12 @@ bool supported(const latent_moe_args& a) {
   for (const latent_factor* f : fs)
     if (f->int8_bitmap != nullptr) return false;  // per-group INT8 layers take the general path
   if ((reinterpret_cast<uintptr_t>(a.x) & 15u) != 0) return false;
+  // Direct 16-byte code loads and 4-byte scale-pair loads: 64-column multiples
+  // and aligned factor arrays; at most kMaxBlocks exponent blocks per row.
+  if (a.n_embd % 64 || a.n_ff % 64 || a.max_rank % 64) return false;
+  if (a.n_ff > kMaxBlocks * kNT || a.max_rank > kMaxBlocks * kNT) return false;
+  for (const latent_factor* f : fs)
+    if ((reinterpret_cast<uintptr_t>(f->codes) & 15u) || (reinterpret_cast<uintptr_t>(f->scales) & 3u)) return false;
   return true;
 }
 
