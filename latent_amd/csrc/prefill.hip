@@ -11,12 +11,19 @@
 //   D    y[p]   = dl[p] . B_d                              K = R,  N = d
 //   out[t] = sum over the token's slots of w * y (reduced), or y per slot
 //
-// Each GEMM tile is 128 pairs x 128 columns on 4 waves (2 x 2 of 64 x 64,
-// v_mfma_f32_32x32x16_f16, fp32 accumulation).  Per 32-row K slice the NF4
-// factor slice is dequantized (level * scale in fp32, rounded to fp16) into
-// LDS transposed to [column][k], the activation slice is gathered and
-// converted to fp16 into LDS as [pair][k]; both are double-buffered and the
-// next slice's global loads are in flight while the current one multiplies.
+// BC1 runs as two GEMMs: SiLU of the gate product is stored (fp16, exponent
+// blocks) into the h buffer, and the up GEMM's epilogue reads it back in place
+// and stores h = SiLU(g) * u.
+//
+// A workgroup (4 waves) owns one M tile of up to 128 pairs of one expert and a
+// run of column tiles.  Per 32-row K slice it dequantizes 256 factor columns
+// (two halves of 128; NF4 level in fp16 times the group scale, packed fp16)
+// into LDS as [column][k] and multiplies them on v_mfma_f32_32x32x16_f16 with
+// fp32 accumulation; each wave owns 64 pairs x 128 columns, one exponent
+// block of the output.  Activation rows, NF4
+// codes and scales reach LDS by direct global->LDS loads through a ring of
+// kStages slices, so the next slices are in flight while one is decoded and
+// another multiplied; the ring runs on across the column tiles of a work item.
 // Intermediates (gu, h, dl, y) are stored in fp16 per pair; a per-token
 // combine kernel sums the weighted slot rows in slot order (reduced mode), or
 // the last GEMM stores fp32 rows per slot.
@@ -42,16 +49,21 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;  // 4 waves
-constexpr int kMT = 128;       // pairs per tile
-constexpr int kNT = 128;       // output columns per tile
-constexpr int kKS = 32;        // K rows staged per slice
-constexpr int kLds = 40;       // halfs per LDS row: 32 + 8 pad keeps 16-byte fragment reads conflict-free
+constexpr int kThreads = 256;   // 4 waves: 2 row halves x 2 column halves of a tile
+constexpr int kMT = 128;        // pairs per tile
+constexpr int kHalf = 128;      // factor columns per decoded half
+constexpr int kNT = 2 * kHalf;  // decoded columns per K slice
+constexpr int kKS = 32;         // K rows per slice
+constexpr int kBlk = 128;       // columns per exponent block of an intermediate row
+constexpr int kStages = 3;      // raw K slices in the load ring
+constexpr int kMaxBlocks = 16;  // exponent blocks in one K range (K <= 2048)
 constexpr int kTileThreads = 1024;
 constexpr int kExpMin = -120, kExpMax = 120;
 
 enum ASrc { kFromX = 0, kFromPairs = 1 };
-enum Epi { kStoreHalf = 0, kSwiGLU = 1, kToOutput = 2 };
+// kStoreSiLU stores SiLU of the product; kSwiGLU multiplies the product into
+// what dst holds on entry (SiLU of the gate product) and stores the result.
+enum Epi { kStoreHalf = 0, kSwiGLU = 1, kToOutput = 2, kStoreSiLU = 3 };
 
 struct Params {
   Grouping g;
@@ -59,245 +71,124 @@ struct Params {
   const int* tile_r0;
   const _Float16* xh;  // kFromX: scaled fp16 x [T][d], row tok(p)
   int d;
-  const _Float16* a;  // kFromPairs: a[p * lda + col], scaled by 2^a_exp[p][col / 128]
+  const _Float16* a;  // kFromPairs: a[p * lda + col], scaled by 2^a_exp[p][col / kBlk]
   int64_t lda;
-  int a_col0, a_col1;  // A columns of the first / second product
+  int a_col;           // first A column read
   const int* a_exp;    // kFromPairs: [P][a_exp_ld] block exponents; kFromX: [T] row exponents of x
   int a_exp_ld;
-  int a_part, a_part_blocks;  // the A rows were written as parts of a_part columns, ceil(a_part / 128) blocks each
   int K;
-  Factor f0, f1;  // second factor: the u side of SwiGLU, or the blockIdx.z == 1 factor
-  int ncols;      // output columns of one factor
-  int zdim;       // products per tile: 2 for [A_g | A_u], else 1
+  Factor f0, f1;  // the output columns are [f0 | f1] (nfac factors)
+  int ncols;      // columns of one factor, a multiple of kHalf
+  int nfac;       // 1 or 2
+  int nsub;       // column tiles (kNT output columns) per M tile
+  int spc;        // column tiles per work item
   _Float16* dst;  // kStoreHalf / kSwiGLU: dst[p * ldd + col]
   int64_t ldd;
-  int dst_col1;   // column offset of the blockIdx.z == 1 product
-  int* dst_exp;   // [P][dst_exp_ld] exponents of the stored blocks
+  int* dst_exp;  // [P][dst_exp_ld] exponents of the stored blocks
   int dst_exp_ld;
-  float* out;     // kToOutput: per-slot rows out[(tok * k + slot) * ncols + col]
+  float* out;  // kToOutput: per-slot rows out[(tok * k + slot) * ncols + col]
   int wbd, n_expert_used;
 };
 
-// LDS: a ring of kStages raw K slices filled by direct global->LDS loads
-// (activations as fp16 16-byte chunks, NF4 codes, fp16 scales), and the
-// decoded factor slice, double-buffered, as fp16 [column][k].  Every ring
-// stage and decode buffer is its own __shared__ variable and is indexed at
-// compile time, so the compiler can tell which direct loads an LDS read
-// depends on (one shared object would make every LDS read wait for all of
-// them).
-constexpr int kStages = 4;
-constexpr int kMaxBlocks = 16;  // 128-column exponent blocks per operand row (K <= 2048)
-
-// Bank-conflict-free placements (checked for 32 and 64 banks of 4 bytes):
-//   activation chunk c (8 halfs) of row r  -> 16-byte slot r*4 + (c ^ a_swz(r))
-//   code chunk c (16 bytes) of factor row r -> 16-byte slot code_row(r)*4 + (c ^ code_swz(r))
+// LDS placements, free of bank conflicts for the access patterns below (64
+// lanes against 32 or 64 banks of 4 bytes):
+//   activation chunk c (8 halfs) of tile row r  -> 16-byte slot r*4 + (c ^ a_swz(r))
+//   decoded chunk c (8 k) of column n            -> 16-byte slot n*4 + (c ^ b_swz(n))
+//   NF4 code row r of a half                     -> 64-byte slot r ^ ((r >> 2) & 3),
+//     its 16-byte segment s                      -> position s ^ ((r >> 3) & 3)
 __device__ __forceinline__ int a_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
-__device__ __forceinline__ int code_row(int r) { return (r >> 1) + 16 * (r & 1); }
-__device__ __forceinline__ int code_swz(int r) { return (r >> 3) & 3; }
+__device__ __forceinline__ int b_swz(int n) { return ((n >> 1) ^ (n >> 2)) & 3; }
 
-struct Stage {
-  _Float16 a[kMT * kKS];       // activations [row][4 chunks of 8 halfs], swizzled
-  uint32_t bc[kKS * kNT / 8];  // NF4 codes [32 rows][4 chunks of 16 bytes], rows and chunks permuted
-  uint32_t bs[2 * 64];         // scales: [32 rows][4 fp16]; the second half takes a balancing load
+// One raw K slice: the activation slice, the codes of both decoded halves,
+// and their scales as [32 rows][4 groups] fp16; scale[2], scale[3] receive the
+// balancing loads that keep every wave's direct-load count per slice equal.
+struct alignas(16) Stage {
+  _Float16 a[kMT * kKS];
+  uint32_t code[2][kKS * kHalf / 8];
+  uint32_t scale[4][kKS * kHalf / kGroup / 2];
 };
 
-struct Decoded {
-  _Float16 b[kNT * kLds];      // decoded factor slice [column][k]
+struct alignas(16) Decoded {
+  _Float16 b[kNT * kKS];
 };
 
+template <bool kShift>
 struct Smem {
-  float lut[16];
-  int cexp[2][kMT];                  // per-row exponent of the operand rows (both products)
-  int8_t shift[2][kMT][kMaxBlocks];  // per-row, per-block exponent change to reach cexp
-  float rmax[2][kMT];                // row maxima of the two column halves of the output tile
+  _Float16 lut[16];
+  int cexp[kMT];                                     // row exponent of each operand row
+  int8_t shift[kShift ? kMT : 1][kMaxBlocks];        // per-block change to reach cexp
   int tok[kMT];
   int slot[kMT];
   float w[kMT];
+  int dro[kMT];  // (p0 + row) * ldd: output row offsets
+  int dxo[kMT];  // (p0 + row) * dst_exp_ld: exponent row offsets
 };
 
-struct Lds {
-  Smem& m;
-  Stage &s0, &s1, &s2, &s3;
-  Decoded &d0, &d1;
-  template <int I>
-  __device__ __forceinline__ Stage& stage() const {
-    if constexpr (I % kStages == 0) return s0;
-    else if constexpr (I % kStages == 1) return s1;
-    else if constexpr (I % kStages == 2) return s2;
-    else return s3;
-  }
-  template <int I>
-  __device__ __forceinline__ Decoded& dec() const {
-    if constexpr (I % 2 == 0) return d0;
-    else return d1;
-  }
-};
-
-// Exponent block of column `col` of an intermediate row.
-__device__ __forceinline__ int a_block(const Params& p, int col) {
-  return (col / p.a_part) * p.a_part_blocks + (col % p.a_part) / kNT;
+// Direct global -> LDS loads: lane l's 16 (4) bytes land at LDS byte address
+// lds + 16 l (4 l); lds is wave-uniform.  Inline assembly, so that the
+// compiler does not make every later LDS read wait for them (vmcnt(0)); the
+// pipeline waits for them itself (slice_barrier).  The scalar-base forms take
+// a 32-bit lane offset.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "m0");
 }
-
-// Direct global -> LDS loads: lane l's 16 (4) bytes land at lds + 16 l (4 l).
-// Written as inline assembly so the compiler does not treat every later LDS
-// read as dependent on them (it would wait for all of them, vmcnt(0)); the
-// pipeline waits for them itself (slice_barrier).  lds must be wave-uniform.
-__device__ __forceinline__ uint32_t lds_u32(void* lds) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)(lds))));
+// A wave-uniform 64-bit address in scalar registers (the scalar-base forms
+// need it there).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
-__device__ __forceinline__ void dma16(const void* src, void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_u32(lds))
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(uniform_ptr(base)),
+               "s"(lds)
                : "m0");
 }
-__device__ __forceinline__ void dma4(const void* src, void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds_u32(lds))
+__device__ __forceinline__ void dma4s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(uniform_ptr(base)),
+               "s"(lds)
                : "m0");
 }
 
-// Issue K slice sl into ring stage st: every wave issues exactly three direct
-// loads (two groups of activation rows, then codes or scales), so one vmcnt
-// value covers a whole slice.
-template <int kA>
-__device__ __forceinline__ void issue_slice(const Params& p, const Smem& m, Stage& st, const Factor& f, int64_t e,
-                                            int p0, int rows, int n0, int acol, int sl) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int k0 = sl * kKS;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = (2 * w + i) * 64 + lane;  // LDS chunk position
-    const int r = q >> 2, c = (q & 3) ^ a_swz(r);  // holds chunk c of row r
-    const int rr = r < rows ? r : 0;                     // pad rows re-read row 0 (finite; never stored)
-    const _Float16* src = kA == kFromX ? p.xh + static_cast<int64_t>(m.tok[rr]) * p.d + k0 + 8 * c
-                                       : p.a + static_cast<int64_t>(p0 + rr) * p.lda + acol + k0 + 8 * c;
-    dma16(src, &st.a[(2 * w + i) * 512]);
-  }
-  const int64_t cstride = f.cols / 2, sstride = f.cols / kGroup;
-  if (w < 2) {
-    const int pr = 16 * w + (lane >> 2);                 // LDS row position
-    const int row = 2 * (pr & 15) + (pr >> 4);           // factor row held there
-    const int col = n0 + 32 * ((lane & 3) ^ code_swz(row));
-    const int colc = col < p.ncols ? col : n0;  // chunks past the factor's columns re-read chunk 0 (decoded as zero)
-    dma16(f.codes + (e * f.rows + k0 + row) * cstride + colc / 2, &st.bc[w * 256]);
-  } else {
-    const int row = lane >> 1, g0 = n0 / kGroup + 2 * (lane & 1);
-    const int g = g0 * kGroup < p.ncols ? g0 : n0 / kGroup;
-    dma4(f.scales + (e * f.rows + k0 + row) * sstride + g, &st.bs[(w - 2) * 64]);
-  }
+// LDS access by byte address.
+template <typename T>
+__device__ __forceinline__ T lds_ld(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
 }
 
-// Workgroup barrier for the slice pipeline.  __syncthreads() would fence
-// every outstanding direct load (vmcnt(0)); instead each wave waits until at
-// most c slices (3 direct loads each) are in flight and its LDS writes are
-// done (s_waitcnt vmcnt(3c) lgkmcnt(0)), then meets the others at s_barrier.
-// The signal fences keep the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void slice_barrier(int c) {
+// LDS byte address of a __shared__ object.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T& obj) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)(&obj)));
+}
+
+// Workgroup barrier of the slice pipeline: each wave waits until at most n of
+// its direct loads are in flight and its LDS accesses are done (s_waitcnt
+// vmcnt(n) lgkmcnt(0)), then meets the others.  __syncthreads() would wait for
+// every direct load.  The signal fences keep the compiler from moving LDS
+// accesses across it.
+template <int kN>
+__device__ __forceinline__ void slice_barrier() {
+  static_assert(kN >= 0 && kN < 16, "vmcnt field");
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if (c >= 2)
-    __builtin_amdgcn_s_waitcnt(0x0070 | 6);
-  else if (c == 1)
-    __builtin_amdgcn_s_waitcnt(0x0070 | 3);
-  else
-    __builtin_amdgcn_s_waitcnt(0x0070);
+  __builtin_amdgcn_s_waitcnt(0x0070 | kN);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Barrier for LDS data only; direct loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Decode a ring stage into a decode buffer (thread: rows 2rp, 2rp+1; columns
-// 8cg .. 8cg+7) and, for intermediate operands, bring each activation chunk of
-// the stage to its row exponent (multiply by 2^shift, exact).
-template <int kA>
-__device__ __forceinline__ void prepare_slice(const Params& p, const Smem& m, Stage& st, Decoded& d, int n0, int acol,
-                                              int q, int sl) {
-  const int tid = threadIdx.x, rp = tid & 15, cg = tid >> 4;
-  {
-    const int r0 = 2 * rp, r1 = 2 * rp + 1;
-    const uint32_t c0 = st.bc[4 * (4 * code_row(r0) + ((cg >> 2) ^ code_swz(r0))) + (cg & 3)];
-    const uint32_t c1 = st.bc[4 * (4 * code_row(r1) + ((cg >> 2) ^ code_swz(r1))) + (cg & 3)];
-    const uint16_t* sh = reinterpret_cast<const uint16_t*>(st.bs);
-    const bool ok = n0 + 8 * cg < p.ncols;
-    const float s0 = ok ? half_bits_to_float(sh[(2 * rp) * 4 + (cg >> 2)]) : 0.f;
-    const float s1 = ok ? half_bits_to_float(sh[(2 * rp + 1) * 4 + (cg >> 2)]) : 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      half2v v;
-      v[0] = static_cast<_Float16>(m.lut[(c0 >> (4 * j)) & 15u] * s0);
-      v[1] = static_cast<_Float16>(m.lut[(c1 >> (4 * j)) & 15u] * s1);
-      *reinterpret_cast<half2v*>(&d.b[(8 * cg + j) * kLds + 2 * rp]) = v;
-    }
-  }
-  if constexpr (kA == kFromPairs) {
-    const int r = tid >> 1;
-    const int sft = m.shift[q][r][a_block(p, acol + sl * kKS) - a_block(p, acol)];
-    if (sft != 0) {
-      const _Float16 mul = sft < -24 ? static_cast<_Float16>(0.f) : static_cast<_Float16>(__builtin_ldexpf(1.f, sft));
-#pragma unroll
-      for (int c = 2 * (tid & 1); c < 2 * (tid & 1) + 2; ++c) {
-        half8* v = reinterpret_cast<half8*>(&st.a[(r * 4 + (c ^ a_swz(r))) * 8]);
-        *v = *v * mul;
-      }
-    }
-  }
+// SiLU with the hardware exp2 and reciprocal (relative error near 1e-7, far
+// below the fp16 storage of h); exp overflow gives g * 0 for very negative g.
+__device__ __forceinline__ float silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
 }
-
-__device__ __forceinline__ void mfma_slice(const Stage& st, const Decoded& d, f32x16 (&acc)[2][2]) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w & 1, wn = w >> 1;
-#pragma unroll
-  for (int ks = 0; ks < kKS; ks += 16) {
-    half8 af[2], bf[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = 64 * wm + 32 * i + (lane & 31), c = (ks >> 3) + (lane >> 5);
-      af[i] = *reinterpret_cast<const half8*>(&st.a[(r * 4 + (c ^ a_swz(r))) * 8]);
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      bf[j] = *reinterpret_cast<const half8*>(&d.b[(64 * wn + 32 * j + (lane & 31)) * kLds + ks + 8 * (lane >> 5)]);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-  }
-}
-
-// One pipeline step for slice sl = sl0 + I (stage I % kStages, decode buffer
-// I % 2): wait for slice sl + 1, refill the stage slice sl - 1 used, prepare
-// slice sl + 1, multiply slice sl.
-template <int kA, int I>
-__device__ __forceinline__ void k_step(const Params& p, const Lds& L, const Factor& f, int64_t e, int p0, int rows,
-                                       int n0, int acol, int q, int sl0, int n, f32x16 (&acc)[2][2]) {
-  const int sl = sl0 + I;
-  if (sl >= n) return;
-  // Slices issued so far: 0 .. min(n - 1, sl + kStages - 2); slice sl + 1 must have landed.
-  slice_barrier(sl + 1 < n ? min(n - 1, sl + kStages - 2) - (sl + 1) : 0);
-  if (sl + kStages - 1 < n)
-    issue_slice<kA>(p, L.m, L.template stage<I + kStages - 1>(), f, e, p0, rows, n0, acol, sl + kStages - 1);
-  if (sl + 1 < n)
-    prepare_slice<kA>(p, L.m, L.template stage<I + 1>(), L.template dec<I + 1>(), n0, acol, q, sl + 1);
-  mfma_slice(L.template stage<I>(), L.template dec<I>(), acc);
-}
-
-// acc[i][j] += A[rows 64*wm + 32*i ..][K] . B[K][cols 64*wn + 32*j ..] over the
-// whole K of the tile, for factor f (expert e) and activation column acol.
-template <int kA>
-__device__ __forceinline__ void run_k(const Params& p, const Lds& L, const Factor& f, int64_t e, int p0, int rows,
-                                      int n0, int acol, int q, f32x16 (&acc)[2][2]) {
-  const int n = p.K / kKS;  // >= 1
-  issue_slice<kA>(p, L.m, L.s0, f, e, p0, rows, n0, acol, 0);
-  if (n > 1) issue_slice<kA>(p, L.m, L.s1, f, e, p0, rows, n0, acol, 1);
-  if (n > 2) issue_slice<kA>(p, L.m, L.s2, f, e, p0, rows, n0, acol, 2);
-  slice_barrier(min(n - 1, kStages - 2));  // slice 0 landed
-  prepare_slice<kA>(p, L.m, L.s0, L.d0, n0, acol, q, 0);
-  for (int sl0 = 0; sl0 < n; sl0 += kStages) {
-    k_step<kA, 0>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
-    k_step<kA, 1>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
-    k_step<kA, 2>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
-    k_step<kA, 3>(p, L, f, e, p0, rows, n0, acol, q, sl0, n, acc);
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 // Exponent e with m * 2^e in [2^14, 2^15) (0 for m == 0 or not finite).
 __device__ __forceinline__ int block_exponent(float m) {
@@ -306,156 +197,371 @@ __device__ __forceinline__ int block_exponent(float m) {
   return min(kExpMax, max(kExpMin, 14 - ilog));
 }
 
+// Maximum over the 32 lanes that hold one row of an MFMA result (lanes l and
+// l ^ 32 hold different rows).
+__device__ __forceinline__ float max32(float m) {
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  return m;
+}
+
 template <int kA, int kEpi>
-__global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {  // two workgroups per CU
-  __shared__ Smem s;
-  __shared__ Stage st0, st1, st2, st3;
-  __shared__ Decoded dc0, dc1;
-  const Lds L{s, st0, st1, st2, st3, dc0, dc1};
-  // Work items (tile, product z, column tile) in expert order, cut into 8
+__global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
+  constexpr bool kShift = kA == kFromPairs;
+  constexpr int kDma = 4;  // direct loads per wave per slice
+  __shared__ Smem<kShift> s;
+  __shared__ Stage ring[kStages];
+  __shared__ Decoded dec[2];
+
+  // Work items (M tile, run of column tiles) in expert order, cut into 8
   // contiguous runs, one per XCD (workgroup b runs on XCD b % 8): a tile's
-  // column tiles share its activation rows, an expert's tiles share its factor
+  // column runs share its activation rows, an expert's tiles share its factor
   // slices, both in one L2.
-  const int nn = (p.ncols + kNT - 1) / kNT, per_tile = nn * p.zdim;
-  const int total = p.g.meta[2] * per_tile;
-  const int per_xcd = (total + 7) / 8;
-  const int j = blockIdx.x >> 3, item = (blockIdx.x & 7) * per_xcd + j;
-  if (j >= per_xcd || item >= total) return;
-  const int tile = item / per_tile, rem = item - tile * per_tile;
-  const int a = p.tile_a[tile], r0 = p.tile_r0[tile];
-  const int rows = min(kMT, p.g.act_count[a] - r0);
-  const int p0 = p.g.act_start[a] + r0;
-  const int64_t e = p.g.act_expert[a];
-  const int z = rem / nn;
-  const int n0 = (rem - z * nn) * kNT;
-  const int tid = threadIdx.x;
-  if (tid < 16) s.lut[tid] = nf4_level(tid);
+  const int nchunk = (p.nsub + p.spc - 1) / p.spc;
+  const int total_items = p.g.meta[2] * nchunk;
+  const int per_xcd = (total_items + 7) / 8;
+  const int jb = blockIdx.x >> 3, item = (blockIdx.x & 7) * per_xcd + jb;
+  if (jb >= per_xcd || item >= total_items) return;
+  const int tile = item / nchunk, chunk = item - tile * nchunk;
+  const int u0 = chunk * p.spc, nu = min(p.spc, p.nsub - u0);
+  const int ta = p.tile_a[tile], r0 = p.tile_r0[tile];
+  const int rows = min(kMT, p.g.act_count[ta] - r0);
+  const int p0 = p.g.act_start[ta] + r0;
+  const int64_t e = p.g.act_expert[ta];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w & 1, wn = w >> 1;
+
+  if (tid < 16) s.lut[tid] = static_cast<_Float16>(nf4_level(tid));
   if (tid < kMT) {
     const bool ok = tid < rows;
     s.tok[tid] = ok ? p.g.pair_tok[p0 + tid] : 0;
     s.slot[tid] = ok ? p.g.pair_slot[p0 + tid] : 0;
     s.w[tid] = ok ? p.g.pair_w[p0 + tid] : 0.f;
-  }
-  __syncthreads();
-  // Operand row exponents: x rows carry one; intermediate rows are rescaled to
-  // the smallest block exponent over the K range each product reads.
-  constexpr int kProducts = kEpi == kSwiGLU ? 2 : 1;
-  for (int i = tid; i < kProducts * kMT; i += kThreads) {
-    const int q = i / kMT, r = i % kMT;
+    s.dro[tid] = static_cast<int>((p0 + tid) * p.ldd);
+    s.dxo[tid] = (p0 + tid) * p.dst_exp_ld;
+    // Operand row exponents: x rows carry one; intermediate rows are rescaled
+    // to the smallest block exponent over the K range they are read in.
     int c = 0;
-    if (r < rows) {
-      if constexpr (kA == kFromX) {
-        c = p.a_exp[s.tok[r]];
-      } else {
-        const int acol = q ? p.a_col1 : p.a_col0;
-        const int b0 = a_block(p, acol), b1 = a_block(p, acol + p.K - 1);
-        const int* ex = p.a_exp + static_cast<int64_t>(p0 + r) * p.a_exp_ld;
+    if constexpr (kA == kFromX) {
+      if (ok) c = p.a_exp[s.tok[tid]];
+    } else {
+      const int nb = p.K / kBlk;
+      if (ok) {
+        const int* ex = p.a_exp + static_cast<int64_t>(p0 + tid) * p.a_exp_ld + p.a_col / kBlk;
         c = kExpMax;
-        for (int b = b0; b <= b1; ++b) c = min(c, ex[b]);
-        for (int b = b0; b <= b1; ++b) s.shift[q][r][b - b0] = static_cast<int8_t>(max(-128, c - ex[b]));
+        for (int b = 0; b < nb; ++b) c = min(c, ex[b]);
+        for (int b = 0; b < nb; ++b) s.shift[tid][b] = static_cast<int8_t>(max(-128, c - ex[b]));
+      } else {
+        for (int b = 0; b < nb; ++b) s.shift[tid][b] = 0;
       }
-    } else if constexpr (kA == kFromPairs) {
-      for (int b = 0; b < kMaxBlocks; ++b) s.shift[q][r][b] = 0;
     }
-    s.cexp[q][r] = c;
+    s.cexp[tid] = c;
   }
   __syncthreads();
 
-  f32x16 acc[2][2];
+  // ---- direct-load sources (per lane) ----
+  const int nk = p.K / kKS;   // K slices per column tile (a multiple of 4)
+  const int total = nu * nk;  // slices of this item
+  const char* asrc[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  run_k<kA>(p, L, z ? p.f1 : p.f0, e, p0, rows, n0, z ? p.a_col1 : p.a_col0, 0, acc);
-
-  const int lane = tid & 63, w = tid >> 6, wm = w & 1, wn = w >> 1;
-  if constexpr (kEpi == kSwiGLU) {
-    f32x16 acc_u[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc_u[i][j][r] = 0.f;
-    run_k<kA>(p, L, p.f1, e, p0, rows, n0, p.a_col1, 1, acc_u);
-    // h = SiLU(g) * u (* w), in place of g.
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          const float g = __builtin_ldexpf(acc[i][j][r], -s.cexp[0][row]);
-          const float u = __builtin_ldexpf(acc_u[i][j][r], -s.cexp[1][row]);
-          float h = silu_f32(g) * u;
-          if (p.wbd) h *= s.w[row];
-          acc[i][j][r] = h;
-        }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          acc[i][j][r] = __builtin_ldexpf(acc[i][j][r], -s.cexp[0][row]);
-        }
+  for (int i = 0; i < 2; ++i) {
+    const int qp = (2 * w + i) * 64 + lane;  // 16-byte slot
+    const int r = qp >> 2, c = (qp & 3) ^ a_swz(r);
+    const int rr = r < rows ? r : 0;  // pad rows re-read row 0 (finite; never stored)
+    asrc[i] = kA == kFromX
+                  ? reinterpret_cast<const char*>(p.xh + static_cast<int64_t>(s.tok[rr]) * p.d + 8 * c)
+                  : reinterpret_cast<const char*>(p.a + static_cast<int64_t>(p0 + rr) * p.lda + p.a_col + 8 * c);
   }
+  const int hw = w >> 1;  // the half whose codes and scales this wave loads and decodes
+  const uint32_t cstride = static_cast<uint32_t>(p.ncols / 2), sstride = static_cast<uint32_t>(p.ncols / kGroup) * 2;
+  uint32_t code_off, scale_off;
+  {
+    const int sg = (w & 1) * 64 + lane;  // 16-byte segment of the half slice
+    const int rs = sg >> 2, r = rs ^ ((rs >> 2) & 3), seg = (sg & 3) ^ ((r >> 3) & 3);
+    code_off = r * cstride + 16 * seg;
+    scale_off = (lane >> 1) * sstride + 4 * (lane & 1);
+  }
+  const int64_t cstep = static_cast<int64_t>(kKS) * cstride, sstep = static_cast<int64_t>(kKS) * sstride;
+  int iu = 0, ik = 0;  // next slice to issue: column tile (of the item), K slice
+  const char* cbase = nullptr;
+  const char* sbase = nullptr;
+  auto set_half_base = [&](int u) __attribute__((always_inline)) {
+    int v = (u0 + u) * kNT + hw * kHalf;
+    if (v >= p.nfac * p.ncols) v = (u0 + u) * kNT;  // empty half: reload the first (never stored)
+    const bool second = v >= p.ncols;
+    const Factor* f = second ? &p.f1 : &p.f0;
+    const int col = second ? v - p.ncols : v;
+    cbase = reinterpret_cast<const char*>(f->codes) + e * f->rows * cstride + col / 2;
+    sbase = reinterpret_cast<const char*>(f->scales) + e * f->rows * sstride + (col / kGroup) * 2;
+  };
+  set_half_base(0);
+  const uint32_t ring_lds = lds_addr(ring[0]);
+  auto issue = [&](int stg) __attribute__((always_inline)) {
+    if (ik == nk) {
+      ik = 0;
+      ++iu;
+      set_half_base(iu);
+    }
+    const uint32_t base = ring_lds + stg * static_cast<uint32_t>(sizeof(Stage));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      dma16(asrc[i] + ik * (kKS * 2), base + offsetof(Stage, a) + (2 * w + i) * 1024);
+    dma16s(cbase + ik * cstep, code_off, base + offsetof(Stage, code) + (hw * 512 + (w & 1) * 256) * 4);
+    dma4s(sbase + ik * sstep, scale_off, base + offsetof(Stage, scale) + (hw + 2 * (w & 1)) * 256);
+    ++ik;
+  };
 
-  if constexpr (kEpi == kToOutput) {
+  // ---- decode (per thread: K rows 4kq .. 4kq+3, factor columns 8cg .. 8cg+7) ----
+  // Decoded column n of a half holds factor column 4 (n % 32) + n / 32 of it,
+  // so that the 4 accumulators of a lane for one row are 4 adjacent output
+  // columns.  The thread mapping and the rotation rot of the write order keep
+  // the code reads and decoded writes free of bank conflicts.
+  const int kq = (tid & 1) | (((tid >> 5) & 1) << 1) | (((tid >> 1) & 1) << 2);
+  const int cg = ((tid >> 2) & 7) | ((tid >> 6) << 3), wd = cg & 15, seg = wd >> 2, rot = kq;
+  uint32_t code_word[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) code_word[i] = (4 * kq + (i ^ (kq & 3))) * 16 + 4 * (seg ^ ((kq >> 1) & 3)) + (wd & 3);
+  uint32_t woff[8];  // byte offset of factor column 8cg + ((j + rot) & 7), k 4kq .. 4kq+3
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int fc = 8 * wd + ((j + rot) & 7);                 // factor column in the half
+    const int n = kHalf * (cg >> 4) + 32 * (fc & 3) + (fc >> 2);  // its decoded column
+    woff[j] = n * 64 + 16 * ((kq >> 1) ^ b_swz(n)) + 8 * (kq & 1);
+  }
+  const char* lut = reinterpret_cast<const char*>(s.lut);
+  // Ring stages are addressed through a base taken with readfirstlane, opaque
+  // to the compiler: with a visible stage index it keeps a copy of every
+  // per-lane address for each of the kStages stages in registers.
+  uint32_t code_addr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) code_addr[i] = ring_lds + offsetof(Stage, code) + hw * 2048 + code_word[i] * 4;
+  const uint32_t scale_addr = ring_lds + offsetof(Stage, scale) + hw * 256 + ((4 * kq) * 4 + seg) * 2;
+  auto stage_off = [&](int stg) __attribute__((always_inline)) {
+    return __builtin_amdgcn_readfirstlane(stg * static_cast<uint32_t>(sizeof(Stage)));
+  };
+  auto prepare = [&](int stg, int db) __attribute__((always_inline)) {
+    const uint32_t so = stage_off(stg);
+    uint32_t c[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = lds_ld<uint32_t>(code_addr[i] + so);
+    half2v s01, s23;
+    s01[0] = lds_ld<_Float16>(scale_addr + so);
+    s01[1] = lds_ld<_Float16>(scale_addr + so + 8);
+    s23[0] = lds_ld<_Float16>(scale_addr + so + 16);
+    s23[1] = lds_ld<_Float16>(scale_addr + so + 24);
+    uint32_t ev[4], od[4];  // LUT byte offsets (2 * code) of the even / odd nibbles, one per byte
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = __builtin_amdgcn_alignbit(c[i], c[i], 4 * rot);  // nibble j <- column (j + rot) & 7
+      ev[i] = (r << 1) & 0x1E1E1E1Eu;
+      od[i] = (r >> 3) & 0x1E1E1E1Eu;
+    }
+    char* D = reinterpret_cast<char*>(dec[db].b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int sh = 8 * (j >> 1);
+      half2v v01, v23;
+      const uint32_t* src = (j & 1) ? od : ev;
+      v01[0] = *reinterpret_cast<const _Float16*>(lut + ((src[0] >> sh) & 0xFFu));
+      v01[1] = *reinterpret_cast<const _Float16*>(lut + ((src[1] >> sh) & 0xFFu));
+      v23[0] = *reinterpret_cast<const _Float16*>(lut + ((src[2] >> sh) & 0xFFu));
+      v23[1] = *reinterpret_cast<const _Float16*>(lut + ((src[3] >> sh) & 0xFFu));
+      v01 *= s01;
+      v23 *= s23;
+      uint2 o;
+      o.x = __builtin_bit_cast(uint32_t, v01);
+      o.y = __builtin_bit_cast(uint32_t, v23);
+      *reinterpret_cast<uint2*>(D + woff[j]) = o;
+    }
+  };
+
+  // ---- multiply ----
+  f32x16 acc[2][4];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = n0 + 64 * wn + 32 * j + (lane & 31);
-        if (col >= p.ncols) continue;
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (row >= rows) continue;
-          p.out[(static_cast<int64_t>(s.tok[row]) * p.n_expert_used + s.slot[row]) * p.ncols + col] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  };
+  zero_acc();
+  half2v amul[2];  // 2^shift of the lane's A rows for the current exponent block
+#pragma unroll
+  for (int i = 0; i < 2; ++i) amul[i] = half2v{1.f, 1.f};
+  uint32_t a_addr[2][2];  // [ks / 16][i]
+#pragma unroll
+  for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = 64 * wm + 32 * i + (lane & 31), c = 2 * k2 + (lane >> 5);
+      a_addr[k2][i] = ring_lds + offsetof(Stage, a) + (r * 4 + (c ^ a_swz(r))) * 16;
+    }
+  auto mfma = [&](int stg, int db) __attribute__((always_inline)) {
+    const uint32_t so = stage_off(stg);
+#pragma unroll
+    for (int ks = 0; ks < kKS; ks += 16) {
+      const int c = (ks >> 3) + (lane >> 5);
+      half8 af[2], bf[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = lds_ld<half8>(a_addr[ks >> 4][i] + so);
+        if constexpr (kShift) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            half2v v{af[i][2 * t], af[i][2 * t + 1]};
+            v *= amul[i];
+            af[i][2 * t] = v[0];
+            af[i][2 * t + 1] = v[1];
+          }
         }
       }
-    return;
-  }
-
-  // fp16 store with a per-(row, 128-column block) exponent.  Row maxima: over
-  // the lane's two column blocks, the 32 lanes of a row, then the two waves
-  // that share the rows.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 4; ++j) {
+        const int n = kHalf * wn + 32 * j + (lane & 31);
+        bf[j] = *reinterpret_cast<const half8*>(&dec[db].b[(n * 4 + (c ^ b_swz(n))) * 8]);
+      }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float m = 0.f;
+      for (int i = 0; i < 2; ++i) {
+        if (64 * wm + 32 * i >= rows) continue;  // all-padding row block
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (n0 + 64 * wn + 32 * j + (lane & 31) < p.ncols) m = fmaxf(m, fabsf(acc[i][j][r]));
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-      if ((lane & 31) == 0) s.rmax[wn][64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = m;
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
     }
-  __syncthreads();
-  const int blk = z * nn + n0 / kNT;
-  if (tid < rows) p.dst_exp[static_cast<int64_t>(p0 + tid) * p.dst_exp_ld + blk] = block_exponent(fmaxf(s.rmax[0][tid], s.rmax[1][tid]));
+  };
+
+  // ---- epilogue of column tile ut: this wave's 64 rows x 128 columns ----
+  auto epilogue = [&](int ut) __attribute__((always_inline)) {
+    const int vcol = ut * kNT + wn * kHalf;  // first output column of this wave
+    if (vcol >= p.nfac * p.ncols) return;    // empty half
+    // The lane index, opaque to the compiler, so that the epilogue's row
+    // addresses are formed here instead of being hoisted out of the K loop
+    // into registers the loop needs.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    auto row_of = [&](int i, int r) __attribute__((always_inline)) {
+      return 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (ln >> 5) + (r & 3);
+    };
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + 64 * wn + 32 * j + (lane & 31);
-      if (col >= p.ncols) continue;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = 64 * wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int ce = s.cexp[row_of(i, r)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j][r] = __builtin_ldexpf(acc[i][j][r], -ce);
+      }
+    if constexpr (kEpi == kToOutput) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row_of(i, r);
+          if (row >= rows) continue;
+          float* o = p.out + (static_cast<int64_t>(s.tok[row]) * p.n_expert_used + s.slot[row]) * p.ncols + vcol +
+                     4 * (ln & 31);
+          *reinterpret_cast<float4*>(o) = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+        }
+      return;
+    }
+    const int blk = vcol / kBlk;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (kEpi == kStoreSiLU) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j][r] = silu_f32(acc[i][j][r]);
+      }
+      if constexpr (kEpi == kSwiGLU) {
+        // dst holds SiLU(g) * 2^sexp in fp16.  Loads of 8 rows first (pad rows read row 0).
+#pragma unroll
+        for (int r0 = 0; r0 < 16; r0 += 8) {
+          uint2 gw[8];
+          int gx[8];
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const int row = row_of(i, r0 + r), rr = row < rows ? row : 0;
+            gw[r] = *reinterpret_cast<const uint2*>(p.dst + s.dro[rr] + vcol + 4 * (ln & 31));
+            gx[r] = p.dst_exp[s.dxo[rr] + blk];
+          }
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            const float wr = __builtin_ldexpf(p.wbd ? s.w[row_of(i, r0 + r)] : 1.f, -gx[r]);
+            const uint32_t q[4] = {gw[r].x & 0xFFFFu, gw[r].x >> 16, gw[r].y & 0xFFFFu, gw[r].y >> 16};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[i][j][r0 + r] *= half_bits_to_float(static_cast<uint16_t>(q[j])) * wr;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float m = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, fabsf(acc[i][j][r]));
+        m = max32(m);
+        const int row = row_of(i, r);
         if (row >= rows) continue;
-        const int ex = block_exponent(fmaxf(s.rmax[0][row], s.rmax[1][row]));
-        p.dst[static_cast<int64_t>(p0 + row) * p.ldd + (z ? p.dst_col1 : 0) + col] =
-            static_cast<_Float16>(__builtin_ldexpf(acc[i][j][r], ex));
+        const int ex = block_exponent(m);
+        half2v h01, h23;
+        h01[0] = static_cast<_Float16>(__builtin_ldexpf(acc[i][0][r], ex));
+        h01[1] = static_cast<_Float16>(__builtin_ldexpf(acc[i][1][r], ex));
+        h23[0] = static_cast<_Float16>(__builtin_ldexpf(acc[i][2][r], ex));
+        h23[1] = static_cast<_Float16>(__builtin_ldexpf(acc[i][3][r], ex));
+        *reinterpret_cast<uint2*>(p.dst + s.dro[row] + vcol + 4 * (ln & 31)) =
+            make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+        if ((ln & 31) == 0) p.dst_exp[s.dxo[row] + blk] = ex;
       }
     }
+  };
+
+  // ---- pipeline ----
+  // Step s: wait until slice s + 1 has landed (and every wave is done with
+  // step s - 1), refill the stage slice s - 1 used with slice s + kAhead,
+  // decode slice s + 1 into the free decode buffer, multiply slice s.
+  constexpr int kAhead = kStages - 1;  // slices issued ahead of the one multiplied
+  static_assert((kAhead - 2) * kDma < 16, "vmcnt field");
+#pragma unroll
+  for (int i = 0; i < kAhead; ++i)
+    if (i < total) issue(i);
+  if (total >= kAhead)
+    slice_barrier<(kAhead - 1) * kDma>();  // slice 0 landed
+  else
+    slice_barrier<0>();
+  prepare(0, 0);
+  int kk0 = 0;  // K slice of the group's first step
+  for (int s0 = 0; s0 < total; s0 += 4) {
+    if constexpr (kShift) {
+      // One exponent block per 4 slices (kBlk = 4 * kKS; operand columns start on a block).
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int sft = s.shift[64 * wm + 32 * i + (lane & 31)][kk0 >> 2];
+        const _Float16 m = sft < -24 ? static_cast<_Float16>(0.f) : static_cast<_Float16>(__builtin_ldexpf(1.f, sft));
+        amul[i] = half2v{m, m};
+      }
+    }
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      const int sl = s0 + I;
+      // Issued so far: slices 0 .. min(total - 1, sl + kAhead - 1); slice sl + 1 must land.
+      if (sl + kAhead - 1 < total)
+        slice_barrier<(kAhead - 2) * kDma>();
+      else
+        slice_barrier<0>();
+      if (sl + kAhead < total) issue((sl + kAhead) % kStages);
+      if (sl + 1 < total) prepare((sl + 1) % kStages, (I + 1) & 1);
+      mfma(sl % kStages, I & 1);
+    }
+    kk0 += 4;
+    if (kk0 == nk) {
+      epilogue(u0 + s0 / nk);
+      zero_acc();
+      kk0 = 0;
+    }
+  }
 }
 
 // x rows to fp16: xh[t] = fp16(x[t] * 2^e[t]) with 2^e * max|x[t]| in [2^14, 2^15).
@@ -533,7 +639,7 @@ __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, co
       const int pos = pos_of[t * k + sl];
       if (pos < 0) continue;
       const half8 h = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
-      const float w = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kNT]);
+      const float w = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kBlk]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, static_cast<float>(h[i]), acc[i]);
     }
@@ -571,6 +677,7 @@ __global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int* ti
   if (tid == kTileThreads - 1) g.meta[2] = scan[tid];
 }
 
+
 size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
 
 int64_t max_tiles(const latent_moe_args& a) {
@@ -578,10 +685,15 @@ int64_t max_tiles(const latent_moe_args& a) {
   return (P + kMT - 1) / kMT + std::min<int64_t>(a.n_expert, P);
 }
 
+// Column tiles per work item: about 32 K slices of work per item, so short-K
+// GEMMs keep the load ring running across several column tiles.
+int tiles_per_item(int K, int nsub) { return std::max(1, std::min(nsub, (32 * kKS) / K)); }
+
 template <int kA, int kEpi>
-int launch(Params p, int64_t tiles, int ncols, int zdim, hipStream_t s) {
-  p.zdim = zdim;
-  const int64_t items = tiles * ((ncols + kNT - 1) / kNT) * zdim;
+int launch(Params p, int64_t tiles, hipStream_t s) {
+  p.nsub = (p.nfac * p.ncols + kNT - 1) / kNT;
+  p.spc = tiles_per_item(p.K, p.nsub);
+  const int64_t items = tiles * ((p.nsub + p.spc - 1) / p.spc);
   const dim3 grid(static_cast<unsigned>(8 * ((items + 7) / 8)));
   hipLaunchKernelGGL((gemm_kernel<kA, kEpi>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
@@ -597,10 +709,11 @@ bool supported(const latent_moe_args& a) {
   for (const latent_factor* f : fs)
     if (f->int8_bitmap != nullptr) return false;  // per-group INT8 layers take the general path
   if ((reinterpret_cast<uintptr_t>(a.x) & 15u) != 0) return false;
-  // Direct 16-byte code loads and 4-byte scale-pair loads: 64-column multiples
-  // and aligned factor arrays; at most kMaxBlocks exponent blocks per row.
-  if (a.n_embd % 64 || a.n_ff % 64 || a.max_rank % 64) return false;
-  if (a.n_ff > kMaxBlocks * kNT || a.max_rank > kMaxBlocks * kNT) return false;
+  // Whole 128-column halves and exponent blocks, whole 4-slice groups of K;
+  // at most kMaxBlocks exponent blocks in a K range; 16-byte code rows and
+  // 4-byte scale pairs for the direct loads.
+  if (a.n_embd % kBlk || a.n_ff % kBlk || a.max_rank % kBlk) return false;
+  if (a.n_ff > kMaxBlocks * kBlk || a.max_rank > kMaxBlocks * kBlk) return false;
   for (const latent_factor* f : fs)
     if ((reinterpret_cast<uintptr_t>(f->codes) & 15u) || (reinterpret_cast<uintptr_t>(f->scales) & 3u)) return false;
   return true;
@@ -612,7 +725,7 @@ Layout layout_for(const latent_moe_args& a) {
   size_t off = 0;
   L.tile_a = off;  off = align_up(off + T * sizeof(int));
   L.tile_r0 = off; off = align_up(off + T * sizeof(int));
-  const int64_t rb = (R + kNT - 1) / kNT, fb = (a.n_ff + kNT - 1) / kNT;
+  const int64_t rb = R / kBlk, fb = a.n_ff / kBlk, db = a.n_embd / kBlk;
   L.xexp = off;    off = align_up(off + a.n_tokens * sizeof(int));
   L.xh = off;      off = align_up(off + a.n_tokens * a.n_embd * sizeof(_Float16));
   L.gu = off;      off = align_up(off + P * 2 * R * sizeof(_Float16));
@@ -621,7 +734,6 @@ Layout layout_for(const latent_moe_args& a) {
   L.h_exp = off;   off = align_up(off + P * fb * sizeof(int));
   L.dl = off;      off = align_up(off + P * R * sizeof(_Float16));
   L.dl_exp = off;  off = align_up(off + P * rb * sizeof(int));
-  const int64_t db = (a.n_embd + kNT - 1) / kNT;
   L.pos_of = off;  off = align_up(off + P * sizeof(int));
   L.y = off;       off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * a.n_embd * sizeof(_Float16) : 0));
   L.y_exp = off;   off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * db * sizeof(int) : 0));
@@ -648,7 +760,7 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   const int K = static_cast<int>(a.n_expert_used);
   const int P = static_cast<int>(a.n_tokens * a.n_expert_used);
   const int R = static_cast<int>(a.max_rank), d = static_cast<int>(a.n_embd), ff = static_cast<int>(a.n_ff);
-  const int rb = (R + kNT - 1) / kNT, fb = (ff + kNT - 1) / kNT;
+  const int rb = R / kBlk, fb = ff / kBlk, db = d / kBlk;
   hipLaunchKernelGGL(x_prep_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype, d,
                      xh, xexp, pos_of, K);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
@@ -674,69 +786,64 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   p.f0 = fac[0];
   p.f1 = fac[2];
   p.ncols = R;
+  p.nfac = 2;
   p.dst = gu;
   p.ldd = 2 * R;
-  p.dst_col1 = R;
   p.dst_exp = gu_exp;
   p.dst_exp_ld = 2 * rb;
-  int st = launch<kFromX, kStoreHalf>(p, tiles, R, 2, s);
+  int st = launch<kFromX, kStoreHalf>(p, tiles, s);
   if (st != LATENT_OK) return st;
-  // BC1: h = SiLU(g . B_g) * (u . B_u)
+  // BC1: h = SiLU(g . B_g) * (u . B_u): the gate product into h, then the up
+  // product, whose epilogue reads it back.
   p.K = R;
   p.a = gu;
   p.lda = 2 * R;
-  p.a_col0 = 0;
-  p.a_col1 = R;
+  p.a_col = 0;
   p.a_exp = gu_exp;
   p.a_exp_ld = 2 * rb;
-  p.a_part = R;
-  p.a_part_blocks = rb;
-  p.f0 = fac[1];
-  p.f1 = fac[3];
+  p.f0 = p.f1 = fac[1];
   p.ncols = ff;
+  p.nfac = 1;
   p.dst = h;
   p.ldd = ff;
-  p.dst_col1 = 0;
   p.dst_exp = h_exp;
   p.dst_exp_ld = fb;
-  st = launch<kFromPairs, kSwiGLU>(p, tiles, ff, 1, s);
+  st = launch<kFromPairs, kStoreSiLU>(p, tiles, s);
+  if (st != LATENT_OK) return st;
+  p.a_col = R;
+  p.f0 = p.f1 = fac[3];
+  st = launch<kFromPairs, kSwiGLU>(p, tiles, s);
   if (st != LATENT_OK) return st;
   // BC2: dl = h . A_d
   p.K = ff;
   p.a = h;
   p.lda = ff;
-  p.a_col0 = p.a_col1 = 0;
+  p.a_col = 0;
   p.a_exp = h_exp;
   p.a_exp_ld = fb;
-  p.a_part = ff;
-  p.a_part_blocks = fb;
   p.f0 = p.f1 = fac[4];
   p.ncols = R;
   p.dst = dl;
   p.ldd = R;
   p.dst_exp = dl_exp;
   p.dst_exp_ld = rb;
-  st = launch<kFromPairs, kStoreHalf>(p, tiles, R, 1, s);
+  st = launch<kFromPairs, kStoreHalf>(p, tiles, s);
   if (st != LATENT_OK) return st;
-  // D: out += w * (dl . B_d)
+  // D: y = dl . B_d
   p.K = R;
   p.a = dl;
   p.lda = R;
   p.a_exp = dl_exp;
   p.a_exp_ld = rb;
-  p.a_part = R;
-  p.a_part_blocks = rb;
   p.f0 = p.f1 = fac[5];
   p.ncols = d;
-  if (a.out_mode == LATENT_OUT_PER_SLOT) return launch<kFromPairs, kToOutput>(p, tiles, d, 1, s);
+  if (a.out_mode == LATENT_OUT_PER_SLOT) return launch<kFromPairs, kToOutput>(p, tiles, s);
   // Reduced: y rows in fp16, then the per-token weighted sum.
-  const int db = (d + kNT - 1) / kNT;
   p.dst = y;
   p.ldd = d;
-  p.dst_col1 = 0;
   p.dst_exp = y_exp;
   p.dst_exp_ld = db;
-  st = launch<kFromPairs, kStoreHalf>(p, tiles, d, 1, s);
+  st = launch<kFromPairs, kStoreHalf>(p, tiles, s);
   if (st != LATENT_OK) return st;
   hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, y, y_exp, db, pos_of,
                      g.pair_w, K, d, p.wbd, static_cast<float*>(a.out));
