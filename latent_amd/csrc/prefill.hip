@@ -114,7 +114,7 @@ struct alignas(16) Decoded {
 
 template <bool kShift>
 struct Smem {
-  _Float16 lut[16];
+  uint32_t lut2[256];  // entry a | b << 4: half2(level a, level b) (two K rows of one column)
   int cexp[kMT];                                     // row exponent of each operand row
   int8_t shift[kShift ? kMT : 1][kMaxBlocks];        // per-block change to reach cexp
   int tok[kMT];
@@ -233,7 +233,13 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w & 1, wn = w >> 1;
 
-  if (tid < 16) s.lut[tid] = static_cast<_Float16>(nf4_level(tid));
+  {
+    half2v v;
+    v[0] = static_cast<_Float16>(nf4_level(tid & 15));
+    v[1] = static_cast<_Float16>(nf4_level(tid >> 4));
+    s.lut2[tid] = __builtin_bit_cast(uint32_t, v);
+  }
+  static_assert(kThreads == 256, "one level-pair entry per thread");
   if (tid < kMT) {
     const bool ok = tid < rows;
     s.tok[tid] = ok ? p.g.pair_tok[p0 + tid] : 0;
@@ -284,33 +290,39 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
     scale_off = (lane >> 1) * sstride + 4 * (lane & 1);
   }
   const int64_t cstep = static_cast<int64_t>(kKS) * cstride, sstep = static_cast<int64_t>(kKS) * sstride;
-  int iu = 0, ik = 0;  // next slice to issue: column tile (of the item), K slice
-  const char* cbase = nullptr;
-  const char* sbase = nullptr;
-  auto set_half_base = [&](int u) __attribute__((always_inline)) {
-    int v = (u0 + u) * kNT + hw * kHalf;
-    if (v >= p.nfac * p.ncols) v = (u0 + u) * kNT;  // empty half: reload the first (never stored)
+  // Source of this wave's half of the item's first slice.  Column tiles of an
+  // item are adjacent tiles of one factor (the host sets one tile per item
+  // when the output columns span two factors or end in a half tile), so the
+  // next tile starts kNT / 2 code bytes to the right.
+  const char* cptr;
+  const char* sptr;
+  {
+    int v = u0 * kNT + hw * kHalf;
+    v = v >= p.nfac * p.ncols ? u0 * kNT : v;  // empty half: load the first (never stored)
     const bool second = v >= p.ncols;
-    const Factor* f = second ? &p.f1 : &p.f0;
+    const Factor& f = second ? p.f1 : p.f0;
     const int col = second ? v - p.ncols : v;
-    cbase = reinterpret_cast<const char*>(f->codes) + e * f->rows * cstride + col / 2;
-    sbase = reinterpret_cast<const char*>(f->scales) + e * f->rows * sstride + (col / kGroup) * 2;
-  };
-  set_half_base(0);
+    cptr = reinterpret_cast<const char*>(f.codes) + e * f.rows * cstride + col / 2;
+    sptr = reinterpret_cast<const char*>(f.scales) + e * f.rows * sstride + (col / kGroup) * 2;
+  }
+  const int64_t cwrap = kNT / 2 - (nk - 1) * cstep, swrap = (kNT / kGroup) * 2 - (nk - 1) * sstep;
+  int ik = 0, aoff = 0, left = total;  // K slice of the next issue, its activation byte offset, slices to issue
   const uint32_t ring_lds = lds_addr(ring[0]);
+  // Every step issues exactly one slice (uniform vmcnt bookkeeping, no
+  // branches in the step): past the item's last slice, that slice is loaded
+  // again into the free stage and never used.  Scalar selects only.
   auto issue = [&](int stg) __attribute__((always_inline)) {
-    if (ik == nk) {
-      ik = 0;
-      ++iu;
-      set_half_base(iu);
-    }
     const uint32_t base = ring_lds + stg * static_cast<uint32_t>(sizeof(Stage));
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(asrc[i] + ik * (kKS * 2), base + offsetof(Stage, a) + (2 * w + i) * 1024);
-    dma16s(cbase + ik * cstep, code_off, base + offsetof(Stage, code) + (hw * 512 + (w & 1) * 256) * 4);
-    dma4s(sbase + ik * sstep, scale_off, base + offsetof(Stage, scale) + (hw + 2 * (w & 1)) * 256);
-    ++ik;
+    for (int i = 0; i < 2; ++i) dma16(asrc[i] + aoff, base + offsetof(Stage, a) + (2 * w + i) * 1024);
+    dma16s(cptr, code_off, base + offsetof(Stage, code) + (hw * 512 + (w & 1) * 256) * 4);
+    dma4s(sptr, scale_off, base + offsetof(Stage, scale) + (hw + 2 * (w & 1)) * 256);
+    const bool adv = --left > 0;
+    const bool wrap = ++ik == nk;
+    ik = wrap ? 0 : ik;
+    cptr += adv ? (wrap ? cwrap : cstep) : 0;
+    sptr += adv ? (wrap ? swrap : sstep) : 0;
+    aoff = adv ? (wrap ? 0 : aoff + kKS * 2) : aoff;
   };
 
   // ---- decode (per thread: K rows 4kq .. 4kq+3, factor columns 8cg .. 8cg+7) ----
@@ -330,7 +342,6 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
     const int n = kHalf * (cg >> 4) + 32 * (fc & 3) + (fc >> 2);  // its decoded column
     woff[j] = n * 64 + 16 * ((kq >> 1) ^ b_swz(n)) + 8 * (kq & 1);
   }
-  const char* lut = reinterpret_cast<const char*>(s.lut);
   // Ring stages are addressed through a base taken with readfirstlane, opaque
   // to the compiler: with a visible stage index it keeps a copy of every
   // per-lane address for each of the kStages stages in registers.
@@ -351,23 +362,24 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
     s01[1] = lds_ld<_Float16>(scale_addr + so + 8);
     s23[0] = lds_ld<_Float16>(scale_addr + so + 16);
     s23[1] = lds_ld<_Float16>(scale_addr + so + 24);
-    uint32_t ev[4], od[4];  // LUT byte offsets (2 * code) of the even / odd nibbles, one per byte
+    // Code pairs of K rows (4kq, 4kq+1) and (4kq+2, 4kq+3): per byte, the
+    // nibble of the first row | the nibble of the second row << 4, the index
+    // of the level pair; even columns in ev, odd columns in od.
+    uint32_t ev[2], od[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t r = __builtin_amdgcn_alignbit(c[i], c[i], 4 * rot);  // nibble j <- column (j + rot) & 7
-      ev[i] = (r << 1) & 0x1E1E1E1Eu;
-      od[i] = (r >> 3) & 0x1E1E1E1Eu;
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t a = __builtin_amdgcn_alignbit(c[2 * q], c[2 * q], 4 * rot);  // nibble j <- column (j + rot) & 7
+      const uint32_t b = __builtin_amdgcn_alignbit(c[2 * q + 1], c[2 * q + 1], 4 * rot);
+      ev[q] = (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
+      od[q] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
     }
     char* D = reinterpret_cast<char*>(dec[db].b);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int sh = 8 * (j >> 1);
-      half2v v01, v23;
       const uint32_t* src = (j & 1) ? od : ev;
-      v01[0] = *reinterpret_cast<const _Float16*>(lut + ((src[0] >> sh) & 0xFFu));
-      v01[1] = *reinterpret_cast<const _Float16*>(lut + ((src[1] >> sh) & 0xFFu));
-      v23[0] = *reinterpret_cast<const _Float16*>(lut + ((src[2] >> sh) & 0xFFu));
-      v23[1] = *reinterpret_cast<const _Float16*>(lut + ((src[3] >> sh) & 0xFFu));
+      half2v v01 = __builtin_bit_cast(half2v, s.lut2[(src[0] >> sh) & 0xFFu]);
+      half2v v23 = __builtin_bit_cast(half2v, s.lut2[(src[1] >> sh) & 0xFFu]);
       v01 *= s01;
       v23 *= s23;
       uint2 o;
@@ -399,38 +411,42 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
       const int r = 64 * wm + 32 * i + (lane & 31), c = 2 * k2 + (lane >> 5);
       a_addr[k2][i] = ring_lds + offsetof(Stage, a) + (r * 4 + (c ^ a_swz(r))) * 16;
     }
-  auto mfma = [&](int stg, int db) __attribute__((always_inline)) {
+  // Fragments of one slice: A rows (2 row blocks) and decoded B columns (4
+  // column blocks) for both 16-deep K steps.
+  half8 af[2][2], bf[2][4];
+  auto load_frags = [&](int stg, int db) __attribute__((always_inline)) {
     const uint32_t so = stage_off(stg);
 #pragma unroll
-    for (int ks = 0; ks < kKS; ks += 16) {
-      const int c = (ks >> 3) + (lane >> 5);
-      half8 af[2], bf[4];
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int c = 2 * k2 + (lane >> 5);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        af[i] = lds_ld<half8>(a_addr[ks >> 4][i] + so);
+        af[k2][i] = lds_ld<half8>(a_addr[k2][i] + so);
         if constexpr (kShift) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            half2v v{af[i][2 * t], af[i][2 * t + 1]};
+            half2v v{af[k2][i][2 * t], af[k2][i][2 * t + 1]};
             v *= amul[i];
-            af[i][2 * t] = v[0];
-            af[i][2 * t + 1] = v[1];
+            af[k2][i][2 * t] = v[0];
+            af[k2][i][2 * t + 1] = v[1];
           }
         }
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int n = kHalf * wn + 32 * j + (lane & 31);
-        bf[j] = *reinterpret_cast<const half8*>(&dec[db].b[(n * 4 + (c ^ b_swz(n))) * 8]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        if (64 * wm + 32 * i >= rows) continue;  // all-padding row block
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        bf[k2][j] = *reinterpret_cast<const half8*>(&dec[db].b[(n * 4 + (c ^ b_swz(n))) * 8]);
       }
     }
+  };
+  auto run_mfma = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[k2][i], bf[k2][j], acc[i][j], 0, 0, 0);
   };
 
   // ---- epilogue of column tile ut: this wave's 64 rows x 128 columns ----
@@ -521,17 +537,15 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
   // ---- pipeline ----
   // Step s: wait until slice s + 1 has landed (and every wave is done with
   // step s - 1), refill the stage slice s - 1 used with slice s + kAhead,
-  // decode slice s + 1 into the free decode buffer, multiply slice s.
+  // multiply slice s while decoding slice s + 1 into the free decode buffer.
   constexpr int kAhead = kStages - 1;  // slices issued ahead of the one multiplied
   static_assert((kAhead - 2) * kDma < 16, "vmcnt field");
 #pragma unroll
-  for (int i = 0; i < kAhead; ++i)
-    if (i < total) issue(i);
-  if (total >= kAhead)
-    slice_barrier<(kAhead - 1) * kDma>();  // slice 0 landed
-  else
-    slice_barrier<0>();
+  for (int i = 0; i < kAhead; ++i) issue(i);
+  slice_barrier<(kAhead - 1) * kDma>();  // slice 0 landed
   prepare(0, 0);
+  auto next_stage = [](int x) __attribute__((always_inline)) { return x + 1 == kStages ? 0 : x + 1; };
+  int st_mul = 0, st_prep = 1 % kStages, st_issue = kAhead % kStages;  // ring stages of slices sl, sl + 1, sl + kAhead
   int kk0 = 0;  // K slice of the group's first step
   for (int s0 = 0; s0 < total; s0 += 4) {
     if constexpr (kShift) {
@@ -545,15 +559,23 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
     }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      const int sl = s0 + I;
-      // Issued so far: slices 0 .. min(total - 1, sl + kAhead - 1); slice sl + 1 must land.
-      if (sl + kAhead - 1 < total)
-        slice_barrier<(kAhead - 2) * kDma>();
-      else
-        slice_barrier<0>();
-      if (sl + kAhead < total) issue((sl + kAhead) % kStages);
-      if (sl + 1 < total) prepare((sl + 1) % kStages, (I + 1) & 1);
-      mfma(sl % kStages, I & 1);
+      // Issued so far: slices 0 .. sl + kAhead - 1 (sl = s0 + I); slice sl + 1 must land.
+      slice_barrier<(kAhead - 2) * kDma>();
+      issue(st_issue);
+      load_frags(st_mul, I & 1);
+      run_mfma();
+      prepare(st_prep, (I + 1) & 1);  // past the last slice: decodes a stage never used
+      st_mul = next_stage(st_mul);
+      st_prep = next_stage(st_prep);
+      st_issue = next_stage(st_issue);
+      // Interleave the decode of slice sl + 1 with the 16 MFMAs of slice sl.
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+      }
     }
     kk0 += 4;
     if (kk0 == nk) {
@@ -562,6 +584,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
       kk0 = 0;
     }
   }
+  // Past-the-end loads must land before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0070);
 }
 
 // x rows to fp16: xh[t] = fp16(x[t] * 2^e[t]) with 2^e * max|x[t]| in [2^14, 2^15).
@@ -687,12 +711,13 @@ int64_t max_tiles(const latent_moe_args& a) {
 
 // Column tiles per work item: about 32 K slices of work per item, so short-K
 // GEMMs keep the load ring running across several column tiles.
-int tiles_per_item(int K, int nsub) { return std::max(1, std::min(nsub, (32 * kKS) / K)); }
+int tiles_per_item(int K, int nsub) { return std::max(1, std::min({nsub, 4, (32 * kKS) / K})); }
 
 template <int kA, int kEpi>
 int launch(Params p, int64_t tiles, hipStream_t s) {
   p.nsub = (p.nfac * p.ncols + kNT - 1) / kNT;
-  p.spc = tiles_per_item(p.K, p.nsub);
+  // Several tiles per item only within one factor and whole tiles.
+  p.spc = (p.nfac == 1 && p.ncols % kNT == 0) ? tiles_per_item(p.K, p.nsub) : 1;
   const int64_t items = tiles * ((p.nsub + p.spc - 1) / p.spc);
   const dim3 grid(static_cast<unsigned>(8 * ((items + 7) / 8)));
   hipLaunchKernelGGL((gemm_kernel<kA, kEpi>), grid, dim3(kThreads), 0, s, p);
