@@ -166,6 +166,103 @@ __device__ void route_block(const MoeParams& p) {
   }
 }
 
+// Multi-workgroup grouping for large batches (the single-workgroup route_block
+// serializes on its LDS counters): per-chunk histograms, one scan over
+// (expert, chunk), then a scatter.  hist is [E + 1][nchunk] (the last row
+// counts invalid ids); the scan turns it into each chunk's insert positions.
+// Pairs of one expert land in an order that can vary from call to call; every
+// consumer of the grouping computes each pair independently of the others in
+// its expert, so results do not depend on it.
+constexpr int kHistInts = 16384;  // (E + 1) * nchunk bound: the scan holds the histograms in LDS
+
+__global__ void __launch_bounds__(kRouteThreads) group_count_kernel(MoeParams p, int* hist, int chunk) {
+  __shared__ int cnt[kMaxExperts + 1];
+  const int tid = threadIdx.x, E = p.E, P = p.T * p.K;
+  for (int e = tid; e <= E; e += kRouteThreads) cnt[e] = 0;
+  __syncthreads();
+  const int i0 = blockIdx.x * chunk, i1 = min(P, i0 + chunk);
+  for (int i = i0 + tid; i < i1; i += kRouteThreads) {
+    const int e = p.ids[i];
+    if (e >= 0 && e < E)
+      atomicAdd(&cnt[e], 1);
+    else if (e >= E)
+      atomicAdd(&cnt[E], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += kRouteThreads) hist[e * gridDim.x + blockIdx.x] = cnt[e];
+}
+
+__global__ void __launch_bounds__(kRouteThreads) group_scan_kernel(MoeParams p, int* hist, int nchunk) {
+  __shared__ int h[kHistInts];
+  __shared__ int scan_c[kRouteThreads];
+  __shared__ int scan_a[kRouteThreads];
+  const int tid = threadIdx.x, E = p.E, n = (E + 1) * nchunk;
+  for (int i = tid; i < n; i += kRouteThreads) h[i] = hist[i];
+  __syncthreads();
+  const int per = (E + kRouteThreads - 1) / kRouteThreads;
+  const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+  int sc = 0, sa = 0;
+  for (int e = e0; e < e1; ++e) {
+    int c = 0;
+    for (int k = 0; k < nchunk; ++k) c += h[e * nchunk + k];
+    sc += c;
+    sa += c > 0;
+  }
+  scan_c[tid] = sc;
+  scan_a[tid] = sa;
+  __syncthreads();
+  for (int off = 1; off < kRouteThreads; off <<= 1) {
+    const int vc = tid >= off ? scan_c[tid - off] : 0;
+    const int va = tid >= off ? scan_a[tid - off] : 0;
+    __syncthreads();
+    scan_c[tid] += vc;
+    scan_a[tid] += va;
+    __syncthreads();
+  }
+  int start = scan_c[tid] - sc;
+  int act = scan_a[tid] - sa;
+  for (int e = e0; e < e1; ++e) {
+    const int s0 = start;
+    for (int k = 0; k < nchunk; ++k) {  // chunk insert positions, in chunk order
+      const int c = h[e * nchunk + k];
+      h[e * nchunk + k] = start;
+      start += c;
+    }
+    if (start > s0) {
+      p.act_expert[act] = e;
+      p.act_start[act] = s0;
+      p.act_count[act] = start - s0;
+      ++act;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < E * nchunk; i += kRouteThreads) hist[i] = h[i];
+  if (tid == kRouteThreads - 1) {
+    int bad = 0;
+    for (int k = 0; k < nchunk; ++k) bad += h[E * nchunk + k];
+    p.meta[0] = scan_a[kRouteThreads - 1];
+    p.meta[1] = bad;
+    p.meta[3] = scan_c[kRouteThreads - 1];  // routed pairs
+  }
+}
+
+__global__ void __launch_bounds__(kRouteThreads) group_scatter_kernel(MoeParams p, const int* hist, int chunk) {
+  __shared__ int fill[kMaxExperts];
+  const int tid = threadIdx.x, E = p.E, P = p.T * p.K;
+  for (int e = tid; e < E; e += kRouteThreads) fill[e] = hist[e * gridDim.x + blockIdx.x];
+  __syncthreads();
+  const int i0 = blockIdx.x * chunk, i1 = min(P, i0 + chunk);
+  for (int i = i0 + tid; i < i1; i += kRouteThreads) {
+    const int e = p.ids[i];
+    if (e >= 0 && e < E) {
+      const int pos = atomicAdd(&fill[e], 1);
+      p.pair_tok[pos] = i / p.K;
+      p.pair_slot[pos] = i - (i / p.K) * p.K;
+      p.pair_w[pos] = load_act(p.weights, p.w_dtype, i);
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
   if (blockIdx.x == 0) {
     route_block(p);
@@ -494,8 +591,18 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, gu, dl, total;
+  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, hist, gu, dl, total;
 };
+
+// Pairs per chunk of the multi-workgroup grouping: multiples of the block
+// size, few enough chunks for the scan's LDS copy of the histograms.
+int64_t group_chunk(int64_t P, int64_t E) {
+  const int64_t max_chunks = std::max<int64_t>(1, kHistInts / (E + 1));
+  int64_t chunk = kRouteThreads;
+  while ((P + chunk - 1) / chunk > max_chunks) chunk += kRouteThreads;
+  return chunk;
+}
+int64_t group_chunks(int64_t P, int64_t E) { const int64_t c = group_chunk(P, E); return (P + c - 1) / c; }
 
 Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
   Layout L{};
@@ -509,6 +616,7 @@ Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
   L.pair_tok = off;   off = align_up(off + P * sizeof(int));
   L.pair_slot = off;  off = align_up(off + P * sizeof(int));
   L.pair_w = off;     off = align_up(off + P * sizeof(float));
+  L.hist = off;       off = align_up(off + group_chunks(P, E) * (E + 1) * sizeof(int));
   L.gu = off;         off += P * 2 * R * sizeof(float);  // gu and dl contiguous (one clear)
   L.dl = off;         off = align_up(off + P * R * sizeof(float));
   L.total = off;
@@ -668,7 +776,17 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
                                                                                   : P * a.n_embd / 4);
   const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));
-  hipLaunchKernelGGL(prep_kernel, dim3(1 + zero_blocks), dim3(kRouteThreads), 0, s, p);
+  if (use_prefill) {
+    // Large batch: the multi-workgroup grouping; nothing to clear.
+    int* hist = reinterpret_cast<int*>(ws + L.hist);
+    const int chunk = static_cast<int>(group_chunk(P, a.n_expert));
+    const int nchunk = static_cast<int>(group_chunks(P, a.n_expert));
+    hipLaunchKernelGGL(group_count_kernel, dim3(nchunk), dim3(kRouteThreads), 0, s, p, hist, chunk);
+    hipLaunchKernelGGL(group_scan_kernel, dim3(1), dim3(kRouteThreads), 0, s, p, hist, nchunk);
+    hipLaunchKernelGGL(group_scatter_kernel, dim3(nchunk), dim3(kRouteThreads), 0, s, p, hist, chunk);
+  } else {
+    hipLaunchKernelGGL(prep_kernel, dim3(1 + zero_blocks), dim3(kRouteThreads), 0, s, p);
+  }
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   if (use_prefill) {
     const prefill::Grouping g{p.meta, p.act_expert, p.act_start, p.act_count, p.pair_tok, p.pair_slot, p.pair_w};

@@ -652,20 +652,32 @@ __global__ void __launch_bounds__(kThreads) slots_kernel(Grouping g, int* pos_of
 }
 
 // out[t] = sum over slots (in slot order) of w * y[pos_of[t][slot]] * 2^-exp,
-// y rows in fp16 with one exponent per 128 columns.  One workgroup per token.
+// y rows in fp16 with one exponent per 128 columns.  One workgroup per token;
+// the slots' rows are loaded together (kCombineSlots at a time) before the
+// sum, so a thread keeps that many 16-byte loads in flight.
+constexpr int kCombineSlots = 8;
 __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, const int* yexp, int yexp_ld,
                                                            const int* pos_of, const float* pair_w, int k, int d, int wbd,
                                                            float* out) {
   const int t = blockIdx.x;
   for (int c = threadIdx.x * 8; c < d; c += kThreads * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int sl = 0; sl < k; ++sl) {
-      const int pos = pos_of[t * k + sl];
-      if (pos < 0) continue;
-      const half8 h = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
-      const float w = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kBlk]);
+    for (int s0 = 0; s0 < k; s0 += kCombineSlots) {
+      half8 h[kCombineSlots];
+      float w[kCombineSlots];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] = fmaf(w, static_cast<float>(h[i]), acc[i]);
+      for (int i = 0; i < kCombineSlots; ++i) {
+        const int sl = s0 + i;
+        const int pos = sl < k ? pos_of[t * k + sl] : -1;
+        const int pr = pos < 0 ? 0 : pos;  // dropped slot: row 0 with weight 0
+        h[i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pr) * d + c);
+        const float wv = pos < 0 ? 0.f : (wbd ? 1.f : pair_w[pr]);
+        w[i] = __builtin_ldexpf(wv, -yexp[static_cast<int64_t>(pr) * yexp_ld + c / kBlk]);
+      }
+#pragma unroll
+      for (int i = 0; i < kCombineSlots; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(w[i], static_cast<float>(h[i][j]), acc[j]);
     }
     float4* o = reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * d + c);
     o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
