@@ -113,6 +113,7 @@ struct SmemLayout {
   int pos_of[kMaxP];
   int nvalid[kMaxP];
   int misc[16];
+  alignas(16) char emit[64];
   union {
     struct {
       int ids[kMaxP];
@@ -127,6 +128,8 @@ struct SmemLayout {
     } work;
   } u;
 };
+
+struct EmitArgs;
 
 struct Smem {
   FactorArgs* fac; // [6] factor descriptors (kept in LDS, not in scalar registers)
@@ -147,6 +150,7 @@ struct Smem {
   float* vin;      // [kMB][kVMax]
   float* hs;       // [kMB][cb]  (g of the BC slice, then h)
   float* red;      // cross-wave partials
+  EmitArgs* emit;  // the current tile's output description
 };
 
 __device__ __forceinline__ Smem carve(SmemLayout& m) {
@@ -166,6 +170,7 @@ __device__ __forceinline__ Smem carve(SmemLayout& m) {
   s.pos_of = m.pos_of;
   s.nvalid = m.nvalid;
   s.misc = m.misc;
+  s.emit = reinterpret_cast<EmitArgs*>(m.emit);
   s.vin = m.u.work.vin;
   s.hs = m.u.work.hs;
   s.red = m.u.work.red;
@@ -400,12 +405,39 @@ __device__ __forceinline__ T pick_t(int t, const T (&a)[kMB]) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
-__device__ __forceinline__ void emit_one(const Job& j, int64_t rowoff, float scale, int col, float v) {
-  float* q = j.dst + rowoff + col;
-  if (j.coherent)
+// What a tile's final pass needs to write its rows.  It is staged in LDS by
+// thread 0 when the tile starts and read back after the tile's fold barriers,
+// so none of it stays in registers through the streaming loop.
+struct EmitArgs {
+  float* dst;
+  int64_t rowoff[kMB];
+  float scale[kMB];
+  int swiglu;
+  int coherent;
+};
+
+static_assert(sizeof(EmitArgs) <= 64, "LDS slot of the emit arguments");
+
+__device__ __forceinline__ void stage_emit(const Job& j, lptr<EmitArgs> ea) {
+  if (threadIdx.x == 0) {
+    ea->dst = j.dst;
+#pragma unroll
+    for (int t = 0; t < kMB; ++t) {
+      ea->rowoff[t] = j.rowoff[t];
+      ea->scale[t] = j.scale[t];
+    }
+    ea->swiglu = j.swiglu;
+    ea->coherent = j.coherent;
+  }
+}
+
+__device__ __forceinline__ void emit_one(lptr<const EmitArgs> ea, int t, int col, float v) {
+  const float scale = ea->scale[t];
+  float* q = ea->dst + ea->rowoff[t] + col;
+  if (ea->coherent)
     st_coh(q, v * scale);
   else
-    *q = j.swiglu ? silu_f32(*q) * v * scale : v * scale;
+    *q = ea->swiglu ? silu_f32(*q) * v * scale : v * scale;
 }
 
 // A lane owns half a group: 16 columns (8 code bytes) of one row per step.
@@ -466,6 +498,109 @@ __device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, in
   return (bm[gg >> 5] >> (gg & 31)) & 1u;
 }
 
+// Row-lane reduction + cross-wave fold of a tile's accumulators.
+//
+// Lanes of one half group h are spread over rpw row lanes (lane = ro * lph + hl).
+// With rpw <= 4 the row lanes are reduced by a transposing butterfly of lane-half
+// swaps (permlane32 for ro ^ 2 or lph = 32, permlane16 for ro ^ 1): each step
+// adds two accumulators of a lane pair and keeps one of them per lane, so the
+// values a lane holds halve per step and every lane ends with a distinct share
+// of the reduced half group: value i is acc[t][c] with n = t * 16 + c =
+//   rpw 1: i          rpw 2: 2 i + ro          rpw 4: 4 i + 2 (ro & 1) + (ro >> 1).
+// The shares then go through an LDS fold over the wr row waves: waves
+// wri < wr/2 store, the others add into slot wri - wr/2 (one slot and no adds
+// for wr == 1), and the caller sums the slots in order and emits whole rows.
+__device__ __forceinline__ float2 swap32(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap16(float a, float b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <int M, int RPW>
+__device__ __forceinline__ void fold_rows(float (&acc)[M][kHalf], lptr<float> red, int h, int ro, bool hvalid, int wri,
+                                          int wr, int ncols) {
+  constexpr int N = M * kHalf, NV = N / RPW;
+  float v[NV];
+  if constexpr (RPW == 1) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = acc[i / kHalf][i % kHalf];
+  } else {
+    constexpr int N2 = N / 2;
+    float w[N2];
+#pragma unroll
+    for (int i = 0; i < N2; ++i) {
+      const float2 r = swap32(acc[(2 * i) / kHalf][(2 * i) % kHalf], acc[(2 * i + 1) / kHalf][(2 * i + 1) % kHalf]);
+      w[i] = r.x + r.y;
+    }
+    if constexpr (RPW == 2) {
+#pragma unroll
+      for (int i = 0; i < N2; ++i) v[i] = w[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const float2 r = swap16(w[2 * i], w[2 * i + 1]);
+        v[i] = r.x + r.y;
+      }
+    }
+  }
+  const int sel = RPW == 4 ? 2 * (ro & 1) + (ro >> 1) : (RPW == 2 ? ro : 0);
+  const int slots = wr > 1 ? wr / 2 : 1;
+  if (hvalid && wri < slots) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int n = RPW * i + sel, t = n / kHalf, c = n % kHalf;
+      red[(wri * M + t) * ncols + h * kHalf + c] = v[i];
+    }
+  }
+  __syncthreads();
+  if (wr == 1) return;
+  if (hvalid && wri >= slots) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int n = RPW * i + sel, t = n / kHalf, c = n % kHalf;
+      red[((wri - slots) * M + t) * ncols + h * kHalf + c] += v[i];
+    }
+  }
+  __syncthreads();
+}
+
+// Same for rpw >= 8 (tiles narrower than 16 half groups): xor shuffles over the
+// row lanes, then row lane 0 holds the whole half group.
+template <int M>
+__device__ __forceinline__ void fold_rows_shfl(float (&acc)[M][kHalf], lptr<float> red, int h, int ro, bool hvalid,
+                                               int wri, int wr, int ncols, int lph) {
+  for (int off = lph; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int t = 0; t < M; ++t)
+#pragma unroll
+      for (int c = 0; c < kHalf; ++c) acc[t][c] += __shfl_xor(acc[t][c], off);
+  }
+  const bool writer = ro == 0 && hvalid;
+  const int slots = wr > 1 ? wr / 2 : 1;
+  if (writer && wri < slots) {
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      lptr<float> dst = red + (wri * M + t) * ncols + h * kHalf;
+#pragma unroll
+      for (int c = 0; c < kHalf; ++c) dst[c] = acc[t][c];
+    }
+  }
+  __syncthreads();
+  if (wr == 1) return;
+  if (writer && wri >= slots) {
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      lptr<float> dst = red + ((wri - slots) * M + t) * ncols + h * kHalf;
+#pragma unroll
+      for (int c = 0; c < kHalf; ++c) dst[c] += acc[t][c];
+    }
+  }
+  __syncthreads();
+}
+
 // Tile GEMV over half groups: H = 2G half groups, lanes along half groups (lph
 // per row; 16 lanes = one 128-byte row segment) x rows; waves along half
 // groups (wg) x rows (wr).  The in-wave sum runs over the row lanes; the
@@ -473,7 +608,9 @@ __device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, in
 // then adds the lower slices in order (fixed order, deterministic).  M is the
 // token capacity of the accumulators, m <= M the tokens present.
 template <int M, bool kInt8>
-__device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> lut, lptr<float> red) {
+__device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> lut, lptr<float> red,
+                                          lptr<EmitArgs> ea) {
+  stage_emit(j, ea);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int H = 2 * j.G, h_valid = 2 * j.g_valid;
   int lph, wg;
@@ -532,7 +669,7 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   // kRing steps ahead right after it is consumed.  Four-token tiles spend
   // their registers on accumulators and do 4x the arithmetic per row, so a
   // shallower ring keeps them inside 128 VGPRs without starving the loads.
-  constexpr int kRing = M >= 4 ? 4 : 8;
+  constexpr int kRing = M >= 3 ? 4 : 8;
   // Scales stay raw fp16 bits in the ring: converting at load time would make
   // the refill wait for its own load.
   u32x2 ring[kRing];
@@ -577,70 +714,38 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
     sk += kRing * sdelta;
     vk += kRing * rstep;
   }
-  // In-wave reduction over the rpw row lanes.
-  for (int off = lph; off < kWave; off <<= 1) {
-#pragma unroll
-    for (int t = 0; t < M; ++t)
-#pragma unroll
-      for (int c = 0; c < kHalf; ++c) acc[t][c] += __shfl_xor(acc[t][c], off);
-  }
   const int ncols = H * kHalf;
-  const bool writer = ro == 0 && hvalid;
-  if (wr == 1) {
-    if (writer) {
-#pragma unroll
-      for (int t = 0; t < M; ++t) {
-        if (t < m) {
-#pragma unroll
-          for (int c = 0; c < kHalf; ++c) emit_one(j, j.rowoff[t], j.scale[t], h * kHalf + c, acc[t][c]);
-        }
-      }
-    }
-    __syncthreads();
-    return;
-  }
-  // Cross-wave: slices wri < wr/2 store, slices wri >= wr/2 add into slot
-  // wri - wr/2, then the wr/2 slots are summed in order.
-  const int slots = wr / 2;
-  if (writer && wri < slots) {
-#pragma unroll
-    for (int t = 0; t < M; ++t) {
-      lptr<float> dst = red + (wri * M + t) * ncols + h * kHalf;
-#pragma unroll
-      for (int c = 0; c < kHalf; ++c) dst[c] = acc[t][c];
-    }
-  }
-  __syncthreads();
-  if (writer && wri >= slots) {
-#pragma unroll
-    for (int t = 0; t < M; ++t) {
-      lptr<float> dst = red + ((wri - slots) * M + t) * ncols + h * kHalf;
-#pragma unroll
-      for (int c = 0; c < kHalf; ++c) dst[c] += acc[t][c];
-    }
-  }
-  __syncthreads();
+  const int slots = wr > 1 ? wr / 2 : 1;
+  // lph = 16 whenever H >= 16 (at most 64 half groups per tile), so the row
+  // lanes are 4 there; narrower tiles have 8 or more.
+  if (rpw == 4 && M <= 2)
+    fold_rows<M, 4>(acc, red, h, ro, hvalid, wri, wr, ncols);
+  else
+    fold_rows_shfl<M>(acc, red, h, ro, hvalid, wri, wr, ncols, lph);
   const int nvalid_cols = h_valid * kHalf;
   for (int i = tid; i < m * nvalid_cols; i += kNT) {
     const int t = i / nvalid_cols, col = i - t * nvalid_cols;
     float v = 0.f;
     for (int w = 0; w < slots; ++w) v += red[(w * M + t) * ncols + col];
-    emit_one(j, pick_t(t, j.rowoff), pick_t(t, j.scale), col, v);
+    emit_one(ea, t, col, v);
   }
   __syncthreads();
 }
 
-// The one place the tile is expanded (accumulator capacities 1, 2 and 4 tokens).
+// The one place the tile is expanded (accumulator capacities 1 to 4 tokens).
 template <bool kInt8>
 __device__ __forceinline__ void run_tile(const Job& j, int m, const Smem& s) {
   const lptr<const char> lut = reinterpret_cast<lptr<const char>>(as_lds(static_cast<const float2*>(s.lut)));
   const lptr<float> red = as_lds(s.red);
+  const lptr<EmitArgs> ea = as_lds(s.emit);
   if (m == 1)
-    tile_gemv<1, kInt8>(j, 1, lut, red);
+    tile_gemv<1, kInt8>(j, 1, lut, red, ea);
   else if (m == 2)
-    tile_gemv<2, kInt8>(j, 2, lut, red);
+    tile_gemv<2, kInt8>(j, 2, lut, red, ea);
+  else if (m == 3)
+    tile_gemv<3, kInt8>(j, 3, lut, red, ea);
   else
-    tile_gemv<4, kInt8>(j, m, lut, red);
+    tile_gemv<4, kInt8>(j, m, lut, red, ea);
 }
 
 // ---------------------------------------------------------------------------
