@@ -29,6 +29,7 @@
 #include "fused.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 namespace latent {
@@ -99,6 +100,7 @@ struct FactorArgs;
 // (ids, w, cnt, start) is only live inside route() and shares its space with
 // the activation / slice / cross-wave buffers used afterwards.
 constexpr int kMaxP = 512;                    // routed pairs (T * k)
+static_assert(kMaxP <= kNT, "route() ranks the active experts with one thread each");
 constexpr int kMaxEx = 512;                   // experts
 constexpr int kVMax = 1024;                   // staged activation floats per token
 constexpr int kCbMax = 512;                   // ff columns of a BC slice
@@ -114,7 +116,7 @@ struct SmemLayout {
   int nvalid[kMaxP];
   int misc[16];
   alignas(16) char emit[64];
-  union {
+  union alignas(16) {
     struct {
       int ids[kMaxP];
       float w[kMaxP];
@@ -200,12 +202,16 @@ __device__ void route(const Params& p, const Smem& s) {
   }
   __syncthreads();
   if (tid < kWave) {
-    // One wave scans the expert counts (E <= kMaxE).
+    // One wave scans the expert counts (E <= kMaxE).  An expert with more than
+    // kMB pairs is split into work units ("active entries") of at most kMB
+    // pairs each, so no item runs a second batch and the units of one expert
+    // run side by side.
     int run = 0, act = 0;
     for (int base = 0; base < p.E; base += kWave) {
       const int e = base + tid;
       const int c = e < p.E ? s.cnt[e] : 0;
-      int incl = c, ai = c > 0;
+      const int nu = (c + kMB - 1) / kMB;
+      int incl = c, ai = nu;
       for (int off = 1; off < kWave; off <<= 1) {
         const int v = __shfl_up(incl, off);
         const int va = __shfl_up(ai, off);
@@ -216,11 +222,11 @@ __device__ void route(const Params& p, const Smem& s) {
       }
       if (e < p.E) {
         s.start[e] = run + incl - c;
-        if (c > 0) {
-          const int a = act + ai - 1;
+        for (int u = 0; u < nu; ++u) {
+          const int a = act + ai - nu + u;
           s.act_e[a] = e;
-          s.act_s[a] = run + incl - c;
-          s.act_c[a] = c;
+          s.act_s[a] = run + incl - c + u * kMB;
+          s.act_c[a] = min(kMB, c - u * kMB);
         }
       }
       run += __shfl(incl, kWave - 1);
@@ -229,28 +235,64 @@ __device__ void route(const Params& p, const Smem& s) {
     if (tid == 0) s.misc[0] = act;
   }
   __syncthreads();
-  // Placement: thread j owns experts j, j+kNT, ... and scans the pairs in order.
-  for (int e = tid; e < p.E; e += kNT) {
-    if (s.cnt[e] == 0) continue;
-    int pos = s.start[e];
-    for (int i = 0; i < p.P; ++i) {
-      if (s.ids[i] == e) {
-        s.pr_tok[pos] = i / p.K;
-        s.pr_slot[pos] = i - (i / p.K) * p.K;
-        s.pr_w[pos] = s.w[i];
-        s.pos_of[i] = pos;
-        ++pos;
-      }
+  // Placement: pair i goes to start[e] + (number of earlier pairs of its
+  // expert e), so the pairs of one expert keep their order.  The count reads
+  // the routed ids four at a time (every lane of a wave reads the same words).
+  const int4* ids4 = reinterpret_cast<const int4*>(s.ids);
+  for (int i = tid; i < p.P; i += kNT) {
+    const int e = s.ids[i];
+    if (e < 0 || e >= p.E) continue;
+    int rank = 0;
+    const int n4 = i >> 2;
+#pragma unroll 4
+    for (int j = 0; j < n4; ++j) {
+      const int4 v = ids4[j];
+      rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
     }
+    for (int j = n4 << 2; j < i; ++j) rank += s.ids[j] == e;
+    const int pos = s.start[e] + rank;
+    const int tok = i / p.K;
+    s.pr_tok[pos] = tok;
+    s.pr_slot[pos] = i - tok * p.K;
+    s.pr_w[pos] = s.w[i];
+    s.pos_of[i] = pos;
+  }
+  // Active entries by pair count, largest first (ties by index), so each queue
+  // starts its longest items first.
+  const int n_active = s.misc[0];
+  int my_e = 0, my_s = 0, my_c = 0, rank = 0;
+  if (tid < n_active) {
+    my_e = s.act_e[tid];
+    my_s = s.act_s[tid];
+    my_c = s.act_c[tid];
+#pragma unroll 4
+    for (int b = 0; b < n_active; ++b) {
+      const int c = s.act_c[b];
+      rank += (c > my_c) || (c == my_c && b < tid);
+    }
+  }
+  __syncthreads();
+  if (tid < n_active) {
+    s.act_e[rank] = my_e;
+    s.act_s[rank] = my_s;
+    s.act_c[rank] = my_c;
   }
   __syncthreads();
 }
 
 // ---------------------------------------------------------------------------
-// Item bookkeeping.  Queue q holds active experts a = q, q+8, q+16, ...
+// Item bookkeeping.  Queue q holds active experts queue_expert(q, k), k = 0, 1, ...
 // Items of a queue: [A: nq*2*nca][BC: nq*ncb][D: nq*ncd][Z: zero rows]
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int experts_in_queue(int n_active, int q) { return n_active > q ? (n_active - q + 7) / 8 : 0; }
+// Active experts are ranked by token count (largest first) and dealt to the
+// queues in a snake order: ranks 8k .. 8k+7 go to queues 0..7 for even k and
+// 7..0 for odd k, so every queue gets a like mix of heavy and light experts.
+__device__ __forceinline__ int queue_expert(int q, int k) { return 8 * k + ((k & 1) ? 7 - q : q); }
+__device__ __forceinline__ int experts_in_queue(int n_active, int q) {
+  const int full = n_active / 8, r = n_active % 8;
+  const bool extra = (full & 1) ? (7 - q) < r : q < r;
+  return full + (extra ? 1 : 0);
+}
 
 // Zero work for outputs no D item writes: tokens with no valid slot (reduced
 // mode) or dropped slots (per-slot mode); one item per (row, d slice).
@@ -682,7 +724,12 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   }
   uint32_t ck = c_first, sk = s_first;
   int vk = v_first;
-  for (int k0 = 0; k0 < nsteps; k0 += kRing) {
+  // One block of kRing steps; with kRefill each consumed slot is reloaded with
+  // the row kRing steps ahead.  The last block runs without refills, so no
+  // load is left in flight when the tile ends (a dangling load would make the
+  // next tile wait for it, and for every store before it, once its register
+  // is reused).
+  auto block = [&](int k0, auto refill) {
 #pragma unroll
     for (int u = 0; u < kRing; ++u) {
       const int k = k0 + u;
@@ -700,20 +747,25 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
         }
       }
       if (!done) fma_half_nf4<M>(ring[u], xs, lut, lanebase, acc);
-      // Pin the refill between this step and the next.  Hoisted above the
-      // step, its load would need a fresh register and a copy at the loop
-      // latch, and that copy waits for every load in flight; sunk below, it
-      // loses the distance to its use.  Either way the ring stops hiding the
-      // memory latency.
-      __builtin_amdgcn_sched_barrier(0);
-      ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(ck + (u + kRing) * cdelta, c_last));
-      sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(sk + (u + kRing) * sdelta, s_last));
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (decltype(refill)::value) {
+        // Pin the refill between this step and the next.  Hoisted above the
+        // step, its load would need a fresh register and a copy at the loop
+        // latch, and that copy waits for every load in flight; sunk below, it
+        // loses the distance to its use.  Either way the ring stops hiding the
+        // memory latency.
+        __builtin_amdgcn_sched_barrier(0);
+        ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(ck + (u + kRing) * cdelta, c_last));
+        sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(sk + (u + kRing) * sdelta, s_last));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     ck += kRing * cdelta;
     sk += kRing * sdelta;
     vk += kRing * rstep;
-  }
+  };
+  int k0 = 0;
+  for (; k0 + kRing < nsteps; k0 += kRing) block(k0, std::true_type{});
+  if (k0 < nsteps) block(k0, std::false_type{});
   const int ncols = H * kHalf;
   const int slots = wr > 1 ? wr / 2 : 1;
   // lph = 16 whenever H >= 16 (at most 64 half groups per tile), so the row
@@ -1060,16 +1112,16 @@ __global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 wave
     if (t < nA) {
       const int per = 2 * p.nca, r = t % per;
       it.type = kItemA;
-      it.a = q + 8 * (t / per);
+      it.a = queue_expert(q, t / per);
       it.kind = r / p.nca;
       it.chunk = r % p.nca;
     } else if ((t -= nA) < nB) {
       it.type = kItemBC;
-      it.a = q + 8 * (t / p.ncb);
+      it.a = queue_expert(q, t / p.ncb);
       it.chunk = t % p.ncb;
     } else if ((t -= nB) < nD) {
       it.type = kItemD;
-      it.a = q + 8 * (t / p.ncd);
+      it.a = queue_expert(q, t / p.ncd);
       it.chunk = t % p.ncd;
     } else {
       t -= nD;
@@ -1142,7 +1194,7 @@ static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi)
 
 bool make_plan(const latent_moe_args& a, Plan& pl) {
   const int64_t T = a.n_tokens, K = a.n_expert_used, E = a.n_expert, R = a.max_rank, d = a.n_embd, ff = a.n_ff;
-  const int64_t P = T * K, A = std::min(E, P);
+  const int64_t P = T * K, A = P;  // active entries: at most one per routed pair
   const double est = static_cast<double>(E) * (1.0 - std::pow(1.0 - static_cast<double>(K) / E, static_cast<double>(T)));
   const double per_xcd = std::max(1.0, std::ceil(est / 8.0));
   const double wgs_per_xcd = 32.0 * kWgPerCu;
