@@ -97,7 +97,7 @@ struct FactorArgs;
 
 // Fixed LDS layout (compile-time offsets: every LDS access uses an immediate
 // address, so no scalar registers hold array bases).  The routing scratch
-// (ids, w, cnt, start) is only live inside route() and shares its space with
+// (w, cnt, start, whist) is only live inside route() and shares its space with
 // the activation / slice / cross-wave buffers used afterwards.
 constexpr int kMaxP = 512;                    // routed pairs (T * k)
 static_assert(kMaxP <= kNT, "route() ranks the active experts with one thread each");
@@ -118,10 +118,10 @@ struct SmemLayout {
   alignas(16) char emit[64];
   union alignas(16) {
     struct {
-      int ids[kMaxP];
       float w[kMaxP];
       int cnt[kMaxEx];
       int start[kMaxEx];
+      int whist[kW][kMaxEx];  // pairs of each expert per wave
     } route;
     struct {
       float vin[kMB * kVMax];
@@ -136,10 +136,10 @@ struct EmitArgs;
 struct Smem {
   FactorArgs* fac; // [6] factor descriptors (kept in LDS, not in scalar registers)
   float2* lut;     // [256][kLutCopies]
-  int* ids;        // [P]
   float* w;        // [P]
   int* cnt;        // [E]
   int* start;      // [E]
+  int* whist;      // [kW][kMaxEx]
   int* act_e;      // [A]
   int* act_s;      // [A]
   int* act_c;      // [A]
@@ -159,10 +159,10 @@ __device__ __forceinline__ Smem carve(SmemLayout& m) {
   Smem s;
   s.fac = reinterpret_cast<FactorArgs*>(m.fac);
   s.lut = m.lut;
-  s.ids = m.u.route.ids;
   s.w = m.u.route.w;
   s.cnt = m.u.route.cnt;
   s.start = m.u.route.start;
+  s.whist = &m.u.route.whist[0][0];
   s.act_e = m.act_e;
   s.act_s = m.act_s;
   s.act_c = m.act_c;
@@ -184,21 +184,39 @@ __device__ __forceinline__ Smem carve(SmemLayout& m) {
 // experts ascending, pairs of one expert in increasing t*K + slot).
 // ---------------------------------------------------------------------------
 __device__ void route(const Params& p, const Smem& s) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < p.P; i += kNT) {
-    s.ids[i] = p.ids[i];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  // One routed pair per thread (P <= kMaxP <= kNT).
+  const int i = tid;
+  int e = -1;
+  if (i < p.P) {
+    e = p.ids[i];
     s.w[i] = load_act(p.weights, p.w_dtype, i);
     s.pos_of[i] = -1;
   }
-  for (int e = tid; e < p.E; e += kNT) s.cnt[e] = 0;
+  const bool valid = e >= 0 && e < p.E;
+  for (int k = tid; k < kW * p.E; k += kNT) s.whist[(k / p.E) * kMaxEx + k % p.E] = 0;
   for (int t = tid; t < p.T; t += kNT) s.nvalid[t] = 0;
   __syncthreads();
-  for (int i = tid; i < p.P; i += kNT) {
-    const int e = s.ids[i];
-    if (e >= 0 && e < p.E) {
-      atomicAdd(&s.cnt[e], 1);
-      atomicAdd(&s.nvalid[i / p.K], 1);
-    }
+  if (valid) atomicAdd(&s.nvalid[i / p.K], 1);
+  // Within each wave, group the lanes by expert (one ballot per distinct
+  // expert of the wave): a pair's rank among the wave's earlier pairs of its
+  // expert, and the wave's count of each expert.
+  int my_rank = 0;
+  uint64_t rem = __ballot(valid);
+  while (rem != 0) {
+    const int leader = __ffsll(static_cast<unsigned long long>(rem)) - 1;
+    const int e0 = __shfl(e, leader);
+    const uint64_t m = __ballot(valid && e == e0);
+    if (valid && e == e0) my_rank = __popcll(m & ((uint64_t{1} << lane) - 1));
+    if (lane == leader) s.whist[wave * kMaxEx + e0] = __popcll(m);
+    rem &= ~m;
+  }
+  __syncthreads();
+  for (int ee = tid; ee < p.E; ee += kNT) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) c += s.whist[w * kMaxEx + ee];
+    s.cnt[ee] = c;
   }
   __syncthreads();
   if (tid < kWave) {
@@ -235,22 +253,11 @@ __device__ void route(const Params& p, const Smem& s) {
     if (tid == 0) s.misc[0] = act;
   }
   __syncthreads();
-  // Placement: pair i goes to start[e] + (number of earlier pairs of its
-  // expert e), so the pairs of one expert keep their order.  The count reads
-  // the routed ids four at a time (every lane of a wave reads the same words).
-  const int4* ids4 = reinterpret_cast<const int4*>(s.ids);
-  for (int i = tid; i < p.P; i += kNT) {
-    const int e = s.ids[i];
-    if (e < 0 || e >= p.E) continue;
-    int rank = 0;
-    const int n4 = i >> 2;
-#pragma unroll 4
-    for (int j = 0; j < n4; ++j) {
-      const int4 v = ids4[j];
-      rank += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
-    }
-    for (int j = n4 << 2; j < i; ++j) rank += s.ids[j] == e;
-    const int pos = s.start[e] + rank;
+  // Placement: pair i goes to start[e] + (pairs of e in earlier waves) + (its
+  // rank in its wave), so the pairs of one expert keep their order.
+  if (valid) {
+    int pos = s.start[e] + my_rank;
+    for (int w = 0; w < wave; ++w) pos += s.whist[w * kMaxEx + e];
     const int tok = i / p.K;
     s.pr_tok[pos] = tok;
     s.pr_slot[pos] = i - tok * p.K;
@@ -258,17 +265,33 @@ __device__ void route(const Params& p, const Smem& s) {
     s.pos_of[i] = pos;
   }
   // Active entries by pair count, largest first (ties by index), so each queue
-  // starts its longest items first.
+  // starts its longest items first.  Counts are 1..kMB: the rank is the number
+  // of entries with a larger count plus the earlier entries with the same one
+  // (wave ballots within a wave, per-wave totals through LDS across waves).
+  __syncthreads();
   const int n_active = s.misc[0];
-  int my_e = 0, my_s = 0, my_c = 0, rank = 0;
+  int my_e = 0, my_s = 0, my_c = 0;
   if (tid < n_active) {
     my_e = s.act_e[tid];
     my_s = s.act_s[tid];
     my_c = s.act_c[tid];
-#pragma unroll 4
-    for (int b = 0; b < n_active; ++b) {
-      const int c = s.act_c[b];
-      rank += (c > my_c) || (c == my_c && b < tid);
+  }
+  int below = 0;
+#pragma unroll
+  for (int v = 1; v <= kMB; ++v) {
+    const uint64_t mask = __ballot(my_c == v);
+    if (my_c == v) below = __popcll(mask & ((uint64_t{1} << lane) - 1));
+    if (lane == 0) s.cnt[wave * kMB + v - 1] = __popcll(mask);
+  }
+  __syncthreads();
+  int rank = below;
+  if (tid < n_active) {
+    for (int w = 0; w < kW; ++w) {
+#pragma unroll
+      for (int v = 1; v <= kMB; ++v) {
+        const int n = s.cnt[w * kMB + v - 1];
+        rank += (v > my_c || (v == my_c && w < wave)) ? n : 0;
+      }
     }
   }
   __syncthreads();
