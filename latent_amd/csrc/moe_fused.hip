@@ -572,9 +572,8 @@ __device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, in
 // values a lane holds halve per step and every lane ends with a distinct share
 // of the reduced half group: value i is acc[t][c] with n = t * 16 + c =
 //   rpw 1: i          rpw 2: 2 i + ro          rpw 4: 4 i + 2 (ro & 1) + (ro >> 1).
-// The shares then go through an LDS fold over the wr row waves: waves
-// wri < wr/2 store, the others add into slot wri - wr/2 (one slot and no adds
-// for wr == 1), and the caller sums the slots in order and emits whole rows.
+// The shares then go to an LDS slot per row wave, and the caller sums the wr
+// slots in order and emits whole rows.
 __device__ __forceinline__ float2 swap32(float a, float b) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -611,22 +610,15 @@ __device__ __forceinline__ void fold_rows(float (&acc)[M][kHalf], lptr<float> re
       }
     }
   }
+  // Every row wave stores its own slot (wr * M * ncols = kW * 16 * kHalf * M
+  // <= kRedFloats floats for M <= 2), so one barrier ends the fold.
+  static_assert(M <= 2, "one fold slot per row wave");
   const int sel = RPW == 4 ? 2 * (ro & 1) + (ro >> 1) : (RPW == 2 ? ro : 0);
-  const int slots = wr > 1 ? wr / 2 : 1;
-  if (hvalid && wri < slots) {
+  if (hvalid) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int n = RPW * i + sel, t = n / kHalf, c = n % kHalf;
       red[(wri * M + t) * ncols + h * kHalf + c] = v[i];
-    }
-  }
-  __syncthreads();
-  if (wr == 1) return;
-  if (hvalid && wri >= slots) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int n = RPW * i + sel, t = n / kHalf, c = n % kHalf;
-      red[((wri - slots) * M + t) * ncols + h * kHalf + c] += v[i];
     }
   }
   __syncthreads();
@@ -790,13 +782,21 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   for (; k0 + kRing < nsteps; k0 += kRing) block(k0, std::true_type{});
   if (k0 < nsteps) block(k0, std::false_type{});
   const int ncols = H * kHalf;
-  const int slots = wr > 1 ? wr / 2 : 1;
   // lph = 16 whenever H >= 16 (at most 64 half groups per tile), so the row
   // lanes are 4 there; narrower tiles have 8 or more.
-  if (rpw == 4 && M <= 2)
-    fold_rows<M, 4>(acc, red, h, ro, hvalid, wri, wr, ncols);
-  else
+  int slots;
+  if constexpr (M <= 2) {
+    if (rpw == 4) {
+      fold_rows<M, 4>(acc, red, h, ro, hvalid, wri, wr, ncols);
+      slots = wr;
+    } else {
+      fold_rows_shfl<M>(acc, red, h, ro, hvalid, wri, wr, ncols, lph);
+      slots = wr > 1 ? wr / 2 : 1;
+    }
+  } else {
     fold_rows_shfl<M>(acc, red, h, ro, hvalid, wri, wr, ncols, lph);
+    slots = wr > 1 ? wr / 2 : 1;
+  }
   const int nvalid_cols = h_valid * kHalf;
   for (int i = tid; i < m * nvalid_cols; i += kNT) {
     const int t = i / nvalid_cols, col = i - t * nvalid_cols;
