@@ -566,14 +566,13 @@ __device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, in
 // Row-lane reduction + cross-wave fold of a tile's accumulators.
 //
 // Lanes of one half group h are spread over rpw row lanes (lane = ro * lph + hl).
-// With rpw <= 4 the row lanes are reduced by a transposing butterfly of lane-half
-// swaps (permlane32 for ro ^ 2 or lph = 32, permlane16 for ro ^ 1): each step
-// adds two accumulators of a lane pair and keeps one of them per lane, so the
-// values a lane holds halve per step and every lane ends with a distinct share
-// of the reduced half group: value i is acc[t][c] with n = t * 16 + c =
-//   rpw 1: i          rpw 2: 2 i + ro          rpw 4: 4 i + 2 (ro & 1) + (ro >> 1).
-// The shares then go to an LDS slot per row wave, and the caller sums the wr
-// slots in order and emits whole rows.
+// With rpw == 4 (lph == 16) the row lanes are reduced by a transposing
+// butterfly of lane-half swaps (permlane32 pairs ro with ro ^ 2, permlane16 ro
+// with ro ^ 1): each step adds two accumulators of a lane pair and keeps one of
+// them per lane, so the values a lane holds halve per step and every lane ends
+// with a distinct quarter of the reduced half group: value i is acc[t][c] with
+// t * 16 + c = 4 i + 2 (ro & 1) + (ro >> 1).  The shares then go to an LDS slot
+// per row wave, and the caller sums the wr slots in order and emits whole rows.
 __device__ __forceinline__ float2 swap32(float a, float b) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -583,41 +582,29 @@ __device__ __forceinline__ float2 swap16(float a, float b) {
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int M, int RPW>
+template <int M>
 __device__ __forceinline__ void fold_rows(float (&acc)[M][kHalf], lptr<float> red, int h, int ro, bool hvalid, int wri,
-                                          int wr, int ncols) {
-  constexpr int N = M * kHalf, NV = N / RPW;
-  float v[NV];
-  if constexpr (RPW == 1) {
+                                          int ncols) {
+  constexpr int N = M * kHalf, NV = N / 4;
+  float w[N / 2], v[NV];
 #pragma unroll
-    for (int i = 0; i < N; ++i) v[i] = acc[i / kHalf][i % kHalf];
-  } else {
-    constexpr int N2 = N / 2;
-    float w[N2];
+  for (int i = 0; i < N / 2; ++i) {
+    const float2 r = swap32(acc[(2 * i) / kHalf][(2 * i) % kHalf], acc[(2 * i + 1) / kHalf][(2 * i + 1) % kHalf]);
+    w[i] = r.x + r.y;
+  }
 #pragma unroll
-    for (int i = 0; i < N2; ++i) {
-      const float2 r = swap32(acc[(2 * i) / kHalf][(2 * i) % kHalf], acc[(2 * i + 1) / kHalf][(2 * i + 1) % kHalf]);
-      w[i] = r.x + r.y;
-    }
-    if constexpr (RPW == 2) {
-#pragma unroll
-      for (int i = 0; i < N2; ++i) v[i] = w[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const float2 r = swap16(w[2 * i], w[2 * i + 1]);
-        v[i] = r.x + r.y;
-      }
-    }
+  for (int i = 0; i < NV; ++i) {
+    const float2 r = swap16(w[2 * i], w[2 * i + 1]);
+    v[i] = r.x + r.y;
   }
   // Every row wave stores its own slot (wr * M * ncols = kW * 16 * kHalf * M
   // <= kRedFloats floats for M <= 2), so one barrier ends the fold.
   static_assert(M <= 2, "one fold slot per row wave");
-  const int sel = RPW == 4 ? 2 * (ro & 1) + (ro >> 1) : (RPW == 2 ? ro : 0);
+  const int sel = 2 * (ro & 1) + (ro >> 1);
   if (hvalid) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int n = RPW * i + sel, t = n / kHalf, c = n % kHalf;
+      const int n = 4 * i + sel, t = n / kHalf, c = n % kHalf;
       red[(wri * M + t) * ncols + h * kHalf + c] = v[i];
     }
   }
@@ -787,7 +774,7 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   int slots;
   if constexpr (M <= 2) {
     if (rpw == 4) {
-      fold_rows<M, 4>(acc, red, h, ro, hvalid, wri, wr, ncols);
+      fold_rows<M>(acc, red, h, ro, hvalid, wri, ncols);
       slots = wr;
     } else {
       fold_rows_shfl<M>(acc, red, h, ro, hvalid, wri, wr, ncols, lph);
