@@ -5,6 +5,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/latent_ffn.h"
 
 namespace latent {
@@ -34,6 +36,39 @@ __device__ __forceinline__ float load_act(const void* p, int dtype, int64_t i) {
   if (dtype == LATENT_F16) return half_bits_to_float(b);
   return __uint_as_float(static_cast<uint32_t>(b) << 16);  // bf16
 }
+
+// Cross-lane reductions without LDS traffic (__shfl_xor compiles to
+// ds_bpermute): DPP inside 16-lane rows, lane-half swaps across rows.
+// op_over(v, lo, hi) combines v over the lanes l ^ b for the b in [lo, hi)
+// that are multiples of lo (lo, hi powers of two, 1 <= lo <= hi <= 64, and
+// hi >= 16 when lo <= 4), every lane ending with the group's result.  The 4-
+// and 8-lane steps use row rotations, which cover the same lane sets as xor 4
+// and xor 8 once both are applied.
+template <typename Op>
+__device__ __forceinline__ float op_over(float v, int lo, int hi, Op op) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  if (lo <= 1 && hi > 1) v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));  // quad_perm [1,0,3,2]: lane ^ 1
+  if (lo <= 2 && hi > 2) v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));  // quad_perm [2,3,0,1]: lane ^ 2
+  if (lo <= 4 && hi > 4) v = op(v, dpp(v, std::integral_constant<int, 0x124>{})); // row_ror:4
+  if (lo <= 8 && hi > 8) v = op(v, dpp(v, std::integral_constant<int, 0x128>{})); // row_ror:8 (lane ^ 8)
+  if (lo <= 16 && hi > 16) {  // rows r and r ^ 1
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  if (lo <= 32 && hi > 32) {  // lane halves
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  return v;
+}
+struct OpAdd {
+  __device__ __forceinline__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+  __device__ __forceinline__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
 
 // Lookup of an expert's per-group INT8 extension (see latent_factor).
 struct Int8Ext {

@@ -380,10 +380,8 @@ __device__ __forceinline__ void wave_reduce_store(float (&acc)[MB][kGroup], int 
 #pragma unroll
   for (int t = 0; t < MB; ++t) {
     if (t < m) {
-      for (int off = lpr; off < kWave; off <<= 1) {
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) acc[t][j] += __shfl_xor(acc[t][j], off);
-      }
+      for (int j = 0; j < kGroup; ++j) acc[t][j] = op_over(acc[t][j], lpr, kWave, OpAdd{});
     }
   }
   if (lane < lpr && lane < ngroups) {

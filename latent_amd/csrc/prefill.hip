@@ -199,11 +199,7 @@ __device__ __forceinline__ int block_exponent(float m) {
 
 // Maximum over the 32 lanes that hold one row of an MFMA result (lanes l and
 // l ^ 32 hold different rows).
-__device__ __forceinline__ float max32(float m) {
-#pragma unroll
-  for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-  return m;
-}
+__device__ __forceinline__ float max32(float m) { return op_over(m, 1, 32, OpMax{}); }
 
 template <int kA, int kEpi>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
@@ -625,7 +621,7 @@ __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_d
 #pragma unroll
     for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
   }
-  for (int off = 1; off < kWave; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  m = op_over(m, 1, kWave, OpMax{});
   if ((tid & (kWave - 1)) == 0) red[tid / kWave] = m;
   __syncthreads();
   if (tid == 0) {
