@@ -50,6 +50,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU-baseline sample time")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run one device-to-device copy of this many MiB first (counter calibration)")
+    p.add_argument("--stack", type=int, default=58,
+                   help="layers of the graph-captured stacked decode (0 to skip)")
+    p.add_argument("--stack-batch", type=int, default=32)
+    p.add_argument("--stack-steps", type=int, default=10)
     p.add_argument("--zipf-gamma", type=float, default=0.11,
                    help="prefill router skew; 0.11 gives about 70..400 tokens per expert at 4096 tokens")
     return p.parse_args()
@@ -132,6 +136,54 @@ def prefill_point(torch, latent, gsynth, layers, tokens, steps, zipf_gamma):
         "path": latent.moe_path(layers[0], x, K),
         "zipf_gamma": zipf_gamma,
     }
+
+
+def stack_point(torch, latent, gsynth, n_layers, batch, steps):
+    """n_layers DeepSeek-V3-shaped LATENT MoE layers, each with its own seeded
+    router (W_r ~ N(0, 1/d), fp32) and a residual add, decoded as one HIP graph."""
+    t0 = time.time()
+    layers = [gsynth.make_layer(seed=500_000 + 7919 * l, n_expert=E, d=D, ff=FF, max_rank=R) for l in range(n_layers)]
+    routers = []
+    for l in range(n_layers):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(900_000 + l)
+        w = torch.randn((D, E), generator=g, device="cuda") / np.sqrt(D)
+        routers.append(latent.Router(w, K))
+    torch.cuda.synchronize()
+    gen_s = time.time() - t0
+    stack = latent.DecodeStack(layers, routers, batch)
+    x0 = gsynth.bf16_input(seed=777, n_tokens=batch, d=D).float()
+    stack.load(x0)
+    # Eager (one host call per kernel) for comparison, then the captured graph.
+    eager_ms = time_loop(lambda i: stack.forward(), 3, 1, torch)
+    stack.capture()
+    ms = time_loop(lambda i: stack.replay(), steps, 2, torch)
+    ids = [t.cpu().numpy() for t in stack.layer_ids()]
+    step_bytes = float(sum(realized_bytes(ids)))
+    resident = stack.resident_bytes()
+    dense_bf16 = n_layers * E * 2 * (3 * D * FF)
+    gbps = step_bytes / (ms * 1e-3) / 1e9
+    out = {
+        "layers": n_layers,
+        "batch": batch,
+        "graph": "torch.cuda.CUDAGraph (HIP graph): per layer 2 router kernels + expert FFN + residual add",
+        "ms_per_step": ms,
+        "us_per_layer": ms * 1e3 / n_layers,
+        "tokens_per_s": batch / (ms * 1e-3),
+        "layer_tokens_per_s": batch * n_layers / (ms * 1e-3),
+        "eager_ms_per_step": eager_ms,
+        "bytes_per_step": step_bytes,
+        "hbm_gbps": gbps,
+        "roofline_frac": gbps / HBM_PEAK_GBPS,
+        "router_bytes_per_step": stack.router_bytes(),
+        "resident_bytes": resident,
+        "dense_bf16_bytes": dense_bf16,
+        "compression_vs_dense_bf16": dense_bf16 / resident,
+        "generate_s": gen_s,
+    }
+    del stack, layers, routers
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(torch, layer, routes, xs, batch, min_seconds):
@@ -227,6 +279,13 @@ def main():
     if args.prefill:
         prefill = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps, args.zipf_gamma)
         print(f"# prefill T={args.prefill}: {prefill['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
+    stack = None
+    if args.stack:
+        stack = stack_point(torch, latent, gsynth, args.stack, args.stack_batch, args.stack_steps)
+        print(f"# stack {args.stack} layers B={args.stack_batch}: {stack['ms_per_step']:.2f} ms/step "
+              f"({stack['us_per_layer']:.1f} us/layer, {stack['hbm_gbps']:.0f} GB/s; eager "
+              f"{stack['eager_ms_per_step']:.2f} ms; generated in {stack['generate_s']:.1f} s)",
+              file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch, args.cpu_seconds)
@@ -267,6 +326,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "prefill": prefill,
+        "stack": stack,
     }
     print(json.dumps(result), flush=True)
 

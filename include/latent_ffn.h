@@ -169,6 +169,54 @@ int latent_pack_nf4(const float* values, int64_t rows, int64_t cols, uint8_t* co
  */
 int latent_pack_int8(const float* values, int64_t n_groups, int8_t* q, uint16_t* scales, latent_stream_t stream);
 
+/* ---- router front end ---------------------------------------------------- */
+/* Drop rules applied after top-k (dropped slot => id -1, weight 0; the kept
+ * weights are not renormalised again). */
+#define LATENT_DROP_NONE 0
+/* Drop a slot whose renormalised weight is below drop_param. */
+#define LATENT_DROP_BELOW 1
+/* Keep the leading slots whose cumulative weight stays within drop_param of
+ * the top-k total: adaptive_topk_inclusive / adaptive_topk_batch
+ * (loader/adaptive_topk.py:29-90); drop_param in (0, 1]. */
+#define LATENT_DROP_INCLUSIVE 2
+
+/*
+ * One router call.  Either logits = x . router (fp32 accumulation, summed over
+ * 128-row slices of d in a fixed order) or caller logits (logits_in).  Then
+ * softmax over the E experts, top-k by descending probability (ties -> lower
+ * expert id), weights renormalised over the k kept slots, then the drop rule.
+ * Produces the ids / weights operands of latent_moe_ffn_forward.
+ */
+typedef struct latent_route_args {
+  const void* x;         /* [T][d] of x_dtype (unused when logits_in != NULL) */
+  int32_t x_dtype;       /* LATENT_F32 | LATENT_F16 | LATENT_BF16 */
+  const void* router;    /* [d][E] of router_dtype */
+  int32_t router_dtype;  /* LATENT_F32 | LATENT_BF16 */
+  const float* logits_in; /* [T][E] f32, or NULL => computed from x and router */
+  float* logits_out;     /* [T][E] f32 written when not NULL */
+  int32_t* ids;          /* [T][k] out; -1 for a dropped slot */
+  float* weights;        /* [T][k] out */
+  int64_t n_tokens;      /* T */
+  int64_t n_embd;        /* d */
+  int64_t n_expert;      /* E <= 1024 */
+  int64_t n_expert_used; /* k <= 64 and <= E */
+  int32_t drop_rule;     /* LATENT_DROP_* */
+  float drop_param;
+  void* workspace;       /* >= latent_route_workspace_size() bytes, device */
+  size_t workspace_bytes;
+} latent_route_args;
+
+/* Workspace bytes required by latent_route (0 when logits_in is given). */
+int latent_route_workspace_size(const latent_route_args* args, size_t* bytes);
+
+/*
+ * Router logits, softmax, top-k, renormalisation and drop on the device.
+ * No counterpart kernel in the reference: routing belongs to the graph
+ * builder there (build_moe_ffn_latent, README.md:111-113), and the drop rule
+ * to loader/adaptive_topk.py:29-90.  Stream ordered; allocates nothing.
+ */
+int latent_route(const latent_route_args* args, latent_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -2,6 +2,7 @@
 
     from latent_amd import StackedLayer, moe_forward        # MoE layer (ggml op)
     from latent_amd.runtime import load_pair, swiglu_expert # loader/latent_runtime.py
+    from latent_amd import route, Router, DecodeStack        # GPU routing, stacked decode
 
 The compute runs in `liblatent_hip.so` (hand-written HIP for gfx950, C ABI in
 include/latent_ffn.h); torch provides device memory and streams.  Importing
@@ -27,6 +28,8 @@ from .moe import (  # noqa: F401
     unpack,
     workspace_size,
 )
+from .router import Router, route  # noqa: F401
+from .stack import DecodeStack  # noqa: F401
 
 __version__ = "0.1.0"
 

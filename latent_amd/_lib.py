@@ -39,7 +39,13 @@ EXPORTED = (
     "latent_unpack",
     "latent_pack_nf4",
     "latent_pack_int8",
+    "latent_route_workspace_size",
+    "latent_route",
 )
+
+LATENT_DROP_NONE = 0
+LATENT_DROP_BELOW = 1
+LATENT_DROP_INCLUSIVE = 2
 
 
 class LatentFactor(ctypes.Structure):
@@ -82,6 +88,27 @@ class LatentMoeArgs(ctypes.Structure):
     ]
 
 
+class LatentRouteArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_dtype", ctypes.c_int32),
+        ("router", ctypes.c_void_p),
+        ("router_dtype", ctypes.c_int32),
+        ("logits_in", ctypes.c_void_p),
+        ("logits_out", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p),
+        ("weights", ctypes.c_void_p),
+        ("n_tokens", ctypes.c_int64),
+        ("n_embd", ctypes.c_int64),
+        ("n_expert", ctypes.c_int64),
+        ("n_expert_used", ctypes.c_int64),
+        ("drop_rule", ctypes.c_int32),
+        ("drop_param", ctypes.c_float),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class LatentError(RuntimeError):
     def __init__(self, status: int, what: str):
         super().__init__(f"{what}: {status_string(status)} ({status})")
@@ -113,6 +140,10 @@ def _load() -> ctypes.CDLL:
     ]
     lib.latent_pack_int8.restype = ctypes.c_int
     lib.latent_pack_int8.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.latent_route_workspace_size.restype = ctypes.c_int
+    lib.latent_route_workspace_size.argtypes = [ctypes.POINTER(LatentRouteArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.latent_route.restype = ctypes.c_int
+    lib.latent_route.argtypes = [ctypes.POINTER(LatentRouteArgs), ctypes.c_void_p]
     return lib
 
 

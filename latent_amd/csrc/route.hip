@@ -1,0 +1,254 @@
+// Router front end of a LATENT MoE layer on gfx950: logits, softmax, top-k,
+// renormalisation and the optional drop rules, producing the (ids, weights)
+// operands of latent_moe_ffn_forward on the device.
+//
+// The reference leaves routing to the graph builder (build_moe_ffn_latent,
+// README.md:111-113, patch 004 empty) and restates the adaptive drop on the
+// host (loader/adaptive_topk.py:29-90).  Here it is two kernels, so a whole
+// decode layer (route + expert FFN) is stream-ordered device work that a HIP
+// graph can hold:
+//
+//   logits_kernel  partial logits of x . W_r over one 128-row slice of d for a
+//                  64-expert x 32-token tile; slices go to their own slot of the
+//                  workspace (no atomics, fixed summation order).
+//   topk_kernel    one wave per token: sum the slices in slice order (or read
+//                  caller logits), top-k by repeated wave arg-max (ties -> the
+//                  lower expert id), weights exp(l - max) renormalised over the
+//                  kept k, then the drop rule.
+//
+// Work per call: the router matrix is read once per 32-token block (d*E*4 B in
+// fp32 = 7.3 MB at d=7168, E=256) and is HBM-bound; top-k is latency-bound.
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace latent {
+namespace route {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kRows = 128;     // rows of d per logits workgroup
+constexpr int kCols = 64;      // experts per logits workgroup
+constexpr int kTok = 32;       // tokens per logits workgroup
+constexpr int kMaxE = 1024;    // experts: 16 per lane in topk_kernel
+constexpr int kPerLane = kMaxE / kWave;
+constexpr int kMaxK = kWave;  // slot s lives in lane s
+
+struct Params {
+  const void* x;
+  int x_dtype;
+  const void* router;
+  int router_dtype;
+  const float* logits_in;
+  float* logits_out;
+  int32_t* ids;
+  float* weights;
+  float* partial;  // [nslice][T][E]
+  int T, d, E, K, nslice, drop_rule;
+  float drop_param;
+};
+
+__device__ __forceinline__ float load_router(const void* p, int dtype, int64_t i) {
+  if (dtype == LATENT_F32) return static_cast<const float*>(p)[i];
+  return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);  // bf16
+}
+
+// grid (ceil(E/64), nslice, ceil(T/32)); 256 threads.  Thread (wave w, lane c)
+// owns expert column c of the tile and tokens 8w..8w+7.
+__global__ void __launch_bounds__(kThreads) logits_kernel(Params p) {
+  __shared__ float xs[kTok][kRows + 1];
+  __shared__ float ws[kRows][kCols];
+  const int tid = threadIdx.x;
+  const int e0 = blockIdx.x * kCols, r0 = blockIdx.y * kRows, t0 = blockIdx.z * kTok;
+  const int nr = min(kRows, p.d - r0), nt = min(kTok, p.T - t0), ne = min(kCols, p.E - e0);
+  for (int i = tid; i < kRows * kCols; i += kThreads) {
+    const int r = i / kCols, c = i - r * kCols;
+    ws[r][c] = (r < nr && c < ne) ? load_router(p.router, p.router_dtype, static_cast<int64_t>(r0 + r) * p.E + e0 + c)
+                                  : 0.f;
+  }
+  for (int i = tid; i < kTok * kRows; i += kThreads) {
+    const int t = i / kRows, r = i - t * kRows;
+    xs[t][r] = (t < nt && r < nr) ? load_act(p.x, p.x_dtype, static_cast<int64_t>(t0 + t) * p.d + r0 + r) : 0.f;
+  }
+  __syncthreads();
+  const int c = tid & (kWave - 1), tg = (tid >> 6) * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < nr; ++r) {
+    const float w = ws[r][c];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = fmaf(xs[tg + i][r], w, acc[i]);
+  }
+  if (c < ne) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (tg + i < nt)
+        p.partial[(static_cast<int64_t>(blockIdx.y) * p.T + t0 + tg + i) * p.E + e0 + c] = acc[i];
+  }
+}
+
+// Wave arg-max of (v, idx) pairs: larger v wins, equal v -> smaller idx.
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off, kWave);
+    const int oi = __shfl_xor(idx, off, kWave);
+    if (ov > v || (ov == v && oi < idx)) {
+      v = ov;
+      idx = oi;
+    }
+  }
+}
+
+// One wave per token, 4 tokens per 256-thread workgroup.
+__global__ void __launch_bounds__(kThreads) topk_kernel(Params p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
+  if (t >= p.T) return;
+  float l[kPerLane];
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    const int e = j * kWave + lane;
+    float v = -INFINITY;
+    if (e < p.E) {
+      if (p.logits_in) {
+        v = p.logits_in[static_cast<int64_t>(t) * p.E + e];
+      } else {
+        v = 0.f;
+        for (int s = 0; s < p.nslice; ++s) v += p.partial[(static_cast<int64_t>(s) * p.T + t) * p.E + e];
+      }
+      if (p.logits_out) p.logits_out[static_cast<int64_t>(t) * p.E + e] = v;
+      if (v != v) v = -INFINITY;  // NaN never wins a slot
+    }
+    l[j] = v;
+  }
+  // Top-k: k rounds of wave arg-max; a chosen expert is retired with a bit
+  // of `taken`, so it cannot be chosen again even if every logit is -inf.
+  // Lane s keeps the logit and id of slot s.
+  uint32_t taken = 0;
+  float my_l = -INFINITY;
+  int my_e = -1;
+  for (int s = 0; s < p.K; ++s) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const int e = j * kWave + lane;
+      const bool ok = e < p.E && !((taken >> j) & 1u);
+      if (ok && (l[j] > bv || bi == 0x7FFFFFFF)) {
+        bv = l[j];
+        bi = e;
+      }
+    }
+    wave_argmax(bv, bi);
+    if (lane == s) {
+      my_l = bv;
+      my_e = bi;
+    }
+    if (bi != 0x7FFFFFFF && (bi & (kWave - 1)) == lane) taken |= 1u << (bi / kWave);
+  }
+  // Renormalised softmax over the kept k (the full softmax denominator
+  // cancels); sums run serially in slot order.
+  const float m = __shfl(my_l, 0, kWave);
+  float w = lane < p.K ? expf(my_l - m) : 0.f;
+  float wsum = 0.f;
+  for (int s = 0; s < p.K; ++s) wsum += __shfl(w, s, kWave);
+  w = w / wsum;
+  int keep = p.K;
+  if (p.drop_rule == LATENT_DROP_INCLUSIVE) {
+    // loader/adaptive_topk.py:29-55 on the descending top-k scores.
+    float total = 0.f;
+    for (int s = 0; s < p.K; ++s) total += __shfl(w, s, kWave);
+    const float target = p.drop_param * total;
+    float cum = 0.f;
+    for (int s = 0; s < p.K; ++s) {
+      const float ws = __shfl(w, s, kWave);
+      if (cum + ws > target) {
+        keep = s;
+        break;
+      }
+      cum += ws;
+    }
+  }
+  if (lane < p.K) {
+    bool drop = lane >= keep;
+    if (p.drop_rule == LATENT_DROP_BELOW && w < p.drop_param) drop = true;
+    const int64_t o = static_cast<int64_t>(t) * p.K + lane;
+    p.ids[o] = drop ? -1 : my_e;
+    p.weights[o] = drop ? 0.f : w;
+  }
+}
+
+int64_t n_slices(int64_t d) { return (d + kRows - 1) / kRows; }
+
+int validate(const latent_route_args& a) {
+  if (a.n_tokens < 0 || a.n_expert <= 0 || a.n_expert_used <= 0) return LATENT_E_INVALID;
+  if (a.n_expert_used > a.n_expert) return LATENT_E_INVALID;
+  if (a.drop_rule < LATENT_DROP_NONE || a.drop_rule > LATENT_DROP_INCLUSIVE) return LATENT_E_INVALID;
+  if (a.drop_rule == LATENT_DROP_INCLUSIVE && !(a.drop_param > 0.f && a.drop_param <= 1.f)) return LATENT_E_INVALID;
+  if (!a.logits_in) {
+    if (a.n_embd <= 0) return LATENT_E_INVALID;
+    if (a.x_dtype < LATENT_F32 || a.x_dtype > LATENT_BF16) return LATENT_E_INVALID;
+    if (a.router_dtype != LATENT_F32 && a.router_dtype != LATENT_BF16) return LATENT_E_INVALID;
+  }
+  if (a.n_expert > kMaxE || a.n_expert_used > kMaxK) return LATENT_E_UNSUPPORTED;
+  if (a.n_tokens > (1 << 24) || a.n_embd > (1 << 20)) return LATENT_E_UNSUPPORTED;
+  return LATENT_OK;
+}
+
+size_t workspace_bytes(const latent_route_args& a) {
+  if (a.logits_in) return 0;
+  return static_cast<size_t>(n_slices(a.n_embd)) * a.n_tokens * a.n_expert * sizeof(float);
+}
+
+}  // namespace
+}  // namespace route
+}  // namespace latent
+
+using namespace latent;
+
+extern "C" int latent_route_workspace_size(const latent_route_args* args, size_t* bytes) {
+  if (!args || !bytes) return LATENT_E_INVALID;
+  const int st = route::validate(*args);
+  if (st != LATENT_OK) return st;
+  *bytes = route::workspace_bytes(*args);
+  return LATENT_OK;
+}
+
+extern "C" int latent_route(const latent_route_args* args, latent_stream_t stream) {
+  if (!args) return LATENT_E_INVALID;
+  const latent_route_args& a = *args;
+  const int st = route::validate(a);
+  if (st != LATENT_OK) return st;
+  if (a.n_tokens == 0) return LATENT_OK;
+  if (!a.ids || !a.weights) return LATENT_E_INVALID;
+  if (!a.logits_in && (!a.x || !a.router)) return LATENT_E_INVALID;
+  const size_t need = route::workspace_bytes(a);
+  if (need && (!a.workspace || a.workspace_bytes < need)) return LATENT_E_WORKSPACE;
+  route::Params p{};
+  p.x = a.x;
+  p.x_dtype = a.x_dtype;
+  p.router = a.router;
+  p.router_dtype = a.router_dtype;
+  p.logits_in = a.logits_in;
+  p.logits_out = a.logits_out;
+  p.ids = a.ids;
+  p.weights = a.weights;
+  p.partial = static_cast<float*>(a.workspace);
+  p.T = static_cast<int>(a.n_tokens);
+  p.d = static_cast<int>(a.n_embd);
+  p.E = static_cast<int>(a.n_expert);
+  p.K = static_cast<int>(a.n_expert_used);
+  p.nslice = a.logits_in ? 0 : static_cast<int>(route::n_slices(a.n_embd));
+  p.drop_rule = a.drop_rule;
+  p.drop_param = a.drop_param;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  if (!a.logits_in) {
+    const dim3 grid(static_cast<unsigned>((a.n_expert + route::kCols - 1) / route::kCols), static_cast<unsigned>(p.nslice),
+                    static_cast<unsigned>((a.n_tokens + route::kTok - 1) / route::kTok));
+    hipLaunchKernelGGL(route::logits_kernel, grid, dim3(route::kThreads), 0, s, p);
+    if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+  }
+  const unsigned tgrid = static_cast<unsigned>((a.n_tokens + 3) / 4);
+  hipLaunchKernelGGL(route::topk_kernel, dim3(tgrid), dim3(route::kThreads), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}

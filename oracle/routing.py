@@ -65,3 +65,33 @@ def adaptive_topk_inclusive(sorted_scores: np.ndarray, threshold: float = 0.95) 
             return i
         cumulative += score
     return int(scores.size)
+
+
+def router_logits(x: np.ndarray, router: np.ndarray) -> np.ndarray:
+    """x [T, d] . W_r [d, E] in float64 (the GPU sums fp32 products)."""
+    return np.asarray(x, np.float64) @ np.asarray(router, np.float64)
+
+
+def inclusive_drop(ids: np.ndarray, w: np.ndarray, threshold: float):
+    """Per token, keep the leading slots chosen by adaptive_topk_inclusive on the
+    descending top-k weights (adaptive_topk_batch, loader/adaptive_topk.py:58-90);
+    the rest become id -1 / weight 0."""
+    ids = np.array(ids, dtype=np.int32, copy=True)
+    w = np.array(w, dtype=np.float32, copy=True)
+    for t in range(ids.shape[0]):
+        n = adaptive_topk_inclusive(w[t], threshold)
+        ids[t, n:] = -1
+        w[t, n:] = 0.0
+    return ids, w
+
+
+def route(logits: np.ndarray, k: int, drop: str = "none", drop_param: float = 0.0):
+    """softmax_topk followed by the drop rule ('none', 'below', 'inclusive')."""
+    ids, w = softmax_topk(logits, k)
+    if drop == "below":
+        return adaptive_drop(ids, w, drop_param)
+    if drop == "inclusive":
+        return inclusive_drop(ids, w, drop_param)
+    if drop != "none":
+        raise ValueError(drop)
+    return ids, w

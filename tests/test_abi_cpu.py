@@ -126,3 +126,26 @@ def test_codec_entry_points_reject_bad_shapes(L):
     p = buf.ctypes.data + ((-buf.ctypes.data) % 16)
     assert L.lib.latent_pack_nf4(p, 4, 48, p, p, None) == L.LATENT_E_INVALID
     assert L.lib.latent_pack_int8(p, 0, p, p, None) == L.LATENT_E_INVALID
+
+
+def test_route_argument_checks(L):
+    a = L.LatentRouteArgs()
+    a.n_tokens, a.n_embd, a.n_expert, a.n_expert_used = 4, 7168, 256, 8
+    a.x_dtype, a.router_dtype = L.LATENT_BF16, L.LATENT_F32
+    n = ctypes.c_size_t(0)
+    assert L.lib.latent_route_workspace_size(ctypes.byref(a), ctypes.byref(n)) == L.LATENT_OK
+    assert n.value == 56 * 4 * 256 * 4  # one f32 [T][E] slice per 128 rows of d
+    a.logits_in = 16
+    assert L.lib.latent_route_workspace_size(ctypes.byref(a), ctypes.byref(n)) == L.LATENT_OK and n.value == 0
+    for field, value, status in [("n_expert_used", 257, L.LATENT_E_INVALID), ("n_expert", 2048, L.LATENT_E_UNSUPPORTED),
+                                 ("n_expert_used", 65, L.LATENT_E_UNSUPPORTED), ("drop_rule", 7, L.LATENT_E_INVALID)]:
+        b = L.LatentRouteArgs.from_buffer_copy(a)
+        setattr(b, field, value)
+        assert L.lib.latent_route_workspace_size(ctypes.byref(b), ctypes.byref(n)) == status, field
+    b = L.LatentRouteArgs.from_buffer_copy(a)
+    b.drop_rule, b.drop_param = L.LATENT_DROP_INCLUSIVE, 1.5
+    assert L.lib.latent_route(ctypes.byref(b), None) == L.LATENT_E_INVALID
+    b = L.LatentRouteArgs.from_buffer_copy(a)
+    b.logits_in = 0
+    b.router_dtype = L.LATENT_F16  # f16 router matrices are not supported
+    assert L.lib.latent_route(ctypes.byref(b), None) == L.LATENT_E_INVALID

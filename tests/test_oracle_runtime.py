@@ -184,3 +184,27 @@ def test_adaptive_topk_reference_cases():
     assert routing.adaptive_topk_inclusive(np.array([], np.float32), 0.95) == 0
     ids, w = routing.adaptive_drop(np.array([[3, 1, 2]]), np.array([[0.7, 0.26, 0.04]], np.float32), 0.05)
     assert ids.tolist() == [[3, 1, -1]] and w.tolist()[0][2] == 0.0
+
+
+def test_inclusive_drop_matches_per_token_rule():
+    # adaptive_topk_batch (loader/adaptive_topk.py:58-90) keeps a prefix of the
+    # descending scores whose length is adaptive_topk_inclusive of that row.
+    w = np.array([[0.45, 0.22, 0.15, 0.08, 0.05, 0.03], [0.9, 0.05, 0.03, 0.01, 0.005, 0.005]], np.float32)
+    ids = np.arange(12, dtype=np.int32).reshape(2, 6)
+    got_ids, got_w = routing.inclusive_drop(ids, w, 0.95)
+    assert got_ids.tolist() == [[0, 1, 2, 3, -1, -1], [6, -1, -1, -1, -1, -1]]
+    assert got_w[0, 4] == 0.0 and got_w[1, 1:].sum() == 0.0 and got_w[0, 3] == w[0, 3]
+
+
+def test_route_drop_rules_and_logits():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 16))
+    W = rng.standard_normal((16, 10))
+    lg = routing.router_logits(x, W)
+    np.testing.assert_allclose(lg[2, 7], sum(x[2, i] * W[i, 7] for i in range(16)), rtol=1e-12)
+    ids, w = routing.route(lg, 4, "below", 0.2)
+    base_ids, base_w = routing.softmax_topk(lg, 4)
+    assert np.all((ids == -1) == (base_w < np.float32(0.2)))
+    assert np.all(w[ids >= 0] == base_w[ids >= 0])
+    with pytest.raises(ValueError):
+        routing.route(lg, 4, "bogus")
