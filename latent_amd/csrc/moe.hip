@@ -22,6 +22,10 @@
 #include "common.hpp"
 #include "fused.hpp"
 #include "prefill.hpp"
+#include "stream.hpp"
+
+#include <cstdlib>
+#include <cstring>
 
 #include <algorithm>
 
@@ -61,6 +65,10 @@ struct MoeParams {
   float* pair_w;
   float* gu;  // [P][2R]
   float* dl;  // [P][R]
+  int4* unit_info;  // streaming path work units {expert, first pair, pairs, 0} (NULL: not built)
+  int* unit_tok;    // [units][16] token of each unit row (0 past the unit's pairs)
+  int* unit_dst;    // [units][16] token * K + slot
+  float* unit_w;    // [units][16] router weight
   int x_dtype, w_dtype;
   int T, d, ff, E, K, R;
   int wbd, out_mode;
@@ -96,10 +104,12 @@ __device__ __forceinline__ bool map_item(int b, int n_items, int n_active, int& 
 // prep: workgroup 0 groups pairs by expert; the others clear accumulators.
 // ---------------------------------------------------------------------------
 __device__ void route_block(const MoeParams& p) {
-  __shared__ int cnt[kMaxExperts];
+  __shared__ int cnt[kMaxExperts];  // pairs per expert, then the expert's first position
   __shared__ int fill[kMaxExperts];
+  __shared__ int ubase[kMaxExperts];  // first streaming unit of each expert
   __shared__ int scan_c[kRouteThreads];
   __shared__ int scan_a[kRouteThreads];
+  __shared__ int scan_u[kRouteThreads];
   __shared__ int bad;
   const int tid = threadIdx.x;
   const int P = p.T * p.K;
@@ -120,31 +130,49 @@ __device__ void route_block(const MoeParams& p) {
   // Block scan over experts: each thread owns a contiguous run of experts.
   const int per = (p.E + kRouteThreads - 1) / kRouteThreads;
   const int e0 = min(p.E, tid * per), e1 = min(p.E, e0 + per);
-  int sc = 0, sa = 0;
+  int sc = 0, sa = 0, su = 0;
   for (int e = e0; e < e1; ++e) {
     sc += cnt[e];
     sa += cnt[e] > 0;
+    su += (cnt[e] + stream::kMaxM - 1) / stream::kMaxM;
   }
   scan_c[tid] = sc;
   scan_a[tid] = sa;
+  scan_u[tid] = su;
   __syncthreads();
   for (int off = 1; off < kRouteThreads; off <<= 1) {
     const int vc = tid >= off ? scan_c[tid - off] : 0;
     const int va = tid >= off ? scan_a[tid - off] : 0;
+    const int vu = tid >= off ? scan_u[tid - off] : 0;
     __syncthreads();
     scan_c[tid] += vc;
     scan_a[tid] += va;
+    scan_u[tid] += vu;
     __syncthreads();
   }
   int start = scan_c[tid] - sc;
   int act = scan_a[tid] - sa;
+  int unit = scan_u[tid] - su;
   for (int e = e0; e < e1; ++e) {
     const int c = cnt[e];
     fill[e] = start;  // reuse as the running insert position
+    cnt[e] = start;
+    ubase[e] = unit;
     if (c > 0) {
       p.act_expert[act] = e;
       p.act_start[act] = start;
       p.act_count[act] = c;
+      if (p.unit_info) {  // units of at most kMaxM pairs of one expert; rows past the pairs are padding
+        for (int j = 0; j < c; j += stream::kMaxM, ++unit) {
+          const int m = min(stream::kMaxM, c - j);
+          p.unit_info[unit] = make_int4(e, start + j, m, 0);
+          for (int r = m; r < stream::kMaxM; ++r) {
+            p.unit_tok[unit * stream::kMaxM + r] = 0;
+            p.unit_dst[unit * stream::kMaxM + r] = 0;
+            p.unit_w[unit * stream::kMaxM + r] = 0.f;
+          }
+        }
+      }
       ++act;
     }
     start += c;
@@ -153,15 +181,25 @@ __device__ void route_block(const MoeParams& p) {
     p.meta[0] = scan_a[kRouteThreads - 1];
     p.meta[1] = bad;
     p.meta[3] = scan_c[kRouteThreads - 1];  // routed pairs
+    p.meta[4] = scan_u[kRouteThreads - 1];  // streaming work units
   }
   __syncthreads();
   for (int i = tid; i < P; i += kRouteThreads) {
     const int e = p.ids[i];
     if (e >= 0 && e < p.E) {
       const int pos = atomicAdd(&fill[e], 1);
-      p.pair_tok[pos] = i / p.K;
-      p.pair_slot[pos] = i - (i / p.K) * p.K;
-      p.pair_w[pos] = load_act(p.weights, p.w_dtype, i);
+      const int tok = i / p.K, slot = i - (i / p.K) * p.K;
+      const float w = load_act(p.weights, p.w_dtype, i);
+      p.pair_tok[pos] = tok;
+      p.pair_slot[pos] = slot;
+      p.pair_w[pos] = w;
+      if (p.unit_info) {
+        const int rel = pos - cnt[e];
+        const int row = (ubase[e] + rel / stream::kMaxM) * stream::kMaxM + rel % stream::kMaxM;
+        p.unit_tok[row] = tok;
+        p.unit_dst[row] = i;
+        p.unit_w[row] = w;
+      }
     }
   }
 }
@@ -589,7 +627,7 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, hist, gu, dl, total;
+  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, hist, units, gu, dl, total;
 };
 
 // Pairs per chunk of the multi-workgroup grouping: multiples of the block
@@ -615,6 +653,7 @@ Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
   L.pair_slot = off;  off = align_up(off + P * sizeof(int));
   L.pair_w = off;     off = align_up(off + P * sizeof(float));
   L.hist = off;       off = align_up(off + group_chunks(P, E) * (E + 1) * sizeof(int));
+  L.units = off;      off = align_up(off + (4 + 3 * stream::kMaxM) * stream::max_units(P, E) * sizeof(int));
   L.gu = off;         off += P * 2 * R * sizeof(float);  // gu and dl contiguous (one clear)
   L.dl = off;         off = align_up(off + P * R * sizeof(float));
   L.total = off;
@@ -646,6 +685,27 @@ int pick_pow2_chunk(int64_t per_expert_extent, int64_t experts, int64_t target_i
   int c = hi;
   while (c > lo && experts * ((per_expert_extent + c - 1) / c) < target_items) c /= 2;
   return c;
+}
+
+enum { kPathGeneral = 0, kPathFused = 1, kPathPrefill = 2, kPathStream = 3 };
+
+// The implementation for one call shape.  LATENT_MOE_PATH (general | fused |
+// prefill | stream) selects another path that supports the call, for
+// comparisons; the default is the measured fastest supported path.
+int choose_path(const latent_moe_args& a, fused::Plan& pl) {
+  const bool fused_ok = fused::supported(a) && fused::make_plan(a, pl);
+  const bool prefill_ok = prefill::supported(a);
+  const bool stream_ok = stream::supported(a);
+  const char* env = std::getenv("LATENT_MOE_PATH");
+  if (env && *env) {
+    if (!std::strcmp(env, "stream") && stream_ok) return kPathStream;
+    if (!std::strcmp(env, "fused") && fused_ok) return kPathFused;
+    if (!std::strcmp(env, "prefill") && prefill_ok) return kPathPrefill;
+    if (!std::strcmp(env, "general")) return kPathGeneral;
+  }
+  if (fused_ok) return kPathFused;
+  if (prefill_ok) return kPathPrefill;
+  return kPathGeneral;
 }
 
 template <int MB, bool kInt8>
@@ -691,6 +751,7 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   if (prefill::supported(*args)) scratch = std::max(scratch, L.gu + prefill::layout_for(*args).total);
   fused::Plan pl;
   if (fused::supported(*args) && fused::make_plan(*args, pl)) scratch = std::max(scratch, pl.scratch_bytes);
+  if (stream::supported(*args)) scratch = std::max(scratch, L.gu + stream::layout_for(*args).total);
   *bytes = fused::kReserved + scratch;
   return LATENT_OK;
 }
@@ -700,8 +761,7 @@ extern "C" int latent_moe_path(const latent_moe_args* args) {
   const int st = validate(*args);
   if (st != LATENT_OK) return st;
   fused::Plan pl;
-  if (fused::supported(*args) && fused::make_plan(*args, pl)) return 1;
-  return prefill::supported(*args) ? 2 : 0;
+  return choose_path(*args, pl);
 }
 
 extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
@@ -719,8 +779,8 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   (void)hipGetLastError();  // clear a stale error so the checks below see only ours
   fused::Plan pl;
-  if (fused::supported(a) && fused::make_plan(a, pl))
-    return fused::forward(a, s, static_cast<char*>(a.workspace), pl);
+  const int path = choose_path(a, pl);
+  if (path == kPathFused) return fused::forward(a, s, static_cast<char*>(a.workspace), pl);
   const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
 
   MoeParams p{};
@@ -757,9 +817,18 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.out_mode = a.out_mode;
   const int64_t P = a.n_tokens * a.n_expert_used;
   p.a_max = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P)));
-  const bool use_prefill = prefill::supported(a);
-  p.zero_floats = use_prefill ? 0 : P * 3 * a.max_rank;  // the MFMA path writes its intermediates whole
-  p.zero_out = use_prefill ? 0 : 1;                       // and every output row (per-token combine)
+  const bool use_prefill = path == kPathPrefill;
+  const bool use_stream = path == kPathStream;
+  if (use_stream) {
+    const int64_t mu = stream::max_units(P, a.n_expert);
+    p.unit_info = reinterpret_cast<int4*>(ws + L.units);
+    p.unit_tok = reinterpret_cast<int*>(p.unit_info + mu);
+    p.unit_dst = p.unit_tok + mu * stream::kMaxM;
+    p.unit_w = reinterpret_cast<float*>(p.unit_dst + mu * stream::kMaxM);
+  }
+  // The MFMA paths write their intermediates whole, and every output row (per-token combine).
+  p.zero_floats = use_prefill || use_stream ? 0 : P * 3 * a.max_rank;
+  p.zero_out = use_prefill || use_stream ? 0 : 1;
 
   // Work split: enough items to fill 256 CUs even when few experts are routed.
   const int MB = a.n_tokens == 1 ? 1 : 4;
@@ -789,6 +858,10 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   if (use_prefill) {
     const prefill::Grouping g{p.meta, p.act_expert, p.act_start, p.act_count, p.pair_tok, p.pair_slot, p.pair_w};
     return prefill::forward(a, p.fac, g, ws + L.gu, s);
+  }
+  if (use_stream) {
+    const stream::Grouping g{p.meta, p.unit_info, p.unit_tok, p.unit_dst, p.unit_w};
+    return stream::forward(a, p.fac, g, ws + L.gu, s);
   }
   if (MB == 1)
     st = any_int8 ? launch_phases<1, true>(p, s) : launch_phases<1, false>(p, s);

@@ -46,37 +46,76 @@ struct Params {
   float* partial;  // [nslice][T][E]
   int T, d, E, K, nslice, drop_rule;
   float drop_param;
+  bool vec_router, vec_x;  // 4-element vector loads allowed (alignment, row length)
 };
 
-__device__ __forceinline__ float load_router(const void* p, int dtype, int64_t i) {
-  if (dtype == LATENT_F32) return static_cast<const float*>(p)[i];
-  return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);  // bf16
+// Four consecutive elements [i, i+4) of a row of `n` elements (f32 / f16 /
+// bf16), zero beyond n.  `vec`: the row start and i are 4-element aligned and
+// the base is 16-byte (f32) or 8-byte (16-bit types) aligned.
+__device__ __forceinline__ float4 load4(const void* base, int dtype, int64_t row_off, int i, int n, bool vec) {
+  float v[4];
+  if (vec && i + 4 <= n) {
+    if (dtype == LATENT_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + row_off + i);
+    const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + row_off + i);
+    const uint32_t h[4] = {u.x & 0xFFFFu, u.x >> 16, u.y & 0xFFFFu, u.y >> 16};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      v[q] = dtype == LATENT_BF16 ? __uint_as_float(h[q] << 16) : half_bits_to_float(static_cast<uint16_t>(h[q]));
+    return make_float4(v[0], v[1], v[2], v[3]);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = i + q < n ? load_act(base, dtype, row_off + i + q) : 0.f;
+  return make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// grid (ceil(E/64), nslice, ceil(T/32)); 256 threads.  Thread (wave w, lane c)
-// owns expert column c of the tile and tokens 8w..8w+7.
+// grid (ceil(E/64), nslice, ceil(T/32)); 256 threads.  Every thread issues its
+// 8 router chunks and 4 activation chunks (4 elements each) before the first
+// LDS store, so a workgroup costs about one memory round trip.  Thread (wave
+// w, lane c) then owns expert column c of the tile and tokens 8w..8w+7.
 __global__ void __launch_bounds__(kThreads) logits_kernel(Params p) {
-  __shared__ float xs[kTok][kRows + 1];
+  __shared__ float xs[kTok][kRows + 4];
   __shared__ float ws[kRows][kCols];
   const int tid = threadIdx.x;
   const int e0 = blockIdx.x * kCols, r0 = blockIdx.y * kRows, t0 = blockIdx.z * kTok;
   const int nr = min(kRows, p.d - r0), nt = min(kTok, p.T - t0), ne = min(kCols, p.E - e0);
-  for (int i = tid; i < kRows * kCols; i += kThreads) {
-    const int r = i / kCols, c = i - r * kCols;
-    ws[r][c] = (r < nr && c < ne) ? load_router(p.router, p.router_dtype, static_cast<int64_t>(r0 + r) * p.E + e0 + c)
-                                  : 0.f;
+  constexpr int kWChunks = kRows * kCols / 4 / kThreads;  // 8
+  constexpr int kXChunks = kTok * kRows / 4 / kThreads;   // 4
+  float4 wv[kWChunks], xv[kXChunks];
+#pragma unroll
+  for (int u = 0; u < kWChunks; ++u) {
+    const int i = tid + u * kThreads, r = i / (kCols / 4), c = (i % (kCols / 4)) * 4;
+    wv[u] = r < nr ? load4(p.router, p.router_dtype, static_cast<int64_t>(r0 + r) * p.E + e0, c, ne, p.vec_router)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (int i = tid; i < kTok * kRows; i += kThreads) {
-    const int t = i / kRows, r = i - t * kRows;
-    xs[t][r] = (t < nt && r < nr) ? load_act(p.x, p.x_dtype, static_cast<int64_t>(t0 + t) * p.d + r0 + r) : 0.f;
+#pragma unroll
+  for (int u = 0; u < kXChunks; ++u) {
+    const int i = tid + u * kThreads, t = i / (kRows / 4), r = (i % (kRows / 4)) * 4;
+    xv[u] = t < nt ? load4(p.x, p.x_dtype, static_cast<int64_t>(t0 + t) * p.d + r0, r, nr, p.vec_x)
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int u = 0; u < kWChunks; ++u) {
+    const int i = tid + u * kThreads, r = i / (kCols / 4), c = (i % (kCols / 4)) * 4;
+    *reinterpret_cast<float4*>(&ws[r][c]) = wv[u];
+  }
+#pragma unroll
+  for (int u = 0; u < kXChunks; ++u) {
+    const int i = tid + u * kThreads, t = i / (kRows / 4), r = (i % (kRows / 4)) * 4;
+    *reinterpret_cast<float4*>(&xs[t][r]) = xv[u];
   }
   __syncthreads();
   const int c = tid & (kWave - 1), tg = (tid >> 6) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < nr; ++r) {
-    const float w = ws[r][c];
+  for (int r = 0; r < kRows; r += 4) {  // rows beyond nr hold zeros
+    const float w0 = ws[r][c], w1 = ws[r + 1][c], w2 = ws[r + 2][c], w3 = ws[r + 3][c];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = fmaf(xs[tg + i][r], w, acc[i]);
+    for (int i = 0; i < 8; ++i) {
+      const float4 xq = *reinterpret_cast<const float4*>(&xs[tg + i][r]);
+      acc[i] = fmaf(xq.x, w0, acc[i]);
+      acc[i] = fmaf(xq.y, w1, acc[i]);
+      acc[i] = fmaf(xq.z, w2, acc[i]);
+      acc[i] = fmaf(xq.w, w3, acc[i]);
+    }
   }
   if (c < ne) {
 #pragma unroll
@@ -98,22 +137,43 @@ __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
   }
 }
 
-// One wave per token, 4 tokens per 256-thread workgroup.
+// One token per 256-thread workgroup.  Wave w sums slices w, w+4, ... of the
+// partial logits (loads of 4 slices in flight), the waves' sums are added in
+// wave order through LDS, and wave 0 selects the top k.
 __global__ void __launch_bounds__(kThreads) topk_kernel(Params p) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int t = blockIdx.x * (kThreads / kWave) + (threadIdx.x >> 6);
-  if (t >= p.T) return;
+  __shared__ float red[kThreads / kWave][kMaxE];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int t = blockIdx.x;
+  const int nj = (p.E + kWave - 1) / kWave;
+  if (!p.logits_in) {
+    float acc[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) acc[j] = 0.f;
+#pragma unroll 4
+    for (int s = wave; s < p.nslice; s += kThreads / kWave) {
+      const float* src = p.partial + (static_cast<int64_t>(s) * p.T + t) * p.E;
+#pragma unroll
+      for (int j = 0; j < kPerLane; ++j)
+        if (j < nj && j * kWave + lane < p.E) acc[j] += src[j * kWave + lane];
+    }
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      if (j < nj) red[wave][j * kWave + lane] = acc[j];
+    __syncthreads();
+  }
+  if (wave != 0) return;
   float l[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) {
     const int e = j * kWave + lane;
     float v = -INFINITY;
-    if (e < p.E) {
+    if (j < nj && e < p.E) {
       if (p.logits_in) {
         v = p.logits_in[static_cast<int64_t>(t) * p.E + e];
       } else {
-        v = 0.f;
-        for (int s = 0; s < p.nslice; ++s) v += p.partial[(static_cast<int64_t>(s) * p.T + t) * p.E + e];
+        v = red[0][e];
+#pragma unroll
+        for (int w = 1; w < kThreads / kWave; ++w) v += red[w][e];
       }
       if (p.logits_out) p.logits_out[static_cast<int64_t>(t) * p.E + e] = v;
       if (v != v) v = -INFINITY;  // NaN never wins a slot
@@ -240,6 +300,11 @@ extern "C" int latent_route(const latent_route_args* args, latent_stream_t strea
   p.nslice = a.logits_in ? 0 : static_cast<int>(route::n_slices(a.n_embd));
   p.drop_rule = a.drop_rule;
   p.drop_param = a.drop_param;
+  auto aligned = [](const void* q, int dtype) {
+    return (reinterpret_cast<uintptr_t>(q) & (dtype == LATENT_F32 ? 15u : 7u)) == 0;
+  };
+  p.vec_router = a.router && a.n_expert % 4 == 0 && aligned(a.router, a.router_dtype);
+  p.vec_x = a.x && a.n_embd % 4 == 0 && aligned(a.x, a.x_dtype);
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   if (!a.logits_in) {
@@ -248,7 +313,6 @@ extern "C" int latent_route(const latent_route_args* args, latent_stream_t strea
     hipLaunchKernelGGL(route::logits_kernel, grid, dim3(route::kThreads), 0, s, p);
     if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   }
-  const unsigned tgrid = static_cast<unsigned>((a.n_tokens + 3) / 4);
-  hipLaunchKernelGGL(route::topk_kernel, dim3(tgrid), dim3(route::kThreads), 0, s, p);
+  hipLaunchKernelGGL(route::topk_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(route::kThreads), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }

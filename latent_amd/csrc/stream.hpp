@@ -1,0 +1,33 @@
+// Host interface of the streaming MFMA decode path (stream.hip).
+#pragma once
+
+#include "common.hpp"
+
+namespace latent {
+namespace stream {
+
+constexpr int kMaxM = 16;  // routed pairs per work unit (the MFMA row count)
+
+// Token grouping produced by the prep kernel (moe.hip), all device pointers.
+// Pairs are grouped by expert; a work unit is a run of at most kMaxM
+// consecutive grouped pairs of one expert.
+struct Grouping {
+  const int* meta;         // [3] routed pairs, [4] work units
+  const int4* unit_info;   // [units] {expert, first grouped pair, pairs (1..kMaxM), 0}
+  const int* unit_tok;     // [units][kMaxM] token of each row (0 past the unit's pairs)
+  const int* unit_dst;     // [units][kMaxM] token * K + slot
+  const float* unit_w;     // [units][kMaxM] router weight
+};
+
+struct Layout {
+  size_t partA, lat, gu, partC, dlat, ybuf, total;
+};
+
+bool supported(const latent_moe_args& a);
+// Upper bound of work units: every active expert contributes ceil(n_e / kMaxM).
+int64_t max_units(int64_t pairs, int64_t experts);
+Layout layout_for(const latent_moe_args& a);
+int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char* scratch, hipStream_t s);
+
+}  // namespace stream
+}  // namespace latent

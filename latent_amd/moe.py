@@ -240,8 +240,9 @@ def workspace_size(layer: StackedLayer, n_tokens: int, n_expert_used: int) -> in
 
 
 def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
-    """'fused' (one persistent decode kernel), 'prefill' (grouped MFMA) or 'general'
-    (multi-kernel GEMV) for this call shape."""
+    """'fused' (one persistent decode kernel), 'prefill' (grouped MFMA), 'stream'
+    (streaming MFMA decode) or 'general' (multi-kernel GEMV) for this call shape
+    (LATENT_MOE_PATH in the environment selects another supported path)."""
     a = layer.args()
     a.x = x.data_ptr()
     a.n_tokens, a.n_expert_used = int(x.shape[0]), int(n_expert_used)
@@ -249,7 +250,7 @@ def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
     r = lib.latent_moe_path(ctypes.byref(a))
     if r < 0:
         check(r, "latent_moe_path")
-    return {1: "fused", 2: "prefill"}.get(r, "general")
+    return {1: "fused", 2: "prefill", 3: "stream"}.get(r, "general")
 
 
 def moe_forward(
