@@ -138,10 +138,13 @@ int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 
 /*
  * Which implementation latent_moe_ffn_forward uses for these arguments:
- * 1 = single persistent decode kernel (32 to 512 routed pairs, up to 512
- * experts, rank 512), 2 = grouped fp16-MFMA prefill (at least 16 routed pairs
- * per active expert, no INT8 groups), 0 = multi-kernel GEMV path; < 0 =
- * LATENT_E_* for bad arguments.
+ * 2 = grouped fp16-MFMA prefill (at least 16 routed pairs per active expert,
+ * no INT8 groups), 3 = streaming fp16-MFMA decode (32 to 4096 routed pairs,
+ * rank 256, d and ff multiples of 256, no INT8 groups), 1 = single persistent
+ * fp32 decode kernel (32 to 512 routed pairs), 0 = multi-kernel fp32 GEMV
+ * path; < 0 = LATENT_E_* for bad arguments.  The environment variable
+ * LATENT_MOE_PATH (general | fused | prefill | stream) selects another path
+ * that supports the call, for comparisons.
  * Diagnostic only; no counterpart in the reference.
  */
 int latent_moe_path(const latent_moe_args* args);

@@ -68,6 +68,7 @@ struct Params {
   float* dlat;   // [P][256]
   float* ybuf;   // [T*K][d]
   int x_dtype, T, K, E, d, ff, P, wbd, out_mode;
+  int umax;  // units the unit tables hold
   int nks, nbs, nkc, nds;  // slices: A (d/256), B (ff/256), C (ff/256), D (d/256)
 };
 
@@ -153,13 +154,20 @@ __device__ __forceinline__ int items_per_unit(const Params& p) {
 // that waiting for the activations leaves the code loads in flight and each K
 // step waits only for its own rows.
 template <int kPhase>
-__global__ void __launch_bounds__(kT) item_kernel(Params p) {
+__global__ void __launch_bounds__(kT, 5) item_kernel(Params p) {
   __shared__ ItemSmem sm;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Items of a unit are numbered in blocks of 8 (padded); block g runs on XCD
+  // g % 8 (workgroup b runs on XCD b % 8), so the 8 column slices that share
+  // each 128-byte line of scales (phases B and D) are read through one L2.
   const int per = items_per_unit<kPhase>(p);
-  const int unit = blockIdx.x / per;
-  const int sub = blockIdx.x - unit * per;
+  const int per_pad = (per + 7) & ~7;
+  const int b = blockIdx.x, k = b >> 3;
+  const int item = (((k >> 3) << 3) + (b & 7)) * 8 + (k & 7);
+  const int unit = item / per_pad;
+  const int sub = item - unit * per_pad;
+  if (sub >= per || unit >= p.umax) return;
   // Row tables do not depend on unit_info: load them alongside it.
   const int arow = tid >> 4;  // activation row of this thread (16 columns each)
   int atok = 0;
@@ -526,13 +534,17 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   p.nkc = p.ff / kK;
   p.nds = p.d / kN;
   const unsigned U = static_cast<unsigned>(max_units(p.P, a.n_expert));
+  p.umax = static_cast<int>(U);
   auto red_grid = [](int64_t n4) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(2048, (n4 + kT - 1) / kT))); };
-  hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(U * 2 * p.nks), dim3(kT), 0, s, p);
+  // Grids cover every unit's items padded to blocks of 8, rounded to 64
+  // workgroups (a whole block of 8 per XCD).
+  auto item_grid = [&](int64_t per) { return static_cast<unsigned>((U * ((per + 7) / 8 * 8) + 63) / 64 * 64); };
+  hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nks)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(reduce_a_kernel, dim3(red_grid(2LL * p.P * (kN / 4))), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(U * 2 * p.nbs), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(U * p.nkc), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(item_grid(2 * p.nbs)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(item_grid(p.nkc)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(reduce_c_kernel, dim3(red_grid(static_cast<int64_t>(p.P) * (kN / 4))), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(U * p.nds), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(item_grid(p.nds)), dim3(kT), 0, s, p);
   if (a.out_mode == LATENT_OUT_REDUCED)
     hipLaunchKernelGGL(combine_kernel, dim3(red_grid(static_cast<int64_t>(p.T) * p.d / 4)), dim3(kT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;

@@ -181,24 +181,34 @@ def dsv3(gpu):
     return gsynth.make_layer(seed=7, n_expert=256, d=7168, ff=2048, max_rank=256)
 
 
+@pytest.mark.parametrize("path", ["default", "fused"])
 @pytest.mark.parametrize("B", [1, 8, 32, 64])
-def test_dsv3_decode_parity(gpu, dsv3, B):
+def test_dsv3_decode_parity(gpu, dsv3, B, path, monkeypatch):
     import torch
 
     from latent_amd import synth as gsynth
+
+    if path != "default":
+        monkeypatch.setenv("LATENT_MOE_PATH", path)
 
     ids_t, w_t = gsynth.route(seed=1000 + B, n_tokens=B, n_expert=256, k=8)
     x_t = gsynth.bf16_input(seed=2000 + B, n_tokens=B, d=7168)
     out = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
     torch.cuda.synchronize()
     # A second call must reproduce the first: bit for bit on the persistent
-    # decode kernel (fixed summation order, control block left as found); the
-    # multi-kernel path accumulates with float atomics, so only to rounding.
+    # decode kernel (fixed summation order, control block left as found) and
+    # the streaming path (fixed-order reductions); the multi-kernel path
+    # accumulates with float atomics, so only to rounding.
     again = gpu.moe_forward(x_t, ids_t, w_t, dsv3)
     torch.cuda.synchronize()
     from latent_amd.moe import moe_path, workspace_error
 
-    if moe_path(dsv3, x_t, 8) == "fused":
+    used = moe_path(dsv3, x_t, 8)
+    if path == "fused":
+        assert used == ("fused" if B >= 4 else "general")
+    else:
+        assert used == ("stream" if B >= 4 else "general")
+    if used in ("fused", "stream"):
         assert torch.equal(out, again)
     else:
         assert torch.allclose(out, again, rtol=1e-5, atol=1e-6 * out.abs().max().item())
@@ -209,7 +219,7 @@ def test_dsv3_decode_parity(gpu, dsv3, B):
     host = subset_to_host(dsv3, experts)
     want = ref.moe_forward(x, local, w, host)
     err = ref.rel_l2(want, out.cpu().numpy())
-    print(f"dsv3 decode B={B} experts={experts.size} rel_l2={err:.3e}")
+    print(f"dsv3 decode B={B} path={used} experts={experts.size} rel_l2={err:.3e}")
     assert err <= TOL
 
 

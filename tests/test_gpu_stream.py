@@ -24,8 +24,8 @@ def stream_path(monkeypatch):
 
 @pytest.fixture(scope="module")
 def small_layer():
-    # Rank 256 with d and ff multiples of 256: the shapes the streaming path takes.
-    return synth.make_layer(seed=410, n_expert=12, d=512, ff=768, max_rank=256)
+    # Rank 256 with d and ff multiples of 512: the shapes the streaming path takes.
+    return synth.make_layer(seed=410, n_expert=12, d=1024, ff=1024, max_rank=256)
 
 
 @pytest.fixture(scope="module")
@@ -52,7 +52,7 @@ def _run(gpu, dev, x, ids, w, x_dtype="bf16", wbd=False, mode=0):
 @pytest.mark.parametrize("mode", [0, 1])
 def test_stream_small_layer(gpu, stream_path, small_layer, small_dev, T, k, mode):
     rng = np.random.default_rng(T * 10 + k)
-    x = rng.standard_normal((T, 512)).astype(np.float32)
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
     ids, w = routing.softmax_topk(rng.standard_normal((T, 12)), k)
     got, xq = _run(gpu, small_dev, x, ids, w, mode=mode)
     want = ref.moe_forward(xq, ids, w, small_layer, out_mode=mode)
@@ -64,7 +64,7 @@ def test_stream_small_layer(gpu, stream_path, small_layer, small_dev, T, k, mode
 @pytest.mark.parametrize("x_dtype,wbd", [("f32", True), ("f16", False), ("bf16", True)])
 def test_stream_dtypes_and_weighting(gpu, stream_path, small_layer, small_dev, x_dtype, wbd):
     rng = np.random.default_rng(77)
-    x = (rng.standard_normal((9, 512)) * 3.0).astype(np.float32)
+    x = (rng.standard_normal((9, 1024)) * 3.0).astype(np.float32)
     ids, w = routing.softmax_topk(rng.standard_normal((9, 12)), 3)
     for mode in (0, 1):
         got, xq = _run(gpu, small_dev, x, ids, w, x_dtype=x_dtype, wbd=wbd, mode=mode)
@@ -77,7 +77,7 @@ def test_stream_units_dropped_duplicate_and_invalid(gpu, stream_path, small_laye
     # dropped slots, an id beyond E, and a duplicated expert within a token.
     rng = np.random.default_rng(5)
     T = 40
-    x = rng.standard_normal((T, 512)).astype(np.float32)
+    x = rng.standard_normal((T, 1024)).astype(np.float32)
     ids, w = routing.softmax_topk(rng.standard_normal((T, 12)), 4)
     ids[:, 0] = 3
     ids[0, 1] = -1
@@ -96,7 +96,7 @@ def test_stream_all_dropped(gpu, stream_path, small_dev):
 
     ids = -np.ones((4, 2), np.int32)
     w = np.zeros((4, 2), np.float32)
-    got, _ = _run(gpu, small_dev, np.ones((4, 512), np.float32), ids, w)
+    got, _ = _run(gpu, small_dev, np.ones((4, 1024), np.float32), ids, w)
     assert not got.any()
     torch.cuda.synchronize()
 
