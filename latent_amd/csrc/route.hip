@@ -70,11 +70,15 @@ __device__ __forceinline__ float4 load4(const void* base, int dtype, int64_t row
 
 // grid (ceil(E/64), nslice, ceil(T/32)); 256 threads.  Every thread issues its
 // 8 router chunks and 4 activation chunks (4 elements each) before the first
-// LDS store, so a workgroup costs about one memory round trip.  Thread (wave
-// w, lane c) then owns expert column c of the tile and tokens 8w..8w+7.
+// LDS store, so a workgroup costs about one memory round trip.  The 32 x 64
+// tile is then computed on fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32
+// products and accumulation): wave w owns experts 16w..16w+15 and both
+// 16-token halves, 32 steps of 4 rows.
+typedef float float4v __attribute__((ext_vector_type(4)));
+constexpr int kWPitch = kCols + 4;  // router tile row pitch (floats): fewer bank conflicts
 __global__ void __launch_bounds__(kThreads) logits_kernel(Params p) {
   __shared__ float xs[kTok][kRows + 4];
-  __shared__ float ws[kRows][kCols];
+  __shared__ float ws[kRows][kWPitch];
   const int tid = threadIdx.x;
   const int e0 = blockIdx.x * kCols, r0 = blockIdx.y * kRows, t0 = blockIdx.z * kTok;
   const int nr = min(kRows, p.d - r0), nt = min(kTok, p.T - t0), ne = min(kCols, p.E - e0);
@@ -104,24 +108,26 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(Params p) {
     *reinterpret_cast<float4*>(&xs[t][r]) = xv[u];
   }
   __syncthreads();
-  const int c = tid & (kWave - 1), tg = (tid >> 6) * 8;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < kRows; r += 4) {  // rows beyond nr hold zeros
-    const float w0 = ws[r][c], w1 = ws[r + 1][c], w2 = ws[r + 2][c], w3 = ws[r + 3][c];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 xq = *reinterpret_cast<const float4*>(&xs[tg + i][r]);
-      acc[i] = fmaf(xq.x, w0, acc[i]);
-      acc[i] = fmaf(xq.y, w1, acc[i]);
-      acc[i] = fmaf(xq.z, w2, acc[i]);
-      acc[i] = fmaf(xq.w, w3, acc[i]);
-    }
+  // Lane l: A = x[16h + l % 16][k + l / 16], B = W[k + l / 16][16w + l % 16];
+  // C lane l holds rows 4 (l / 16) .. + 3 of column l % 16.
+  const int lane = tid & (kWave - 1), w = tid >> 6;
+  const int lr = lane & 15, lk = lane >> 4;
+  float4v acc[2] = {float4v{0.f, 0.f, 0.f, 0.f}, float4v{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll 8
+  for (int k = 0; k < kRows; k += 4) {  // rows beyond nr hold zeros
+    const float b = ws[k + lk][w * 16 + lr];
+    acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[lr][k + lk], b, acc[0], 0, 0, 0);
+    acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[16 + lr][k + lk], b, acc[1], 0, 0, 0);
   }
+  const int c = w * 16 + lr;
   if (c < ne) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (tg + i < nt)
-        p.partial[(static_cast<int64_t>(blockIdx.y) * p.T + t0 + tg + i) * p.E + e0 + c] = acc[i];
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = h * 16 + lk * 4 + i;
+        if (t < nt) p.partial[(static_cast<int64_t>(blockIdx.y) * p.T + t0 + t) * p.E + e0 + c] = acc[h][i];
+      }
   }
 }
 
@@ -137,48 +143,40 @@ __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
   }
 }
 
-// One token per 256-thread workgroup.  Wave w sums slices w, w+4, ... of the
-// partial logits (loads of 4 slices in flight), the waves' sums are added in
-// wave order through LDS, and wave 0 selects the top k.
+// One token per 256-thread workgroup.  Thread e sums the slices of expert e
+// (all loads in flight at once, added in slice order) into LDS; wave 0 then
+// selects the top k.
 __global__ void __launch_bounds__(kThreads) topk_kernel(Params p) {
-  __shared__ float red[kThreads / kWave][kMaxE];
+  __shared__ float lg[kMaxE];
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int t = blockIdx.x;
   const int nj = (p.E + kWave - 1) / kWave;
-  if (!p.logits_in) {
-    float acc[kPerLane];
+  for (int e = threadIdx.x; e < p.E; e += kThreads) {
+    float v;
+    if (p.logits_in) {
+      v = p.logits_in[static_cast<int64_t>(t) * p.E + e];
+    } else {
+      const float* src = p.partial + static_cast<int64_t>(t) * p.E + e;
+      const int64_t stride = static_cast<int64_t>(p.T) * p.E;
+      float part[16];
+      v = 0.f;
+      for (int s0 = 0; s0 < p.nslice; s0 += 16) {
 #pragma unroll
-    for (int j = 0; j < kPerLane; ++j) acc[j] = 0.f;
-#pragma unroll 4
-    for (int s = wave; s < p.nslice; s += kThreads / kWave) {
-      const float* src = p.partial + (static_cast<int64_t>(s) * p.T + t) * p.E;
+        for (int i = 0; i < 16; ++i) part[i] = s0 + i < p.nslice ? src[(s0 + i) * stride] : 0.f;
 #pragma unroll
-      for (int j = 0; j < kPerLane; ++j)
-        if (j < nj && j * kWave + lane < p.E) acc[j] += src[j * kWave + lane];
+        for (int i = 0; i < 16; ++i) v += part[i];
+      }
     }
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j)
-      if (j < nj) red[wave][j * kWave + lane] = acc[j];
-    __syncthreads();
+    if (p.logits_out) p.logits_out[static_cast<int64_t>(t) * p.E + e] = v;
+    lg[e] = v != v ? -INFINITY : v;  // NaN never wins a slot
   }
+  __syncthreads();
   if (wave != 0) return;
   float l[kPerLane];
 #pragma unroll
   for (int j = 0; j < kPerLane; ++j) {
     const int e = j * kWave + lane;
-    float v = -INFINITY;
-    if (j < nj && e < p.E) {
-      if (p.logits_in) {
-        v = p.logits_in[static_cast<int64_t>(t) * p.E + e];
-      } else {
-        v = red[0][e];
-#pragma unroll
-        for (int w = 1; w < kThreads / kWave; ++w) v += red[w][e];
-      }
-      if (p.logits_out) p.logits_out[static_cast<int64_t>(t) * p.E + e] = v;
-      if (v != v) v = -INFINITY;  // NaN never wins a slot
-    }
-    l[j] = v;
+    l[j] = (j < nj && e < p.E) ? lg[e] : -INFINITY;
   }
   // Top-k: k rounds of wave arg-max; a chosen expert is retired with a bit
   // of `taken`, so it cannot be chosen again even if every logit is -inf.
