@@ -226,18 +226,24 @@ def cpu_baseline(torch, layer, routes, xs, batch, min_seconds):
     }
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "fused_kernel_decode_b64_hbm_traffic.md")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+TRAFFIC_PROFILE = {
+    "stream": ("streaming_decode_b64_hbm_traffic.md", "traffic_bytes_per_step:"),
+    "fused": ("fused_kernel_decode_b64_hbm_traffic.md", "traffic_bytes_per_launch:"),
+}
 
 
-def measured_traffic():
-    """HBM bytes per fused_kernel launch at batch 64 from the committed counter
-    summary (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a
-    1 GiB copy), or None when the summary is absent."""
+def measured_traffic(path):
+    """HBM bytes per batch-64 step of `path` from the committed counter summary
+    (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled by a 1 GiB
+    copy), or None when there is none."""
+    name, key = TRAFFIC_PROFILE.get(path, (None, None))
+    if name is None:
+        return None
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(os.path.join(PROFILES, name)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key):
                     return float(line.split(":", 1)[1])
     except OSError:
         pass
@@ -302,7 +308,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "fp16" if head["path"] in ("stream", "prefill") else "f32",  # fp16 MFMA operands, fp32 accumulation
         "data": "synthetic (seeded closed-form low-rank factors packed NF4 g32 on the GPU; bf16 N(0,1) tokens; "
                 "softmax top-8 routing)",
         "config": {
@@ -317,10 +323,13 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": head["roofline_frac"],
-            "traffic": measured_traffic() if head["path"] == "fused" and args.batch == 64 else None,
-            "traffic_source": "profiles/fused_kernel_decode_b64_hbm_traffic.md (rocprofv3 --pmc)",
-            "kernel": ("fused_kernel (one launch per step)" if head["path"] == "fused"
-                       else "latent_moe_ffn_forward (prep + 3 phase kernels per step)"),
+            "traffic": measured_traffic(head["path"]) if args.batch == 64 else None,
+            "traffic_source": "profiles/%s (rocprofv3 --pmc)" % TRAFFIC_PROFILE.get(head["path"], ("none",))[0],
+            "kernel": {
+                "stream": "latent_moe_ffn_forward, streaming MFMA path: prep + 4 item kernels + 2 reductions + combine "
+                          "(8 launches per step; the step is the unit)",
+                "fused": "fused_kernel (one launch per step)",
+            }.get(head["path"], "latent_moe_ffn_forward (prep + 3 phase kernels per step)"),
             "bytes_per_launch": head["bytes_per_step"],
         },
         "cpu_baseline": cpu,
