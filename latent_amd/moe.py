@@ -189,14 +189,19 @@ class StackedLayer:
         """From the writer's tensor names (loader/write_latent_gguf.py:72-74, 256-265).
 
         Keys `blk.{layer}.ffn_latent_{kind}_{a,b}` (codes) and `..._{a,b}_s`
-        (scales), plus optional `blk.{layer}.ffn_latent_ranks`; with layer=None
+        (scales), optional `..._{a,b}_i8map / _i8off / _i8` (per-group INT8
+        extension), plus optional `blk.{layer}.ffn_latent_ranks`; with layer=None
         the `blk.N.ffn_latent_` prefix is omitted.  Ranks are widened to int32
         (the writer's uint8 table cannot hold 256 or 512).
         """
         prefix = "" if layer is None else f"blk.{layer}.ffn_latent_"
         facs = {}
         for name in FACTOR_NAMES:
-            facs[name] = DeviceFactor.from_numpy(arrays[prefix + name], arrays[prefix + name + "_s"], device=device)
+            key = prefix + name
+            ext = None
+            if key + "_i8map" in arrays:  # per-group INT8 extension (see latent_amd.gguf)
+                ext = (arrays[key + "_i8map"], arrays[key + "_i8off"], arrays[key + "_i8"])
+            facs[name] = DeviceFactor.from_numpy(arrays[key], arrays[key + "_s"], ext, device=device)
         ranks = arrays.get(prefix + "ranks")
         rt = None if ranks is None else torch.from_numpy(np.asarray(ranks).astype(np.int32)).to(device)
         return cls(**facs, ranks=rt)

@@ -135,3 +135,22 @@ def test_stream_dsv3_decode(gpu, stream_path, dsv3, B):
     err = ref.rel_l2(want, out.cpu().numpy())
     print(f"stream dsv3 B={B} experts={experts.size} rel_l2={err:.3e}")
     assert err <= TOL
+
+
+def test_gguf_round_trip_layer_gives_identical_outputs(gpu, small_dev, tmp_path):
+    """A device layer written to GGUF and read back computes bit-identical outputs."""
+    import torch
+
+    from latent_amd import StackedLayer, gguf
+
+    path = tmp_path / "layer.gguf"
+    gguf.write_latent_gguf(path, {5: gguf.layer_to_arrays(small_dev)}, max_rank=256)
+    back = StackedLayer.from_arrays(gguf.read_latent_gguf(path).layer_arrays(5), layer=5)
+    rng = np.random.default_rng(8)
+    x = torch.from_numpy(rng.standard_normal((6, 1024)).astype(np.float32)).cuda().to(torch.bfloat16)
+    ids, w = routing.softmax_topk(rng.standard_normal((6, 12)), 6)
+    it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
+    a = gpu.moe_forward(x, it, wt, small_dev)
+    b = gpu.moe_forward(x, it, wt, back)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
