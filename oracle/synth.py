@@ -126,3 +126,31 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     return r.astype(np.uint32).view(np.float32)
+
+
+def randomized_svd(matrix: np.ndarray, target_rank: int, oversample: int = 16, power_iterations: int = 1,
+                   seed: int = 0):
+    """numpy restatement of randomized_svd (loader/latent_loader.py:66-86): same
+    sketch draw, power iteration, reduced QR and SVD of the projection."""
+    m, n = matrix.shape
+    rank = min(target_rank, m, n)
+    sketch = min(rank + oversample, m, n)
+    omega = np.random.default_rng(seed).standard_normal((n, sketch), dtype=np.float32)
+    y = matrix @ omega
+    for _ in range(power_iterations):
+        y = matrix @ (matrix.T @ y)
+    q, _ = np.linalg.qr(y, mode="reduced")
+    u_hat, s, vt = np.linalg.svd(q.T @ matrix, full_matrices=False)
+    return (q @ u_hat)[:, :rank], s[:rank], vt[:rank, :]
+
+
+def choose_rank(singular_values: np.ndarray, energy: float, min_rank: int, max_rank: int) -> int:
+    """numpy restatement of choose_rank (loader/latent_loader.py:89-97)."""
+    if not 0 < energy <= 1:
+        raise ValueError("energy must be in (0, 1]")
+    s = np.asarray(singular_values, np.float64)
+    total = float(np.sum(s ** 2))
+    if total == 0:
+        return min_rank
+    rank = int(np.searchsorted(np.cumsum(s ** 2) / total, energy) + 1)
+    return max(min_rank, min(rank, max_rank, s.size))
