@@ -103,23 +103,61 @@ __device__ __forceinline__ bool map_item(int b, int n_items, int n_active, int& 
 // ---------------------------------------------------------------------------
 // prep: workgroup 0 groups pairs by expert; the others clear accumulators.
 // ---------------------------------------------------------------------------
+constexpr int kCached = 4;  // pairs per thread held in registers by route_block
+
+// Place routed pair i (expert e, weight w) at the expert's next position and
+// in its streaming unit's row tables.  start[e] is the expert's first
+// position; fill[e] its running insert position.
+__device__ __forceinline__ void scatter_pair(const MoeParams& p, const int* start, int* fill, const int* ubase, int i,
+                                             int e, float w) {
+  if (e < 0 || e >= p.E) return;
+  const int pos = atomicAdd(&fill[e], 1);
+  const int tok = i / p.K, slot = i - tok * p.K;
+  p.pair_tok[pos] = tok;
+  p.pair_slot[pos] = slot;
+  p.pair_w[pos] = w;
+  if (p.unit_info) {
+    const int rel = pos - start[e];
+    const int row = (ubase[e] + rel / stream::kMaxM) * stream::kMaxM + rel % stream::kMaxM;
+    p.unit_tok[row] = tok;
+    p.unit_dst[row] = i;
+    p.unit_w[row] = w;
+  }
+}
+
 __device__ void route_block(const MoeParams& p) {
   __shared__ int cnt[kMaxExperts];  // pairs per expert, then the expert's first position
   __shared__ int fill[kMaxExperts];
   __shared__ int ubase[kMaxExperts];  // first streaming unit of each expert
-  __shared__ int scan_c[kRouteThreads];
-  __shared__ int scan_a[kRouteThreads];
-  __shared__ int scan_u[kRouteThreads];
+  constexpr int kRouteWaves = kRouteThreads / kWave;
+  __shared__ int wave_sum[3][kRouteWaves];
   __shared__ int bad;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int P = p.T * p.K;
   for (int e = tid; e < p.E; e += kRouteThreads) {
     cnt[e] = 0;
     fill[e] = 0;
   }
   if (tid == 0) bad = 0;
+  // The first kCached pairs of each thread stay in registers for the scatter.
+  int my_e[kCached];
+  float my_w[kCached];
+#pragma unroll
+  for (int j = 0; j < kCached; ++j) {
+    const int i = tid + j * kRouteThreads;
+    my_e[j] = i < P ? p.ids[i] : -1;
+    my_w[j] = i < P ? load_act(p.weights, p.w_dtype, i) : 0.f;
+  }
   __syncthreads();
-  for (int i = tid; i < P; i += kRouteThreads) {
+#pragma unroll
+  for (int j = 0; j < kCached; ++j) {
+    const int e = my_e[j];
+    if (e >= 0 && e < p.E)
+      atomicAdd(&cnt[e], 1);
+    else if (e >= p.E)
+      atomicAdd(&bad, 1);
+  }
+  for (int i = tid + kCached * kRouteThreads; i < P; i += kRouteThreads) {
     const int e = p.ids[i];
     if (e >= 0 && e < p.E)
       atomicAdd(&cnt[e], 1);
@@ -136,23 +174,31 @@ __device__ void route_block(const MoeParams& p) {
     sa += cnt[e] > 0;
     su += (cnt[e] + stream::kMaxM - 1) / stream::kMaxM;
   }
-  scan_c[tid] = sc;
-  scan_a[tid] = sa;
-  scan_u[tid] = su;
-  __syncthreads();
-  for (int off = 1; off < kRouteThreads; off <<= 1) {
-    const int vc = tid >= off ? scan_c[tid - off] : 0;
-    const int va = tid >= off ? scan_a[tid - off] : 0;
-    const int vu = tid >= off ? scan_u[tid - off] : 0;
-    __syncthreads();
-    scan_c[tid] += vc;
-    scan_a[tid] += va;
-    scan_u[tid] += vu;
-    __syncthreads();
+  // Inclusive scan: within the wave by shuffles, then across the waves'
+  // totals.
+  int ic = sc, ia = sa, iu = su;
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int vc = __shfl_up(ic, off, kWave), va = __shfl_up(ia, off, kWave), vu = __shfl_up(iu, off, kWave);
+    if (lane >= off) {
+      ic += vc;
+      ia += va;
+      iu += vu;
+    }
   }
-  int start = scan_c[tid] - sc;
-  int act = scan_a[tid] - sa;
-  int unit = scan_u[tid] - su;
+  if (lane == kWave - 1) {
+    wave_sum[0][wave] = ic;
+    wave_sum[1][wave] = ia;
+    wave_sum[2][wave] = iu;
+  }
+  __syncthreads();
+  for (int w = 0; w < wave; ++w) {
+    ic += wave_sum[0][w];
+    ia += wave_sum[1][w];
+    iu += wave_sum[2][w];
+  }
+  int start = ic - sc;
+  int act = ia - sa;
+  int unit = iu - su;
   for (int e = e0; e < e1; ++e) {
     const int c = cnt[e];
     fill[e] = start;  // reuse as the running insert position
@@ -178,29 +224,17 @@ __device__ void route_block(const MoeParams& p) {
     start += c;
   }
   if (tid == kRouteThreads - 1) {
-    p.meta[0] = scan_a[kRouteThreads - 1];
+    p.meta[0] = ia;
     p.meta[1] = bad;
-    p.meta[3] = scan_c[kRouteThreads - 1];  // routed pairs
-    p.meta[4] = scan_u[kRouteThreads - 1];  // streaming work units
+    p.meta[3] = ic;  // routed pairs
+    p.meta[4] = iu;  // streaming work units
   }
   __syncthreads();
-  for (int i = tid; i < P; i += kRouteThreads) {
+#pragma unroll
+  for (int j = 0; j < kCached; ++j) scatter_pair(p, cnt, fill, ubase, tid + j * kRouteThreads, my_e[j], my_w[j]);
+  for (int i = tid + kCached * kRouteThreads; i < P; i += kRouteThreads) {
     const int e = p.ids[i];
-    if (e >= 0 && e < p.E) {
-      const int pos = atomicAdd(&fill[e], 1);
-      const int tok = i / p.K, slot = i - (i / p.K) * p.K;
-      const float w = load_act(p.weights, p.w_dtype, i);
-      p.pair_tok[pos] = tok;
-      p.pair_slot[pos] = slot;
-      p.pair_w[pos] = w;
-      if (p.unit_info) {
-        const int rel = pos - cnt[e];
-        const int row = (ubase[e] + rel / stream::kMaxM) * stream::kMaxM + rel % stream::kMaxM;
-        p.unit_tok[row] = tok;
-        p.unit_dst[row] = i;
-        p.unit_w[row] = w;
-      }
-    }
+    if (e >= 0 && e < p.E) scatter_pair(p, cnt, fill, ubase, i, e, load_act(p.weights, p.w_dtype, i));
   }
 }
 
@@ -704,13 +738,12 @@ int choose_path(const latent_moe_args& a, fused::Plan& pl) {
     if (!std::strcmp(env, "general")) return kPathGeneral;
   }
   // Measured on MI355X at the DeepSeek-V3 shape (d 7168, ff 2048, rank 256,
-  // 256 experts, top-8): below 32 routed pairs the multi-kernel path is the
-  // fastest (its few large items finish in one wave of workgroups); from 32
-  // pairs to the prefill threshold the streaming MFMA path beats the
-  // persistent kernel (batch 8: 111 vs 144 us, 64: 305 vs 370 us).
-  const int64_t P = a.n_tokens * a.n_expert_used;
+  // 256 experts, top-8): below the prefill threshold the streaming MFMA path
+  // is the fastest wherever it applies (batch 1: 49 vs 52 us for the
+  // multi-kernel path; batch 8: 100 vs 144 us and batch 64: 270 vs 370 us
+  // for the persistent kernel).
   if (prefill_ok) return kPathPrefill;
-  if (stream_ok && P >= 32) return kPathStream;
+  if (stream_ok) return kPathStream;
   if (fused_ok) return kPathFused;
   return kPathGeneral;
 }

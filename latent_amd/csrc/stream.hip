@@ -415,6 +415,29 @@ __global__ void __launch_bounds__(kT, 5) item_kernel(Params p) {
   }
 }
 
+constexpr int kSumBatch = 8;
+
+__device__ __forceinline__ void add4(float4& s, const float4& v) {
+  s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+}
+
+// sum_{j < n} src[j * stride], added in j order; the loads of a batch of
+// kBatch terms are all issued before the first add.  Adding the +0 fill of
+// a partial batch leaves the sum unchanged.
+template <int kBatch>
+__device__ __forceinline__ float4 sum_strided(const float4* src, int64_t stride, int n) {
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k0 = 0; k0 < n; k0 += kBatch) {
+    float4 v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      v[j] = k0 + j < n ? src[static_cast<int64_t>(k0 + j) * stride] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) add4(s, v[j]);
+  }
+  return s;
+}
+
 // lat[f][pair][:] = sum over K slices of partA[f][ks][pair][:], slices in order.
 __global__ void __launch_bounds__(kT) reduce_a_kernel(Params p) {
   const int routed = p.g.meta[3];
@@ -424,12 +447,8 @@ __global__ void __launch_bounds__(kT) reduce_a_kernel(Params p) {
     const int64_t rem = i - f * routed * (kN / 4);
     const int64_t pair = rem / (kN / 4), c4 = rem - pair * (kN / 4);
     const float4* src = reinterpret_cast<const float4*>(p.partA + (f * p.nks * p.P + pair) * kN) + c4;
-    float4 s = src[0];
-    for (int ks = 1; ks < p.nks; ++ks) {
-      const float4 v = src[static_cast<int64_t>(ks) * p.P * (kN / 4)];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-    }
-    reinterpret_cast<float4*>(p.lat + (f * p.P + pair) * kN)[c4] = s;
+    reinterpret_cast<float4*>(p.lat + (f * p.P + pair) * kN)[c4] =
+        sum_strided<32>(src, static_cast<int64_t>(p.P) * (kN / 4), p.nks);
   }
 }
 
@@ -440,12 +459,7 @@ __global__ void __launch_bounds__(kT) reduce_c_kernel(Params p) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * kT) {
     const int64_t pair = i / (kN / 4), c4 = i - pair * (kN / 4);
     const float4* src = reinterpret_cast<const float4*>(p.partC + pair * kN) + c4;
-    float4 s = src[0];
-    for (int ks = 1; ks < p.nkc; ++ks) {
-      const float4 v = src[static_cast<int64_t>(ks) * p.P * (kN / 4)];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
-    }
-    reinterpret_cast<float4*>(p.dlat + pair * kN)[c4] = s;
+    reinterpret_cast<float4*>(p.dlat + pair * kN)[c4] = sum_strided<kSumBatch>(src, static_cast<int64_t>(p.P) * (kN / 4), p.nkc);
   }
 }
 
@@ -456,11 +470,17 @@ __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
   for (int64_t i = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * kT) {
     const int64_t t = i / d4, c4 = i - t * d4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < p.K; ++k) {
-      const int e = p.ids[t * p.K + k];
-      if (e < 0 || e >= p.E) continue;
-      const float4 v = reinterpret_cast<const float4*>(p.ybuf + (t * p.K + k) * p.d)[c4];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    for (int k0 = 0; k0 < p.K; k0 += kSumBatch) {
+      float4 v[kSumBatch];
+#pragma unroll
+      for (int j = 0; j < kSumBatch; ++j) {
+        const int k = k0 + j;
+        const int e = k < p.K ? p.ids[t * p.K + k] : -1;
+        v[j] = (e >= 0 && e < p.E) ? reinterpret_cast<const float4*>(p.ybuf + (t * p.K + k) * p.d)[c4]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < kSumBatch; ++j) add4(s, v[j]);
     }
     reinterpret_cast<float4*>(p.out)[i] = s;
   }
