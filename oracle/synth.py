@@ -1,4 +1,5 @@
-"""Seeded numpy generators for the small parity workloads.
+"""Seeded numpy generators for the small parity workloads, and the
+load-time factorization restated in numpy.
 
 TEST INFRASTRUCTURE ONLY (see `oracle/__init__.py`).
 

@@ -20,7 +20,7 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def gpu():
-    """Import the product package on a GPU box; fail loudly if anything is missing."""
+    """Import the product package on a machine with a GPU; fail loudly if anything is missing."""
     import torch
 
     if not torch.cuda.is_available():
