@@ -1,7 +1,8 @@
 """Load-time low-rank factorisation of dense experts on the GPU.
 
 Restates, on torch (rocBLAS / rocSOLVER) in fp32, the reference's offline
-path (loader/latent_loader.py:66-108, 221-249): a randomized SVD with the same
+path (loader/latent_loader.py:66-108, compress_matrix at 195-249): the rank
+from the full spectrum's energy, then a randomized SVD with the same
 sketch (numpy Generator(seed).standard_normal((n, rank + oversample), float32),
 one power iteration, reduced QR, SVD of the small projection), the energy-based
 rank choice, A = U sqrt(S), B = sqrt(S) V^T, then NF4 packing with the
@@ -105,7 +106,7 @@ def stack_experts(
             w = mats[e].to(torch.float32)
             if tuple(w.shape) != shapes[kind]:
                 raise ValueError(f"{kind}[{e}] has shape {tuple(w.shape)}, want {shapes[kind]}")
-            full_s = torch.linalg.svdvals(w)
+            full_s = torch.linalg.svdvals(w)  # rank from the full spectrum, as compress_matrix does
             r = choose_rank(full_s, energy, min_rank, max_rank)
             u, s, vt = randomized_svd(w, r, seed=seed + 3 * e + ki)
             a, b = make_factors(u, s, vt, r)
