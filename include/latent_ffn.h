@@ -58,6 +58,7 @@ typedef struct ihipStream_t* latent_stream_t;
 #define LATENT_E_UNSUPPORTED (-2) /* valid request this build does not implement */
 #define LATENT_E_WORKSPACE (-3)   /* workspace missing or smaller than required */
 #define LATENT_E_HIP (-4)         /* a HIP runtime call or kernel launch failed */
+#define LATENT_E_TIMEOUT (-5)     /* a bounded wait between workgroups expired: that call's output is undefined */
 
 /* ---- element types ------------------------------------------------------ */
 #define LATENT_F32 0
@@ -137,6 +138,17 @@ int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes);
 int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 
 /*
+ * Reads and clears the error word of a workspace.  A decode kernel whose
+ * bounded wait for another workgroup expires sets it and finishes its work
+ * on whatever data it has, so it always terminates; the output of that call
+ * is undefined.  Synchronises `stream`.  Returns LATENT_OK when no call on
+ * this workspace timed out since the last check, LATENT_E_TIMEOUT when one
+ * did.  No counterpart in the reference, whose kernels never wait on each
+ * other.
+ */
+int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t stream);
+
+/*
  * Which implementation latent_moe_ffn_forward uses for these arguments:
  * 2 = grouped fp16-MFMA prefill (at least 16 routed pairs per active expert,
  * no INT8 groups), 3 = streaming fp16-MFMA decode (32 to 4096 routed pairs,
@@ -171,6 +183,62 @@ int latent_pack_nf4(const float* values, int64_t rows, int64_t cols, uint8_t* co
  * (loader/latent_loader.py:148-158).
  */
 int latent_pack_int8(const float* values, int64_t n_groups, int8_t* q, uint16_t* scales, latent_stream_t stream);
+
+/* ---- one expert on the reference's own factor artifacts ------------------ */
+#define LATENT_Q_NF4 0
+#define LATENT_Q_INT8 1
+
+/*
+ * One factor as loader/latent_loader.py stores it (NPZ keys
+ * <name>.{a,b}.{nf4|int8,scales,shape}, :253-260): the logical [rows][cols]
+ * matrix flattened row-major and quantized in groups of group_size
+ * consecutive flat elements, so a group may straddle rows.
+ *   LATENT_Q_NF4   data u8 [ceil(rows*cols/2)], two codes per byte, low
+ *                  nibble = even flat index (quantize_nf4, :111-130)
+ *   LATENT_Q_INT8  data i8 [groups*group_size] (quantize_int8, :148-158)
+ *   scales         f16 [groups], groups = ceil(rows*cols/group_size)
+ * group_size must be a power of two (the reference runtime reads NF4 at 32
+ * and INT8 at 64, loader/latent_runtime.py:25-27).
+ */
+typedef struct latent_flat_factor {
+  const void* data;
+  const uint16_t* scales; /* IEEE binary16 bit patterns */
+  int32_t kind;           /* LATENT_Q_NF4 | LATENT_Q_INT8 */
+  int32_t group_size;
+  int64_t rows;
+  int64_t cols;
+} latent_flat_factor;
+
+/*
+ * Arguments of one single-expert SwiGLU FFN call:
+ *   out = (SiLU(x.A_g.B_g) * (x.A_u.B_u) [* weight]) . A_d . B_d
+ * with gate_a [d][r_g], gate_b [r_g][ff], up_a [d][r_u], up_b [r_u][ff],
+ * down_a [ff][r_d], down_b [r_d][d]; the three ranks may differ.  `weight`
+ * is applied only when weight_before_down is set and ignored otherwise, as in
+ * the reference.
+ */
+typedef struct latent_expert_args {
+  const float* x; /* [T][d] f32 */
+  latent_flat_factor gate_a, gate_b, up_a, up_b, down_a, down_b;
+  int64_t n_tokens; /* T */
+  float weight;
+  int32_t weight_before_down;
+  float* out;      /* [T][d] f32 */
+  void* workspace; /* device scratch, >= latent_expert_workspace_size() */
+  size_t workspace_bytes;
+} latent_expert_args;
+
+/* Workspace bytes required by latent_expert_forward for these dims. */
+int latent_expert_workspace_size(const latent_expert_args* args, size_t* bytes);
+
+/*
+ * swiglu_expert on load_pair'd factors (loader/latent_runtime.py:19-59): the
+ * artifacts are dequantized on the fly exactly as dequantize_nf4 /
+ * dequantize_int8 (loader/latent_loader.py:133-145, 161-170) decode them (one
+ * fp32 multiply per element), and the chain runs in fp32.  Stream ordered;
+ * allocates nothing.
+ */
+int latent_expert_forward(const latent_expert_args* args, latent_stream_t stream);
 
 /* ---- router front end ---------------------------------------------------- */
 /* Drop rules applied after top-k (dropped slot => id -1, weight 0; the kept

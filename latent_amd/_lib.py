@@ -22,6 +22,7 @@ LATENT_E_INVALID = -1
 LATENT_E_UNSUPPORTED = -2
 LATENT_E_WORKSPACE = -3
 LATENT_E_HIP = -4
+LATENT_E_TIMEOUT = -5
 
 LATENT_F32 = 0
 LATENT_F16 = 1
@@ -36,12 +37,19 @@ EXPORTED = (
     "latent_moe_workspace_size",
     "latent_moe_ffn_forward",
     "latent_moe_path",
+    "latent_moe_check",
     "latent_unpack",
     "latent_pack_nf4",
     "latent_pack_int8",
     "latent_route_workspace_size",
     "latent_route",
+    "latent_expert_workspace_size",
+    "latent_expert_forward",
 )
+
+
+LATENT_Q_NF4 = 0
+LATENT_Q_INT8 = 1
 
 LATENT_DROP_NONE = 0
 LATENT_DROP_BELOW = 1
@@ -109,6 +117,35 @@ class LatentRouteArgs(ctypes.Structure):
     ]
 
 
+class LatentFlatFactor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("kind", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+    ]
+
+
+class LatentExpertArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("gate_a", LatentFlatFactor),
+        ("gate_b", LatentFlatFactor),
+        ("up_a", LatentFlatFactor),
+        ("up_b", LatentFlatFactor),
+        ("down_a", LatentFlatFactor),
+        ("down_b", LatentFlatFactor),
+        ("n_tokens", ctypes.c_int64),
+        ("weight", ctypes.c_float),
+        ("weight_before_down", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class LatentError(RuntimeError):
     def __init__(self, status: int, what: str):
         super().__init__(f"{what}: {status_string(status)} ({status})")
@@ -130,6 +167,8 @@ def _load() -> ctypes.CDLL:
     lib.latent_moe_workspace_size.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.latent_moe_ffn_forward.restype = ctypes.c_int
     lib.latent_moe_ffn_forward.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p]
+    lib.latent_moe_check.restype = ctypes.c_int
+    lib.latent_moe_check.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.latent_moe_path.restype = ctypes.c_int
     lib.latent_moe_path.argtypes = [ctypes.POINTER(LatentMoeArgs)]
     lib.latent_unpack.restype = ctypes.c_int
@@ -144,6 +183,10 @@ def _load() -> ctypes.CDLL:
     lib.latent_route_workspace_size.argtypes = [ctypes.POINTER(LatentRouteArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.latent_route.restype = ctypes.c_int
     lib.latent_route.argtypes = [ctypes.POINTER(LatentRouteArgs), ctypes.c_void_p]
+    lib.latent_expert_workspace_size.restype = ctypes.c_int
+    lib.latent_expert_workspace_size.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.latent_expert_forward.restype = ctypes.c_int
+    lib.latent_expert_forward.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.c_void_p]
     return lib
 
 

@@ -16,11 +16,12 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
-SOURCES = ["codec.hip", "moe.hip", "moe_fused.hip", "prefill.hip", "route.hip", "stream.hip"]
+SOURCES = ["codec.hip", "expert.hip", "moe.hip", "moe_fused.hip", "prefill.hip", "route.hip", "stream.hip"]
 LIB = PKG / "liblatent_hip.so"
 ARCH = os.environ.get("LATENT_OFFLOAD_ARCH", "gfx950")
 
@@ -48,14 +49,21 @@ def build(verbose: bool = False) -> Path:
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
     cc = hipcc()
-    objs = []
+    cmds, objs = [], []
     for src in SOURCES:
         obj = objdir / (Path(src).stem + ".o")
-        cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        subprocess.run(cmd, check=True)
+        cmds.append([cc, *HIPCC_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
+    # One compiler process per source, at most `jobs` at a time.
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for cmd in cmds:
+            if verbose:
+                print(" ".join(cmd), flush=True)
+        for result in pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), cmds):
+            sys.stderr.write(result.stderr)
+            if result.returncode != 0:
+                raise subprocess.CalledProcessError(result.returncode, result.args, result.stdout, result.stderr)
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
     if verbose:

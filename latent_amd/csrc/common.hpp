@@ -26,6 +26,15 @@ __host__ __device__ constexpr float nf4_level(int c) {
   return t[c & 15];
 }
 
+// Exponent e that brings a row maximum m into [2^14, 2^15) (0 for m == 0 or
+// not finite): rows of tiny latents are stored as fp16 * 2^e so they keep
+// fp16's full precision; powers of two scale exactly.
+__device__ __forceinline__ int pow2_row_exponent(float m) {
+  if (!(m > 0.f) || !(m < 3.0e38f)) return 0;
+  const int ilog = static_cast<int>((__float_as_uint(m) >> 23) & 0xFFu) - 127;
+  return min(120, max(-120, 14 - ilog));
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
@@ -35,6 +44,29 @@ __device__ __forceinline__ float load_act(const void* p, int dtype, int64_t i) {
   uint16_t b = static_cast<const uint16_t*>(p)[i];
   if (dtype == LATENT_F16) return half_bits_to_float(b);
   return __uint_as_float(static_cast<uint32_t>(b) << 16);  // bf16
+}
+
+// Elements i .. i+7 of an activation array (i % 8 == 0, 16-byte aligned base).
+__device__ __forceinline__ void load_act8(const void* p, int dtype, int64_t i, float v[8]) {
+  if (dtype == LATENT_F32) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    return;
+  }
+  const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t lo = static_cast<uint16_t>(u[j] & 0xFFFFu), hi = static_cast<uint16_t>(u[j] >> 16);
+    if (dtype == LATENT_F16) {
+      v[2 * j] = half_bits_to_float(lo);
+      v[2 * j + 1] = half_bits_to_float(hi);
+    } else {  // bf16
+      v[2 * j] = __uint_as_float(static_cast<uint32_t>(lo) << 16);
+      v[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+    }
+  }
 }
 
 // Cross-lane reductions without LDS traffic (__shfl_xor compiles to

@@ -13,6 +13,9 @@ namespace fused {
 // Workspace bytes at the start of every workspace that the fused path keeps
 // zero between calls (queue tickets, per-expert counters, combine counters).
 constexpr size_t kReserved = 256 * 1024;
+// Byte offset, inside that region, of the int error word a timed-out bounded
+// wait sets (read and cleared by latent_moe_check).
+constexpr size_t kErrorOffset = 36;
 
 struct Plan {
   int ra, nca, cb, ncb, cd, ncd;

@@ -69,6 +69,8 @@ struct MoeParams {
   int* unit_tok;    // [units][16] token of each unit row (0 past the unit's pairs)
   int* unit_dst;    // [units][16] token * K + slot
   float* unit_w;    // [units][16] router weight
+  _Float16* xh;     // streaming path: x as fp16 rows * 2^xexp (NULL: not converted)
+  int* xexp;        // [T] row exponents
   int x_dtype, w_dtype;
   int T, d, ff, E, K, R;
   int wbd, out_mode;
@@ -343,6 +345,40 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
   const int64_t nblk = gridDim.x - 1;
   const int64_t t0 = (blockIdx.x - 1) * static_cast<int64_t>(kRouteThreads) + threadIdx.x;
   const int64_t stride = nblk * kRouteThreads;
+  if (p.xh) {
+    // One workgroup per token, 8 elements per thread and step: the row maximum
+    // picks the exponent that brings it into [2^14, 2^15), then the row is
+    // stored as fp16 * 2^exponent (the streaming path requires d % 8 == 0 and
+    // a 16-byte aligned x).
+    __shared__ float wmax[kRouteThreads / kWave];
+    for (int64_t t = blockIdx.x - 1; t < p.T; t += nblk) {
+      const int64_t row = t * p.d;
+      float mx = 0.f;
+      for (int i = threadIdx.x * 8; i < p.d; i += kRouteThreads * 8) {
+        float v[8];
+        load_act8(p.x, p.x_dtype, row + i, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(v[j]));
+      }
+      mx = op_over(mx, 1, kWave, OpMax{});
+      if (threadIdx.x % kWave == 0) wmax[threadIdx.x / kWave] = mx;
+      __syncthreads();
+#pragma unroll
+      for (int w = 0; w < kRouteThreads / kWave; ++w) mx = fmaxf(mx, wmax[w]);
+      __syncthreads();  // wmax is reused by the next token
+      const int ex = pow2_row_exponent(mx);
+      for (int i = threadIdx.x * 8; i < p.d; i += kRouteThreads * 8) {
+        float v[8];
+        load_act8(p.x, p.x_dtype, row + i, v);
+        typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+        half8_t h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = static_cast<_Float16>(ldexpf(v[j], ex));
+        *reinterpret_cast<half8_t*>(p.xh + row + i) = h;
+      }
+      if (threadIdx.x == 0) p.xexp[t] = ex;
+    }
+  }
   // Accumulators gu and dl are contiguous: zero_floats covers both.
   float4* acc4 = reinterpret_cast<float4*>(p.gu);
   const int64_t n4 = p.zero_floats / 4;
@@ -777,6 +813,7 @@ extern "C" const char* latent_status_string(int status) {
     case LATENT_E_UNSUPPORTED: return "unsupported configuration";
     case LATENT_E_WORKSPACE: return "workspace missing or too small";
     case LATENT_E_HIP: return "HIP runtime error";
+    case LATENT_E_TIMEOUT: return "a bounded wait between workgroups timed out (output undefined)";
     default: return "unknown status";
   }
 }
@@ -794,6 +831,25 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   if (stream::supported(*args)) scratch = std::max(scratch, L.gu + stream::layout_for(*args).total);
   *bytes = fused::kReserved + scratch;
   return LATENT_OK;
+}
+
+namespace latent {
+namespace {
+__global__ void clear_word_kernel(int* word) { *word = 0; }
+}  // namespace
+}  // namespace latent
+
+extern "C" int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t stream) {
+  if (!workspace || workspace_bytes < fused::kReserved) return LATENT_E_WORKSPACE;
+  int* word = reinterpret_cast<int*>(static_cast<char*>(workspace) + fused::kErrorOffset);
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int h = 0;
+  if (hipMemcpyAsync(&h, word, sizeof h, hipMemcpyDeviceToHost, s) != hipSuccess) return LATENT_E_HIP;
+  if (hipStreamSynchronize(s) != hipSuccess) return LATENT_E_HIP;
+  if (h == 0) return LATENT_OK;
+  hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, word);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return LATENT_E_HIP;
+  return LATENT_E_TIMEOUT;
 }
 
 extern "C" int latent_moe_path(const latent_moe_args* args) {
@@ -865,6 +921,9 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.unit_tok = reinterpret_cast<int*>(p.unit_info + mu);
     p.unit_dst = p.unit_tok + mu * stream::kMaxM;
     p.unit_w = reinterpret_cast<float*>(p.unit_dst + mu * stream::kMaxM);
+    const stream::Layout SL = stream::layout_for(a);
+    p.xh = reinterpret_cast<_Float16*>(ws + L.gu + SL.xh);
+    p.xexp = reinterpret_cast<int*>(ws + L.gu + SL.xexp);
   }
   // The MFMA paths write their intermediates whole, and every output row (per-token combine).
   p.zero_floats = use_prefill || use_stream ? 0 : P * 3 * a.max_rank;
@@ -882,7 +941,10 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
 
   const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
                                                                                   : P * a.n_embd / 4);
-  const int zero_blocks = static_cast<int>(std::min<int64_t>(512, std::max<int64_t>(1, zero_work / (kRouteThreads * 8))));
+  // The streaming path also converts x, one workgroup per token.
+  const int64_t conv_blocks = use_stream ? a.n_tokens : 1;
+  const int zero_blocks = static_cast<int>(
+      std::min<int64_t>(512, std::max<int64_t>(conv_blocks, zero_work / (kRouteThreads * 8))));
   if (use_prefill) {
     // Large batch: the multi-workgroup grouping; nothing to clear.
     int* hist = reinterpret_cast<int*>(ws + L.hist);

@@ -29,8 +29,9 @@
 #include "fused.hpp"
 
 #include <algorithm>
-#include <type_traits>
 #include <cmath>
+#include <cstddef>
+#include <type_traits>
 
 namespace latent {
 
@@ -53,6 +54,8 @@ struct Ctrl {
   int error;
   int pad[6];
 };
+
+static_assert(offsetof(Ctrl, error) == kErrorOffset, "error word offset");
 
 struct ExpertSync {
   int cA, rA, cB, rB, cD, pad[3];

@@ -586,13 +586,24 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
 
 // x rows to fp16: xh[t] = fp16(x[t] * 2^e[t]) with 2^e * max|x[t]| in [2^14, 2^15).
 // One workgroup per token; d % 8 == 0 and x 16-byte aligned.
-// Also clears the token's slot entries of pos_of.
+// Also clears the token's slot entries of pos_of and, when per_slot_out is
+// given (per-slot output mode), writes the zero rows of the token's dropped
+// slots (id outside [0, E)): the GEMMs write routed rows only.
 __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_dtype, int d, _Float16* xh, int* xexp,
-                                                          int* pos_of, int k) {
+                                                          int* pos_of, int k, const int32_t* ids, int E,
+                                                          float* per_slot_out) {
   __shared__ float red[kThreads / kWave];
   __shared__ int ex;
   const int t = blockIdx.x, tid = threadIdx.x;
-  if (tid < k) pos_of[t * k + tid] = -1;
+  for (int sl = tid; sl < k; sl += kThreads) pos_of[t * k + sl] = -1;
+  if (per_slot_out) {
+    for (int sl = 0; sl < k; ++sl) {
+      const int e = ids[static_cast<int64_t>(t) * k + sl];
+      if (e >= 0 && e < E) continue;
+      float4* row = reinterpret_cast<float4*>(per_slot_out + (static_cast<int64_t>(t) * k + sl) * d);
+      for (int c = tid; c < d / 4; c += kThreads) row[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
   const int64_t base = static_cast<int64_t>(t) * d;
   auto load8 = [&](int c, float (&v)[8]) {
     if (x_dtype == LATENT_F32) {
@@ -665,10 +676,13 @@ __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, co
       for (int i = 0; i < kCombineSlots; ++i) {
         const int sl = s0 + i;
         const int pos = sl < k ? pos_of[t * k + sl] : -1;
-        const int pr = pos < 0 ? 0 : pos;  // dropped slot: row 0 with weight 0
-        h[i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pr) * d + c);
-        const float wv = pos < 0 ? 0.f : (wbd ? 1.f : pair_w[pr]);
-        w[i] = __builtin_ldexpf(wv, -yexp[static_cast<int64_t>(pr) * yexp_ld + c / kBlk]);
+        // A dropped slot adds an exact zero; its (unwritten) row is not read.
+        h[i] = half8{};
+        w[i] = 0.f;
+        if (pos >= 0) {
+          h[i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
+          w[i] = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kBlk]);
+        }
       }
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i)
@@ -795,7 +809,8 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   const int R = static_cast<int>(a.max_rank), d = static_cast<int>(a.n_embd), ff = static_cast<int>(a.n_ff);
   const int rb = R / kBlk, fb = ff / kBlk, db = d / kBlk;
   hipLaunchKernelGGL(x_prep_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype, d,
-                     xh, xexp, pos_of, K);
+                     xh, xexp, pos_of, K, a.ids, static_cast<int>(a.n_expert),
+                     a.out_mode == LATENT_OUT_PER_SLOT ? static_cast<float*>(a.out) : nullptr);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, tile_a, tile_r0);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;

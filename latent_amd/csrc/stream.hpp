@@ -19,8 +19,10 @@ struct Grouping {
   const float* unit_w;     // [units][kMaxM] router weight
 };
 
+// Scratch of the path inside the caller's workspace.  xh / xexp (x as fp16
+// rows * 2^xexp, one exponent per token) are written by the prep kernel.
 struct Layout {
-  size_t partA, lat, gu, partC, dlat, ybuf, total;
+  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, total;
 };
 
 bool supported(const latent_moe_args& a);

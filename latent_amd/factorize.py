@@ -73,6 +73,17 @@ def group_snr(values: torch.Tensor, decoded: torch.Tensor) -> torch.Tensor:
     return x.norm(dim=2) / err.norm(dim=2).clamp_min(1e-12)
 
 
+def int8_group_mask(values: torch.Tensor, decoded: torch.Tensor, snr_threshold: float) -> torch.Tensor:
+    """bool [..., rows, cols/32]: the non-zero row groups whose NF4 decode has SNR
+    below `snr_threshold` (the SNR of quantization_snr_by_group,
+    loader/latent_loader.py:173-185, which the reference thresholds at :227-229)."""
+    rows, cols = values.shape[-2:]
+    lead = values.shape[:-2]
+    snr = group_snr(values.reshape(-1, cols), decoded.reshape(-1, cols)).reshape(*lead, rows, cols // GROUP)
+    nonzero = values.reshape(*lead, rows, cols // GROUP, GROUP).abs().amax(-1) > 0
+    return (snr < snr_threshold) & nonzero
+
+
 def stack_experts(
     gate: Sequence[torch.Tensor],
     up: Sequence[torch.Tensor],
@@ -133,8 +144,7 @@ def _int8_fallback(values: torch.Tensor, f: DeviceFactor, snr_threshold: float) 
     row_offset the index of the row's first INT8 group."""
     E, rows, cols = values.shape
     decoded = torch.stack([unpack(f, e) for e in range(E)])
-    snr = torch.stack([group_snr(values[e], decoded[e]) for e in range(E)])  # [E, rows, groups]
-    mask = (snr < snr_threshold) & (values.reshape(E, rows, cols // GROUP, GROUP).abs().amax(-1) > 0)
+    mask = int8_group_mask(values, decoded, snr_threshold)  # [E, rows, groups]
     if not bool(mask.any()):
         return f
     groups = cols // GROUP

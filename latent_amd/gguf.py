@@ -14,8 +14,9 @@ The layout is the one loader/write_latent_gguf.py produces (:72-74 names,
 
 Two documented extensions:
 
-* the rank table is written as I32 (the reference writes uint8 as I8, which
-  cannot hold 256 or 512); the reader accepts both;
+* the rank table is written as I32 `[E][3]` (the reference writes uint8 as
+  I8, which cannot hold 256 or 512, in the byte order of `ranks.T`, i.e.
+  kind-major `[3][E]` under recorded dims `(E, 3)`); the reader accepts both;
 * per-group INT8 fallback groups (no reference format): `..._{a,b}_i8map`
   (I32 bitmap `[E][rows][words]`), `..._{a,b}_i8off` (I32 `[E][rows]`) and
   `..._{a,b}_i8` (I8 `[n][32]`), as in include/latent_ffn.h.
@@ -97,9 +98,15 @@ class LatentGGUF:
         rk = tensor_name(layer, "ranks")
         if rk in self.arrays:
             r = self.arrays[rk]
-            if r.dtype == np.int8:  # the reference's uint8 table
-                r = r.view(np.uint8)
-            out[rk] = r.astype(np.int32)
+            if r.dtype == np.int8:
+                # The reference's table: uint8 ranks written as I8 from
+                # per_expert_ranks.T (loader/write_latent_gguf.py:262-265,
+                # 432-436), so the bytes are kind-major [3][E] under recorded
+                # dims (E, 3).  Ranks of 256 or more wrapped modulo 256 when
+                # the reference wrote them.
+                n_expert = int(self.tensors[rk].dims[0])
+                r = r.reshape(-1).view(np.uint8).reshape(3, n_expert).T
+            out[rk] = np.ascontiguousarray(r, dtype=np.int32)
         return out
 
 

@@ -227,12 +227,14 @@ class StackedLayer:
         return ws
 
 
-CTRL_ERROR_OFFSET = 36  # int32 error word of the workspace control block
-
-
-def workspace_error(workspace: torch.Tensor) -> int:
-    """Error word the fused kernel sets when a bounded wait times out (0 = none)."""
-    return int(workspace[CTRL_ERROR_OFFSET:CTRL_ERROR_OFFSET + 4].view(torch.int32).item())
+def workspace_error(workspace: torch.Tensor, stream: Optional[torch.cuda.Stream] = None) -> int:
+    """Read and clear the workspace's error word through latent_moe_check:
+    LATENT_E_TIMEOUT when a call since the last check had a bounded wait time
+    out (its output is undefined), else 0.  Synchronises the stream."""
+    r = lib.latent_moe_check(workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(stream))
+    if r not in (_lib.LATENT_OK, _lib.LATENT_E_TIMEOUT):
+        check(r, "latent_moe_check")
+    return int(r)
 
 
 def workspace_size(layer: StackedLayer, n_tokens: int, n_expert_used: int) -> int:
@@ -268,12 +270,17 @@ def moe_forward(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     stream: Optional[torch.cuda.Stream] = None,
+    check_timeout: bool = False,
 ) -> torch.Tensor:
     """Router-weighted LATENT expert FFN of one MoE layer on the GPU.
 
     x [T, d] (f32 / f16 / bf16), ids int32 [T, k] (id < 0 = dropped slot),
     weights [T, k] (f32 / f16).  Returns f32 [T, d] (out_mode 0) or the
     per-slot f32 [T, k, d] of the ggml op (out_mode 1).
+
+    check_timeout=True synchronises after the call and raises LatentError
+    (LATENT_E_TIMEOUT) if a bounded wait between workgroups expired, in
+    which case the output is undefined.
     """
     if x.dim() != 2 or ids.dim() != 2 or weights.shape != ids.shape or x.shape[0] != ids.shape[0]:
         raise ValueError("expected x [T, d], ids [T, k], weights [T, k]")
@@ -306,6 +313,8 @@ def moe_forward(
     a.workspace = workspace.data_ptr()
     a.workspace_bytes = workspace.numel() * workspace.element_size()
     check(lib.latent_moe_ffn_forward(ctypes.byref(a), _stream(stream)), "latent_moe_ffn_forward")
+    if check_timeout:
+        check(workspace_error(workspace, stream), "latent_moe_ffn_forward")
     return out
 
 

@@ -222,6 +222,40 @@ def relative_frobenius_error(reference: np.ndarray, candidate: np.ndarray) -> fl
     return float(np.linalg.norm(np.asarray(reference) - np.asarray(candidate)) / denom)
 
 
+def quantization_snr_by_group(reference: np.ndarray, candidate: np.ndarray, group_size: int) -> np.ndarray:
+    """Per-group ||x|| / max(||x - q||, 1e-12) over the flattened arrays, each
+    zero-padded to whole groups; fp32 norms.  loader/latent_loader.py:173-185."""
+    ref = np.asarray(reference, dtype=np.float32).reshape(-1)
+    cand = np.asarray(candidate, dtype=np.float32).reshape(-1)
+    groups = int(math.ceil(ref.size / group_size))
+    padded_ref = np.zeros(groups * group_size, dtype=np.float32)
+    padded_cand = np.zeros(groups * group_size, dtype=np.float32)
+    padded_ref[: ref.size] = ref
+    padded_cand[: cand.size] = cand
+    signal = np.linalg.norm(padded_ref.reshape(groups, group_size), axis=1)
+    noise = np.linalg.norm((padded_ref - padded_cand).reshape(groups, group_size), axis=1)
+    return signal / np.maximum(noise, 1e-12)
+
+
+def int8_group_mask(values: np.ndarray, snr_threshold: float) -> np.ndarray:
+    """bool [rows, cols/32]: the non-zero row groups of [rows, cols] whose NF4
+    round trip has SNR below `snr_threshold`.
+
+    No reference counterpart as a per-group selector: the reference computes
+    this SNR (quantization_snr_by_group of quantize_nf4 / dequantize_nf4,
+    loader/latent_loader.py:173-185, 216-223) and switches a whole factor to
+    INT8 when too many groups fall below the threshold (:227-229).  With
+    cols % 32 == 0 the per-row groups are the reference's flat groups.
+    """
+    v = np.asarray(values, dtype=np.float32)
+    rows, cols = v.shape
+    codes, scales = pack_rows(v)
+    decoded = unpack_rows(codes, scales)
+    snr = quantization_snr_by_group(v, decoded, GROUP).reshape(rows, cols // GROUP)
+    nonzero = np.abs(v.reshape(rows, cols // GROUP, GROUP)).max(axis=2) > 0
+    return (snr < np.float32(snr_threshold)) & nonzero
+
+
 def rel_l2(reference: np.ndarray, candidate: np.ndarray) -> float:
     """Relative L2 error in float64 (the parity metric)."""
     ref = np.asarray(reference, dtype=np.float64)
@@ -342,15 +376,17 @@ def unpack_rows_mixed(codes: np.ndarray, scales: np.ndarray, ext: Optional[Int8G
     rows, cols = vals.shape
     groups = cols // GROUP
     s = np.asarray(scales[e]).astype(np.float32)
-    for r in range(rows):
-        off = int(ext.row_offset[e, r])
-        n = 0
-        for g in range(groups):
-            if (int(ext.bitmap[e, r, g // 32]) >> (g % 32)) & 1:
-                q = ext.data[off + n].astype(np.float32)
-                vals[r, g * GROUP:(g + 1) * GROUP] = q * s[r, g]
-                n += 1
-    return vals
+    # flagged[r, g]: bit g % 32 of word g // 32 of row r's bitmap.
+    words = np.asarray(ext.bitmap[e], dtype=np.uint32)
+    g = np.arange(groups)
+    flagged = ((words[:, g // 32] >> (g % 32).astype(np.uint32)) & np.uint32(1)).astype(bool)
+    # A flagged group's values sit at data[row_offset + (flagged groups before it in the row)].
+    before = np.cumsum(flagged, axis=1) - 1
+    idx = np.asarray(ext.row_offset[e], dtype=np.int64)[:, None] + before
+    q = np.asarray(ext.data)[idx[flagged]].astype(np.float32)  # [n, 32]
+    grouped = vals.reshape(rows, groups, GROUP)
+    grouped[flagged] = q * s[flagged][:, None]
+    return grouped.reshape(rows, cols)
 
 
 # ----------------------------------------------------------------------------

@@ -155,3 +155,61 @@ def choose_rank(singular_values: np.ndarray, energy: float, min_rank: int, max_r
         return min_rank
     rank = int(np.searchsorted(np.cumsum(s ** 2) / total, energy) + 1)
     return max(min_rank, min(rank, max_rank, s.size))
+
+
+def compress_matrix(name: str, matrix: np.ndarray, energy: float = 0.95, min_rank: int = 16, max_rank: int = 128,
+                    group_size: int = 32, int8_group_size: int = 64, error_threshold: float = 0.02,
+                    snr_threshold: float = 3.0, low_snr_fraction_threshold: float = 0.05, seed: int = 0):
+    """numpy restatement of compress_matrix (loader/latent_loader.py:195-285);
+    defaults are the CLI's (:292-303).
+
+    Rank from the full spectrum's energy, randomized SVD, A = U sqrt(S),
+    B = sqrt(S) V^T, flat NF4 of both factors; the whole pair switches to INT8
+    (group int8_group_size) when more than low_snr_fraction_threshold of the
+    NF4 groups have SNR below snr_threshold and INT8 reconstructs the matrix
+    better; a dense fp16 copy is added when the error still exceeds
+    error_threshold.  Returns (arrays with the artifact's NPZ keys, report dict).
+    """
+    matrix = np.asarray(matrix, dtype=np.float32)
+    full_s = np.linalg.svd(matrix, compute_uv=False)
+    rank = choose_rank(full_s, energy, min_rank, max_rank)
+    u, s, vt = randomized_svd(matrix, rank, seed=seed)
+    root = np.sqrt(s[:rank]).astype(np.float32)
+    a = u[:, :rank].astype(np.float32) * root[np.newaxis, :]
+    b = root[:, np.newaxis] * vt[:rank, :].astype(np.float32)
+    dense_error = ref.relative_frobenius_error(matrix, a @ b)
+    a_packed, a_scales, a_shape = ref.quantize_nf4(a, group_size=group_size)
+    b_packed, b_scales, b_shape = ref.quantize_nf4(b, group_size=group_size)
+    aq = ref.dequantize_nf4(a_packed, a_scales, a_shape, group_size=group_size)
+    bq = ref.dequantize_nf4(b_packed, b_scales, b_shape, group_size=group_size)
+    quant_error = ref.relative_frobenius_error(matrix, aq @ bq)
+    snr = np.concatenate([ref.quantization_snr_by_group(a, aq, group_size),
+                          ref.quantization_snr_by_group(b, bq, group_size)])
+    low_snr_fraction = float(np.mean(snr < snr_threshold)) if snr.size else 0.0
+    quantization = "nf4_g%d" % group_size
+    use_int8 = low_snr_fraction > low_snr_fraction_threshold
+    arrays: Dict[str, np.ndarray] = {}
+    if use_int8:
+        a_i8, a_i8s, _ = ref.quantize_int8(a, group_size=int8_group_size)
+        b_i8, b_i8s, _ = ref.quantize_int8(b, group_size=int8_group_size)
+        aq8 = ref.dequantize_int8(a_i8, a_i8s, a_shape, group_size=int8_group_size)
+        bq8 = ref.dequantize_int8(b_i8, b_i8s, b_shape, group_size=int8_group_size)
+        int8_error = ref.relative_frobenius_error(matrix, aq8 @ bq8)
+        if int8_error < quant_error:
+            quant_error = int8_error
+            arrays = {f"{name}.a.int8": a_i8, f"{name}.a.scales": a_i8s,
+                      f"{name}.b.int8": b_i8, f"{name}.b.scales": b_i8s}
+            quantization = "int8_g%d" % int8_group_size
+        else:
+            use_int8 = False
+    if not use_int8:
+        arrays = {f"{name}.a.nf4": a_packed, f"{name}.a.scales": a_scales,
+                  f"{name}.b.nf4": b_packed, f"{name}.b.scales": b_scales}
+    arrays[f"{name}.a.shape"] = np.array(a_shape, dtype=np.int32)
+    arrays[f"{name}.b.shape"] = np.array(b_shape, dtype=np.int32)
+    fallback = quant_error > error_threshold
+    if fallback:
+        arrays[f"{name}.dense_fallback"] = matrix.astype(np.float16)
+    report = {"rank": rank, "dense_relative_error": dense_error, "quantized_relative_error": quant_error,
+              "low_snr_group_fraction": low_snr_fraction, "quantization": quantization, "fallback": fallback}
+    return arrays, report

@@ -26,18 +26,37 @@ def to_device(layer: ref.StackedLayer):
     return StackedLayer(**facs, ranks=ranks)
 
 
+def _int8_subset(f, experts: np.ndarray) -> ref.Int8Groups:
+    """The INT8 groups of `experts` of a device factor, with row offsets rebased.
+
+    The side buffer holds the flagged groups in (expert, row, group) order, so
+    expert e's groups are the contiguous run that starts at row_offset[e, 0]
+    and holds as many groups as e's bitmap has bits set."""
+    bitmap = f.int8_bitmap.cpu().numpy().view(np.uint32)
+    row_offset = f.int8_row_offset.cpu().numpy().astype(np.int64)
+    data = f.int8_data.cpu().numpy()
+    counts = np.array([int(np.unpackbits(bitmap[e].view(np.uint8)).sum()) for e in experts], np.int64)
+    parts, offs, base = [], [], 0
+    for e, n in zip(experts, counts):
+        start = int(row_offset[e, 0])
+        parts.append(data[start:start + n])
+        offs.append(row_offset[e] - start + base)
+        base += int(n)
+    data_sub = np.concatenate(parts) if parts else np.zeros((0, 32), np.int8)
+    return ref.Int8Groups(bitmap=bitmap[experts], data=data_sub, row_offset=np.stack(offs).astype(np.int32))
+
+
 def subset_to_host(dev_layer, experts: Sequence[int]) -> ref.StackedLayer:
-    """Oracle StackedLayer holding only `experts` (NF4 only) of a device layer."""
+    """Oracle StackedLayer holding only `experts` of a device layer (INT8 groups included)."""
     import torch
 
-    sel = torch.as_tensor(np.asarray(experts, dtype=np.int64), device=dev_layer.gate_a.codes.device)
+    ex = np.asarray(experts, dtype=np.int64)
+    sel = torch.as_tensor(ex, device=dev_layer.gate_a.codes.device)
     facs = {}
     for name, f in dev_layer.factors().items():
-        if f.has_int8:
-            raise NotImplementedError("subset copy of INT8 groups")
         codes = f.codes.index_select(0, sel).cpu().numpy()
         scales = f.scales.index_select(0, sel).cpu().numpy().view(np.float16)
-        facs[name] = ref.StackedFactor(codes, scales)
+        facs[name] = ref.StackedFactor(codes, scales, _int8_subset(f, ex) if f.has_int8 else None)
     ranks = None if dev_layer.ranks is None else dev_layer.ranks.index_select(0, sel).cpu().numpy()
     return ref.StackedLayer(factors=facs, d=dev_layer.d, ff=dev_layer.ff, max_rank=dev_layer.max_rank, ranks=ranks)
 

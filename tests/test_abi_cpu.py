@@ -149,3 +149,76 @@ def test_route_argument_checks(L):
     b.logits_in = 0
     b.router_dtype = L.LATENT_F16  # f16 router matrices are not supported
     assert L.lib.latent_route(ctypes.byref(b), None) == L.LATENT_E_INVALID
+
+
+def _expert_args(L, d=16, ff=12, r=(4, 4, 4), T=3, kinds=(0, 0, 0, 0, 0, 0), group=(32, 32, 32, 32, 32, 32)):
+    keep = []
+
+    def fac(rows, cols, kind, g):
+        data = np.zeros(rows * cols + 64, np.uint8)
+        s = np.zeros(rows * cols // g + 2, np.uint16)
+        keep.extend([data, s])
+        return L.LatentFlatFactor(data=data.ctypes.data, scales=s.ctypes.data, kind=kind, group_size=g,
+                                  rows=rows, cols=cols)
+
+    a = L.LatentExpertArgs()
+    shapes = [(d, r[0]), (r[0], ff), (d, r[1]), (r[1], ff), (ff, r[2]), (r[2], d)]
+    for name, (rows, cols), kind, g in zip(("gate_a", "gate_b", "up_a", "up_b", "down_a", "down_b"), shapes, kinds,
+                                           group):
+        setattr(a, name, fac(rows, cols, kind, g))
+    a.n_tokens = T
+    return a, keep
+
+
+def test_expert_workspace_and_argument_checks(L):
+    # the reference test's shapes (tests/test_latent_loader.py:100-127) and an odd rank
+    for r in ((4, 4, 4), (37, 33, 5)):
+        a, keep = _expert_args(L, r=r)
+        n = ctypes.c_size_t(0)
+        assert L.lib.latent_expert_workspace_size(ctypes.byref(a), ctypes.byref(n)) == L.LATENT_OK and n.value > 0
+    a, keep = _expert_args(L, kinds=(0, 1, 0, 0, 1, 0), group=(32, 64, 32, 32, 64, 32))
+    assert L.lib.latent_expert_workspace_size(ctypes.byref(a), ctypes.byref(ctypes.c_size_t())) == L.LATENT_OK
+    cases = [
+        (lambda a: setattr(a.gate_b, "rows", 5), L.LATENT_E_INVALID),   # rank mismatch with gate_a
+        (lambda a: setattr(a.down_b, "cols", 15), L.LATENT_E_INVALID),  # output width != d
+        (lambda a: setattr(a.up_a, "kind", 3), L.LATENT_E_INVALID),
+        (lambda a: setattr(a.up_a, "data", None), L.LATENT_E_INVALID),
+        (lambda a: setattr(a.up_a, "group_size", 48), L.LATENT_E_UNSUPPORTED),
+        (lambda a: setattr(a, "n_tokens", -1), L.LATENT_E_INVALID),
+    ]
+    for mutate, status in cases:
+        a, keep = _expert_args(L)
+        mutate(a)
+        assert L.lib.latent_expert_workspace_size(ctypes.byref(a), ctypes.byref(ctypes.c_size_t())) == status
+        assert L.lib.latent_expert_forward(ctypes.byref(a), None) == status
+    a, keep = _expert_args(L)
+    assert L.lib.latent_expert_forward(ctypes.byref(a), None) == L.LATENT_E_INVALID  # no x / out
+    x = np.zeros(64, np.float32)
+    a.x = a.out = x.ctypes.data
+    assert L.lib.latent_expert_forward(ctypes.byref(a), None) == L.LATENT_E_WORKSPACE
+    a.n_tokens = 0
+    assert L.lib.latent_expert_forward(ctypes.byref(a), None) == L.LATENT_OK
+
+
+def test_check_rejects_missing_workspace(L):
+    assert L.lib.latent_moe_check(None, 0, None) == L.LATENT_E_WORKSPACE
+    assert L.status_string(L.LATENT_E_TIMEOUT) != "unknown status"
+
+
+def test_runtime_load_pair_keeps_artifacts_flat():
+    from latent_amd import runtime
+    from oracle import synth
+
+    rng = np.random.default_rng(5)
+    m = rng.standard_normal((40, 37)).astype(np.float32) @ rng.standard_normal((37, 48)).astype(np.float32)
+    arrays, rep = synth.compress_matrix("w", m, energy=1.0, min_rank=37, max_rank=37, error_threshold=1e9)
+    pair = runtime.load_pair(arrays, "w")
+    assert (pair.n_in, pair.rank, pair.n_out) == (40, 37, 48)
+    assert pair.a.kind == 0 and pair.a.group_size == 32 and pair.a.groups == (40 * 37 + 31) // 32
+    assert np.array_equal(pair.a.data, arrays["w.a.nf4"])  # no repacking: the artifact's bytes as they are
+    with pytest.raises(KeyError):
+        runtime.load_pair(arrays, "nope")
+    bad = dict(arrays)
+    bad["w.a.scales"] = bad["w.a.scales"][:-1]
+    with pytest.raises(ValueError):
+        runtime.load_pair(bad, "w")

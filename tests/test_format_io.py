@@ -156,10 +156,40 @@ def test_reference_uint8_rank_table_and_wide_ranks(tmp_path):
     p = tmp_path / "r.gguf"
     gguf.write_latent_gguf(p, {3: arrays}, max_rank=32)
     assert np.array_equal(gguf.read_latent_gguf(p).layer_arrays(3)["blk.3.ffn_latent_ranks"], arrays["ranks"])
-    # A table written the reference's way (uint8 bytes as I8) reads back as 0..255.
+
+
+
+def test_reference_written_rank_table(tmp_path):
+    # The reference writes per_expert_ranks.T.astype(uint8) as I8 with recorded
+    # dims (E, 3) (loader/write_latent_gguf.py:262-265, 432-436): the file bytes
+    # are the C order of the (3, E) transpose, i.e. kind-major.  Build the
+    # tensor exactly that way inside a file and read the table back.
+    E = 5
+    layer = synth.make_layer(seed=9, n_expert=E, d=64, ff=64, max_rank=32)
+    arrays = _host_arrays(layer)
+    p = tmp_path / "refranks.gguf"
+    gguf.write_latent_gguf(p, {0: arrays}, max_rank=32)
+    per_expert_ranks = np.array([[1, 2, 3], [4, 5, 6], [7, 8, 9], [10, 11, 12], [200, 16, 32]], np.uint8)
+    table = per_expert_ranks.T.astype(np.uint8)  # what the reference hands to add_tensor
+    assert table.shape == (3, E)
+    file_bytes = table.tobytes(order="C")  # numpy writes a tensor's data in C order
+    assert file_bytes[:E] == bytes([1, 4, 7, 10, 200])  # kind-major, not expert-major
     g = gguf.read_latent_gguf(p)
-    g.arrays["blk.3.ffn_latent_ranks"] = np.array([[200, 16, 32], [7, 8, 9]], np.uint8).view(np.int8)
-    assert g.layer_arrays(3)["blk.3.ffn_latent_ranks"].tolist() == [[200, 16, 32], [7, 8, 9]]
+    name = "blk.0.ffn_latent_ranks"
+    g.tensors[name] = gguf.TensorInfo(name, (E, 3), gguf.GGML_I8, 0)  # dims recorded reversed: (E, 3)
+    g.arrays[name] = np.frombuffer(file_bytes, np.int8).reshape(E, 3)  # the reader's view of those bytes
+    got = g.layer_arrays(0)[name]
+    assert got.dtype == np.int32 and got.tolist() == per_expert_ranks.astype(np.int32).tolist()
+    # and the ranks drive the forward as the oracle's own table does
+    host = ref.StackedLayer(factors=layer.factors, d=64, ff=64, max_rank=32,
+                            ranks=np.minimum(got, 32).astype(np.int32))
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 64)).astype(np.float32)
+    ids = np.array([[0, 4], [2, 1]], np.int32)
+    w = np.full((2, 2), 0.5, np.float32)
+    want = ref.moe_forward(x, ids, w, ref.StackedLayer(factors=layer.factors, d=64, ff=64, max_rank=32,
+                                                        ranks=np.minimum(per_expert_ranks, 32).astype(np.int32)))
+    assert np.array_equal(ref.moe_forward(x, ids, w, host), want)
 
 
 def test_writer_rejects_bad_operands(tmp_path):

@@ -6,6 +6,8 @@ own properties, literal per-row loops of the writer, and brute-force loops
 over (token, slot).
 """
 
+import math
+
 import numpy as np
 import pytest
 from scipy.special import expit
@@ -208,3 +210,141 @@ def test_route_drop_rules_and_logits():
     assert np.all(w[ids >= 0] == base_w[ids >= 0])
     with pytest.raises(ValueError):
         routing.route(lg, 4, "bogus")
+
+
+# ----------------------------------------------------------------------------
+# quantization_snr_by_group / compress_matrix / int8_group_mask
+# ----------------------------------------------------------------------------
+def test_snr_by_group_known_answers():
+    x = np.zeros(70, np.float32)
+    x[:32] = 3.0                      # group 0: noise = signal / 2 exactly
+    x[32:64] = np.linspace(-1, 1, 32)  # group 1: exact reconstruction
+    x[64:] = 4.0                      # group 2: 6 values, zero-padded to 32
+    cand = x.copy()
+    cand[:32] = 1.5
+    cand[64:] = 2.0
+    snr = ref.quantization_snr_by_group(x, cand, 32)
+    assert snr.shape == (3,)
+    assert snr[0] == pytest.approx(2.0, rel=1e-6)
+    assert snr[1] == pytest.approx(np.linalg.norm(x[32:64]) / 1e-12, rel=1e-6)  # noise floor 1e-12
+    assert snr[2] == pytest.approx(2.0, rel=1e-6)  # ||4|| / ||2|| over the 6 real values; the pad adds zeros
+    # scale invariance and shape independence (flat groups cross rows)
+    assert np.allclose(ref.quantization_snr_by_group(5 * x, 5 * cand, 32)[[0, 2]], snr[[0, 2]], rtol=1e-6)
+    assert np.array_equal(ref.quantization_snr_by_group(x.reshape(7, 10), cand.reshape(7, 10), 32), snr)
+
+
+def test_snr_by_group_brute_force():
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((9, 29)).astype(np.float32)
+    q = x + 0.01 * rng.standard_normal(x.shape).astype(np.float32)
+    flat, fq = x.reshape(-1).tolist(), q.reshape(-1).tolist()
+    want = []
+    for g in range(0, len(flat), 32):
+        s = math.sqrt(sum(v * v for v in flat[g:g + 32]))
+        n = math.sqrt(sum((a - b) ** 2 for a, b in zip(flat[g:g + 32], fq[g:g + 32])))
+        want.append(s / max(n, 1e-12))
+    assert np.allclose(ref.quantization_snr_by_group(x, q, 32), want, rtol=1e-5)
+
+
+def _low_rank(rows, cols, rank, seed):
+    rng = np.random.default_rng(seed)
+    return rng.standard_normal((rows, rank), dtype=np.float32) @ rng.standard_normal((rank, cols), dtype=np.float32)
+
+
+def test_compress_matrix_matches_the_reference_tests():
+    # tests/test_latent_loader.py:41-62
+    arrays, rep = synth.compress_matrix("blk.0.ffn_gate.0", _low_rank(64, 48, 8, 123), energy=0.999, min_rank=4,
+                                        max_rank=16, group_size=32, int8_group_size=64, error_threshold=0.35,
+                                        snr_threshold=0.0, low_snr_fraction_threshold=1.0, seed=7)
+    assert rep["rank"] >= 8 and rep["dense_relative_error"] < 1e-4 and rep["quantized_relative_error"] < 0.35
+    assert not rep["fallback"] and "blk.0.ffn_gate.0.a.nf4" in arrays
+    assert "blk.0.ffn_gate.0.dense_fallback" not in arrays
+    # tests/test_latent_loader.py:100-127: the artifact's swiglu stays within 0.35 of the dense one
+    rng = np.random.default_rng(99)
+    x = rng.standard_normal((3, 16), dtype=np.float32)
+    mats = {"gate": _low_rank(16, 12, 4, 1), "up": _low_rank(16, 12, 4, 2), "down": _low_rank(12, 16, 4, 3)}
+    arrays = {}
+    for name, m in mats.items():
+        a, r = synth.compress_matrix(name, m, energy=0.999, min_rank=4, max_rank=8, error_threshold=1.0,
+                                     snr_threshold=0.0, low_snr_fraction_threshold=1.0, seed=10)
+        assert not r["fallback"]
+        arrays.update(a)
+    latent = ref.swiglu_expert(x, ref.load_pair(arrays, "gate"), ref.load_pair(arrays, "up"), ref.load_pair(arrays, "down"))
+    dense = ref.dense_swiglu_expert(x, mats["gate"], mats["up"], mats["down"])
+    assert ref.relative_frobenius_error(dense, latent) < 0.35
+
+
+def test_compress_matrix_int8_and_dense_fallbacks():
+    m = _low_rank(40, 30, 37, 4)
+    # every group below an infinite SNR threshold: the pair goes INT8 at group 64 when that is better
+    arrays, rep = synth.compress_matrix("w", m, energy=1.0, min_rank=30, max_rank=30, snr_threshold=np.inf,
+                                        low_snr_fraction_threshold=0.0, error_threshold=1.0)
+    assert rep["quantization"] == "int8_g64" and "w.a.int8" in arrays and "w.a.nf4" not in arrays
+    assert arrays["w.a.scales"].size == -(-40 * 30 // 64)
+    aq = ref.load_factor(arrays, "w", "a")
+    assert aq.shape == (40, 30) and ref.relative_frobenius_error(m, aq @ ref.load_factor(arrays, "w", "b")) < 0.05
+    # an error threshold nothing can meet adds the fp16 dense copy
+    arrays, rep = synth.compress_matrix("w", m, energy=0.5, min_rank=1, max_rank=2, error_threshold=0.0)
+    assert rep["fallback"] and arrays["w.dense_fallback"].dtype == np.float16
+
+
+def test_int8_group_mask_brute_force():
+    rng = np.random.default_rng(21)
+    v = (rng.standard_normal((6, 96)) * np.exp(rng.standard_normal((6, 96)))).astype(np.float32)
+    v[2, 32:64] = 0.0  # an all-zero group is never selected
+    for thr in (5.0, 12.0, 20.0):
+        mask = ref.int8_group_mask(v, thr)
+        for r in range(6):
+            for g in range(3):
+                grp = v[r, 32 * g:32 * (g + 1)]
+                packed, scales, shape = ref.quantize_nf4(grp, group_size=32)
+                dec = ref.dequantize_nf4(packed, scales, shape, group_size=32)
+                snr = np.linalg.norm(grp) / max(np.linalg.norm(grp - dec), 1e-12)
+                assert mask[r, g] == (snr < thr and np.abs(grp).max() > 0), (thr, r, g)
+    assert ref.int8_group_mask(v, 1e9).sum() == 6 * 3 - 1
+
+
+def test_mixed_decode_matches_a_per_group_walk():
+    # 64 groups per row (two bitmap words), random flags: the vectorised decode
+    # against a walk over each row's groups that counts flagged groups in order.
+    rng = np.random.default_rng(17)
+    st = rng.standard_normal((3, 5, 2048)).astype(np.float32)
+    mask = rng.random((3, 5, 64)) < 0.3
+    codes, scales, ext = ref.pack_rows_mixed(st, mask)
+    for e in range(3):
+        got = ref.unpack_rows_mixed(codes, scales, ext, e)
+        want = ref.unpack_rows(codes[e], scales[e])
+        for r in range(5):
+            n = 0
+            for g in range(64):
+                if (int(ext.bitmap[e, r, g // 32]) >> (g % 32)) & 1:
+                    q = ext.data[int(ext.row_offset[e, r]) + n].astype(np.float32)
+                    want[r, 32 * g:32 * g + 32] = q * np.float32(scales[e, r, g])
+                    n += 1
+            assert n == mask[e, r].sum()
+        np.testing.assert_array_equal(got, want)
+
+
+def test_int8_subset_rebases_offsets():
+    from tests._layers import _int8_subset
+
+    class Dev:  # the fields of a device factor, as host arrays with a .cpu().numpy() chain
+        def __init__(self, a):
+            self.a = a
+
+        def cpu(self):
+            return self
+
+        def numpy(self):
+            return self.a
+
+    rng = np.random.default_rng(3)
+    st = rng.standard_normal((4, 6, 96)).astype(np.float32)
+    mask = rng.random((4, 6, 3)) < 0.4
+    codes, scales, ext = ref.pack_rows_mixed(st, mask)
+    f = type("F", (), {})()
+    f.int8_bitmap, f.int8_row_offset, f.int8_data = Dev(ext.bitmap.view(np.int32)), Dev(ext.row_offset), Dev(ext.data)
+    sub = _int8_subset(f, np.array([3, 1]))
+    for j, e in enumerate((3, 1)):
+        np.testing.assert_array_equal(ref.unpack_rows_mixed(codes[[3, 1]], scales[[3, 1]], sub, j),
+                                      ref.unpack_rows_mixed(codes, scales, ext, e))
