@@ -138,6 +138,21 @@ int latent_moe_workspace_size(const latent_moe_args* args, size_t* bytes);
 int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 
 /*
+ * latent_moe_ffn_forward without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * args->workspace and args->workspace_bytes are ignored: scratch comes from a
+ * library-owned array of LATENT_NOALLOC_SCRATCH_BYTES on each GPU (held until
+ * the process ends); a call whose latent_moe_workspace_size exceeds that
+ * returns LATENT_E_WORKSPACE.  No call allocates.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other host threads) race; calls in order on one stream do not.
+ */
+#define LATENT_NOALLOC_SCRATCH_BYTES (64u << 20)
+#define LATENT_NOALLOC_CONTROL_BYTES (256u << 10)
+int latent_moe_ffn_forward_noalloc(const latent_moe_args* args, latent_stream_t stream);
+
+/*
  * Reads and clears the error word of a workspace.  A decode kernel whose
  * bounded wait for another workgroup expires sets it and finishes its work
  * on whatever data it has, so it always terminates; the output of that call

@@ -36,6 +36,7 @@ EXPORTED = (
     "latent_status_string",
     "latent_moe_workspace_size",
     "latent_moe_ffn_forward",
+    "latent_moe_ffn_forward_noalloc",
     "latent_moe_path",
     "latent_moe_check",
     "latent_unpack",
@@ -47,6 +48,7 @@ EXPORTED = (
     "latent_expert_forward",
 )
 
+LATENT_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 LATENT_Q_NF4 = 0
 LATENT_Q_INT8 = 1
@@ -169,6 +171,8 @@ def _load() -> ctypes.CDLL:
     lib.latent_moe_ffn_forward.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p]
     lib.latent_moe_check.restype = ctypes.c_int
     lib.latent_moe_check.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.latent_moe_ffn_forward_noalloc.restype = ctypes.c_int
+    lib.latent_moe_ffn_forward_noalloc.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p]
     lib.latent_moe_path.restype = ctypes.c_int
     lib.latent_moe_path.argtypes = [ctypes.POINTER(LatentMoeArgs)]
     lib.latent_unpack.restype = ctypes.c_int
