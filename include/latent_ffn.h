@@ -119,6 +119,10 @@ typedef struct latent_moe_args {
   void* out;                /* f32, shape per out_mode */
   void* workspace;          /* device scratch, >= latent_moe_workspace_size() */
   size_t workspace_bytes;
+  /* Optional: the layer's factors in the streaming tile layout
+   * (latent_stream_tiles_pack), read by the streaming decode path instead of
+   * the six factors above; NULL => that path is not used. */
+  const void* stream_tiles;
 } latent_moe_args;
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -151,6 +155,21 @@ int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 #define LATENT_NOALLOC_SCRATCH_BYTES (64u << 20)
 #define LATENT_NOALLOC_CONTROL_BYTES (256u << 10)
 int latent_moe_ffn_forward_noalloc(const latent_moe_args* args, latent_stream_t stream);
+
+/*
+ * The layer's six factors in the streaming tile layout of the decode path:
+ * every 256x256 block of a factor as 32 KB of NF4 codes in MFMA-operand order
+ * followed by its 4 KB of scales, so the path reads each block as one
+ * contiguous stream (no reference counterpart; a backend builds it once when
+ * it loads the layer's tensors, as ggml backends repack weights for their
+ * kernels).  Applies to pure-NF4 layers with max_rank == 256 and n_embd,
+ * n_ff multiples of 256; for any other layer *bytes is 0.  The size equals
+ * the packed factors' (the layout only reorders them).
+ */
+int latent_stream_tiles_size(const latent_moe_args* args, size_t* bytes);
+/* Writes the tile layout of args' factors to `tiles` (16-byte aligned,
+ * >= latent_stream_tiles_size bytes); stream ordered. */
+int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t tiles_bytes, latent_stream_t stream);
 
 /*
  * Reads and clears the error word of a workspace.  A decode kernel whose

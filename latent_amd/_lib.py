@@ -46,6 +46,8 @@ EXPORTED = (
     "latent_route",
     "latent_expert_workspace_size",
     "latent_expert_forward",
+    "latent_stream_tiles_size",
+    "latent_stream_tiles_pack",
 )
 
 LATENT_NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -95,6 +97,7 @@ class LatentMoeArgs(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
+        ("stream_tiles", ctypes.c_void_p),
     ]
 
 
@@ -191,6 +194,10 @@ def _load() -> ctypes.CDLL:
     lib.latent_expert_workspace_size.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.latent_expert_forward.restype = ctypes.c_int
     lib.latent_expert_forward.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.c_void_p]
+    lib.latent_stream_tiles_size.restype = ctypes.c_int
+    lib.latent_stream_tiles_size.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.POINTER(ctypes.c_size_t)]
+    lib.latent_stream_tiles_pack.restype = ctypes.c_int
+    lib.latent_stream_tiles_pack.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     return lib
 
 

@@ -67,8 +67,7 @@ struct MoeParams {
   float* dl;  // [P][R]
   int4* unit_info;  // streaming path work units {expert, first pair, pairs, 0} (NULL: not built)
   int* unit_tok;    // [units][16] token of each unit row (0 past the unit's pairs)
-  int* unit_dst;    // [units][16] token * K + slot
-  float* unit_w;    // [units][16] router weight
+  int* pos_of;      // [T*K] grouped position of each routed slot (streaming path)
   _Float16* xh;     // streaming path: x as fp16 rows * 2^xexp (NULL: not converted)
   int* xexp;        // [T] row exponents
   int x_dtype, w_dtype;
@@ -122,8 +121,7 @@ __device__ __forceinline__ void scatter_pair(const MoeParams& p, const int* star
     const int rel = pos - start[e];
     const int row = (ubase[e] + rel / stream::kMaxM) * stream::kMaxM + rel % stream::kMaxM;
     p.unit_tok[row] = tok;
-    p.unit_dst[row] = i;
-    p.unit_w[row] = w;
+    p.pos_of[i] = pos;
   }
 }
 
@@ -216,8 +214,6 @@ __device__ void route_block(const MoeParams& p) {
           p.unit_info[unit] = make_int4(e, start + j, m, 0);
           for (int r = m; r < stream::kMaxM; ++r) {
             p.unit_tok[unit * stream::kMaxM + r] = 0;
-            p.unit_dst[unit * stream::kMaxM + r] = 0;
-            p.unit_w[unit * stream::kMaxM + r] = 0.f;
           }
         }
       }
@@ -378,6 +374,7 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
       }
       if (threadIdx.x == 0) p.xexp[t] = ex;
     }
+    return;  // the streaming path clears nothing: its kernels write every output
   }
   // Accumulators gu and dl are contiguous: zero_floats covers both.
   float4* acc4 = reinterpret_cast<float4*>(p.gu);
@@ -723,7 +720,7 @@ Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
   L.pair_slot = off;  off = align_up(off + P * sizeof(int));
   L.pair_w = off;     off = align_up(off + P * sizeof(float));
   L.hist = off;       off = align_up(off + group_chunks(P, E) * (E + 1) * sizeof(int));
-  L.units = off;      off = align_up(off + (4 + 3 * stream::kMaxM) * stream::max_units(P, E) * sizeof(int));
+  L.units = off;      off = align_up(off + (4 + stream::kMaxM) * stream::max_units(P, E) * sizeof(int));
   L.gu = off;         off += P * 2 * R * sizeof(float);  // gu and dl contiguous (one clear)
   L.dl = off;         off = align_up(off + P * R * sizeof(float));
   L.total = off;
@@ -919,9 +916,8 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     const int64_t mu = stream::max_units(P, a.n_expert);
     p.unit_info = reinterpret_cast<int4*>(ws + L.units);
     p.unit_tok = reinterpret_cast<int*>(p.unit_info + mu);
-    p.unit_dst = p.unit_tok + mu * stream::kMaxM;
-    p.unit_w = reinterpret_cast<float*>(p.unit_dst + mu * stream::kMaxM);
     const stream::Layout SL = stream::layout_for(a);
+    p.pos_of = reinterpret_cast<int*>(ws + L.gu + SL.pos_of);
     p.xh = reinterpret_cast<_Float16*>(ws + L.gu + SL.xh);
     p.xexp = reinterpret_cast<int*>(ws + L.gu + SL.xexp);
   }
@@ -939,8 +935,10 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.cd = pick_pow2_chunk(p.d, p.a_max, 2048, 128, 512);
   p.n_d = (p.d + p.cd - 1) / p.cd;
 
-  const int64_t zero_work = p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
-                                                                                  : P * a.n_embd / 4);
+  const int64_t zero_work =
+      use_stream ? 0
+                 : p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
+                                                                         : P * a.n_embd / 4);
   // The streaming path also converts x, one workgroup per token.
   const int64_t conv_blocks = use_stream ? a.n_tokens : 1;
   const int zero_blocks = static_cast<int>(
@@ -962,8 +960,8 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     return prefill::forward(a, p.fac, g, ws + L.gu, s);
   }
   if (use_stream) {
-    const stream::Grouping g{p.meta, p.unit_info, p.unit_tok, p.unit_dst, p.unit_w};
-    return stream::forward(a, p.fac, g, ws + L.gu, s);
+    const stream::Grouping g{p.meta, p.unit_info, p.unit_tok};
+    return stream::forward(a, g, ws + L.gu, s);
   }
   if (MB == 1)
     st = any_int8 ? launch_phases<1, true>(p, s) : launch_phases<1, false>(p, s);

@@ -8,40 +8,50 @@
 // 16 pairs of one expert; every unit is one 16-row MFMA tile, so the work per
 // factor byte does not grow with the number of tokens an expert receives.
 //
-//   A   x . A_g | A_u               K slices of 256 rows -> partial latents (reduce_a)
-//   B   g = g_lat . B_g, u = u_lat . B_u, h = SiLU(g) * u [* w]
-//                                   N slices of 256, gate and up paired
-//   C   h . A_d                     K slices of 256 rows -> partial d latent (reduce_c)
-//   D   d_lat . B_d                 N slices of 256      -> y rows, then the combine
+//   A   x . A_g | A_u              K tiles of 256 rows -> partial latents (reduce A)
+//   B   [g | u] = lat . [B_g | B_u], h = SiLU(g) * u
+//                                  tiles of 128 gate + 128 up columns, h formed in-lane
+//   C   h . A_d                    K tiles of 256 rows -> partial d latent (reduce C)
+//   D   d_lat . B_d                N tiles of 256 columns -> y rows, then the combine
 //
-// Every activation a phase reads is an fp16 row with one power-of-two
-// exponent per row and 256-column slice (row maximum in [2^14, 2^15)): the
-// prep kernel writes x that way, reduce_a / reduce_c the latents and phase B
-// h, so the latents of a LATENT chain (1e-3 ... 1e-9 here) keep fp16's full
-// precision.
+// The factors are read from a tile layout built once per layer
+// (latent_stream_tiles_pack): every 256 x 256 block of a factor is 32 KB of
+// NF4 codes followed by 4 KB of fp16 scales, in the order the lanes consume
+// them, so each lane reads its MFMA operand bytes with one 128-bit load per
+// 32-row step and every tile is one contiguous 36 KB stream:
+//   * wave w owns tile columns 64w .. 64w+63 over all 256 rows; lane
+//     (n = lane & 15, kq = lane >> 4) holds, per 32-row step s, the code
+//     pairs of rows s*32 + kq*8 + (2q, 2q+1), q = 0..3, for columns
+//     64w + 4n + j, j = 0..3 (byte 4j + q, low nibble = even row): dword j
+//     is the B operand of v_mfma_f32_16x16x32_f16 number j, whose N block is
+//     the columns 4n + j of the wave;
+//   * scales: half2 (scale(2P, G), scale(2P + 1, G)) for group G = 0..7 and
+//     row pair P at dword G * 128 + (P ^ 8 (G & 1)) (the xor spreads the
+//     lanes of one LDS read over all banks);
+//   * phase B's tiles interleave the two factors: for lane n of wave w the
+//     columns j = 0, 1 are gate columns 32w + 2n + j of the 128-column block
+//     and j = 2, 3 the up columns of the same outputs, so each lane forms
+//     h = SiLU(g) * u of its two columns itself; groups 0..3 are the gate
+//     groups of waves 0..3, groups 4..7 the up groups.
+// A byte (two rows of one column) is looked up in a 256-entry table of
+// (level, level) fp16 pairs in LDS, one copy per LDS bank, and one
+// v_pk_mul_f16 by the two rows' scales gives one K pair of the B operand.
 //
-// One 256-thread workgroup runs a group of consecutive slices of one unit.
-// Per slice (a 256 x 256 block of a factor):
-//   * wave w owns column half ch = w & 1 and K half kh = w >> 1; lane
-//     (cq = lane & 15, kq = lane >> 4) loads one code dword (columns
-//     ch*128 + 8cq .. +7) of rows kq*8 .. kq*8+7 of each 32-row step: 32
-//     buffer loads per slice into registers, issued one slice ahead;
-//   * the slice's fp16 scales (4 KB) and, for K slices, its activation rows
-//     (8 KB) and their exponents go global -> LDS by direct loads
-//     (global_load_lds), issued two slices ahead into double buffers;
-//   * the nibbles of row pairs (k, k+1) are interleaved into bytes, each byte
-//     is looked up in a 256-entry table of (level, level) fp16 pairs in LDS,
-//     and one v_pk_mul_f16 by the two rows' fp16 scales gives one K pair of an
-//     MFMA B fragment: column j of the dword feeds v_mfma_f32_16x16x32_f16
-//     number j, whose N block is the columns 8n + j of the half;
-//   * the two K halves are added through LDS.
-// K-sliced phases (A, C) accumulate a group's slices in registers (rescaled
-// when the next slice's row exponents differ) and write one partial sum per
-// group; N-sliced phases (B, D) write every slice.
+// Every activation a phase reads is an fp16 row with a power-of-two exponent
+// (row maximum in [2^14, 2^15)): the prep kernel writes x that way (one
+// exponent per token), the reduce kernels the latents (one per row) and
+// phase B h (one per row and 128-column block), so the small latents of a
+// LATENT chain keep fp16's full precision.
 //
-// Units run on XCD (unit mod 8) -- workgroup b runs on XCD b mod 8 -- so all
-// slices of a unit, which share activation rows and 128-byte lines of scales,
-// are read through one L2.
+// Work split: each phase is one persistent launch of two workgroups per CU;
+// workgroup b takes the contiguous tile range [b*chunk, (b+1)*chunk) of the
+// phase's tile list (unit-major), so every workgroup streams the same number
+// of tiles.  Tile i + 2's loads are issued while tile i is computed: its codes
+// into registers, its scales, activations and exponents into registers that
+// are stored to LDS at the end of tile i + 1.  All are ordinary buffer loads,
+// so the compiler places every wait.  K-tiled phases (A, C) accumulate
+// consecutive tiles of one (unit, factor) in registers and write one partial
+// sum per segment; the reduce kernels add a row's partials in workgroup order.
 //
 // Arithmetic: fp16 operands (levels and scales exact in fp16 up to one
 // rounding of level * scale and of the scaled activation), fp32 accumulation.
@@ -49,48 +59,57 @@
 #include "stream.hpp"
 
 #include <algorithm>
-#include <type_traits>
+#include <mutex>
 
 namespace latent {
 namespace stream {
 namespace {
 
-constexpr int kT = 256;                    // threads per workgroup
-constexpr int kK = 256;                    // K rows per slice
-constexpr int kN = 256;                    // N columns per slice
-constexpr int kSliceGroups = kN / kGroup;  // scale groups per slice row
-constexpr int kActChunks = kK / 8;         // 16-byte chunks of an fp16 activation row
-constexpr int kLutCopies = 32;            // one table copy per LDS bank
-constexpr int kMaxNB = 8;                  // N (or K) slices per workgroup
-enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
+constexpr int kT = 256;                               // threads per workgroup
+constexpr int kK = 256;                               // rows of a tile
+constexpr int kN = 256;                               // columns of a tile
+constexpr int kSteps = kK / 32;                       // MFMA K steps per tile
+constexpr int kCodeBytes = kK * kN / 2;               // 32 KB
+constexpr int kScaleBytes = kK * kN / kGroup * 2;     // 4 KB
+constexpr int kTileBytes = kCodeBytes + kScaleBytes;  // 36 KB
+constexpr int kHBlock = kN / 2;                       // h columns of a phase-B tile
+constexpr int kLutCopies = 32;                        // one table copy per LDS bank
+constexpr int kActChunks = kK / 8;                    // 16-byte chunks of an fp16 activation row
+constexpr int kGroupsPerCU = 2;                       // resident workgroups per CU of the item kernels
 enum Phase { kPhaseA = 0, kPhaseB, kPhaseC, kPhaseD };
+enum { T_GATE_A = 0, T_UP_A, T_GU_B, T_DOWN_A, T_DOWN_B, kTileArrays };
+enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct Params {
-  Factor fac[6];
-  Grouping g;
+  const uint8_t* tiles[kTileArrays];
+  const int* meta;        // [4] work units
+  const int4* unit_info;  // [units] {expert, first grouped pair, pairs, 0}
+  const int* unit_tok;    // [units][16] token of each row
+  const int* pos_of;      // [T*K] grouped pair of each routed slot
   const int32_t* ids;
+  const void* weights;
+  int w_dtype;
   float* out;
   const _Float16* xh;  // [T][d] fp16 x * 2^xexp
   const int* xexp;     // [T]
-  float* partA;        // [2][gA][P][256]
-  _Float16* lath;      // [2][P][256]
+  float* partA;        // [slots][16][256]
+  _Float16* lat;       // [2][P][256]
   int* lexp;           // [2][P]
   _Float16* hh;        // [P][ff]
-  int* hexp;           // [P][ff/256]
-  float* partC;        // [gC][P][256]
-  _Float16* dlath;     // [P][256]
+  int* hexp;           // [P][ff/128]
+  float* partC;        // [slots][16][256]
+  _Float16* dlat;      // [P][256]
   int* dexp;           // [P]
-  float* ybuf;         // [T*K][d]
+  float* ybuf;         // [P][d]
   int T, K, E, d, ff, P, wbd, out_mode;
-  int umax;                // units the unit tables hold
-  int nks, nbs, nkc, nds;  // slices: A (d/256), B (ff/256), C (ff/256), D (d/256)
-  int nb[4];               // slices per group, per phase (B: N slices, each run for gate and up)
-  int gA, gB, gC, gD;      // groups: A per factor, B/C/D per unit
+  int nka, nb, nkc, nd;  // tiles per unit and factor: A (d/256), B (ff/128), C (ff/256), D (d/256)
+  int G;                 // workgroups the tile ranges are cut for
 };
 
 // LDS byte address of a __shared__ object and raw LDS loads.
@@ -103,466 +122,435 @@ __device__ __forceinline__ T lds_ld(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
 }
 
-// A wave-uniform 64-bit address in scalar registers.
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-  const uint64_t v = reinterpret_cast<uintptr_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+// Loads through the scalar unit: the address must be the same in every lane.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int sload(const int* p) { return *(const __attribute__((address_space(4))) int*)(p); }
+__device__ __forceinline__ i32x4 sload4(const int4* p) {
+  return *(const __attribute__((address_space(4))) i32x4*)(p);
 }
-
-// Direct global -> LDS loads.  Lane l's bytes land at LDS byte lds + 16 l
-// (dwordx4) or lds + 4 l (dword); lds is wave-uniform.  Inline assembly keeps
-// the compiler from making later LDS reads wait on them: the kernel counts
-// them itself (vmcnt) before the barrier that publishes the data.
-// Uniform base + per-lane 32-bit offset:
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(uniform_ptr(base)),
-               "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "m0", "memory");
-}
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Raw (byte-addressed) buffer resource over `bytes` bytes from `base`
 // (wave-uniform); loads beyond them return zero.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_ptr(base)), static_cast<short>(0),
-                                           static_cast<int>(bytes), 0x00020000);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
+}
+
+// Barrier for LDS data only: this wave's LDS operations complete, then
+// s_barrier.  (__syncthreads() would also wait for every outstanding global
+// load, which would drain the loads issued ahead for later tiles.)
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // SiLU with the hardware exponential and reciprocal (each within about 1 ulp);
 // g -> -inf gives -0, g -> +inf gives g.
 __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
-// s_waitcnt vmcnt(n): at most n vector memory operations of this wave left
-// outstanding.  Inline assembly: the compiler does not see the direct loads
-// this wait is for, so it would drop a wait it thinks satisfied.
-template <int kCount>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(kCount >= 0 && kCount < 63, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kCount) : "memory");
-}
-// Barrier for LDS data: lgkmcnt(0) + s_barrier; direct loads stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Shared memory of one workgroup (about 73 KB: two resident per CU).
-struct alignas(16) ItemSmem {
-  uint32_t lut[256 * kLutCopies];         // [byte][copy]: half2(level(lo nibble), level(hi nibble))
-  uint16_t scales[2][kK * kSliceGroups];  // [buffer][row][group] fp16 bits
-  uint4 act[2][kMaxM * kActChunks];       // [buffer][row][chunk ^ row]: fp16 rows * 2^rexp
-  float fold[2 * kMaxM * 128];            // K half 1 of both column halves ([ch][row][128])
-  int rexp[2][kMaxM];                     // row exponents of act[buffer]
-  float hmax[2][kMaxM];                   // phase B: row maxima of h per column half
-  uint32_t row_dst[kMaxM];                // phase D: output row offset of each row
-  float row_w[kMaxM];                     // router weight applied to each row (1 if none)
-};
-
-// Chunk c of activation row r sits at chunk (c ^ (r & 15)) of the row: the 16
-// rows an MFMA fragment read touches then hit 16 different bank groups.
+// Chunk c of activation row r sits at chunk (c ^ (r & 15)) of the row.
 __device__ __forceinline__ int act_slot(int row, int chunk) { return row * kActChunks + (chunk ^ (row & 15)); }
 
+// ---------------------------------------------------------------------------
+// Per-phase shape of the work
+// ---------------------------------------------------------------------------
 template <int kPhase>
-__device__ __forceinline__ int groups_per_unit(const Params& p) {
-  return kPhase == kPhaseA ? 2 * p.gA : kPhase == kPhaseB ? p.gB : kPhase == kPhaseC ? p.gC : p.gD;
-}
+struct Shape {
+  static constexpr bool kSliceK = kPhase == kPhaseA || kPhase == kPhaseC;  // tiles along K (partial sums)
+  static constexpr int kActBlocks = kPhase == kPhaseB ? 2 : 1;  // activation blocks per tile (B: gate and up latents)
+  static constexpr int kActLoads = 2 * kActBlocks;              // 16-byte activation chunks per thread
+  static constexpr int kExps = kPhase == kPhaseB || kPhase == kPhaseC ? 32 : 16;
+};
 
-// Direct loads per run: scales, plus for K slices 2 activation loads and the exponents.
+// Tiles per unit, and per key (a K-tiled phase's segment: one unit and factor).
 template <int kPhase>
-constexpr int run_dma() {
-  return kPhase == kPhaseA || kPhase == kPhaseC ? 4 : 1;
+__device__ __forceinline__ int tiles_per_unit(const Params& p) {
+  return kPhase == kPhaseA ? 2 * p.nka : kPhase == kPhaseB ? p.nb : kPhase == kPhaseC ? p.nkc : p.nd;
+}
+template <int kPhase>
+__device__ __forceinline__ int tiles_per_key(const Params& p) {
+  return kPhase == kPhaseA ? p.nka : kPhase == kPhaseC ? p.nkc : 1;
 }
 
-// Direct load of 4 bytes at base + off (base wave-uniform, off per lane):
-// lane l's bytes land at LDS byte lds + 4 l.
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(uniform_ptr(base)),
-               "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "m0", "memory");
+template <int kPhase>
+struct alignas(16) Smem {
+  uint32_t lut[256 * kLutCopies];                              // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[2][kScaleBytes / 16];                           // [buffer]: the tile's scale block
+  u32x4 act[2][Shape<kPhase>::kActBlocks][kMaxM * kActChunks];  // [buffer][block][row][chunk ^ row]
+  int rexp[2][32];                                             // row exponents of act[buffer]
+  float hmax[4][kMaxM];                                        // phase B: row maxima of h per wave
+};
+
+// Registers a tile's non-code loads land in before they are stored to LDS.
+template <int kPhase>
+struct StageAct {
+  u32x4 act[Shape<kPhase>::kActLoads];
+  int ex;
+};
+
+// Phase B issues a tile's activation loads one step later than its codes
+// (from the latents in L2, into one staging slot), which keeps its registers
+// within two waves per SIMD; the others issue them with the codes.
+template <int kPhase>
+constexpr bool late_act() {
+  return kPhase == kPhaseB;
 }
 
-// A 256-wide fp16 activation block of the unit's 16 rows into act buffer
-// `buf`: thread tid loads chunk (tid % 32) of rows tid / 32 and 8 + tid / 32,
-// at byte offsets off0 and off1 from `base` (the chunk position is added here).
-__device__ __forceinline__ void dma_act(ItemSmem& sm, int buf, int tid, int wave, const void* base, uint32_t off0,
-                                        uint32_t off1) {
-  const int r0 = tid / kActChunks;
-  const uint32_t c0 = (tid % kActChunks) ^ (r0 & 15), c1 = (tid % kActChunks) ^ ((r0 + 8) & 15);
-  dma16(base, off0 + c0 * 16, lds_addr(sm.act[buf][0]) + wave * kWave * 16);
-  dma16(base, off1 + c1 * 16, lds_addr(sm.act[buf][0]) + (kT + wave * kWave) * 16);
+// Phase A's per-lane token rows of a tile: the rows of the thread's two
+// activation chunks and of exponent row lane & 15.
+struct Toks {
+  int a0, a1, e;
+};
+
+// Scalar description of a tile: its unit and position in the unit.
+struct TileRef {
+  int e, start, m, r;  // expert, first grouped pair, pairs, tile index within the unit
+};
+
+template <int kPhase>
+__device__ __forceinline__ TileRef tile_ref(const Params& p, int t) {
+  const int per = tiles_per_unit<kPhase>(p);
+  const int u = uniform(t / per);
+  const i32x4 info = sload4(p.unit_info + u);
+  return TileRef{uniform(info[0]), uniform(info[1]), uniform(info[2]), t - u * per};
 }
 
-// The 16 row exponents into rexp[buf]: lane l < 16 loads row l's, at byte
-// offset `off` from `base`.  Every wave loads the same values, so every wave
-// counts the same loads.
-__device__ __forceinline__ void dma_exp(ItemSmem& sm, int buf, int lane, const void* base, uint32_t off) {
-  if (lane < kMaxM) dma4(base, off, lds_addr(sm.rexp[buf][0]));
+// Tile array, tile index and K tile of a tile.
+template <int kPhase>
+__device__ __forceinline__ const uint8_t* tile_ptr(const Params& p, const TileRef& tr, int& ks) {
+  int arr, idx;
+  ks = 0;
+  if constexpr (kPhase == kPhaseA) {
+    const int f = tr.r >= p.nka;
+    ks = tr.r - f * p.nka;
+    arr = f ? T_UP_A : T_GATE_A;
+    idx = tr.e * p.nka + ks;
+  } else if constexpr (kPhase == kPhaseB) {
+    arr = T_GU_B;
+    idx = tr.e * p.nb + tr.r;
+  } else if constexpr (kPhase == kPhaseC) {
+    ks = tr.r;
+    arr = T_DOWN_A;
+    idx = tr.e * p.nkc + ks;
+  } else {
+    arr = T_DOWN_B;
+    idx = tr.e * p.nd + tr.r;
+  }
+  return p.tiles[arr] + static_cast<int64_t>(idx) * kTileBytes;
 }
 
-// Issue the code loads of a slice: rows kh*128 + s*32 + kq*8 + i, dword
-// ch*16 + cq of the slice row.  Buffer loads: one lane offset register, the
-// row offset (s*32 + i) * code_row in a scalar register.
-__device__ __forceinline__ void load_codes(uint32_t (&d)[4][8], const uint8_t* codes, uint32_t code_row, int ch, int kh,
-                                           int cq, int kq) {
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(codes, kK * code_row);
-  const uint32_t lane_off = (kh * 128 + kq * 8) * code_row + (ch * 16 + cq) * 4;
+// The loads below take `valid`: when false they are issued against empty
+// buffer ranges, fetch nothing and return zeros, so every step issues the same
+// loads and the compiler's wait counts hold on every path.
+
+// A tile's scale block into `sc`, then its codes into `cb`.
+template <int kPhase>
+__device__ __forceinline__ void issue_codes(const Params& p, const TileRef& tr, int tid, int lane, int wave, bool valid,
+                                            u32x4& sc, u32x4 (&cb)[kSteps]) {
+  int ks;
+  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile_ptr<kPhase>(p, tr, ks), valid ? kTileBytes : 0);
+  sc = ld128(rt, tid * 16, kCodeBytes);
+  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) d[s][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, lane_off, (s * 32 + i) * code_row, 0);
+  for (int s = 0; s < kSteps; ++s) cb[s] = ld128(rt, cbase, s * kWave * 16);
 }
 
-// Decode + MFMA of one slice for this wave's four 32-row steps.
-__device__ __forceinline__ void k_loop(const ItemSmem& sm, int sbuf, int abuf, const uint32_t (&d)[4][8], int ch,
-                                       int kh, int cq, int kq, uint32_t lut_lane, float4v (&acc)[8]) {
-  const int c = ch * 4 + (cq >> 2);
-  const uint32_t scale_base = lds_addr(const_cast<ItemSmem&>(sm).scales[sbuf][0]) + c * 2;
+// A tile's activation chunks and row exponents.  Chunk tid + 256 h is 16-byte
+// chunk tid % 32 of row (tid / 32 + 8 h) % 16 of activation block h / 2;
+// exponent lane l is row l & 15 (of block (l >> 4) & 1 where there are two).
+template <int kPhase>
+__device__ __forceinline__ void issue_act(const Params& p, const TileRef& tr, const Toks& tk, int tid, int lane,
+                                          bool valid, StageAct<kPhase>& st) {
+  const uint32_t live = valid ? 0xFFFFFFFFu : 0u;  // masks every buffer range
+  int ks = 0;
+  if constexpr (kPhase == kPhaseA) ks = tr.r >= p.nka ? tr.r - p.nka : tr.r;
+  if constexpr (kPhase == kPhaseC) ks = tr.r;
+  auto pair_of = [&](int r) { return tr.start + min(r, tr.m - 1); };
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+  if constexpr (kPhase == kPhaseA) {
+    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.xh, (static_cast<uint32_t>(p.T) * p.d * 2) & live);
+    const uint32_t col = ks * kK * 2 + chunk * 16;
+    st.act[0] = ld128(rx, static_cast<uint32_t>(tk.a0) * p.d * 2 + col, 0);
+    st.act[1] = ld128(rx, static_cast<uint32_t>(tk.a1) * p.d * 2 + col, 0);
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.xexp, (p.T * 4) & live);
+    st.ex = static_cast<int>(ld32(re, tk.e * 4));
+  } else if constexpr (kPhase == kPhaseB) {
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.lat, (2u * p.P * kK * 2) & live);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int k0 = kh * 128 + s * 32 + kq * 8;
-    const half8 a = __builtin_bit_cast(half8, sm.act[abuf][act_slot(cq, k0 / 8)]);
-    uint32_t sp[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t s0 = lds_ld<uint16_t>(scale_base + (k0 + 2 * q) * (kSliceGroups * 2));
-      const uint32_t s1 = lds_ld<uint16_t>(scale_base + (k0 + 2 * q + 1) * (kSliceGroups * 2));
-      sp[q] = s0 | (s1 << 16);
+    for (int h = 0; h < 4; ++h) {
+      const int row = (r0 + 8 * h) % kMaxM, f = h / 2;
+      st.act[h] = ld128(rl, (static_cast<uint32_t>(f) * p.P + pair_of(row)) * kK * 2 + chunk * 16, 0);
     }
-    // Byte t of lo[q] holds column 2t of rows (2q, 2q+1), byte t of hi[q] column 2t+1.
-    uint32_t lo[4], hi[4];
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.lexp, (2u * p.P * 4) & live);
+    st.ex = static_cast<int>(ld32(re, (((lane >> 4) & 1) * p.P + pair_of(lane & 15)) * 4));
+  } else if constexpr (kPhase == kPhaseC) {
+    const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(p.hh, (static_cast<uint32_t>(p.P) * p.ff * 2) & live);
+    const uint32_t col = ks * kK * 2 + chunk * 16;
+    st.act[0] = ld128(rh, static_cast<uint32_t>(pair_of(r0)) * p.ff * 2 + col, 0);
+    st.act[1] = ld128(rh, static_cast<uint32_t>(pair_of(r0 + 8)) * p.ff * 2 + col, 0);
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.hexp, (static_cast<uint32_t>(p.P) * p.nb * 4) & live);
+    st.ex = static_cast<int>(ld32(re, (pair_of(lane & 15) * p.nb + 2 * ks + ((lane >> 4) & 1)) * 4));
+  } else {
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.dlat, (static_cast<uint32_t>(p.P) * kK * 2) & live);
+    st.act[0] = ld128(rl, static_cast<uint32_t>(pair_of(r0)) * kK * 2 + chunk * 16, 0);
+    st.act[1] = ld128(rl, static_cast<uint32_t>(pair_of(r0 + 8)) * kK * 2 + chunk * 16, 0);
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.dexp, (p.P * 4) & live);
+    st.ex = static_cast<int>(ld32(re, pair_of(lane & 15) * 4));
+  }
+}
+
+// Store a staged tile into LDS buffer `buf`.
+template <int kPhase>
+__device__ __forceinline__ void store_stage(Smem<kPhase>& sm, int buf, const u32x4& sc, const StageAct<kPhase>& st,
+                                            int tid, int lane, int wave) {
+  sm.scales[buf][tid] = sc;
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      lo[q] = (d[s][2 * q] & 0x0F0F0F0Fu) | ((d[s][2 * q + 1] << 4) & 0xF0F0F0F0u);
-      hi[q] = ((d[s][2 * q] >> 4) & 0x0F0F0F0Fu) | (d[s][2 * q + 1] & 0xF0F0F0F0u);
+  for (int h = 0; h < Shape<kPhase>::kActLoads; ++h) {
+    const int row = (r0 + 8 * h) % kMaxM;
+    sm.act[buf][h / 2][act_slot(row, chunk)] = st.act[h];
+  }
+  if (wave == 0 && lane < Shape<kPhase>::kExps) sm.rexp[buf][lane] = st.ex;
+}
+
+// MFMA steps [s0, s1) of a tile: acc[j] += act . (codes dword j, decoded and scaled).
+template <int kPhase>
+__device__ __forceinline__ void mfma_steps(const Smem<kPhase>& sm, int buf, const u32x4 (&cb)[kSteps], int s0, int s1,
+                                           int n, int kq, int wave, uint32_t lut_lane, float4v (&acc)[4]) {
+  const uint32_t sbase = lds_addr(const_cast<Smem<kPhase>&>(sm).scales[buf][0]);
+#pragma unroll
+  for (int s = s0; s < s1; ++s) {
+    const int chunk = s * 4 + kq;
+    const half8 a0 = __builtin_bit_cast(half8, sm.act[buf][0][act_slot(n, chunk)]);
+    const int P0 = s * 16 + kq * 4;
+    u32x4 sc0, sc1;
+    half8 a1;
+    if constexpr (kPhase == kPhaseB) {
+      a1 = __builtin_bit_cast(half8, sm.act[buf][1][act_slot(n, chunk)]);
+      const int Gg = wave, Gu = 4 + wave;
+      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
+      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+    } else {
+      const int G = 2 * wave + (n >> 3);
+      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc1 = sc0;
+      a1 = a0;
     }
-    // Columns 2bb and 2bb + 1: their four K pairs, then their two MFMAs.
 #pragma unroll
-    for (int bb = 0; bb < 4; ++bb) {
-      uint32_t fe[4], fo[4];
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = cb[s][j];
+      const u32x4 sc = j < 2 ? sc0 : sc1;
+      uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const half2v sc = __builtin_bit_cast(half2v, sp[q]);
-        const uint32_t pe = lds_ld<uint32_t>(lut_lane + (((lo[q] >> (8 * bb)) & 0xFFu) << 7));
-        const uint32_t po = lds_ld<uint32_t>(lut_lane + (((hi[q] >> (8 * bb)) & 0xFFu) << 7));
-        fe[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pe) * sc);
-        fo[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, po) * sc);
+        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        // Through a scalar: __builtin_bit_cast of a vector element reads element 0.
+        const uint32_t sq = sc[q];
+        f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
       }
-      acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          a, __builtin_bit_cast(half8, make_uint4(fe[0], fe[1], fe[2], fe[3])), acc[2 * bb], 0, 0, 0);
-      acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          a, __builtin_bit_cast(half8, make_uint4(fo[0], fo[1], fo[2], fo[3])), acc[2 * bb + 1], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1,
+                                                      __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3])),
+                                                      acc[j], 0, 0, 0);
     }
   }
 }
 
-// Add the K halves: K-half-1 waves write rows < m to LDS, K-half-0 waves add
-// them (after the call they hold the slice sums; the others are consumed).
-__device__ __forceinline__ void fold_halves(ItemSmem& sm, float4v (&acc)[8], int ch, int kh, int cq, int kq, int m) {
-  if (kh == 1) {
-#pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-      const int row = kq * 4 + vv;
-      if (row >= m) continue;
-      float4* dst = reinterpret_cast<float4*>(&sm.fold[(ch * kMaxM + row) * 128 + cq * 8]);
-      dst[0] = make_float4(acc[0][vv], acc[1][vv], acc[2][vv], acc[3][vv]);
-      dst[1] = make_float4(acc[4][vv], acc[5][vv], acc[6][vv], acc[7][vv]);
-    }
-  }
-  lds_barrier();
-  if (kh == 0) {
-#pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-      const int row = kq * 4 + vv;
-      if (row >= m) continue;
-      const float4* src = reinterpret_cast<const float4*>(&sm.fold[(ch * kMaxM + row) * 128 + cq * 8]);
-      const float4 f0 = src[0], f1 = src[1];
-      acc[0][vv] += f0.x; acc[1][vv] += f0.y; acc[2][vv] += f0.z; acc[3][vv] += f0.w;
-      acc[4][vv] += f1.x; acc[5][vv] += f1.y; acc[6][vv] += f1.z; acc[7][vv] += f1.w;
-    }
-  }
+// Partial-sum slot of segment key `key` in workgroup b's range (K-tiled phases).
+__device__ __forceinline__ int part_slot(int b, int key, int chunk, int per_key, int maxj) {
+  return b * maxj + key - (b * chunk) / per_key;
 }
 
-// K-half-0 waves store rows < m of the sums scaled by 2^-rexp[buf][row] times
-// scale(row) to dst_row(row) + the wave's 8 columns.
-template <typename DstRow, typename RowScale>
-__device__ __forceinline__ void store_rows(const ItemSmem& sm, int buf, const float4v (&acc)[8], int ch, int cq, int kq,
-                                           int m, DstRow dst_row, RowScale scale) {
-#pragma unroll
-  for (int vv = 0; vv < 4; ++vv) {
-    const int row = kq * 4 + vv;
-    if (row >= m) continue;
-    float* dst = dst_row(row) + ch * 128 + cq * 8;
-    const float sc = scale(row) * ldexpf(1.0f, -sm.rexp[buf][row]);
-    reinterpret_cast<float4*>(dst)[0] = make_float4(acc[0][vv] * sc, acc[1][vv] * sc, acc[2][vv] * sc, acc[3][vv] * sc);
-    reinterpret_cast<float4*>(dst)[1] = make_float4(acc[4][vv] * sc, acc[5][vv] * sc, acc[6][vv] * sc, acc[7][vv] * sc);
-  }
-}
-
-// One workgroup per (unit, group of consecutive slices).
 template <int kPhase>
-__global__ void __launch_bounds__(kT, 2) item_kernel(Params p) {
-  __shared__ ItemSmem sm;
-  constexpr bool kSliceK = kPhase == kPhaseA || kPhase == kPhaseC;  // slices along K (else along N)
+__global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
+  using S = Shape<kPhase>;
+  __shared__ Smem<kPhase> sm;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ch = wave & 1, kh = wave >> 1;
-  const int cq = lane & 15, kq = lane >> 4;
-  // Workgroup b runs on XCD b % 8 and takes units u == b (mod 8) in order.
-  const int gpu = groups_per_unit<kPhase>(p);
-  const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
-  const int unit = xcd + 8 * (j / gpu);
-  const int grp = j - (j / gpu) * gpu;
-  if (unit >= p.umax || unit >= p.g.meta[4]) return;
-  const int4 info = p.g.unit_info[unit];
-  const int e = __builtin_amdgcn_readfirstlane(info.x);
-  const int start = __builtin_amdgcn_readfirstlane(info.y);
-  const int m = __builtin_amdgcn_readfirstlane(info.z);
-  // Pair (grouped order) of activation row r; rows past the unit's pairs read
-  // the last pair's row (their products are never stored).
-  auto pair_of = [&](int r) { return start + min(r, m - 1); };
-  // Per-row values this thread needs, read before any streaming load so that
-  // no wait for them lands among the streaming loads: its two activation rows
-  // (tid / 32, 8 + tid / 32), its exponent row (lane & 15) and the 4 output
-  // rows kq*4 + vv it stores.
-  const int ar0 = tid / kActChunks, ar1 = ar0 + kT / kActChunks, er = lane & 15;
-  // Byte offsets of the activation rows (from the block's base) and of the
-  // exponent row: A rows are tokens, the other phases' rows are pairs.
-  uint32_t aoff0, aoff1, eoff;
-  if constexpr (kPhase == kPhaseA) {
-    aoff0 = static_cast<uint32_t>(p.g.unit_tok[unit * kMaxM + ar0]) * p.d * 2;
-    aoff1 = static_cast<uint32_t>(p.g.unit_tok[unit * kMaxM + ar1]) * p.d * 2;
-    eoff = static_cast<uint32_t>(p.g.unit_tok[unit * kMaxM + er]) * 4;
-  } else {
-    const uint32_t apitch = kPhase == kPhaseC ? p.ff * 2 : kK * 2;
-    aoff0 = static_cast<uint32_t>(pair_of(ar0)) * apitch;
-    aoff1 = static_cast<uint32_t>(pair_of(ar1)) * apitch;
-    eoff = static_cast<uint32_t>(pair_of(er)) * (kPhase == kPhaseC ? p.nkc * 4 : 4);
-  }
-  // Output row offsets (D, floats) and weights (D reduced, B with the weight
-  // before down) of the unit's rows, kept in LDS.
-  if (tid < kMaxM) {
-    const int row = min(tid, m - 1);
-    sm.row_dst[tid] = kPhase == kPhaseD ? static_cast<uint32_t>(p.g.unit_dst[unit * kMaxM + row]) * p.d : 0u;
-    const bool weighted =
-        (kPhase == kPhaseD && !p.wbd && p.out_mode == LATENT_OUT_REDUCED) || (kPhase == kPhaseB && p.wbd);
-    sm.row_w[tid] = weighted ? p.g.unit_w[unit * kMaxM + row] : 1.0f;
-  }
+  const int wave = uniform(tid >> 6);
+  const int n = lane & 15, kq = lane >> 4;
+  const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
+  const int U = uniform(sload(p.meta + 4));
+  const int total = U * per_unit;
+  const int b = blockIdx.x;
+  const int chunk = (total + p.G - 1) / p.G;
+  const int lo = b * chunk, hi = min(total, lo + chunk);
+  if (lo >= hi) return;
+  const int ntile = hi - lo;
+  const int maxj = (chunk + per_key - 1) / per_key + 1;
 
-  // The group: factor(s) and slices [s0, s0 + ns) of the factor's nsl slices.
-  int f = 0, gi, nsl;
-  if (kPhase == kPhaseA) {
-    f = grp / p.gA;
-    gi = grp - f * p.gA;
-    nsl = p.nks;
-  } else {
-    gi = grp;
-    nsl = kPhase == kPhaseB ? p.nbs : kPhase == kPhaseC ? p.nkc : p.nds;
-  }
-  const int nb = p.nb[kPhase];
-  const int s0 = gi * nb;
-  const int ns = min(nb, nsl - s0);
-  const int nrun = kPhase == kPhaseB ? 2 * ns : ns;  // B runs (gate, up) per N slice
-  const int fi0 = kPhase == kPhaseA ? (f ? F_UP_A : F_GATE_A) : kPhase == kPhaseB ? F_GATE_B
-                  : kPhase == kPhaseC ? F_DOWN_A : F_DOWN_B;
-  // Run q reads factor fi(q), slice sl(q): B alternates gate and up.
-  auto fi_of = [&](int q) { return kPhase == kPhaseB ? ((q & 1) ? F_UP_B : F_GATE_B) : fi0; };
-  auto sl_of = [&](int q) { return s0 + (kPhase == kPhaseB ? q >> 1 : q); };
-  const uint32_t code_row = static_cast<uint32_t>(p.fac[fi0].code_stride());  // gate and up share shapes
-  const uint32_t srow_bytes = static_cast<uint32_t>(p.fac[fi0].scale_stride() * 2);
-
-  // Direct loads of run q: scales into buffer q & 1; K slices also their
-  // activation rows and exponents.
-  auto issue_dma = [&](int q) __attribute__((always_inline)) {
-    const Factor& F = p.fac[fi_of(q)];
-    const int sl = sl_of(q);
-    const int64_t frow = static_cast<int64_t>(e) * F.rows + (kSliceK ? sl * kK : 0);
-    const uint16_t* scales = F.scales + frow * F.scale_stride() + (kSliceK ? 0 : sl * kN / kGroup);
-    dma16(scales, tid * srow_bytes, lds_addr(sm.scales[q & 1][0]) + wave * kWave * 16);
-    if constexpr (kPhase == kPhaseA) {
-      dma_act(sm, q & 1, tid, wave, p.xh + sl * kK, aoff0, aoff1);
-      dma_exp(sm, q & 1, lane, p.xexp, eoff);
-    } else if constexpr (kPhase == kPhaseC) {
-      dma_act(sm, q & 1, tid, wave, p.hh + sl * kK, aoff0, aoff1);
-      dma_exp(sm, q & 1, lane, p.hexp + sl, eoff);
-    }
-  };
-  auto codes_of = [&](int q) {
-    const Factor& F = p.fac[fi_of(q)];
-    const int sl = sl_of(q);
-    const int64_t frow = static_cast<int64_t>(e) * F.rows + (kSliceK ? sl * kK : 0);
-    return F.codes + frow * F.code_stride() + (kSliceK ? 0 : sl * kN / 2);
-  };
-
-  // Level-pair table (one entry per thread, kLutCopies copies), built before
-  // the streaming loads: its level lookups would otherwise wait for them.
+  // Level-pair table: thread tid fills entry tid's copies (rotated start, so
+  // the lanes of one store spread over the banks).
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
     const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
     uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
-    // Rotated start: the lanes of one store spread over the banks.
 #pragma unroll
     for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
   }
   const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
 
-  // Prologue.  N-sliced phases read one activation block for the whole group
-  // (B: the gate latent into buffer 0, the up latent into buffer 1).
-  if constexpr (kPhase == kPhaseB) {
-#pragma unroll
-    for (int fb = 0; fb < 2; ++fb) {
-      dma_act(sm, fb, tid, wave, p.lath + static_cast<int64_t>(fb) * p.P * kK, aoff0, aoff1);
-      dma_exp(sm, fb, lane, p.lexp + static_cast<int64_t>(fb) * p.P, eoff);
+  // Phase A's token rows of tile t (loaded one tile before the tile's loads).
+  const int ar0 = tid / kActChunks, ar1 = ar0 + 8;
+  auto load_toks = [&](int t, bool valid, Toks& tk) __attribute__((always_inline)) {
+    if constexpr (kPhase == kPhaseA) {
+      const int u = uniform(min(t, hi - 1) / per_unit);
+      const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(p.unit_tok + static_cast<int64_t>(u) * kMaxM, valid ? kMaxM * 4 : 0);
+      tk.a0 = static_cast<int>(ld32(ru, ar0 * 4));
+      tk.a1 = static_cast<int>(ld32(ru, ar1 * 4));
+      tk.e = static_cast<int>(ld32(ru, (lane & 15) * 4));
     }
-  } else if constexpr (kPhase == kPhaseD) {
-    dma_act(sm, 0, tid, wave, p.dlath, aoff0, aoff1);
-    dma_exp(sm, 0, lane, p.dexp, eoff);
-  }
-  uint32_t d0[4][8], d1[4][8];
-  issue_dma(0);
-  load_codes(d0, codes_of(0), code_row, ch, kh, cq, kq);
-  if (nrun > 1) issue_dma(1);
-
-  float4v acc[8];
-#pragma unroll
-  for (int jj = 0; jj < 8; ++jj) acc[jj] = float4v{0.f, 0.f, 0.f, 0.f};
-  int prev_exp[4] = {0, 0, 0, 0};  // K slices: row exponent of the running sums (rows kq*4 + vv)
-  float4v gkeep[8];                // B: the gate product of the current N slice (K-half-0 waves)
-
-  // Run q (parity kOdd = q & 1, known where each copy is expanded): `cur`
-  // holds its codes, `nxt` receives run q + 1's.
-  auto run = [&](int q, auto odd, uint32_t (&cur)[4][8], uint32_t (&nxt)[4][8]) __attribute__((always_inline)) {
-    constexpr int kOdd = decltype(odd)::value;
-    // Loads complete in issue order.  After run q's direct loads come its 32
-    // code loads (issued one run earlier) and run q + 1's direct loads, if
-    // any (issued at the end of run q - 1): wait until no more are outstanding.
-    if (q + 1 < nrun)
-      wait_vm<32 + run_dma<kPhase>()>();
-    else
-      wait_vm<32>();
-    lds_barrier();
-    // Run q + 1's code loads; the last run loads its own codes again (an L2
-    // hit), so that every run issues the same loads and the compiler's waits
-    // for run q's codes never reach the ones issued here.
-    load_codes(nxt, codes_of(min(q + 1, nrun - 1)), code_row, ch, kh, cq, kq);
-    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the slice's MFMAs
-    constexpr int abuf = (kPhase == kPhaseB || kSliceK) ? kOdd : 0;
-    if constexpr (kPhase == kPhaseC) {
-      // Bring the running sums to this slice's row exponents (phase A's rows
-      // are tokens, whose one exponent holds for every slice).
-#pragma unroll
-      for (int vv = 0; vv < 4; ++vv) {
-        const int ex = sm.rexp[kOdd][kq * 4 + vv];
-        if (q > 0) {
-          const float sc = ldexpf(1.0f, ex - prev_exp[vv]);
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) acc[jj][vv] *= sc;
-        }
-        prev_exp[vv] = ex;
-      }
-    }
-    k_loop(sm, kOdd, abuf, cur, ch, kh, cq, kq, lut_lane, acc);
-    if constexpr (kPhase == kPhaseB) {
-      fold_halves(sm, acc, ch, kh, cq, kq, m);
-      if constexpr (!kOdd) {
-        // Gate: keep g = acc * 2^-rexp_g for the up run of this N slice (the
-        // K-half-1 waves keep values they never use).
-#pragma unroll
-        for (int vv = 0; vv < 4; ++vv) {
-          const float sc = ldexpf(1.0f, -sm.rexp[0][kq * 4 + vv]);
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) gkeep[jj][vv] = acc[jj][vv] * sc;
-        }
-      } else {
-        // Up: h = SiLU(g) * u [* w] with u = acc * 2^-rexp_u, stored fp16 with
-        // one exponent per row and slice; the row maximum spans both column
-        // halves and is exchanged through LDS.  Only the K-half-0 waves hold
-        // the folded sums.
-        const int sl = sl_of(q);
-        float hv[8][4];
-        if (kh == 0) {
-#pragma unroll
-          for (int vv = 0; vv < 4; ++vv) {
-            const int row = kq * 4 + vv;
-            const float rs = ldexpf(1.0f, -sm.rexp[1][row]) * sm.row_w[row];
-            float mx = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-              hv[jj][vv] = silu(gkeep[jj][vv]) * (acc[jj][vv] * rs);
-              mx = fmaxf(mx, fabsf(hv[jj][vv]));
-            }
-            mx = op_over(mx, 1, 16, OpMax{});
-            if (cq == 0) sm.hmax[ch][row] = mx;
-          }
-        }
-        lds_barrier();
-        if (kh == 0) {
-#pragma unroll
-          for (int vv = 0; vv < 4; ++vv) {
-            const int row = kq * 4 + vv;
-            if (row >= m) continue;
-            const int ex = pow2_row_exponent(fmaxf(sm.hmax[0][row], sm.hmax[1][row]));
-            half8 hb;
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) hb[jj] = static_cast<_Float16>(ldexpf(hv[jj][vv], ex));
-            const int64_t prow = start + row;
-            *reinterpret_cast<half8*>(p.hh + prow * p.ff + sl * kN + ch * 128 + cq * 8) = hb;
-            if (ch == 0 && cq == 0) p.hexp[prow * p.nkc + sl] = ex;
-          }
-        }
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) acc[jj] = float4v{0.f, 0.f, 0.f, 0.f};
-    } else if constexpr (kPhase == kPhaseD) {
-      const int col0 = sl_of(q) * kN;
-      fold_halves(sm, acc, ch, kh, cq, kq, m);
-      if (kh == 0) {
-        float* base = p.out_mode == LATENT_OUT_REDUCED ? p.ybuf : p.out;
-        store_rows(
-            sm, 0, acc, ch, cq, kq, m, [&](int row) { return base + sm.row_dst[row] + col0; },
-            [&](int row) { return sm.row_w[row]; });
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) acc[jj] = float4v{0.f, 0.f, 0.f, 0.f};
-    }
-    lds_barrier();  // run q's LDS buffers are free for run q + 2
-    if (q + 2 < nrun) issue_dma(q + 2);
   };
-  for (int q = 0; q < nrun; q += 2) {
-    run(q, std::integral_constant<int, 0>{}, d0, d1);
-    if (q + 1 < nrun) run(q + 1, std::integral_constant<int, 1>{}, d1, d0);
-  }
-  if constexpr (kSliceK) {
-    // K-sliced: fold the group's sum and store it as one partial.
-    fold_halves(sm, acc, ch, kh, cq, kq, m);
-    if (kh == 0) {
-      const int lb = (nrun - 1) & 1;  // exponents of the last slice
-      float* part = kPhase == kPhaseA ? p.partA + (static_cast<int64_t>(f) * p.gA + gi) * p.P * kN
-                                      : p.partC + static_cast<int64_t>(gi) * p.P * kN;
-      store_rows(
-          sm, lb, acc, ch, cq, kq, m, [&](int row) { return part + static_cast<int64_t>(start + row) * kN; },
-          [](int) { return 1.0f; });
+
+  constexpr bool kLate = late_act<kPhase>();
+  u32x4 cb[3][kSteps];
+  u32x4 sc[3];
+  StageAct<kPhase> sa[kLate ? 1 : 3];
+  Toks tk[3] = {};
+  TileRef ref[3];
+  float4v acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: tiles 0 and 1 in flight, tile 0 staged in LDS buffer 0.  Tiles
+  // past the range (here and in the steps) issue empty loads.
+  load_toks(lo, true, tk[0]);
+  load_toks(lo + 1, ntile > 1, tk[1]);
+  load_toks(lo + 2, ntile > 2, tk[2]);
+  ref[0] = tile_ref<kPhase>(p, lo);
+  ref[1] = tile_ref<kPhase>(p, min(lo + 1, hi - 1));
+  issue_act<kPhase>(p, ref[0], tk[0], tid, lane, true, sa[0]);
+  issue_codes<kPhase>(p, ref[0], tid, lane, wave, true, sc[0], cb[0]);
+  if constexpr (!kLate) issue_act<kPhase>(p, ref[1], tk[1], tid, lane, ntile > 1, sa[1]);
+  issue_codes<kPhase>(p, ref[1], tid, lane, wave, ntile > 1, sc[1], cb[1]);
+  store_stage<kPhase>(sm, 0, sc[0], sa[0], tid, lane, wave);
+
+  // Tile i sits in slot c = i % 3; tiles i + 1 and i + 2 in the other two.
+  auto step = [&](int i, auto cs) __attribute__((always_inline)) {
+    constexpr int c = decltype(cs)::value, c1 = (c + 1) % 3, c2 = (c + 2) % 3;
+    const int buf = i & 1;
+    lds_barrier();  // LDS buffer `buf` holds tile i; every wave is done with tile i - 1
+    // Loads of tile i + 2 (and, late, tile i + 1's activations first: loads
+    // complete in order, so the wait for them at the end of this step leaves
+    // tile i + 2's in flight).
+    if constexpr (kLate) issue_act<kPhase>(p, ref[c1], tk[c1], tid, lane, i + 1 < ntile, sa[0]);
+    load_toks(lo + i + 3, i + 3 < ntile, tk[c]);
+    ref[c2] = tile_ref<kPhase>(p, min(lo + i + 2, hi - 1));
+    if constexpr (!kLate) issue_act<kPhase>(p, ref[c2], tk[c2], tid, lane, i + 2 < ntile, sa[c2]);
+    issue_codes<kPhase>(p, ref[c2], tid, lane, wave, i + 2 < ntile, sc[c2], cb[c2]);
+    const TileRef& tr = ref[c];
+    if constexpr (kPhase == kPhaseC) {
+      // Two exponent blocks per tile (rows 0..127 and 128..255 of h's
+      // columns): each half's products are scaled back before they join the
+      // running sum, which holds true values.
+      float4v part[4];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[j] = float4v{0.f, 0.f, 0.f, 0.f};
+        mfma_steps<kPhase>(sm, buf, cb[c], half * kSteps / 2, (half + 1) * kSteps / 2, n, kq, wave, lut_lane, part);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float sc = ldexpf(1.0f, -sm.rexp[buf][half * 16 + kq * 4 + v]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j][v] = fmaf(part[j][v], sc, acc[j][v]);
+        }
+      }
+    } else {
+      mfma_steps<kPhase>(sm, buf, cb[c], 0, kSteps, n, kq, wave, lut_lane, acc);
     }
+    const int t = lo + i;
+    if constexpr (S::kSliceK) {
+      // End of a segment (last tile of the range or of this key): one partial.
+      if (i + 1 == ntile || (t + 1) % per_key == 0) {
+        const int key = t / per_key;
+        float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
+                      static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kMaxM * kN;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = kq * 4 + v;
+          if (row < tr.m) {
+            // A: x's one exponent per token is the same in every tile.
+            const float sc = kPhase == kPhaseA ? ldexpf(1.0f, -sm.rexp[buf][row]) : 1.0f;
+            *reinterpret_cast<float4*>(part + row * kN + wave * 64 + n * 4) =
+                make_float4(acc[0][v] * sc, acc[1][v] * sc, acc[2][v] * sc, acc[3][v] * sc);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      }
+    } else if constexpr (kPhase == kPhaseB) {
+      // h = SiLU(g) * u of columns 32w + 2n + jj of the tile's 128, fp16 with
+      // one exponent per row over the 128 columns (maximum across the waves).
+      float hv[2][4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float sg = ldexpf(1.0f, -sm.rexp[buf][row]), su = ldexpf(1.0f, -sm.rexp[buf][16 + row]);
+        float mx = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          hv[jj][v] = silu(acc[jj][v] * sg) * (acc[jj + 2][v] * su);
+          mx = fmaxf(mx, fabsf(hv[jj][v]));
+        }
+        mx = op_over(mx, 1, 16, OpMax{});
+        if (n == 0) sm.hmax[wave][row] = mx;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < tr.m) {
+          const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
+          const int ex = pow2_row_exponent(mx);
+          half2v hb;
+          hb[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
+          hb[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
+          const int64_t prow = tr.start + row;
+          *reinterpret_cast<half2v*>(p.hh + prow * p.ff + tr.r * kHBlock + wave * 32 + n * 2) = hb;
+          if (wave == 0 && n == 0) p.hexp[prow * p.nb + tr.r] = ex;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    } else {
+      // D: the y rows of the tile's 256 columns, by grouped pair.
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < tr.m) {
+          const float sc = ldexpf(1.0f, -sm.rexp[buf][row]);
+          float* dst = p.ybuf + static_cast<int64_t>(tr.start + row) * p.d + tr.r * kN + wave * 64 + n * 4;
+          *reinterpret_cast<float4*>(dst) = make_float4(acc[0][v] * sc, acc[1][v] * sc, acc[2][v] * sc, acc[3][v] * sc);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
+    // Tile i + 1's scales and activations into the other LDS buffer (last
+    // read by tile i - 1, which every wave finished before this step's barrier).
+    store_stage<kPhase>(sm, buf ^ 1, sc[c1], sa[kLate ? 0 : c1], tid, lane, wave);
+  };
+  // Whole triples without branches between the steps, then the last one or two.
+  int i = 0;
+  for (; i + 3 <= ntile; i += 3) {
+    step(i, std::integral_constant<int, 0>{});
+    step(i + 1, std::integral_constant<int, 1>{});
+    step(i + 2, std::integral_constant<int, 2>{});
   }
+  if (i < ntile) step(i, std::integral_constant<int, 0>{});
+  if (i + 1 < ntile) step(i + 1, std::integral_constant<int, 1>{});
 }
 
-// Sum of n partial rows [j][pair][256] (j in order) -> fp16 row * 2^e and e.
-// One wave per (factor, pair) row, 4 columns per lane.
-__device__ __forceinline__ void reduce_row(const float* part, int64_t stride, int n, _Float16* dst, int* dexp, int lane) {
-  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  constexpr int kBatch = 8;
-  for (int k0 = 0; k0 < n; k0 += kBatch) {
-    float4 v[kBatch];
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j)
-      v[j] = k0 + j < n ? reinterpret_cast<const float4*>(part + (k0 + j) * stride)[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int j = 0; j < kBatch; ++j) {
-      s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
-    }
-  }
+// A row of 256 sums -> fp16 row * 2^e and e (one wave, 4 columns per lane).
+__device__ __forceinline__ void finish_row(float4 s, _Float16* dst, int* dexp, int lane) {
   const float mx = op_over(fmaxf(fmaxf(fabsf(s.x), fabsf(s.y)), fmaxf(fabsf(s.z), fabsf(s.w))), 1, kWave, OpMax{});
   const int ex = pow2_row_exponent(mx);
   half4v h;
@@ -574,51 +562,170 @@ __device__ __forceinline__ void reduce_row(const float* part, int64_t stride, in
   if (lane == 0) *dexp = ex;
 }
 
-// lat[f][pair] = sum over the K groups of partA[f][g][pair], in group order.
-__global__ void __launch_bounds__(kT) reduce_a_kernel(Params p) {
-  const int routed = p.g.meta[3];
+// lat (phase A) / dlat (phase C) rows: the partial sums of each (unit,
+// factor, row) added in workgroup order.  One wave per (key, row).
+template <int kPhase>
+__global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   const int lane = threadIdx.x & (kWave - 1);
-  for (int64_t row = blockIdx.x * (kT / kWave) + (threadIdx.x >> 6); row < 2LL * routed;
-       row += static_cast<int64_t>(gridDim.x) * (kT / kWave)) {
-    const int64_t f = row / routed, pair = row - f * routed;
-    reduce_row(p.partA + (f * p.gA * p.P + pair) * kN, static_cast<int64_t>(p.P) * kN, p.gA,
-               p.lath + (f * p.P + pair) * kN, p.lexp + f * p.P + pair, lane);
+  const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
+  const int keys_per_unit = per_unit / per_key;
+  const int U = p.meta[4];
+  const int total = U * per_unit;
+  const int chunk = (total + p.G - 1) / p.G;
+  const int maxj = (chunk + per_key - 1) / per_key + 1;
+  const float* part = kPhase == kPhaseA ? p.partA : p.partC;
+  const int nrows = U * keys_per_unit * kMaxM;
+  for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nrows;
+       w += gridDim.x * (kT / kWave)) {
+    const int key = w / kMaxM, row = w % kMaxM;
+    const int u = key / keys_per_unit, f = key - u * keys_per_unit;
+    const int4 info = p.unit_info[u];
+    if (row >= info.z) continue;
+    const int b0 = (key * per_key) / chunk, b1 = (key * per_key + per_key - 1) / chunk;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int bb = b0; bb <= b1; ++bb) {
+      const float4 v = reinterpret_cast<const float4*>(
+          part + (static_cast<int64_t>(part_slot(bb, key, chunk, per_key, maxj)) * kMaxM + row) * kN)[lane];
+      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    }
+    const int64_t pair = info.y + row;
+    if (kPhase == kPhaseA)
+      finish_row(s, p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
+    else
+      finish_row(s, p.dlat + pair * kK, p.dexp + pair, lane);
   }
 }
 
-// dlat[pair] = sum over the K groups of partC[g][pair], in group order.
-__global__ void __launch_bounds__(kT) reduce_c_kernel(Params p) {
-  const int routed = p.g.meta[3];
-  const int lane = threadIdx.x & (kWave - 1);
-  for (int64_t pair = blockIdx.x * (kT / kWave) + (threadIdx.x >> 6); pair < routed;
-       pair += static_cast<int64_t>(gridDim.x) * (kT / kWave))
-    reduce_row(p.partC + pair * kN, static_cast<int64_t>(p.P) * kN, p.gC, p.dlath + pair * kN, p.dexp + pair, lane);
-}
-
-constexpr int kSumBatch = 8;
-
-// out[t][:] = sum over the token's valid slots, in slot order, of ybuf[t*K + slot][:].
+// out from the y rows of the routed slots, in slot order: reduced mode sums
+// w * y over the token's slots; per-slot mode writes y (times w when the weight
+// goes before the down projection: y is linear in h) and zero for a dropped slot.
 __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
   const int64_t d4 = p.d / 4;
-  const int64_t n4 = static_cast<int64_t>(p.T) * d4;
+  const int64_t rows = p.out_mode == LATENT_OUT_REDUCED ? p.T : static_cast<int64_t>(p.T) * p.K;
+  const int64_t n4 = rows * d4;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * kT) {
-    const int64_t t = i / d4, c4 = i - t * d4;
+    const int64_t r = i / d4, c4 = i - r * d4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k0 = 0; k0 < p.K; k0 += kSumBatch) {
-      float4 v[kSumBatch];
-#pragma unroll
-      for (int j = 0; j < kSumBatch; ++j) {
-        const int k = k0 + j;
-        const int e = k < p.K ? p.ids[t * p.K + k] : -1;
-        v[j] = (e >= 0 && e < p.E) ? reinterpret_cast<const float4*>(p.ybuf + (t * p.K + k) * p.d)[c4]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p.out_mode == LATENT_OUT_REDUCED) {
+      for (int k = 0; k < p.K; ++k) {
+        const int64_t slot = r * p.K + k;
+        const int e = p.ids[slot];
+        if (e < 0 || e >= p.E) continue;
+        const float w = load_act(p.weights, p.w_dtype, slot);
+        const float4 v = reinterpret_cast<const float4*>(p.ybuf + static_cast<int64_t>(p.pos_of[slot]) * p.d)[c4];
+        s.x += w * v.x; s.y += w * v.y; s.z += w * v.z; s.w += w * v.w;
       }
-#pragma unroll
-      for (int j = 0; j < kSumBatch; ++j) {
-        s.x += v[j].x; s.y += v[j].y; s.z += v[j].z; s.w += v[j].w;
+    } else {
+      const int e = p.ids[r];
+      if (e >= 0 && e < p.E) {
+        s = reinterpret_cast<const float4*>(p.ybuf + static_cast<int64_t>(p.pos_of[r]) * p.d)[c4];
+        if (p.wbd) {
+          const float w = load_act(p.weights, p.w_dtype, r);
+          s.x *= w; s.y *= w; s.z *= w; s.w *= w;
+        }
       }
     }
     reinterpret_cast<float4*>(p.out)[i] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Tile layout (latent_stream_tiles_pack)
+// ---------------------------------------------------------------------------
+struct PackParams {
+  Factor fac[6];  // gate_a, gate_b, up_a, up_b, down_a, down_b
+  uint8_t* dst[kTileArrays];
+  int64_t ntiles[kTileArrays];  // tiles of each array (all experts)
+  int per_expert[kTileArrays];
+  int64_t total16;              // 16-byte units over all arrays
+};
+
+__device__ __forceinline__ int nibble(const Factor& f, int64_t e, int64_t row, int64_t col) {
+  const uint8_t v = f.codes[(e * f.rows + row) * f.code_stride() + col / 2];
+  return (v >> ((col & 1) * 4)) & 15;
+}
+
+// Source factor, first row and column of tile column c of tile t of array arr.
+__device__ __forceinline__ const Factor& src_col(const PackParams& pp, int arr, int t, int c, int64_t& row0,
+                                                 int64_t& col) {
+  if (arr == T_GU_B) {
+    const int w = c >> 6, nn = (c >> 2) & 15, j = c & 3;
+    row0 = 0;
+    col = static_cast<int64_t>(t) * kHBlock + 32 * w + 2 * nn + (j & 1);
+    return pp.fac[j < 2 ? F_GATE_B : F_UP_B];
+  }
+  if (arr == T_DOWN_B) {
+    row0 = 0;
+    col = static_cast<int64_t>(t) * kN + c;
+    return pp.fac[F_DOWN_B];
+  }
+  row0 = static_cast<int64_t>(t) * kK;
+  col = c;
+  return pp.fac[arr == T_GATE_A ? F_GATE_A : arr == T_UP_A ? F_UP_A : F_DOWN_A];
+}
+
+// Source factor, first row and scale group of tile group G of tile t of array arr.
+__device__ __forceinline__ const Factor& src_group(const PackParams& pp, int arr, int t, int G, int64_t& row0,
+                                                   int64_t& grp) {
+  if (arr == T_GU_B) {
+    row0 = 0;
+    grp = static_cast<int64_t>(t) * (kHBlock / kGroup) + (G & 3);
+    return pp.fac[G < 4 ? F_GATE_B : F_UP_B];
+  }
+  if (arr == T_DOWN_B) {
+    row0 = 0;
+    grp = static_cast<int64_t>(t) * (kN / kGroup) + G;
+    return pp.fac[F_DOWN_B];
+  }
+  row0 = static_cast<int64_t>(t) * kK;
+  grp = G;
+  return pp.fac[arr == T_GATE_A ? F_GATE_A : arr == T_UP_A ? F_UP_A : F_DOWN_A];
+}
+
+__global__ void __launch_bounds__(kT) pack_kernel(PackParams pp) {
+  constexpr int kUnits = kTileBytes / 16;  // 16-byte units per tile
+  for (int64_t g = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; g < pp.total16;
+       g += static_cast<int64_t>(gridDim.x) * kT) {
+    int arr = 0;
+    int64_t rem = g;
+    while (arr < kTileArrays - 1 && rem >= pp.ntiles[arr] * kUnits) {
+      rem -= pp.ntiles[arr] * kUnits;
+      ++arr;
+    }
+    const int64_t tile = rem / kUnits;
+    const int k16 = static_cast<int>(rem - tile * kUnits);
+    const int64_t e = tile / pp.per_expert[arr];
+    const int t = static_cast<int>(tile - e * pp.per_expert[arr]);
+    uint32_t out[4];
+    if (k16 < kCodeBytes / 16) {
+      const int w = k16 / (kSteps * kWave), s = (k16 / kWave) % kSteps, lane = k16 % kWave;
+      const int nn = lane & 15, kq = lane >> 4;
+      const int r0 = s * 32 + kq * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int64_t row0, col;
+        const Factor& f = src_col(pp, arr, t, 64 * w + 4 * nn + j, row0, col);
+        uint32_t word = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int lo = nibble(f, e, row0 + r0 + 2 * q, col), hi = nibble(f, e, row0 + r0 + 2 * q + 1, col);
+          word |= static_cast<uint32_t>(lo | (hi << 4)) << (8 * q);
+        }
+        out[j] = word;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dw = (k16 - kCodeBytes / 16) * 4 + i;
+        const int G = dw / 128, P = (dw % 128) ^ ((G & 1) << 3);
+        int64_t row0, grp;
+        const Factor& f = src_group(pp, arr, t, G, row0, grp);
+        const uint16_t s0 = f.scales[(e * f.rows + row0 + 2 * P) * f.scale_stride() + grp];
+        const uint16_t s1 = f.scales[(e * f.rows + row0 + 2 * P + 1) * f.scale_stride() + grp];
+        out[i] = static_cast<uint32_t>(s0) | (static_cast<uint32_t>(s1) << 16);
+      }
+    }
+    reinterpret_cast<uint4*>(pp.dst[arr] + tile * kTileBytes)[k16] = make_uint4(out[0], out[1], out[2], out[3]);
   }
 }
 
@@ -630,88 +737,125 @@ __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
 // Host side
 // ===========================================================================
 namespace latent {
+
+Factor make_factor(const latent_factor& f);
+
 namespace stream {
 
 static bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
-bool supported(const latent_moe_args& a) {
+// Layers the tile layout exists for: pure NF4, rank 256, d and ff multiples of 256.
+static bool tiles_shape_ok(const latent_moe_args& a) {
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   for (const latent_factor* f : fs) {
     if (f->int8_bitmap || f->int8_row_offset || f->int8_data) return false;
-    if (!aligned16(f->codes) || !aligned16(f->scales)) return false;
+    if (!f->codes || !f->scales) return false;
   }
+  return a.max_rank == kK && a.n_embd % kK == 0 && a.n_ff % kK == 0 && a.n_expert >= 1 && a.n_expert <= 4096 &&
+         a.n_embd <= (1 << 16) && a.n_ff <= (1 << 16);
+}
+
+struct TileSizes {
+  int64_t ntiles[kTileArrays];
+  int per_expert[kTileArrays];
+  size_t offset[kTileArrays];
+  size_t total;
+};
+
+static TileSizes tile_sizes(const latent_moe_args& a) {
+  TileSizes ts{};
+  const int nka = static_cast<int>(a.n_embd / kK), nb = static_cast<int>(a.n_ff / kHBlock);
+  const int nkc = static_cast<int>(a.n_ff / kK), nd = static_cast<int>(a.n_embd / kN);
+  const int per[kTileArrays] = {nka, nka, nb, nkc, nd};
+  size_t off = 0;
+  for (int i = 0; i < kTileArrays; ++i) {
+    ts.per_expert[i] = per[i];
+    ts.ntiles[i] = a.n_expert * per[i];
+    ts.offset[i] = off;
+    off += static_cast<size_t>(ts.ntiles[i]) * kTileBytes;
+  }
+  ts.total = off;
+  return ts;
+}
+
+bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
-  return a.max_rank == kK && a.n_embd % kK == 0 && a.n_ff % kK == 0 && P >= 1 && P <= 4096 && aligned16(a.x) &&
-         a.n_expert <= 4096 && a.n_embd <= (1 << 16) && a.n_ff <= (1 << 16);
+  return a.stream_tiles != nullptr && aligned16(a.stream_tiles) && tiles_shape_ok(a) && P >= 1 && P <= 4096 &&
+         aligned16(a.x);
 }
 
 int64_t max_units(int64_t pairs, int64_t experts) { return std::min(pairs, experts) + pairs / kMaxM; }
 
-// Slices per workgroup for a phase with `per_unit` slices in each of `units`
-// units: about four rounds of the 512 workgroups resident on the chip.
-static int pick_nb(int64_t units, int64_t per_unit) {
-  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kMaxNB, units * per_unit / 2048)));
+// Workgroups the item kernels' tile ranges are cut for: two per CU.
+static int grid_size() {
+  static std::mutex mu;
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return kGroupsPerCU * 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cache[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cache[dev] = kGroupsPerCU * cus;
+  }
+  return cache[dev];
 }
 
-struct Split {
-  int nb[4], gA, gB, gC, gD;
-};
-
-static Split split_for(const latent_moe_args& a) {
-  const int64_t P = a.n_tokens * a.n_expert_used;
-  const int64_t U = max_units(P, a.n_expert);
-  const int nks = static_cast<int>(a.n_embd / kK), nbs = static_cast<int>(a.n_ff / kN);
-  const int nkc = static_cast<int>(a.n_ff / kK), nds = static_cast<int>(a.n_embd / kN);
-  Split s{};
-  s.nb[kPhaseA] = pick_nb(U, 2 * nks);
-  s.nb[kPhaseB] = std::max(1, pick_nb(U, 2 * nbs) / 2);  // each B slice is a gate and an up run
-  s.nb[kPhaseC] = pick_nb(U, nkc);
-  s.nb[kPhaseD] = pick_nb(U, nds);
-  s.gA = (nks + s.nb[kPhaseA] - 1) / s.nb[kPhaseA];
-  s.gB = (nbs + s.nb[kPhaseB] - 1) / s.nb[kPhaseB];
-  s.gC = (nkc + s.nb[kPhaseC] - 1) / s.nb[kPhaseC];
-  s.gD = (nds + s.nb[kPhaseD] - 1) / s.nb[kPhaseD];
-  return s;
+// Partial-sum slots of a K-tiled phase (per_unit tiles per unit, per_key per
+// segment key) for at most `units` units on G workgroups.
+static int64_t part_slots(int64_t units, int per_unit, int per_key, int G) {
+  const int64_t total = units * per_unit;
+  const int64_t chunk = (total + G - 1) / G;
+  const int64_t maxj = (chunk + per_key - 1) / per_key + 1;
+  return static_cast<int64_t>(G) * maxj;
 }
 
 Layout layout_for(const latent_moe_args& a) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const int64_t T = a.n_tokens, P = a.n_tokens * a.n_expert_used, d = a.n_embd, ff = a.n_ff;
-  const Split sp = split_for(a);
+  const int64_t U = max_units(P, a.n_expert);
+  const int G = grid_size();
+  const int nka = static_cast<int>(d / kK), nkc = static_cast<int>(ff / kK);
   Layout L{};
   size_t off = 0;
-  L.xh = off;    off = al(off + static_cast<size_t>(T) * d * 2);
-  L.xexp = off;  off = al(off + static_cast<size_t>(T) * 4);
-  L.partA = off; off = al(off + 2ull * sp.gA * P * kN * 4);
-  L.lath = off;  off = al(off + 2ull * P * kN * 2);
-  L.lexp = off;  off = al(off + 2ull * P * 4);
-  L.hh = off;    off = al(off + static_cast<size_t>(P) * ff * 2);
-  L.hexp = off;  off = al(off + static_cast<size_t>(P) * (ff / kN) * 4);
-  L.partC = off; off = al(off + static_cast<size_t>(sp.gC) * P * kN * 4);
-  L.dlath = off; off = al(off + static_cast<size_t>(P) * kN * 2);
-  L.dexp = off;  off = al(off + static_cast<size_t>(P) * 4);
-  L.ybuf = off;  off = al(off + static_cast<size_t>(P) * d * 4);
+  L.xh = off;     off = al(off + static_cast<size_t>(T) * d * 2);
+  L.xexp = off;   off = al(off + static_cast<size_t>(T) * 4);
+  L.partA = off;  off = al(off + static_cast<size_t>(part_slots(U, 2 * nka, nka, G)) * kMaxM * kN * 4);
+  L.lath = off;   off = al(off + 2ull * P * kK * 2);
+  L.lexp = off;   off = al(off + 2ull * P * 4);
+  L.hh = off;     off = al(off + static_cast<size_t>(P) * ff * 2);
+  L.hexp = off;   off = al(off + static_cast<size_t>(P) * (ff / kHBlock) * 4);
+  L.partC = off;  off = al(off + static_cast<size_t>(part_slots(U, nkc, nkc, G)) * kMaxM * kN * 4);
+  L.dlath = off;  off = al(off + static_cast<size_t>(P) * kK * 2);
+  L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
+  L.ybuf = off;   off = al(off + static_cast<size_t>(P) * d * 4);
+  L.pos_of = off; off = al(off + static_cast<size_t>(P) * 4);
   L.total = off;
   return L;
 }
 
-int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char* scratch, hipStream_t s) {
+int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStream_t s) {
   const Layout L = layout_for(a);
-  const Split sp = split_for(a);
+  const TileSizes ts = tile_sizes(a);
   Params p{};
-  for (int i = 0; i < 6; ++i) p.fac[i] = fac[i];
-  p.g = g;
+  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  p.meta = g.meta;
+  p.unit_info = g.unit_info;
+  p.unit_tok = g.unit_tok;
+  p.pos_of = reinterpret_cast<const int*>(scratch + L.pos_of);
   p.ids = a.ids;
+  p.weights = a.weights;
+  p.w_dtype = a.weights_dtype;
   p.out = static_cast<float*>(a.out);
   p.xh = reinterpret_cast<const _Float16*>(scratch + L.xh);
   p.xexp = reinterpret_cast<const int*>(scratch + L.xexp);
   p.partA = reinterpret_cast<float*>(scratch + L.partA);
-  p.lath = reinterpret_cast<_Float16*>(scratch + L.lath);
+  p.lat = reinterpret_cast<_Float16*>(scratch + L.lath);
   p.lexp = reinterpret_cast<int*>(scratch + L.lexp);
   p.hh = reinterpret_cast<_Float16*>(scratch + L.hh);
   p.hexp = reinterpret_cast<int*>(scratch + L.hexp);
   p.partC = reinterpret_cast<float*>(scratch + L.partC);
-  p.dlath = reinterpret_cast<_Float16*>(scratch + L.dlath);
+  p.dlat = reinterpret_cast<_Float16*>(scratch + L.dlath);
   p.dexp = reinterpret_cast<int*>(scratch + L.dexp);
   p.ybuf = reinterpret_cast<float*>(scratch + L.ybuf);
   p.T = static_cast<int>(a.n_tokens);
@@ -722,34 +866,66 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   p.P = p.T * p.K;
   p.wbd = a.weight_before_down ? 1 : 0;
   p.out_mode = a.out_mode;
-  p.nks = p.d / kK;
-  p.nbs = p.ff / kN;
+  p.nka = p.d / kK;
+  p.nb = p.ff / kHBlock;
   p.nkc = p.ff / kK;
-  p.nds = p.d / kN;
-  for (int i = 0; i < 4; ++i) p.nb[i] = sp.nb[i];
-  p.gA = sp.gA;
-  p.gB = sp.gB;
-  p.gC = sp.gC;
-  p.gD = sp.gD;
-  const unsigned U = static_cast<unsigned>(max_units(p.P, a.n_expert));
-  p.umax = static_cast<int>(U);
+  p.nd = p.d / kN;
+  p.G = grid_size();
+  const int64_t U = max_units(p.P, a.n_expert);
   auto blocks = [](int64_t n) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(2048, n))); };
-  // Workgroup b takes unit (b mod 8) + 8 (b / 8 / groups) and that unit's
-  // group (b / 8) mod groups: 8 * ceil(U / 8) * groups workgroups.
-  auto item_grid = [&](int64_t groups) { return static_cast<unsigned>(8 * ((U + 7) / 8) * groups); };
+  // At most G workgroups; fewer when the phase has fewer tiles than that even
+  // at the largest unit count (the others would find an empty range).
+  auto item_grid = [&](int64_t per_unit) { return static_cast<unsigned>(std::min<int64_t>(p.G, U * per_unit)); };
   const int rows_per_block = kT / kWave;
-  hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.gA)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(reduce_a_kernel, dim3(blocks((2LL * p.P + rows_per_block - 1) / rows_per_block)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(item_grid(p.gB)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(item_grid(p.gC)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(reduce_c_kernel, dim3(blocks((static_cast<int64_t>(p.P) + rows_per_block - 1) / rows_per_block)),
+  hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nka)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(reduce_kernel<kPhaseA>, dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),
                      dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(item_grid(p.gD)), dim3(kT), 0, s, p);
-  if (a.out_mode == LATENT_OUT_REDUCED)
-    hipLaunchKernelGGL(combine_kernel, dim3(blocks((static_cast<int64_t>(p.T) * p.d / 4 + kT - 1) / kT)), dim3(kT), 0, s,
-                       p);
+  hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(item_grid(p.nb)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(item_grid(p.nkc)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(reduce_kernel<kPhaseC>, dim3(blocks((U * kMaxM + rows_per_block - 1) / rows_per_block)), dim3(kT),
+                     0, s, p);
+  hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(item_grid(p.nd)), dim3(kT), 0, s, p);
+  const int64_t out4 = (a.out_mode == LATENT_OUT_REDUCED ? p.T : static_cast<int64_t>(p.P)) * p.d / 4;
+  hipLaunchKernelGGL(combine_kernel, dim3(blocks((out4 + kT - 1) / kT)), dim3(kT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
 }  // namespace stream
 }  // namespace latent
+
+extern "C" int latent_stream_tiles_size(const latent_moe_args* args, size_t* bytes) {
+  if (!args || !bytes) return LATENT_E_INVALID;
+  *bytes = 0;
+  if (!latent::stream::tiles_shape_ok(*args)) return LATENT_OK;
+  *bytes = latent::stream::tile_sizes(*args).total;
+  return LATENT_OK;
+}
+
+extern "C" int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t tiles_bytes,
+                                        latent_stream_t stream) {
+  using namespace latent;
+  using namespace latent::stream;
+  if (!args || !tiles) return LATENT_E_INVALID;
+  if (!tiles_shape_ok(*args)) return LATENT_E_UNSUPPORTED;
+  const TileSizes ts = tile_sizes(*args);
+  if (tiles_bytes < ts.total || !aligned16(tiles)) return LATENT_E_INVALID;
+  const latent_factor* fs[6] = {&args->gate_a, &args->gate_b, &args->up_a, &args->up_b, &args->down_a, &args->down_b};
+  const int64_t want[6][2] = {{args->n_embd, kK}, {kK, args->n_ff}, {args->n_embd, kK},
+                              {kK, args->n_ff},   {args->n_ff, kK}, {kK, args->n_embd}};
+  PackParams pp{};
+  for (int i = 0; i < 6; ++i) {
+    if (fs[i]->rows != want[i][0] || fs[i]->cols != want[i][1]) return LATENT_E_INVALID;
+    pp.fac[i] = make_factor(*fs[i]);
+  }
+  pp.total16 = 0;
+  for (int i = 0; i < kTileArrays; ++i) {
+    pp.dst[i] = static_cast<uint8_t*>(tiles) + ts.offset[i];
+    pp.ntiles[i] = ts.ntiles[i];
+    pp.per_expert[i] = ts.per_expert[i];
+    pp.total16 += ts.ntiles[i] * (kTileBytes / 16);
+  }
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(pack_kernel, dim3(4096), dim3(kT), 0, s, pp);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}

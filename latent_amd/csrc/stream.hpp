@@ -15,21 +15,22 @@ struct Grouping {
   const int* meta;         // [3] routed pairs, [4] work units
   const int4* unit_info;   // [units] {expert, first grouped pair, pairs (1..kMaxM), 0}
   const int* unit_tok;     // [units][kMaxM] token of each row (0 past the unit's pairs)
-  const int* unit_dst;     // [units][kMaxM] token * K + slot
-  const float* unit_w;     // [units][kMaxM] router weight
 };
 
 // Scratch of the path inside the caller's workspace.  xh / xexp (x as fp16
-// rows * 2^xexp, one exponent per token) are written by the prep kernel.
+// rows * 2^xexp, one exponent per token) and pos_of (grouped pair of each
+// routed slot) are written by the prep kernel.
 struct Layout {
-  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, total;
+  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, pos_of, total;
 };
 
+// The call can take this path: a tile layout is given (latent_stream_tiles_pack)
+// and the batch has at most 4096 routed pairs.
 bool supported(const latent_moe_args& a);
 // Upper bound of work units: every active expert contributes ceil(n_e / kMaxM).
 int64_t max_units(int64_t pairs, int64_t experts);
 Layout layout_for(const latent_moe_args& a);
-int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char* scratch, hipStream_t s);
+int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStream_t s);
 
 }  // namespace stream
 }  // namespace latent

@@ -140,7 +140,9 @@ class StackedLayer:
     down_a: DeviceFactor
     down_b: DeviceFactor
     ranks: Optional[torch.Tensor] = None  # int32 [E, 3] (gate, up, down)
+    stream_tiles: Optional[bool] = None  # build the streaming tile layout (None: when the layer qualifies)
     _workspace: Dict[int, torch.Tensor] = field(default_factory=dict, repr=False)
+    _tiles: Optional[torch.Tensor] = field(default=None, repr=False)
 
     def __post_init__(self) -> None:
         E, d, R = self.n_expert, self.d, self.max_rank
@@ -156,6 +158,26 @@ class StackedLayer:
             if self.ranks.dtype != torch.int32 or tuple(self.ranks.shape) != (E, 3) or not self.ranks.is_cuda:
                 raise ValueError("ranks must be a CUDA int32 [E, 3] tensor")
             self.ranks = self.ranks.contiguous()
+        if self.stream_tiles is not False:
+            self.build_stream_tiles(required=bool(self.stream_tiles))
+
+    def build_stream_tiles(self, required: bool = False) -> bool:
+        """Pack the factors into the streaming decode path's tile layout
+        (latent_stream_tiles_pack; same size as the packed factors).  Returns
+        False, or raises when `required`, for a layer the layout does not apply
+        to (INT8 groups, rank other than 256, d or ff not a multiple of 256)."""
+        a = self.args()
+        n = ctypes.c_size_t(0)
+        check(lib.latent_stream_tiles_size(ctypes.byref(a), ctypes.byref(n)), "latent_stream_tiles_size")
+        if n.value == 0:
+            if required:
+                raise ValueError("this layer has no streaming tile layout (needs pure NF4, rank 256, d and ff % 256 == 0)")
+            return False
+        tiles = torch.empty(int(n.value), dtype=torch.uint8, device=self.gate_a.codes.device)
+        check(lib.latent_stream_tiles_pack(ctypes.byref(a), tiles.data_ptr(), int(n.value), _stream()),
+              "latent_stream_tiles_pack")
+        self._tiles = tiles
+        return True
 
     @property
     def n_expert(self) -> int:
@@ -177,6 +199,7 @@ class StackedLayer:
         return {n: getattr(self, n) for n in FACTOR_NAMES}
 
     def nbytes(self) -> int:
+        """Bytes of the six factors (the tile layout, when built, holds the same bytes again)."""
         return sum(f.nbytes() for f in self.factors().values())
 
     @classmethod
@@ -212,6 +235,7 @@ class StackedLayer:
             setattr(a, name, getattr(self, name).c_struct())
         a.ranks = _ptr(self.ranks)
         a.n_embd, a.n_ff, a.n_expert, a.max_rank = self.d, self.ff, self.n_expert, self.max_rank
+        a.stream_tiles = _ptr(self._tiles)
         return a
 
     def workspace(self, n_tokens: int, n_expert_used: int) -> torch.Tensor:
