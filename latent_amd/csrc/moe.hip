@@ -70,6 +70,8 @@ struct MoeParams {
   int* pos_of;      // [T*K] grouped position of each routed slot (streaming path)
   _Float16* xh;     // streaming path: x as fp16 rows * 2^xexp (NULL: not converted)
   int* xexp;        // [T] row exponents
+  int* flow_cnt;    // streaming path in one launch: counters cleared here (NULL: none)
+  int64_t flow_cnt_n;
   int x_dtype, w_dtype;
   int T, d, ff, E, K, R;
   int wbd, out_mode;
@@ -105,14 +107,13 @@ __device__ __forceinline__ bool map_item(int b, int n_items, int n_active, int& 
 // prep: workgroup 0 groups pairs by expert; the others clear accumulators.
 // ---------------------------------------------------------------------------
 constexpr int kCached = 4;  // pairs per thread held in registers by route_block
+constexpr int kOrderedExperts = 1024;  // route_block places pairs in index order up to this many experts
 
 // Place routed pair i (expert e, weight w) at the expert's next position and
 // in its streaming unit's row tables.  start[e] is the expert's first
 // position; fill[e] its running insert position.
-__device__ __forceinline__ void scatter_pair(const MoeParams& p, const int* start, int* fill, const int* ubase, int i,
-                                             int e, float w) {
-  if (e < 0 || e >= p.E) return;
-  const int pos = atomicAdd(&fill[e], 1);
+__device__ __forceinline__ void place_pair(const MoeParams& p, const int* start, const int* ubase, int i, int e,
+                                           float w, int pos) {
   const int tok = i / p.K, slot = i - tok * p.K;
   p.pair_tok[pos] = tok;
   p.pair_slot[pos] = slot;
@@ -125,11 +126,20 @@ __device__ __forceinline__ void scatter_pair(const MoeParams& p, const int* star
   }
 }
 
+// Same, at the expert's next free position (the order among one expert's
+// pairs then depends on timing).
+__device__ __forceinline__ void scatter_pair(const MoeParams& p, const int* start, int* fill, const int* ubase, int i,
+                                             int e, float w) {
+  if (e < 0 || e >= p.E) return;
+  place_pair(p, start, ubase, i, e, w, atomicAdd(&fill[e], 1));
+}
+
 __device__ void route_block(const MoeParams& p) {
   __shared__ int cnt[kMaxExperts];  // pairs per expert, then the expert's first position
   __shared__ int fill[kMaxExperts];
   __shared__ int ubase[kMaxExperts];  // first streaming unit of each expert
   constexpr int kRouteWaves = kRouteThreads / kWave;
+  __shared__ int ordered_counts[kRouteWaves * kOrderedExperts];
   __shared__ int wave_sum[3][kRouteWaves];
   __shared__ int bad;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
@@ -228,6 +238,61 @@ __device__ void route_block(const MoeParams& p) {
     p.meta[4] = iu;  // streaming work units
   }
   __syncthreads();
+  if (p.E <= kOrderedExperts) {
+    // Pairs of one expert land in pair-index order, so the work units (and
+    // every sum over them) are the same on every call.  Rounds of
+    // kRouteThreads pairs: within a wave, ballots rank the pairs of each
+    // expert and count them; a scan over the waves' counts (per expert, in
+    // wave order, after the earlier rounds) gives each wave's insert base.
+    int* wcnt = ordered_counts;  // [waves][E]
+    const int rounds = (P + kRouteThreads - 1) / kRouteThreads;
+    for (int r = 0; r < rounds; ++r) {
+      const int i = r * kRouteThreads + tid;
+      int e = -1;
+      float w = 0.f;
+      if (r < kCached) {
+#pragma unroll
+        for (int j = 0; j < kCached; ++j) {
+          if (j == r) {
+            e = my_e[j];
+            w = my_w[j];
+          }
+        }
+      } else if (i < P) {
+        e = p.ids[i];
+        w = load_act(p.weights, p.w_dtype, i);
+      }
+      const int key = e >= 0 && e < p.E ? e : -1;
+      for (int x = tid; x < kRouteWaves * p.E; x += kRouteThreads) wcnt[x] = 0;
+      __syncthreads();
+      int rank = 0;
+      uint64_t todo = __ballot(1);
+      while (todo) {
+        const int leader = __ffsll(static_cast<unsigned long long>(todo)) - 1;
+        const int kl = __shfl(key, leader, kWave);
+        const uint64_t same = __ballot(key == kl);
+        if (key == kl) {
+          rank = __popcll(same & ((1ull << lane) - 1ull));
+          if (lane == leader && kl >= 0) wcnt[wave * p.E + kl] = __popcll(same);
+        }
+        todo &= ~same;
+      }
+      __syncthreads();
+      for (int x = tid; x < p.E; x += kRouteThreads) {
+        int run = fill[x];
+        for (int v = 0; v < kRouteWaves; ++v) {
+          const int c = wcnt[v * p.E + x];
+          wcnt[v * p.E + x] = run;
+          run += c;
+        }
+        fill[x] = run;
+      }
+      __syncthreads();
+      if (key >= 0) place_pair(p, cnt, ubase, i, key, w, wcnt[wave * p.E + key] + rank);
+      __syncthreads();
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < kCached; ++j) scatter_pair(p, cnt, fill, ubase, tid + j * kRouteThreads, my_e[j], my_w[j]);
   for (int i = tid + kCached * kRouteThreads; i < P; i += kRouteThreads) {
@@ -374,7 +439,21 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
       }
       if (threadIdx.x == 0) p.xexp[t] = ex;
     }
-    return;  // the streaming path clears nothing: its kernels write every output
+    if (p.flow_cnt) {
+      // One-launch chain: its counters start at zero, and in per-slot mode the
+      // rows of dropped slots are zero (no tile writes them).
+      for (int64_t i = t0; i < p.flow_cnt_n; i += stride) p.flow_cnt[i] = 0;
+      if (p.out_mode == LATENT_OUT_PER_SLOT) {
+        const int64_t rows = static_cast<int64_t>(p.T) * p.K;
+        for (int64_t r = blockIdx.x - 1; r < rows; r += nblk) {
+          const int e = p.ids[r];
+          if (e >= 0 && e < p.E) continue;
+          float4* o4 = reinterpret_cast<float4*>(p.out + r * p.d);
+          for (int c = threadIdx.x; c < p.d / 4; c += kRouteThreads) o4[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+    }
+    return;  // otherwise the streaming path clears nothing: its kernels write every output
   }
   // Accumulators gu and dl are contiguous: zero_floats covers both.
   float4* acc4 = reinterpret_cast<float4*>(p.gu);
@@ -920,6 +999,10 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.pos_of = reinterpret_cast<int*>(ws + L.gu + SL.pos_of);
     p.xh = reinterpret_cast<_Float16*>(ws + L.gu + SL.xh);
     p.xexp = reinterpret_cast<int*>(ws + L.gu + SL.xexp);
+    if (stream::one_launch(a)) {
+      p.flow_cnt = reinterpret_cast<int*>(ws + L.gu + SL.cnt);
+      p.flow_cnt_n = SL.cnt_ints;
+    }
   }
   // The MFMA paths write their intermediates whole, and every output row (per-token combine).
   p.zero_floats = use_prefill || use_stream ? 0 : P * 3 * a.max_rank;
@@ -960,7 +1043,8 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     return prefill::forward(a, p.fac, g, ws + L.gu, s);
   }
   if (use_stream) {
-    const stream::Grouping g{p.meta, p.unit_info, p.unit_tok};
+    const stream::Grouping g{p.meta,      p.unit_info, p.unit_tok, p.pair_tok, p.pair_slot, p.pair_w,
+                             reinterpret_cast<int*>(static_cast<char*>(a.workspace) + fused::kErrorOffset)};
     return stream::forward(a, g, ws + L.gu, s);
   }
   if (MB == 1)

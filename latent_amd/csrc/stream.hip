@@ -59,6 +59,8 @@
 #include "stream.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace latent {
@@ -76,6 +78,9 @@ constexpr int kHBlock = kN / 2;                       // h columns of a phase-B 
 constexpr int kLutCopies = 32;                        // one table copy per LDS bank
 constexpr int kActChunks = kK / 8;                    // 16-byte chunks of an fp16 activation row
 constexpr int kGroupsPerCU = 2;                       // resident workgroups per CU of the item kernels
+constexpr int64_t kFlowSpinTicks = 100000000;         // bounded waits: 1 s of s_memrealtime (100 MHz)
+constexpr int kCombineBatch = 8;                      // slots' rows in flight per output float4 (combine)
+constexpr int kFlowMaxKTiles = 64;                    // one-launch chain: d / 256 at most
 enum Phase { kPhaseA = 0, kPhaseB, kPhaseC, kPhaseD };
 enum { T_GATE_A = 0, T_UP_A, T_GU_B, T_DOWN_A, T_DOWN_B, kTileArrays };
 enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
@@ -110,6 +115,14 @@ struct Params {
   int T, K, E, d, ff, P, wbd, out_mode;
   int nka, nb, nkc, nd;  // tiles per unit and factor: A (d/256), B (ff/128), C (ff/256), D (d/256)
   int G;                 // workgroups the tile ranges are cut for
+  // One-launch chain (flow_kernel) only.
+  const int* pair_tok;    // [P] token of each grouped pair
+  const int* pair_slot;   // [P] slot of each grouped pair
+  const float* pair_w;    // [P] router weight of each grouped pair
+  int* cnt;               // [maxu] A tiles done, [maxu] BC items done, [1] workgroups done (zeroed by prep)
+  int* err;               // set when a bounded wait times out
+  int maxu;               // units bound (counter stride)
+  int maxj;               // partial-sum slots per workgroup in phase A
 };
 
 // LDS byte address of a __shared__ object and raw LDS loads.
@@ -630,6 +643,687 @@ __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// The whole chain in one persistent launch (flow_kernel)
+// ---------------------------------------------------------------------------
+// Workgroup b takes, in each phase, the balanced range [N*b/G, N*(b+1)/G) of
+// that phase's work list, and streams its three ranges in order through one
+// load pipeline:
+//   A   tiles (unit, gate/up, K tile)                      N = U * 2 * nka
+//   BC  items (unit, nb): B tile nb (h for ff columns 128 nb .. 128 nb + 127,
+//       kept in LDS) and the matching 128-row half of C tile nb / 2 (those h
+//       columns times A_d's rows)                          N = U * nb
+//   D   tiles (unit, 256-column tile)                      N = U * nd
+// A tile's codes and scales are issued two tiles ahead whatever its phase,
+// so the factor stream runs on through the phase changes.
+//
+// Dependencies between workgroups:
+//   * a B tile needs the A sums of its unit: every workgroup adds, at the end
+//     of its A range, the tiles it computed of each unit to cnt[u]
+//     (2 * nka when complete) once its partial stores are drained;
+//   * a D tile needs the nb BC partials of its unit (cnt[maxu + u]), added at
+//     the end of each workgroup's BC range.
+// The consumer waits for the count, then sums the partials itself in a fixed
+// order (segment order for A, item order for BC) into fp16 rows with a
+// power-of-two exponent per row in LDS, once per unit it meets.  Partial sums
+// move through coherent (sc1) stores and loads, so no L2 write-back or
+// invalidate is needed.  Every wait is bounded and sets `err` on a timeout.
+// A workgroup never waits before it has published everything the phases
+// before the awaited one need from it (A never waits; BC waits only for A; D
+// only for BC), so with every workgroup resident (two per CU) the chain always
+// completes.
+//
+// Reduced mode ends with a grid-wide arrival count, after which every
+// workgroup sums its share of the output rows from the weighted y rows in slot
+// order; per-slot mode writes the output in phase D.
+
+struct alignas(16) FlowSmem {
+  uint32_t lut[256 * kLutCopies];     // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[2][kScaleBytes / 16];  // [buffer]: the tile's scale block
+  u32x4 xa[2][kMaxM * kActChunks];    // A: x rows of buffer 0 / 1; BC: gate / up latents; D: d latent (block 0)
+  u32x4 hb[kMaxM * kActChunks];       // the BC item's h rows (128 columns); reduction scratch
+  int xexp[2][kMaxM];                 // A: token exponents of buffer 0 / 1
+  int lexp[2][kMaxM];                 // latent exponents (gate / up; D: block 0)
+  int hexp[kMaxM];                    // h exponents
+  float hmax[4][kMaxM];               // per-wave row maxima of h
+  float pw[kMaxM];                    // D: router weight of each row's pair
+  int prow[kMaxM];                    // D: output row (token * k + slot) of each row's pair
+  int segslot[2][kFlowMaxKTiles];     // BC: partial-sum slots of the unit's gate / up A segments
+};
+
+// Coherent (sc1) 128-bit load and store: agent-scope, seen across XCDs.
+__device__ __forceinline__ float4 ld_coh4(const float* base, uint32_t voff) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(base, 0x7FFFFFFF), voff, 0, 16);
+  return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+}
+__device__ __forceinline__ void st_coh4(float* base, uint32_t voff, float4 v) {
+  const u32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, buffer_rsrc(base, 0x7FFFFFFF), voff, 0, 16);
+}
+__device__ __forceinline__ void add4(float4& a, const float4& b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+// Balanced split of N items over G workgroups, and the workgroup owning item
+// t (N * G < 2^32 for the work lists; range_lo64 for the output rows).
+__device__ __forceinline__ int range_lo(int N, int b, int G) {
+  return static_cast<int>(static_cast<uint32_t>(N) * static_cast<uint32_t>(b) / static_cast<uint32_t>(G));
+}
+__device__ __forceinline__ int range_lo64(int N, int b, int G) {
+  return static_cast<int>(static_cast<int64_t>(N) * b / G);
+}
+__device__ __forceinline__ int owner_of(int t, int N, int G) {
+  return static_cast<int>((static_cast<uint32_t>(t + 1) * static_cast<uint32_t>(G) - 1u) / static_cast<uint32_t>(N));
+}
+
+// Workgroup's ranges: A tiles [a0, a0 + na), BC items [b0, b0 + nbc), D tiles
+// [d0, d0 + ndd).  Its tile sequence: the A tiles, empty tiles up to va (na
+// rounded up to a multiple of 3), the BC items' two tiles each, empty tiles up
+// to vd (a multiple of 3), then the D tiles; so every phase starts in load-ring
+// slot 0.
+struct Flow {
+  int NA, a0, na, va, NB, b0, nbc, vd, ND, d0, ndd, total;
+};
+
+// Scalar description of the workgroup's tile i (0 <= i < total).
+struct FTile {
+  int ph;     // kPhaseA .. kPhaseD (phase B and C tiles are the parts of a BC item); -1: empty
+  int u;      // unit
+  int e, start, m;
+  int k;      // A: K tile; B, C: the item's ff block nb; D: column tile
+  int key;    // A: segment key 2u + f
+  int arr, idx;
+};
+
+__device__ __forceinline__ FTile describe(const Params& p, const Flow& fl, int i) {
+  FTile d{};
+  int u;
+  if (i < fl.na) {
+    const int t = fl.a0 + i;
+    const int per = 2 * p.nka;
+    u = t / per;
+    const int r = t - u * per;
+    const int f = r >= p.nka ? 1 : 0;
+    d.ph = kPhaseA;
+    d.k = r - f * p.nka;
+    d.key = t / p.nka;
+    d.arr = f ? T_UP_A : T_GATE_A;
+  } else if (i < fl.va || (i >= fl.va + 2 * fl.nbc && i < fl.vd)) {
+    FTile z{};
+    z.ph = -1;
+    z.arr = T_GATE_A;
+    return z;
+  } else if (i < fl.va + 2 * fl.nbc) {
+    const int j = i - fl.va;
+    const int item = fl.b0 + (j >> 1);
+    u = item / p.nb;
+    d.k = item - u * p.nb;
+    d.ph = (j & 1) ? kPhaseC : kPhaseB;
+    d.arr = (j & 1) ? T_DOWN_A : T_GU_B;
+  } else {
+    const int t = fl.d0 + (i - fl.vd);
+    u = t / p.nd;
+    d.k = t - u * p.nd;
+    d.ph = kPhaseD;
+    d.arr = T_DOWN_B;
+  }
+  const i32x4 info = sload4(p.unit_info + u);
+  d.u = u;
+  d.e = uniform(info[0]);
+  d.start = uniform(info[1]);
+  d.m = uniform(info[2]);
+  if (d.ph == kPhaseA) d.idx = d.e * p.nka + d.k;
+  else if (d.ph == kPhaseB) d.idx = d.e * p.nb + d.k;
+  else if (d.ph == kPhaseC) d.idx = d.e * p.nkc + (d.k >> 1);
+  else d.idx = d.e * p.nd + d.k;
+  return d;
+}
+
+// Codes of tile d into cb (a C tile: its half k & 1, K steps 4h .. 4h + 3, into
+// cb[0..3]), its scale block into sc.  Every tile issues the same nine loads
+// (those it does not need fetch nothing: an empty buffer range, or an offset
+// past it), so the compiler's wait counts hold whatever tiles are in flight.
+__device__ __forceinline__ void flow_codes(const Params& p, const FTile& d, int tid, int lane, int wave, bool valid,
+                                           u32x4& sc, u32x4 (&cb)[kSteps]) {
+  const uint8_t* base = p.tiles[d.arr] + static_cast<int64_t>(d.idx) * kTileBytes;
+  const bool half = d.ph == kPhaseC;
+  const int h = d.k & 1;
+  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(base, valid ? kTileBytes : 0);
+  const __amdgpu_buffer_rsrc_t rhi = buffer_rsrc(base, valid && !half ? kTileBytes : 0);
+  // Half h's scales: row pairs 64h .. 64h + 63, the dwords of the threads with
+  // (tid % 32 >= 16) == h.
+  const bool sc_on = !half || (((tid & 31) >= 16) == (h != 0));
+  sc = ld128(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
+  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
+  const int s0 = half ? 4 * h : 0;
+#pragma unroll
+  for (int s = 0; s < kSteps / 2; ++s) cb[s] = ld128(rt, cbase, (s0 + s) * kWave * 16);
+#pragma unroll
+  for (int s = kSteps / 2; s < kSteps; ++s) cb[s] = ld128(rhi, cbase, s * kWave * 16);
+}
+
+// Tokens of an A tile's rows (the thread's two activation chunks and
+// exponent row lane & 15); rows past the unit's pairs hold token 0.
+__device__ __forceinline__ void flow_toks(const Params& p, const FTile& d, int tid, int lane, bool valid, Toks& tk) {
+  const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(p.unit_tok + static_cast<int64_t>(d.u) * kMaxM, valid ? kMaxM * 4 : 0);
+  const int r0 = tid / kActChunks;
+  tk.a0 = static_cast<int>(ld32(ru, r0 * 4));
+  tk.a1 = static_cast<int>(ld32(ru, (r0 + 8) * 4));
+  tk.e = static_cast<int>(ld32(ru, (lane & 15) * 4));
+}
+
+// An A tile's activation chunks (x rows of K tile d.k) and token exponents.
+__device__ __forceinline__ void flow_act(const Params& p, const FTile& d, const Toks& tk, int tid, bool valid,
+                                         StageAct<kPhaseA>& st) {
+  const uint32_t live = valid ? 0xFFFFFFFFu : 0u;
+  const int chunk = tid % kActChunks;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.xh, (static_cast<uint32_t>(p.T) * p.d * 2) & live);
+  const uint32_t col = d.k * kK * 2 + chunk * 16;
+  st.act[0] = ld128(rx, static_cast<uint32_t>(tk.a0) * p.d * 2 + col, 0);
+  st.act[1] = ld128(rx, static_cast<uint32_t>(tk.a1) * p.d * 2 + col, 0);
+  const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.xexp, (p.T * 4) & live);
+  st.ex = static_cast<int>(ld32(re, tk.e * 4));
+}
+
+// MFMA steps over code registers cb[0 .. ns): register step r is K step
+// srow0 + r of the tile (its scale rows) and activation chunk step r.
+// acc[j] += act . (codes dword j, decoded and scaled); act1 feeds the up
+// columns of a B tile (kTwo).
+template <bool kTwo, int ns>
+__device__ __forceinline__ void flow_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
+                                          const u32x4 (&cb)[kSteps], int srow0, int n, int kq, int wave,
+                                          uint32_t lut_lane, float4v (&acc)[4]) {
+#pragma unroll
+  for (int r = 0; r < ns; ++r) {
+    const int chunk = r * 4 + kq;
+    const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
+    const int P0 = (srow0 + r) * 16 + kq * 4;
+    u32x4 sc0, sc1;
+    half8 a1;
+    if constexpr (kTwo) {
+      a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
+      const int Gg = wave, Gu = 4 + wave;
+      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
+      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+    } else {
+      const int G = 2 * wave + (n >> 3);
+      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc1 = sc0;
+      a1 = a0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = cb[r][j];
+      const u32x4 sc = j < 2 ? sc0 : sc1;
+      uint32_t f[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        const uint32_t sq = sc[q];
+        f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
+      }
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1,
+                                                      __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3])),
+                                                      acc[j], 0, 0, 0);
+    }
+  }
+}
+
+// A row of 256 sums (four per lane) -> fp16 row * 2^e in an LDS activation
+// block (chunk layout of act_slot) and its exponent.
+__device__ __forceinline__ void flow_finish_row(float4 s, u32x4* blk, int* exps, int r, int lane) {
+  const float mx = op_over(fmaxf(fmaxf(fabsf(s.x), fabsf(s.y)), fmaxf(fabsf(s.z), fabsf(s.w))), 1, kWave, OpMax{});
+  const int ex = pow2_row_exponent(mx);
+  half4v h;
+  h[0] = static_cast<_Float16>(ldexpf(s.x, ex));
+  h[1] = static_cast<_Float16>(ldexpf(s.y, ex));
+  h[2] = static_cast<_Float16>(ldexpf(s.z, ex));
+  h[3] = static_cast<_Float16>(ldexpf(s.w, ex));
+  reinterpret_cast<half4v*>(&blk[act_slot(r, lane >> 1)])[lane & 1] = h;
+  if (lane == 0) exps[r] = ex;
+}
+
+// Bounded wait (thread 0) until *c >= target, then a workgroup barrier.
+__device__ __forceinline__ void flow_wait(const Params& p, const int* c, int target) {
+  if (threadIdx.x == 0) {
+    const int64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kFlowSpinTicks) {
+        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  lds_barrier();
+}
+
+// Every wave's stores (and loads) complete, then a barrier: the workgroup's
+// partial sums are visible before its counter adds.
+__device__ __forceinline__ void drain_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+constexpr int kRedBatch = 4;  // partial blocks in flight per lane and row
+
+// Sums of fp32 partial rows into fp16 LDS rows.  Row q < nkeys * m is row
+// q % m of key q / m; key k has S[k] partial blocks ([16][256] fp32) at
+// src(k, s).  A row's sum is the same however many rows there are: the blocks
+// s = j, j + 4, j + 8, ... are summed in order for each j, then the four sums
+// in j order.  With one or two rows wave j takes residue j of both rows (the
+// waves' sums meet in LDS); with more rows each wave takes rows q = wave,
+// wave + 4, ... whole.
+template <typename Src>
+__device__ __forceinline__ void flow_reduce(FlowSmem& sm, int nkeys, int m, int S0, int S1, Src src, int lane,
+                                            int wave) {
+  const int R = nkeys * m;
+  if (R <= 2) {
+    const int k1 = R == 2 ? (nkeys == 2 ? 1 : 0) : 0, r1 = R == 2 ? (nkeys == 2 ? 0 : 1) : 0;
+    const int S1r = k1 ? S1 : S0;
+    float4 acc0 = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc0;
+    const uint32_t o0 = static_cast<uint32_t>(lane * 4) * 4, o1 = static_cast<uint32_t>(r1 * kN + lane * 4) * 4;
+    for (int s = wave; s < max(S0, R == 2 ? S1r : 0); s += 4 * kRedBatch) {
+      float4 v0[kRedBatch], v1[kRedBatch];
+#pragma unroll
+      for (int j = 0; j < kRedBatch; ++j) {
+        const int ss = s + 4 * j;
+        v0[j] = ss < S0 ? ld_coh4(src(0, ss), o0) : make_float4(0.f, 0.f, 0.f, 0.f);
+        v1[j] = R == 2 && ss < S1r ? ld_coh4(src(k1, ss), o1) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < kRedBatch; ++j) {
+        add4(acc0, v0[j]);
+        add4(acc1, v1[j]);
+      }
+    }
+    float4* scratch = reinterpret_cast<float4*>(sm.hb);
+    scratch[(wave * 2) * kWave + lane] = acc0;
+    scratch[(wave * 2 + 1) * kWave + lane] = acc1;
+    lds_barrier();
+    if (wave < R) {
+      float4 t = scratch[wave * kWave + lane];
+      for (int w = 1; w < 4; ++w) add4(t, scratch[(w * 2 + wave) * kWave + lane]);
+      if (wave == 0)
+        flow_finish_row(t, sm.xa[0], sm.lexp[0], 0, lane);
+      else
+        flow_finish_row(t, sm.xa[k1], sm.lexp[k1], r1, lane);
+    }
+    return;
+  }
+  // The same order as above: blocks s = j, j + 4, ... summed per j, then j = 0..3.
+  static_assert(kRedBatch == 4, "one accumulator per block residue mod 4");
+  for (int q = wave; q < R; q += 4) {
+    const int k = q / m, r = q - k * m, S = k ? S1 : S0;
+    const uint32_t off = static_cast<uint32_t>(r * kN + lane * 4) * 4;
+    float4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < S; s += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = s + j < S ? ld_coh4(src(k, s + j), off) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) add4(acc[j], v[j]);
+    }
+    add4(acc[0], acc[1]);
+    add4(acc[0], acc[2]);
+    add4(acc[0], acc[3]);
+    flow_finish_row(acc[0], sm.xa[k], sm.lexp[k], r, lane);
+  }
+}
+
+template <int kOutMode>
+__global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  __shared__ FlowSmem sm;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = uniform(tid >> 6);
+  const int n = lane & 15, kq = lane >> 4;
+  const int U = uniform(sload(p.meta + 4));
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  Flow fl;
+  fl.NA = U * 2 * p.nka;
+  fl.a0 = range_lo(fl.NA, b, G);
+  fl.na = range_lo(fl.NA, b + 1, G) - fl.a0;
+  fl.NB = U * p.nb;
+  fl.b0 = range_lo(fl.NB, b, G);
+  fl.nbc = range_lo(fl.NB, b + 1, G) - fl.b0;
+  fl.ND = U * p.nd;
+  fl.d0 = range_lo(fl.ND, b, G);
+  fl.ndd = range_lo(fl.ND, b + 1, G) - fl.d0;
+  fl.va = (fl.na + 2) / 3 * 3;
+  fl.vd = fl.va + (2 * fl.nbc + 2) / 3 * 3;
+  fl.total = fl.vd + fl.ndd;
+  int* const cntA = p.cnt;
+  int* const cntC = p.cnt + p.maxu;
+  int* const done = p.cnt + 2 * p.maxu;
+
+  {
+    const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
+    const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
+    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
+#pragma unroll
+    for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+  }
+  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+
+  if (fl.total > 0) {
+    const int ntile = fl.total;
+    // Tile j's codes and scales sit in ring slot j % 3 (cb, sc), its A tokens
+    // in tk[j % 3]; tile i + 1's A activations in sa.
+    u32x4 cb[3][kSteps];
+    u32x4 sc[3];
+    StageAct<kPhaseA> sa;
+    Toks tk[3] = {};
+    float4v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    int bunit = -1, dunit = -1;  // units whose latents xa holds (BC) / whose d latent xa[0] holds (D)
+
+    auto stage_act = [&](int buf) __attribute__((always_inline)) {
+      const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+      sm.xa[buf][act_slot(r0, chunk)] = sa.act[0];
+      sm.xa[buf][act_slot(r0 + 8, chunk)] = sa.act[1];
+      if (wave == 0 && lane < kMaxM) sm.xexp[buf][lane] = sa.ex;
+    };
+
+    // Prologue: tile 0's scales (and A activations) staged, tiles 0 and 1 in flight.
+    {
+      const FTile d0 = describe(p, fl, 0);
+      const FTile d1 = describe(p, fl, min(1, ntile - 1));
+      const bool a0 = d0.ph == kPhaseA;
+      flow_toks(p, d0, tid, lane, a0, tk[0]);
+      flow_act(p, d0, tk[0], tid, a0, sa);
+      flow_toks(p, d1, tid, lane, ntile > 1 && d1.ph == kPhaseA, tk[1]);
+      flow_codes(p, d0, tid, lane, wave, d0.ph >= 0, sc[0], cb[0]);
+      flow_codes(p, d1, tid, lane, wave, ntile > 1 && d1.ph >= 0, sc[1], cb[1]);
+      sm.scales[0][tid] = sc[0];
+      if (a0) stage_act(0);
+    }
+
+    // Loads issued by step i, after its waits: tile i + 1's activations (A),
+    // tile i + 2's tokens (A), codes and scales.  Returns whether tile i + 1
+    // is an A tile.  (Only steps of the A range can have an A tile next.)
+    auto issue = [&](int i, auto cs, auto may_a) __attribute__((always_inline)) {
+      constexpr int c1 = (decltype(cs)::value + 1) % 3, c2 = (decltype(cs)::value + 2) % 3;
+      const FTile d2 = describe(p, fl, min(i + 2, ntile - 1));
+      bool act1 = false;
+      if constexpr (decltype(may_a)::value) {
+        const FTile d1 = describe(p, fl, min(i + 1, ntile - 1));
+        act1 = i + 1 < ntile && d1.ph == kPhaseA;
+        flow_act(p, d1, tk[c1], tid, act1, sa);
+        flow_toks(p, d2, tid, lane, i + 2 < ntile && d2.ph == kPhaseA, tk[c2]);
+      }
+      flow_codes(p, d2, tid, lane, wave, i + 2 < ntile && d2.ph >= 0, sc[c2], cb[c2]);
+      return act1;
+    };
+    // End of step i: tile i + 1's scales (and A activations) into the other LDS buffer.
+    auto stage_next = [&](int i, bool act1, auto cs) __attribute__((always_inline)) {
+      constexpr int c1 = (decltype(cs)::value + 1) % 3;
+      sm.scales[(i & 1) ^ 1][tid] = sc[c1];
+      if (act1) stage_act((i & 1) ^ 1);
+    };
+
+    auto stepA = [&](int i, auto cs) __attribute__((always_inline)) {
+      constexpr int c = decltype(cs)::value;
+      const int buf = i & 1;
+      lds_barrier();  // LDS buffer `buf` holds tile i; every wave is done with tile i - 1
+      const bool act1 = issue(i, cs, std::true_type{});
+      if (i >= fl.na) {  // empty tile: only the loads above
+        stage_next(i, act1, cs);
+        return;
+      }
+      const FTile d = describe(p, fl, i);
+      flow_mfma<false, kSteps>(sm.xa[buf], sm.xa[buf], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane,
+                               acc);
+      // End of a segment (last A tile of the range, or of this key): one partial.
+      if (i + 1 == fl.na || (fl.a0 + i + 1) % p.nka == 0) {
+        const int slot = b * p.maxj + d.key - fl.a0 / p.nka;
+        float* part = p.partA + static_cast<int64_t>(slot) * kMaxM * kN;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = kq * 4 + v;
+          if (row < d.m) {
+            const float s = ldexpf(1.0f, -sm.xexp[buf][row]);
+            st_coh4(part, static_cast<uint32_t>(row * kN + wave * 64 + n * 4) * 4,
+                    make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      }
+      if (i + 1 == fl.na) {
+        // Publish: the tiles of each unit this range computed.
+        drain_barrier();
+        const int per = 2 * p.nka;
+        const int u0 = fl.a0 / per, u1 = (fl.a0 + fl.na - 1) / per;
+        if (tid <= u1 - u0) {
+          const int u = u0 + tid;
+          const int lo = max(fl.a0, u * per), hi = min(fl.a0 + fl.na, (u + 1) * per);
+          __hip_atomic_fetch_add(cntA + u, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      stage_next(i, act1, cs);
+    };
+
+    // B tile of a BC item; the first of each unit waits for the unit's A sums
+    // and reduces them into the gate / up latents.
+    auto stepB = [&](int i, auto cs) __attribute__((always_inline)) {
+      constexpr int c = decltype(cs)::value;
+      const int buf = i & 1;
+      lds_barrier();
+      const FTile d = describe(p, fl, i);
+      if (d.u != bunit) {
+        bunit = d.u;
+        // Segments of key 2u + k: the workgroups whose A ranges meet its tiles
+        // (consecutive workgroups when every range is non-empty, else one
+        // workgroup per tile); thread k * 64 + s finds segment s's slot.
+        const bool full = fl.NA >= G;
+        auto nseg = [&](int key) {
+          const int t0 = key * p.nka;
+          return full ? owner_of(t0 + p.nka - 1, fl.NA, G) - owner_of(t0, fl.NA, G) + 1 : p.nka;
+        };
+        const int key0 = 2 * d.u;
+        const int S0 = nseg(key0), S1 = nseg(key0 + 1);
+        {
+          const int k = tid >> 6, s = tid & 63;
+          if (k < 2 && s < (k ? S1 : S0)) {
+            const int key = key0 + k, t0 = key * p.nka;
+            const int ob = full ? owner_of(t0, fl.NA, G) + s : owner_of(t0 + s, fl.NA, G);
+            sm.segslot[k][s] = ob * p.maxj + key - range_lo(fl.NA, ob, G) / p.nka;
+          }
+        }
+        flow_wait(p, cntA + d.u, 2 * p.nka);
+        auto src = [&](int k, int s) { return p.partA + static_cast<int64_t>(sm.segslot[k][s]) * kMaxM * kN; };
+        flow_reduce(sm, 2, d.m, S0, S1, src, lane, wave);
+        lds_barrier();
+      }
+      const bool act1 = issue(i, cs, std::false_type{});
+      flow_mfma<true, kSteps>(sm.xa[0], sm.xa[1], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane, acc);
+      // h = SiLU(g) * u of columns 32w + 2n + jj of the item's 128 into the h
+      // rows, fp16 with one exponent per row.
+      float hv[2][4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float sg = ldexpf(1.0f, -sm.lexp[0][row]), su = ldexpf(1.0f, -sm.lexp[1][row]);
+        float mx = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          hv[jj][v] = silu(acc[jj][v] * sg) * (acc[jj + 2][v] * su);
+          mx = fmaxf(mx, fabsf(hv[jj][v]));
+        }
+        mx = op_over(mx, 1, 16, OpMax{});
+        if (n == 0) sm.hmax[wave][row] = mx;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
+        const int ex = pow2_row_exponent(mx);
+        half2v hh;
+        hh[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
+        hh[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
+        reinterpret_cast<half2v*>(&sm.hb[act_slot(row, 4 * wave + (n >> 2))])[n & 3] = hh;
+        if (wave == 0 && n == 0) sm.hexp[row] = ex;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      stage_next(i, act1, cs);
+    };
+
+    // C half tile of a BC item: the item's h rows times A_d's 128 rows ->
+    // the item's partial d latent.
+    auto stepC = [&](int i, auto cs) __attribute__((always_inline)) {
+      constexpr int c = decltype(cs)::value;
+      const int buf = i & 1;
+      lds_barrier();
+      const FTile d = describe(p, fl, i);
+      const bool act1 = issue(i, cs, std::false_type{});
+      flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[buf][0]), cb[c], 4 * (d.k & 1), n, kq, wave,
+                                   lut_lane, acc);
+      float* part = p.partC + (static_cast<int64_t>(d.u) * p.nb + d.k) * kMaxM * kN;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < d.m) {
+          const float s = ldexpf(1.0f, -sm.hexp[row]);
+          st_coh4(part, static_cast<uint32_t>(row * kN + wave * 64 + n * 4) * 4,
+                  make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      if (i + 1 == fl.va + 2 * fl.nbc) {
+        // Publish: the BC items of each unit this range computed.
+        drain_barrier();
+        const int u0 = fl.b0 / p.nb, u1 = (fl.b0 + fl.nbc - 1) / p.nb;
+        if (tid <= u1 - u0) {
+          const int u = u0 + tid;
+          const int lo = max(fl.b0, u * p.nb), hi = min(fl.b0 + fl.nbc, (u + 1) * p.nb);
+          __hip_atomic_fetch_add(cntC + u, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      stage_next(i, act1, cs);
+    };
+
+    // D tile: the first of each unit waits for its BC partials and reduces
+    // them into the d latent; then y for 256 output columns.
+    auto stepD = [&](int i, auto cs) __attribute__((always_inline)) {
+      constexpr int c = decltype(cs)::value;
+      const int buf = i & 1;
+      lds_barrier();
+      const FTile d = describe(p, fl, i);
+      if (d.u != dunit) {
+        dunit = d.u;
+        // The unit's pair weights and output rows, read here (the wait below
+        // drains the loads anyway) rather than behind the tile's code loads.
+        if (tid < d.m) {
+          const int pair = d.start + tid;
+          sm.pw[tid] = p.pair_w[pair];
+          sm.prow[tid] = p.pair_tok[pair] * p.K + p.pair_slot[pair];
+        }
+        flow_wait(p, cntC + d.u, p.nb);
+        auto src = [&](int, int s) { return p.partC + (static_cast<int64_t>(d.u) * p.nb + s) * kMaxM * kN; };
+        flow_reduce(sm, 1, d.m, p.nb, 0, src, lane, wave);
+        lds_barrier();
+      }
+      const bool act1 = issue(i, cs, std::false_type{});
+      flow_mfma<false, kSteps>(sm.xa[0], sm.xa[0], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane, acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < d.m) {
+          const int pair = d.start + row;
+          const float w = sm.pw[row];
+          const float s = ldexpf(1.0f, -sm.lexp[0][row]);
+          const int col = d.k * kN + wave * 64 + n * 4;
+          if constexpr (kOutMode == LATENT_OUT_PER_SLOT) {
+            const float sw = p.wbd ? s * w : s;
+            const int64_t orow = sm.prow[row];
+            *reinterpret_cast<float4*>(p.out + orow * p.d + col) =
+                make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw);
+          } else {
+            const float sw = s * w;
+            st_coh4(p.ybuf, static_cast<uint32_t>(static_cast<int64_t>(pair) * p.d + col) * 4,
+                    make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw));
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      stage_next(i, act1, cs);
+    };
+
+    // An empty tile: only the loads of later tiles.
+    auto stepE = [&](int i, auto cs) __attribute__((always_inline)) {
+      lds_barrier();
+      stage_next(i, issue(i, cs, std::false_type{}), cs);
+    };
+    // Tile i sits in ring slot i % 3; every phase starts at a multiple of 3.
+    for (int i = 0; i < fl.va; i += 3) {
+      stepA(i, I0{});
+      stepA(i + 1, I1{});
+      stepA(i + 2, I2{});
+    }
+    // BC: three items (six tiles) per pass; positions past the last item up
+    // to vd are empty tiles.
+    for (int i = fl.va; i < fl.vd; i += 6) {
+      const int left = fl.va + 2 * fl.nbc - i;  // BC tiles from i on
+      stepB(i, I0{});
+      stepC(i + 1, I1{});
+      if (left > 2) stepB(i + 2, I2{}); else stepE(i + 2, I2{});
+      if (i + 3 >= fl.vd) break;
+      if (left > 3) stepC(i + 3, I0{}); else stepE(i + 3, I0{});
+      if (left > 4) stepB(i + 4, I1{}); else stepE(i + 4, I1{});
+      if (left > 5) stepC(i + 5, I2{}); else stepE(i + 5, I2{});
+    }
+    for (int i = fl.vd; i < ntile; i += 3) {
+      stepD(i, I0{});
+      if (i + 1 < ntile) stepD(i + 1, I1{});
+      if (i + 2 < ntile) stepD(i + 2, I2{});
+    }
+  }
+
+  if constexpr (kOutMode == LATENT_OUT_REDUCED) {
+    // Every workgroup's y rows are stored: then out rows by slot-order sums.
+    drain_barrier();
+    if (tid == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flow_wait(p, done, G);
+    const int d4 = p.d / 4;
+    const int total4 = p.T * d4;
+    const int lo = range_lo64(total4, b, G), hi = range_lo64(total4, b + 1, G);
+    for (int i = lo + tid; i < hi; i += kT) {
+      const int t = i / d4, c4 = i - t * d4;
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k0 = 0; k0 < p.K; k0 += kCombineBatch) {
+        // A batch of slots' rows in flight, then their sum in slot order.
+        float4 v[kCombineBatch];
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) {
+          const int slot = t * p.K + k0 + j;
+          const int e = k0 + j < p.K ? p.ids[slot] : -1;
+          v[j] = e >= 0 && e < p.E
+                     ? ld_coh4(p.ybuf, static_cast<uint32_t>(static_cast<int64_t>(p.pos_of[slot]) * p.d + c4 * 4) * 4)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < kCombineBatch; ++j) add4(s, v[j]);
+      }
+      reinterpret_cast<float4*>(p.out)[i] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tile layout (latent_stream_tiles_pack)
 // ---------------------------------------------------------------------------
 struct PackParams {
@@ -810,26 +1504,45 @@ static int64_t part_slots(int64_t units, int per_unit, int per_key, int G) {
   return static_cast<int64_t>(G) * maxj;
 }
 
+// Phase-A partial slots per workgroup of the one-launch chain: the keys
+// (unit, gate/up) a balanced range of at most ceil(N/G) tiles can meet.
+static int flow_maxj(int64_t units, int nka, int G) {
+  const int64_t chunk = (units * 2 * nka + G - 1) / G;
+  return static_cast<int>((chunk + nka - 1) / nka + 1);
+}
+
+bool one_launch(const latent_moe_args& a) {
+  const char* env = std::getenv("LATENT_STREAM_LAUNCH");
+  if (!(env && !std::strcmp(env, "one"))) return false;
+  return a.n_embd / kK <= kFlowMaxKTiles;
+}
+
 Layout layout_for(const latent_moe_args& a) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const int64_t T = a.n_tokens, P = a.n_tokens * a.n_expert_used, d = a.n_embd, ff = a.n_ff;
   const int64_t U = max_units(P, a.n_expert);
   const int G = grid_size();
   const int nka = static_cast<int>(d / kK), nkc = static_cast<int>(ff / kK);
+  // Partial blocks: per-phase launches (slots per workgroup range) or the
+  // one-launch chain (A: maxj slots per workgroup; C: one per BC item, nb per unit).
+  const int64_t blocksA = std::max<int64_t>(part_slots(U, 2 * nka, nka, G), static_cast<int64_t>(G) * flow_maxj(U, nka, G));
+  const int64_t blocksC = std::max<int64_t>(part_slots(U, nkc, nkc, G), U * (ff / kHBlock));
   Layout L{};
   size_t off = 0;
   L.xh = off;     off = al(off + static_cast<size_t>(T) * d * 2);
   L.xexp = off;   off = al(off + static_cast<size_t>(T) * 4);
-  L.partA = off;  off = al(off + static_cast<size_t>(part_slots(U, 2 * nka, nka, G)) * kMaxM * kN * 4);
+  L.partA = off;  off = al(off + static_cast<size_t>(blocksA) * kMaxM * kN * 4);
   L.lath = off;   off = al(off + 2ull * P * kK * 2);
   L.lexp = off;   off = al(off + 2ull * P * 4);
   L.hh = off;     off = al(off + static_cast<size_t>(P) * ff * 2);
   L.hexp = off;   off = al(off + static_cast<size_t>(P) * (ff / kHBlock) * 4);
-  L.partC = off;  off = al(off + static_cast<size_t>(part_slots(U, nkc, nkc, G)) * kMaxM * kN * 4);
+  L.partC = off;  off = al(off + static_cast<size_t>(blocksC) * kMaxM * kN * 4);
   L.dlath = off;  off = al(off + static_cast<size_t>(P) * kK * 2);
   L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
   L.ybuf = off;   off = al(off + static_cast<size_t>(P) * d * 4);
   L.pos_of = off; off = al(off + static_cast<size_t>(P) * 4);
+  L.cnt_ints = 2 * U + 1;
+  L.cnt = off;    off = al(off + static_cast<size_t>(L.cnt_ints) * 4);
   L.total = off;
   return L;
 }
@@ -876,6 +1589,20 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   // At most G workgroups; fewer when the phase has fewer tiles than that even
   // at the largest unit count (the others would find an empty range).
   auto item_grid = [&](int64_t per_unit) { return static_cast<unsigned>(std::min<int64_t>(p.G, U * per_unit)); };
+  if (one_launch(a)) {
+    p.pair_tok = g.pair_tok;
+    p.pair_slot = g.pair_slot;
+    p.pair_w = g.pair_w;
+    p.cnt = reinterpret_cast<int*>(scratch + L.cnt);
+    p.err = g.err;
+    p.maxu = static_cast<int>(U);
+    p.maxj = flow_maxj(U, p.nka, p.G);
+    if (a.out_mode == LATENT_OUT_REDUCED)
+      hipLaunchKernelGGL(flow_kernel<LATENT_OUT_REDUCED>, dim3(p.G), dim3(kT), 0, s, p);
+    else
+      hipLaunchKernelGGL(flow_kernel<LATENT_OUT_PER_SLOT>, dim3(p.G), dim3(kT), 0, s, p);
+    return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+  }
   const int rows_per_block = kT / kWave;
   hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nka)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(reduce_kernel<kPhaseA>, dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),

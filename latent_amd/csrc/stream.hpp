@@ -15,14 +15,25 @@ struct Grouping {
   const int* meta;         // [3] routed pairs, [4] work units
   const int4* unit_info;   // [units] {expert, first grouped pair, pairs (1..kMaxM), 0}
   const int* unit_tok;     // [units][kMaxM] token of each row (0 past the unit's pairs)
+  const int* pair_tok;     // [P] token, slot and router weight of each grouped pair
+  const int* pair_slot;
+  const float* pair_w;
+  int* err;                // word a timed-out bounded wait sets (one-launch chain)
 };
 
 // Scratch of the path inside the caller's workspace.  xh / xexp (x as fp16
 // rows * 2^xexp, one exponent per token) and pos_of (grouped pair of each
-// routed slot) are written by the prep kernel.
+// routed slot) are written by the prep kernel, which also clears cnt (the
+// one-launch chain's counters, cnt_ints of them).
 struct Layout {
-  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, pos_of, total;
+  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, pos_of, cnt, total;
+  int64_t cnt_ints;
 };
+
+// One launch for the whole chain (flow_kernel) rather than one per phase:
+// taken with LATENT_STREAM_LAUNCH=one where d <= 16384 (the per-phase
+// launches are measured faster today and are the default).
+bool one_launch(const latent_moe_args& a);
 
 // The call can take this path: a tile layout is given (latent_stream_tiles_pack)
 // and the batch has at most 4096 routed pairs.

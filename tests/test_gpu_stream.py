@@ -1,6 +1,8 @@
 """Streaming MFMA decode path (stream.hip) against the oracle.
 
-The path is selected with LATENT_MOE_PATH=stream for every call here.  Bar:
+The path is selected with LATENT_MOE_PATH=stream for every call here, in both
+launch styles (LATENT_STREAM_LAUNCH=phases: one launch per phase;
+LATENT_STREAM_LAUNCH=one: the whole chain in one persistent launch).  Bar:
 rel-L2 <= 2e-3 against the oracle's fp32 result on the same packed factors
 (fp16 operands, fp32 accumulation), bit-identical results on a repeated call.
 """
@@ -17,9 +19,11 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.fixture
-def stream_path(monkeypatch):
+@pytest.fixture(params=["phases", "one"])
+def stream_path(monkeypatch, request):
+    # Per-phase launches (the default) and the one-launch chain (flow_kernel).
     monkeypatch.setenv("LATENT_MOE_PATH", "stream")
+    monkeypatch.setenv("LATENT_STREAM_LAUNCH", request.param)
 
 
 @pytest.fixture(scope="module")
