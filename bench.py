@@ -12,9 +12,20 @@ timed loop rotates over `--layers` independently generated layers (1 GB of
 packed factors each) and several routings; consecutive steps never touch the
 same layer.
 
-The headline `value` is tokens/s at batch 64; batches 1, 8 and 32 and the
-4096-token prefill are reported under "sweep" / "prefill".  HBM GB/s counts
-the packed factor bytes of the distinct experts each step routes to.
+The headline `value` is tokens/s at batch 64; batches 1, 8 and 32, the
+4096-token prefill, the heterogeneous-rank layer (ranks 64..512, 10% INT8
+groups, drop below 0.05, batches 16 and 256) and the 58-layer graph-captured
+stack are reported under "sweep", "prefill", "hetero" and "stack".  HBM GB/s
+counts the packed factor bytes of the distinct experts each step routes to
+(at each expert's true rank; the heterogeneous layer also reports the bytes
+padded to max_rank).
+
+Prefill routing: the stated skew (popularity proportional to rank^-1.1,
+about 0 to 400 tokens per expert) is not reachable with a Zipf logit bias at
+4096 tokens x top-8 over 256 experts (gamma 0.11 gives about 77..374 tokens
+per expert, gamma 0.4 about 18..1980), so the default bias falls linearly with
+the popularity rank (beta 1.5: about 6..436, some 20 experts below 16); the
+Zipf form is --zipf-gamma.  The tokens-per-expert histogram is reported.
 """
 
 from __future__ import annotations
@@ -47,15 +58,19 @@ def parse():
     p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
     p.add_argument("--routings", type=int, default=8, help="distinct routings per batch size")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0, help="minimum CPU-baseline sample time")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run one device-to-device copy of this many MiB first (counter calibration)")
     p.add_argument("--stack", type=int, default=58,
                    help="layers of the graph-captured stacked decode (0 to skip)")
     p.add_argument("--stack-batch", type=int, default=32)
     p.add_argument("--stack-steps", type=int, default=10)
-    p.add_argument("--zipf-gamma", type=float, default=0.11,
-                   help="prefill router skew; 0.11 gives about 70..400 tokens per expert at 4096 tokens")
+    p.add_argument("--zipf-gamma", type=float, default=0.0,
+                   help="prefill router Zipf skew gamma * (-1.1 ln rank) (0: off)")
+    p.add_argument("--rank-beta", type=float, default=1.5,
+                   help="prefill router skew falling linearly with the popularity rank (about 6..436 at 1.5)")
+    p.add_argument("--hetero", type=str, default="16,256",
+                   help="batches of the heterogeneous-rank layer ('' to skip)")
+    p.add_argument("--cpu-steps", type=int, default=5, help="CPU-baseline steps per setting (median)")
     return p.parse_args()
 
 
@@ -112,8 +127,16 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
     }, routes, xs
 
 
-def prefill_point(torch, latent, gsynth, layers, tokens, steps, zipf_gamma):
-    ids, w = gsynth.route(seed=30_000, n_tokens=tokens, n_expert=E, k=K, zipf_gamma=zipf_gamma)
+def histogram(counts):
+    """Tokens per expert: order statistics and the tail below 16."""
+    c = np.sort(counts)
+    q = lambda f: int(c[min(len(c) - 1, int(f * (len(c) - 1)))])
+    return {"min": int(c[0]), "p10": q(0.1), "p25": q(0.25), "median": q(0.5), "p75": q(0.75), "p90": q(0.9),
+            "max": int(c[-1]), "experts_below_16": int((c < 16).sum()), "experts_empty": int((c == 0).sum())}
+
+
+def prefill_point(torch, latent, gsynth, layers, tokens, steps, zipf_gamma, rank_beta):
+    ids, w = gsynth.route(seed=30_000, n_tokens=tokens, n_expert=E, k=K, zipf_gamma=zipf_gamma, rank_beta=rank_beta)
     x = gsynth.bf16_input(seed=30_001, n_tokens=tokens, d=D)
     out = torch.empty((tokens, D), dtype=torch.float32, device="cuda")
     ws = layers[0].workspace(tokens, K)
@@ -131,11 +154,11 @@ def prefill_point(torch, latent, gsynth, layers, tokens, steps, zipf_gamma):
         "tokens_per_s": tokens / (ms * 1e-3),
         "tflops": tflops,
         "mfma_frac_bf16_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
-        "tokens_per_expert_max": int(counts.max()),
-        "tokens_per_expert_min": int(counts.min()),
+        "tokens_per_expert": histogram(counts),
         "path": latent.moe_path(layers[0], x, K),
         "zipf_gamma": zipf_gamma,
-    }
+        "rank_beta": rank_beta,
+    }, (ids, w, x)
 
 
 def stack_point(torch, latent, gsynth, n_layers, batch, steps):
@@ -186,44 +209,162 @@ def stack_point(torch, latent, gsynth, n_layers, batch, steps):
     return out
 
 
-def cpu_baseline(torch, layer, routes, xs, batch, min_seconds):
-    """The oracle (numpy port of loader/latent_runtime.py) on decode steps of the
-    same workload, 1 thread, repeated over the routings until min_seconds."""
+def _host_subset(torch, layer, ids, ref):
+    """The routed experts of one step as an oracle layer (copied out of the
+    timed region), and the ids renumbered to it."""
+    experts = np.unique(ids[(ids >= 0) & (ids < E)])
+    lut = -np.ones(E, np.int64)
+    lut[experts] = np.arange(experts.size)
+    local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
+    sel = torch.as_tensor(experts, device="cuda")
+    facs = {}
+    for name, f in layer.factors().items():
+        facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
+                                       f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
+    return ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R), local, experts.size
+
+
+def cpu_baseline(torch, layer, routes, xs, batch, steps, prefill_inputs, prefill_tokens):
+    """The oracle (numpy restatement of loader/latent_runtime.py, each routed
+    expert dequantized once per step) on the same workloads, timed on the
+    host: decode steps at `batch` with all host threads the GPU box grants
+    (OMP_NUM_THREADS) and with one, median of `steps` steps each; and one
+    prefill step on the first `prefill_tokens` tokens of the prefill batch
+    (all threads)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from threadpoolctl import threadpool_limits
 
     from oracle import latent_ref as ref
 
-    total, steps, experts_seen = 0.0, 0, 0
-    while total < min_seconds and steps < len(routes):
-        ids = routes[steps][0].cpu().numpy()
-        w = routes[steps][1].cpu().numpy()
-        x = xs[steps].float().cpu().numpy()
-        experts = np.unique(ids[(ids >= 0) & (ids < E)])
-        lut = -np.ones(E, np.int64)
-        lut[experts] = np.arange(experts.size)
-        local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
-        sel = torch.as_tensor(experts, device="cuda")
-        facs = {}
-        for name, f in layer.factors().items():
-            facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
-                                           f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
-        host = ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R)
-        with threadpool_limits(limits=1):
+    threads_all = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    decode = {}
+    experts_seen = 0
+    for threads in (threads_all, 1):
+        times = []
+        for s in range(steps):
+            ids = routes[s % len(routes)][0].cpu().numpy()
+            w = routes[s % len(routes)][1].cpu().numpy()
+            x = xs[s % len(xs)].float().cpu().numpy()
+            host, local, n_exp = _host_subset(torch, layer, ids, ref)
+            experts_seen += n_exp
+            with threadpool_limits(limits=threads):
+                t0 = time.perf_counter()
+                ref.moe_forward(x, local, w, host)
+                times.append(time.perf_counter() - t0)
+        decode[threads] = float(np.median(times))
+    prefill = None
+    if prefill_inputs is not None and prefill_tokens:
+        ids_p, w_p, x_p = prefill_inputs
+        ids = ids_p[:prefill_tokens].cpu().numpy()
+        w = w_p[:prefill_tokens].cpu().numpy()
+        x = x_p[:prefill_tokens].float().cpu().numpy()
+        host, local, n_exp = _host_subset(torch, layer, ids, ref)
+        with threadpool_limits(limits=threads_all):
             t0 = time.perf_counter()
             ref.moe_forward(x, local, w, host)
-            total += time.perf_counter() - t0
-        steps += 1
-        experts_seen += experts.size
+            dt = time.perf_counter() - t0
+        prefill = {"value": prefill_tokens / dt, "unit": "tokens/s", "cores": threads_all, "kind": "port",
+                   "sample": f"one prefill step on the first {prefill_tokens} of the prefill batch's tokens "
+                             f"({n_exp} distinct experts, each dequantized once; numpy fp32), {dt:.1f} s"}
+    per_step = experts_seen / (2 * steps)
     return {
-        "value": batch * steps / total,
+        "value": batch / decode[threads_all],
         "unit": "tokens/s",
-        "cores": 1,
+        "cores": threads_all,
         "kind": "port",
-        "sample": f"{steps} decode steps at batch {batch} ({experts_seen / steps:.0f} distinct experts per step, "
-                  f"each dequantized once; numpy fp32, 1 BLAS thread; {os.cpu_count()} host cores visible), "
-                  f"{total:.1f} s of CPU time",
+        "sample": f"median of {steps} decode steps at batch {batch} ({per_step:.0f} distinct experts per step, "
+                  f"each dequantized once; numpy fp32 with {threads_all} BLAS threads; {os.cpu_count()} host cores "
+                  f"visible); data generation and host copies excluded",
+        "single_thread": {"value": batch / decode[1], "unit": "tokens/s", "cores": 1,
+                          "sample": f"the same {steps} steps, median, 1 BLAS thread"},
+        "prefill": prefill,
     }
+
+
+def expert_bytes(torch, layer):
+    """Packed bytes of each expert's six factors, at its true rank and padded
+    to max_rank: NF4 codes and fp16 scales, plus the INT8 side bytes of its
+    flagged groups (32 per group, in place of the group's 16 code bytes) and
+    the per-row bitmap words and offsets a kernel reads for a factor that has
+    them.  Returns two float64 arrays [E]."""
+    ranks = layer.ranks[:, 0].to(torch.int64)
+    true_b = torch.zeros(layer.n_expert, dtype=torch.float64, device=ranks.device)
+    pad_b = torch.zeros_like(true_b)
+    for name, f in layer.factors().items():
+        rows, cols = f.rows, f.cols
+        if name.endswith("_a"):  # [n_in, R]: the rank is the column count
+            t_elems = rows * torch.clamp(ranks, max=cols)
+        else:  # [R, n_out]: the rank is the row count
+            t_elems = torch.clamp(ranks, max=rows) * cols
+        true_b += t_elems.double() / 2 + t_elems.double() / 32 * 2
+        pad_b += rows * cols / 2 + rows * cols / 32 * 2
+        if f.has_int8:
+            v = f.int8_bitmap.to(torch.int64) & 0xFFFFFFFF
+            bits = torch.zeros_like(v)
+            for _ in range(32):
+                bits += v & 1
+                v >>= 1
+            per_e = bits.reshape(layer.n_expert, -1).sum(1).double()
+            extra = 16 * per_e + rows * (f.int8_bitmap.shape[-1] * 4 + 4)
+            true_b += extra
+            pad_b += extra
+    return true_b.cpu().numpy(), pad_b.cpu().numpy()
+
+
+R_H = 512  # heterogeneous layer: max_rank
+
+
+def hetero_point(torch, latent, gsynth, batches, steps, warmup):
+    """Heterogeneous compression at the decode shapes: ranks drawn from
+    {64, 128, 256, 512} per expert, padded to max_rank 512, 10% of the groups
+    INT8, routed slots with renormalised weight below 0.05 dropped."""
+    rng = np.random.default_rng(40_000)
+    ranks = [int(v) for v in rng.choice([64, 128, 256, 512], size=E)]
+    t0 = time.time()
+    layers = [gsynth.make_layer(seed=41_000 + 13 * i, n_expert=E, d=D, ff=FF, max_rank=R_H, ranks=ranks,
+                                int8_fraction=0.1) for i in range(2)]
+    torch.cuda.synchronize()
+    gen_s = time.time() - t0
+    true_b, pad_b = expert_bytes(torch, layers[0])
+    out = []
+    for batch in batches:
+        routes = [gsynth.route(seed=42_000 + 31 * batch + r, n_tokens=batch, n_expert=E, k=K, drop_below=0.05)
+                  for r in range(4)]
+        xs = [gsynth.bf16_input(seed=43_000 + 37 * batch + r, n_tokens=batch, d=D) for r in range(4)]
+        y = torch.empty((batch, D), dtype=torch.float32, device="cuda")
+        ws = layers[0].workspace(batch, K)
+        for L in layers:
+            L.workspace(batch, K)
+
+        def step(i):
+            ids, w = routes[i % 4]
+            latent.moe_forward(xs[i % 4], ids, w, layers[i % 2], out=y, workspace=ws)
+
+        ms = time_loop(step, steps, warmup, torch)
+        tb, pb, dropped = [], [], 0
+        for ids, _ in routes:
+            h = ids.cpu().numpy()
+            ex = np.unique(h[(h >= 0) & (h < E)])
+            tb.append(float(true_b[ex].sum()))
+            pb.append(float(pad_b[ex].sum()))
+            dropped += int((h < 0).sum())
+        tbytes, pbytes = float(np.mean(tb)), float(np.mean(pb))
+        out.append({
+            "batch": batch,
+            "path": latent.moe_path(layers[0], xs[0], K),
+            "ms_per_step": ms,
+            "tokens_per_s": batch / (ms * 1e-3),
+            "bytes_per_step_true_rank": tbytes,
+            "bytes_per_step_padded": pbytes,
+            "hbm_gbps_true_rank": tbytes / (ms * 1e-3) / 1e9,
+            "hbm_gbps_padded": pbytes / (ms * 1e-3) / 1e9,
+            "roofline_frac_true_rank": tbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "dropped_slots_frac": dropped / (4 * batch * K),
+        })
+    mean_rank = float(np.mean(ranks))
+    del layers
+    torch.cuda.empty_cache()
+    return {"ranks_mean": mean_rank, "int8_fraction": 0.1, "max_rank": R_H, "generate_s": gen_s, "points": out}
 
 
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
@@ -281,10 +422,20 @@ def main():
         sweep.append(pt)
         print(f"# decode B={b}: {pt['ms_per_step'] * 1e3:.1f} us/step, {pt['hbm_gbps']:.0f} GB/s",
               file=sys.stderr, flush=True)
-    prefill = None
+    prefill, prefill_inputs = None, None
     if args.prefill:
-        prefill = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps, args.zipf_gamma)
-        print(f"# prefill T={args.prefill}: {prefill['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
+        prefill, prefill_inputs = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps,
+                                                args.zipf_gamma, args.rank_beta)
+        print(f"# prefill T={args.prefill}: {prefill['ms_per_step']:.2f} ms/step, tokens per expert "
+              f"{prefill['tokens_per_expert']}", file=sys.stderr, flush=True)
+    hetero = None
+    if args.hetero:
+        hetero = hetero_point(torch, latent, gsynth, [int(v) for v in args.hetero.split(",") if v.strip()],
+                              max(10, args.steps // 4), 3)
+        for pt in hetero["points"]:
+            print(f"# hetero B={pt['batch']} ({pt['path']}): {pt['ms_per_step'] * 1e3:.1f} us/step, "
+                  f"{pt['hbm_gbps_true_rank']:.0f} GB/s at true rank ({pt['hbm_gbps_padded']:.0f} padded)",
+                  file=sys.stderr, flush=True)
     stack = None
     if args.stack:
         stack = stack_point(torch, latent, gsynth, args.stack, args.stack_batch, args.stack_steps)
@@ -294,8 +445,11 @@ def main():
               file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch, args.cpu_seconds)
-        print(f"# cpu baseline: {cpu['value']:.2f} tokens/s", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch, args.cpu_steps,
+                           prefill_inputs if args.prefill else None, min(args.prefill, 1024))
+        print(f"# cpu baseline: {cpu['value']:.2f} tokens/s ({cpu['cores']} threads), "
+              f"{cpu['single_thread']['value']:.2f} (1 thread); prefill "
+              f"{cpu['prefill']['value'] if cpu['prefill'] else 0:.1f} tokens/s", file=sys.stderr, flush=True)
 
     result = {
         "metric": METRIC,
@@ -335,6 +489,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "prefill": prefill,
+        "hetero": hetero,
         "stack": stack,
     }
     print(json.dumps(result), flush=True)

@@ -112,7 +112,7 @@ typedef struct latent_moe_args {
   int64_t n_embd;           /* d */
   int64_t n_ff;             /* ff (per expert) */
   int64_t n_expert;         /* E */
-  int64_t n_expert_used;    /* k */
+  int64_t n_expert_used;    /* k, 1..64 */
   int64_t max_rank;         /* R, a multiple of 32 */
   int32_t weight_before_down;
   int32_t out_mode;         /* LATENT_OUT_REDUCED | LATENT_OUT_PER_SLOT */
@@ -183,12 +183,18 @@ int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t ti
 int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t stream);
 
 /*
- * Which implementation latent_moe_ffn_forward uses for these arguments:
- * 2 = grouped fp16-MFMA prefill (at least 16 routed pairs per active expert,
- * no INT8 groups), 3 = streaming fp16-MFMA decode (32 to 4096 routed pairs,
- * rank 256, d and ff multiples of 256, no INT8 groups), 1 = single persistent
- * fp32 decode kernel (32 to 512 routed pairs), 0 = multi-kernel fp32 GEMV
- * path; < 0 = LATENT_E_* for bad arguments.  The environment variable
+ * Which implementation latent_moe_ffn_forward uses for these arguments, the
+ * first that supports the call in this order:
+ *   2 = grouped fp16-MFMA prefill: on average at least 16 routed pairs per
+ *       active expert, no INT8 groups, n_embd / n_ff / max_rank multiples of
+ *       128 with n_ff and max_rank <= 2048, 16-byte aligned x and codes;
+ *   3 = streaming fp16-MFMA decode: a stream_tiles layout is given (pure NF4,
+ *       max_rank 256, n_embd and n_ff multiples of 256), 1 to 4096 routed
+ *       pairs, 16-byte aligned x;
+ *   1 = single persistent fp32 decode kernel: 32 to 512 routed pairs,
+ *       2 * max_rank <= 1024, 16-byte aligned x (INT8 groups allowed);
+ *   0 = multi-kernel fp32 GEMV path: any call.
+ * < 0 = LATENT_E_* for bad arguments.  The environment variable
  * LATENT_MOE_PATH (general | fused | prefill | stream) selects another path
  * that supports the call, for comparisons.
  * Diagnostic only; no counterpart in the reference.

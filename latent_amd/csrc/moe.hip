@@ -45,6 +45,7 @@ __constant__ float kLevelsMoe[16] = {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxExperts = 4096;  // LDS histogram of the prep kernel
+constexpr int kMaxExpertUsed = 64;  // slots per token (the router's limit)
 constexpr int kMaxRank = 512;
 constexpr int kRouteThreads = 1024;
 enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
@@ -821,7 +822,7 @@ int validate(const latent_moe_args& a) {
     if (st != LATENT_OK) return st;
     if (fs[i]->rows != rows[i] || fs[i]->cols != cols[i]) return LATENT_E_INVALID;
   }
-  if (a.n_expert > kMaxExperts || a.max_rank > kMaxRank) return LATENT_E_UNSUPPORTED;
+  if (a.n_expert > kMaxExperts || a.max_rank > kMaxRank || a.n_expert_used > kMaxExpertUsed) return LATENT_E_UNSUPPORTED;
   const int64_t P = a.n_tokens * a.n_expert_used;
   if (a.n_tokens > (1 << 24) || P > (1 << 26) || a.n_embd > (1 << 20) || a.n_ff > (1 << 20)) return LATENT_E_UNSUPPORTED;
   return LATENT_OK;

@@ -92,6 +92,7 @@ def test_workspace_size_scales_with_pairs(L):
         (lambda a: setattr(a.down_a, "codes", None), "LATENT_E_INVALID"),
         (lambda a: setattr(a.up_a, "int8_bitmap", 4096), "LATENT_E_INVALID"),
         (lambda a: setattr(a, "n_expert", 5000), "LATENT_E_UNSUPPORTED"),
+        (lambda a: setattr(a, "n_expert_used", 65), "LATENT_E_UNSUPPORTED"),
         (lambda a: setattr(a, "max_rank", 1024) or setattr(a.gate_a, "cols", 1024) or setattr(a.up_a, "cols", 1024)
          or setattr(a.down_a, "cols", 1024) or setattr(a.gate_b, "rows", 1024) or setattr(a.up_b, "rows", 1024)
          or setattr(a.down_b, "rows", 1024), "LATENT_E_UNSUPPORTED"),
