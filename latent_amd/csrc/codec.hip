@@ -119,6 +119,7 @@ Factor make_factor(const latent_factor& f) {
   r.ext.bitmap = f.int8_bitmap;
   r.ext.row_offset = f.int8_row_offset;
   r.ext.data = f.int8_data;
+  r.ext.word_offset = nullptr;
   r.rows = f.rows;
   r.cols = f.cols;
   return r;

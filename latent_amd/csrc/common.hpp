@@ -104,9 +104,11 @@ struct OpMax {
 
 // Lookup of an expert's per-group INT8 extension (see latent_factor).
 struct Int8Ext {
-  const uint32_t* bitmap;     // [E][rows][words]
-  const int32_t* row_offset;  // [E][rows]
-  const int8_t* data;         // [n][32]
+  const uint32_t* bitmap;      // [E][rows][words]
+  const int32_t* row_offset;   // [E][rows]
+  const int8_t* data;          // [n][32]
+  const int32_t* word_offset;  // [E][rows][words]: index of each bitmap word's first INT8
+                               // group (row_offset itself when words == 1); NULL: not built
 };
 
 // One stacked factor with the expert strides resolved.
@@ -135,9 +137,13 @@ __device__ __forceinline__ void decode_group(const Factor& f, int64_t e, int64_t
     const uint32_t* bm = f.ext.bitmap + erow * f.words();
     const uint32_t word = bm[g >> 5];
     if ((word >> (g & 31)) & 1u) {
-      int before = popc(word & ((1u << (g & 31)) - 1u));
-      for (int w = 0; w < (g >> 5); ++w) before += popc(bm[w]);
-      const int64_t idx = static_cast<int64_t>(f.ext.row_offset[erow]) + before;
+      int64_t idx = popc(word & ((1u << (g & 31)) - 1u));
+      if (f.ext.word_offset) {
+        idx += f.ext.word_offset[erow * f.words() + (g >> 5)];
+      } else {
+        for (int w = 0; w < (g >> 5); ++w) idx += popc(bm[w]);
+        idx += f.ext.row_offset[erow];
+      }
       const uint4* q = reinterpret_cast<const uint4*>(f.ext.data + idx * kGroup);
       const uint4 q0 = q[0], q1 = q[1];
       const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};

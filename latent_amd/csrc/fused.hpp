@@ -8,6 +8,9 @@
 #include "../../include/latent_ffn.h"
 
 namespace latent {
+
+struct Factor;
+
 namespace fused {
 
 // Workspace bytes at the start of every workspace that the fused path keeps
@@ -25,7 +28,8 @@ struct Plan {
 
 bool supported(const latent_moe_args& a);
 bool make_plan(const latent_moe_args& a, Plan& plan);
-int forward(const latent_moe_args& a, hipStream_t s, char* workspace, const Plan& plan);
+// fac: the six factors (make_factor) with their INT8 word offsets set.
+int forward(const latent_moe_args& a, hipStream_t s, char* workspace, const Plan& plan, const Factor (&fac)[6]);
 
 }  // namespace fused
 }  // namespace latent

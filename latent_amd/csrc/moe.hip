@@ -876,6 +876,56 @@ int launch_phases(const MoeParams& p, hipStream_t s) {
   return LATENT_OK;
 }
 
+// Index of each bitmap word's first INT8 group: row_offset plus the set bits
+// of the row's earlier words (one thread per expert row).
+__global__ void __launch_bounds__(kThreads) int8_word_offset_kernel(const uint32_t* bitmap, const int32_t* row_offset,
+                                                                   int32_t* out, int64_t rows_total, int words) {
+  for (int64_t r = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; r < rows_total;
+       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    int run = row_offset[r];
+    for (int w = 0; w < words; ++w) {
+      out[r * words + w] = run;
+      run += popc(bitmap[r * words + w]);
+    }
+  }
+}
+
+// Workspace tail holding the per-word INT8 offsets of the factors whose rows
+// span more than one bitmap word (factors of one word use row_offset).
+size_t int8_word_offset_bytes(const latent_moe_args& a) {
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  size_t n = 0;
+  for (const latent_factor* f : fs) {
+    const int64_t words = (f->cols / kGroup + 31) / 32;
+    if (f->int8_bitmap && words > 1) n += align_up(static_cast<size_t>(a.n_expert * f->rows * words) * sizeof(int32_t));
+  }
+  return n;
+}
+
+// Fill `word_offset` of every INT8 factor: the workspace tail for factors of
+// more than one bitmap word (a kernel per factor), row_offset for the others.
+int set_int8_word_offsets(const latent_moe_args& a, char* tail, Factor (&fac)[6], hipStream_t s) {
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  size_t off = 0;
+  for (int i = 0; i < 6; ++i) {
+    const latent_factor& f = *fs[i];
+    if (!f.int8_bitmap) continue;
+    const int64_t words = (f.cols / kGroup + 31) / 32;
+    if (words == 1) {
+      fac[i].ext.word_offset = f.int8_row_offset;
+      continue;
+    }
+    int32_t* dst = reinterpret_cast<int32_t*>(tail + off);
+    const int64_t rows_total = a.n_expert * f.rows;
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(1024, (rows_total + kThreads - 1) / kThreads));
+    hipLaunchKernelGGL(int8_word_offset_kernel, dim3(blocks), dim3(kThreads), 0, s, f.int8_bitmap, f.int8_row_offset,
+                       dst, rows_total, static_cast<int>(words));
+    fac[i].ext.word_offset = dst;
+    off += align_up(static_cast<size_t>(rows_total * words) * sizeof(int32_t));
+  }
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}
+
 }  // namespace
 }  // namespace latent
 
@@ -906,7 +956,7 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   fused::Plan pl;
   if (fused::supported(*args) && fused::make_plan(*args, pl)) scratch = std::max(scratch, pl.scratch_bytes);
   if (stream::supported(*args)) scratch = std::max(scratch, L.gu + stream::layout_for(*args).total);
-  *bytes = fused::kReserved + scratch;
+  *bytes = fused::kReserved + align_up(scratch) + int8_word_offset_bytes(*args);
   return LATENT_OK;
 }
 
@@ -953,9 +1003,6 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   (void)hipGetLastError();  // clear a stale error so the checks below see only ours
   fused::Plan pl;
   const int path = choose_path(a, pl);
-  if (path == kPathFused) return fused::forward(a, s, static_cast<char*>(a.workspace), pl);
-  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
-
   MoeParams p{};
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   bool any_int8 = false;
@@ -963,6 +1010,16 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.fac[i] = make_factor(*fs[i]);
     any_int8 = any_int8 || fs[i]->int8_bitmap != nullptr;
   }
+  if (any_int8) {
+    // The tail of the workspace (after the largest path's scratch).
+    size_t total = 0;
+    latent_moe_workspace_size(&a, &total);
+    char* tail = static_cast<char*>(a.workspace) + total - int8_word_offset_bytes(a);
+    st = set_int8_word_offsets(a, tail, p.fac, s);
+    if (st != LATENT_OK) return st;
+  }
+  if (path == kPathFused) return fused::forward(a, s, static_cast<char*>(a.workspace), pl, p.fac);
+  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
   char* ws = static_cast<char*>(a.workspace) + fused::kReserved;
   p.x = a.x;
   p.ids = a.ids;

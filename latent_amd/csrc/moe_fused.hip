@@ -426,7 +426,7 @@ struct FactorArgs {
   gptr<uint8_t> codes;
   gptr<uint16_t> scales;
   gptr<uint32_t> bitmap;
-  gptr<int32_t> row_offset;
+  gptr<int32_t> word_offset;  // [E][rows][words]: first INT8 group index of each bitmap word
   gptr<int8_t> data;
   int64_t rows, cols;
 };
@@ -441,7 +441,7 @@ __device__ __forceinline__ void stage_factors(const Params& p, const Smem& s) {
     for (int i = 0; i < 6; ++i) {
       const Factor& f = p.fac[i];
       s.fac[i] = FactorArgs{as_global(f.codes), as_global(f.scales), as_global(f.ext.bitmap),
-                            as_global(f.ext.row_offset), as_global(f.ext.data), f.rows, f.cols};
+                            as_global(f.ext.word_offset), as_global(f.ext.data), f.rows, f.cols};
     }
   }
 }
@@ -536,18 +536,9 @@ __device__ __forceinline__ void fma_half_nf4(const u32x2& c, const float (&xs)[M
   }
 }
 
-// Same for a half group stored as INT8 in the side buffer.
+// Same for a half group stored as INT8: its 16 values, in q.
 template <int M>
-__device__ __forceinline__ void fma_half_int8(const FactorArgs& f, int64_t e, int row, int gg, int half,
-                                              const float (&xs)[M], float (&acc)[M][kHalf]) {
-  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
-  const int64_t erow = e * f.rows + row;
-  const gptr<uint32_t> bm = f.bitmap + erow * words;
-  const uint32_t word = bm[gg >> 5];
-  int before = popc(word & ((1u << (gg & 31)) - 1u));
-  for (int wi = 0; wi < (gg >> 5); ++wi) before += popc(bm[wi]);
-  const int64_t idx = static_cast<int64_t>(f.row_offset[erow]) + before;
-  const u32x4 q = *reinterpret_cast<gptr<u32x4>>(f.data + idx * kGroup + half * kHalf);
+__device__ __forceinline__ void fma_half_int8(const u32x4& q, const float (&xs)[M], float (&acc)[M][kHalf]) {
   const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -560,10 +551,20 @@ __device__ __forceinline__ void fma_half_int8(const FactorArgs& f, int64_t e, in
   }
 }
 
-__device__ __forceinline__ bool is_int8_group(const FactorArgs& f, int64_t e, int row, int gg) {
-  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
-  const gptr<uint32_t> bm = f.bitmap + (e * f.rows + row) * words;
-  return (bm[gg >> 5] >> (gg & 31)) & 1u;
+// Raw buffer over a whole array (on: kFbufBytes of range; off: an empty
+// range), and its loads.  A load at kFbufBytes or beyond (or from an empty
+// range) returns zero without touching memory.
+constexpr uint32_t kFbufBytes = 0x7FFFFF00u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t fbuf(const void* base, bool on) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                           on ? static_cast<int>(kFbufBytes) : 0, 0x00020000);
+}
+__device__ __forceinline__ uint32_t fld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x4 fld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return u32x4{v[0], v[1], v[2], v[3]};
 }
 
 // Row-lane reduction + cross-wave fold of a tile's accumulators.
@@ -716,18 +717,55 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
   // kRing steps ahead right after it is consumed.  Four-token tiles spend
   // their registers on accumulators and do 4x the arithmetic per row, so a
   // shallower ring keeps them inside 128 VGPRs without starving the loads.
-  constexpr int kRing = M >= 3 ? 4 : 8;
+  // Layers with INT8 groups run a second, earlier stage: each row's bitmap
+  // word and word offset are loaded two rings ahead, and the group's INT8
+  // values (an empty load for an NF4 group) one ring ahead, with the codes --
+  // so no load waits on another inside the loop.
+  constexpr int kRing = (M >= 3 || kInt8) ? 4 : 8;
   // Scales stay raw fp16 bits in the ring: converting at load time would make
   // the refill wait for its own load.
   u32x2 ring[kRing];
   uint32_t sring[kRing];  // one register per scale (16-bit packing would force a wait per refill)
+  // INT8 stage (kInt8 only; every load issued, against empty ranges for an NF4 factor).
+  uint32_t bring[kInt8 ? kRing : 1], fring[kInt8 ? kRing : 1];
+  int32_t pring[kInt8 ? kRing : 1];
+  u32x4 qring[kInt8 ? kRing : 1];
+  const bool has8 = kInt8 && f.bitmap != nullptr;
+  const int words = static_cast<int>((f.cols / kGroup + 31) / 32);
+  const uint32_t bit = static_cast<uint32_t>(gg & 31), below = (1u << bit) - 1u;
+  const uint32_t b_first = 4u * (static_cast<uint32_t>(row0) * words + (gg >> 5));
+  const uint32_t b_last = 4u * (static_cast<uint32_t>(rowz) * words + (gg >> 5));
+  const uint32_t bdelta = 4u * static_cast<uint32_t>(rstep) * words;
+  const int64_t eb = j.e * f.rows * words;
+  auto generic = [](auto q) { return reinterpret_cast<const void*>(reinterpret_cast<uintptr_t>(q)); };
+  const __amdgpu_buffer_rsrc_t rbm = fbuf(has8 ? generic(f.bitmap + eb) : nullptr, has8);
+  const __amdgpu_buffer_rsrc_t rwo = fbuf(has8 ? generic(f.word_offset + eb) : nullptr, has8);
+  const __amdgpu_buffer_rsrc_t rdt = fbuf(has8 ? generic(f.data) : nullptr, has8);
+  auto stage_a = [&](int slot, uint32_t boff) __attribute__((always_inline)) {
+    if constexpr (kInt8) {
+      bring[slot] = fld32(rbm, boff);
+      pring[slot] = static_cast<int32_t>(fld32(rwo, boff));
+    }
+  };
+  auto stage_b = [&](int slot) __attribute__((always_inline)) {
+    if constexpr (kInt8) {
+      const uint32_t flag = (bring[slot] >> bit) & 1u;
+      const uint32_t idx = static_cast<uint32_t>(pring[slot]) + static_cast<uint32_t>(popc(bring[slot] & below));
+      qring[slot] = fld128(rdt, flag ? idx * kGroup + half * kHalf : kFbufBytes);
+      fring[slot] = flag;
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < kRing; ++u) stage_a(u, min(b_first + u * bdelta, b_last));
 #pragma unroll
   for (int u = 0; u < kRing; ++u) {
+    stage_b(u);
     ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(c_first + u * cdelta, c_last));
     sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(s_first + u * sdelta, s_last));
+    stage_a(u, min(b_first + (u + kRing) * bdelta, b_last));
     __builtin_amdgcn_sched_barrier(0);  // issue in consumption order
   }
-  uint32_t ck = c_first, sk = s_first;
+  uint32_t ck = c_first, sk = s_first, bk = b_first;
   int vk = v_first;
   // One block of kRing steps; with kRefill each consumed slot is reloaded with
   // the row kRing steps ahead.  The last block runs without refills, so no
@@ -743,15 +781,13 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
       float xs[M];
 #pragma unroll
       for (int t = 0; t < M; ++t) xs[t] = j.vin[t * j.vstride + vr] * sm;
-      bool done = false;
-      if constexpr (kInt8) {
-        const int row = row_l + k * rstep;
-        if (f.bitmap != nullptr && k < nv && is_int8_group(f, j.e, row, gg)) {
-          fma_half_int8<M>(f, j.e, row, gg, half, xs, acc);
-          done = true;
-        }
+      // A branch on the group's format: the lanes of a wave diverge only where
+      // INT8 and NF4 groups meet (a select over both decodes measured 3x slower).
+      if (kInt8 && fring[u] != 0) {
+        if constexpr (kInt8) fma_half_int8<M>(qring[u], xs, acc);
+      } else {
+        fma_half_nf4<M>(ring[u], xs, lut, lanebase, acc);
       }
-      if (!done) fma_half_nf4<M>(ring[u], xs, lut, lanebase, acc);
       if constexpr (decltype(refill)::value) {
         // Pin the refill between this step and the next.  Hoisted above the
         // step, its load would need a fresh register and a copy at the loop
@@ -759,13 +795,16 @@ __device__ __forceinline__ void tile_gemv(const Job& j, int m, lptr<const char> 
         // loses the distance to its use.  Either way the ring stops hiding the
         // memory latency.
         __builtin_amdgcn_sched_barrier(0);
+        stage_b(u);  // row k + kRing, from the bitmap word loaded a ring ago
         ring[u] = *reinterpret_cast<gptr<u32x2>>(cexp + min(ck + (u + kRing) * cdelta, c_last));
         sring[u] = *reinterpret_cast<gptr<uint16_t>>(sexp + min(sk + (u + kRing) * sdelta, s_last));
+        stage_a(u, min(bk + (u + 2 * kRing) * bdelta, b_last));
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     ck += kRing * cdelta;
     sk += kRing * sdelta;
+    bk += kRing * bdelta;
     vk += kRing * rstep;
   };
   int k0 = 0;
@@ -1261,13 +1300,12 @@ static int launch(const Params& p, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
-int forward(const latent_moe_args& a, hipStream_t s, char* ws, const Plan& pl) {
+int forward(const latent_moe_args& a, hipStream_t s, char* ws, const Plan& pl, const Factor (&fac)[6]) {
   Params p{};
-  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   bool any_int8 = false;
   for (int i = 0; i < 6; ++i) {
-    p.fac[i] = make_factor(*fs[i]);
-    any_int8 = any_int8 || fs[i]->int8_bitmap != nullptr;
+    p.fac[i] = fac[i];
+    any_int8 = any_int8 || fac[i].ext.bitmap != nullptr;
   }
   char* scratch = ws + kReserved;
   p.x = a.x;
