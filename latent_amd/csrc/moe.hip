@@ -239,9 +239,44 @@ __device__ void route_block(const MoeParams& p) {
     p.meta[4] = iu;  // streaming work units
   }
   __syncthreads();
-  if (p.E <= kOrderedExperts) {
+  const int words = (P + 31) / 32;
+  if (p.E * words <= kRouteWaves * kOrderedExperts) {
     // Pairs of one expert land in pair-index order, so the work units (and
-    // every sum over them) are the same on every call.  Rounds of
+    // every sum over them) are the same on every call: a bit mask of each
+    // expert's pairs, and a pair's rank is the number of its expert's bits
+    // below its own.
+    uint32_t* mask = reinterpret_cast<uint32_t*>(ordered_counts);  // [E][words]
+    for (int x = tid; x < p.E * words; x += kRouteThreads) mask[x] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kCached; ++j) {
+      const int i = tid + j * kRouteThreads, e = my_e[j];
+      if (e >= 0 && e < p.E) atomicOr(&mask[e * words + (i >> 5)], 1u << (i & 31));
+    }
+    for (int i = tid + kCached * kRouteThreads; i < P; i += kRouteThreads) {
+      const int e = p.ids[i];
+      if (e >= 0 && e < p.E) atomicOr(&mask[e * words + (i >> 5)], 1u << (i & 31));
+    }
+    __syncthreads();
+    auto rank_of = [&](int i, int e) {
+      const uint32_t* m = mask + e * words;
+      int rank = __builtin_popcount(m[i >> 5] & ((1u << (i & 31)) - 1u));
+      for (int x = 0; x < (i >> 5); ++x) rank += __builtin_popcount(m[x]);
+      return rank;
+    };
+#pragma unroll
+    for (int j = 0; j < kCached; ++j) {
+      const int i = tid + j * kRouteThreads, e = my_e[j];
+      if (e >= 0 && e < p.E) place_pair(p, cnt, ubase, i, e, my_w[j], cnt[e] + rank_of(i, e));
+    }
+    for (int i = tid + kCached * kRouteThreads; i < P; i += kRouteThreads) {
+      const int e = p.ids[i];
+      if (e >= 0 && e < p.E) place_pair(p, cnt, ubase, i, e, load_act(p.weights, p.w_dtype, i), cnt[e] + rank_of(i, e));
+    }
+    return;
+  }
+  if (p.E <= kOrderedExperts) {
+    // Same order for layers whose masks do not fit, in rounds of
     // kRouteThreads pairs: within a wave, ballots rank the pairs of each
     // expert and count them; a scan over the waves' counts (per expert, in
     // wave order, after the earlier rounds) gives each wave's insert base.

@@ -40,6 +40,10 @@
 #include "prefill.hpp"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
+
+#include "stream.hpp"
 
 namespace latent {
 namespace prefill {
@@ -659,11 +663,12 @@ __global__ void __launch_bounds__(kThreads) slots_kernel(Grouping g, int* pos_of
 }
 
 // out[t] = sum over slots (in slot order) of w * y[pos_of[t][slot]] * 2^-exp,
-// y rows in fp16 with one exponent per 128 columns.  One workgroup per token;
+// y rows in fp16 with one exponent per 2^blk_log2 columns (row stride
+// yexp_ld).  One workgroup per token;
 // the slots' rows are loaded together (kCombineSlots at a time) before the
 // sum, so a thread keeps that many 16-byte loads in flight.
 constexpr int kCombineSlots = 8;
-__global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, const int* yexp, int yexp_ld,
+__global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, const int* yexp, int yexp_ld, int blk_log2,
                                                            const int* pos_of, const float* pair_w, int k, int d, int wbd,
                                                            float* out) {
   const int t = blockIdx.x;
@@ -681,7 +686,7 @@ __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, co
         w[i] = 0.f;
         if (pos >= 0) {
           h[i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
-          w[i] = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + c / kBlk]);
+          w[i] = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + (c >> blk_log2)]);
         }
       }
 #pragma unroll
@@ -695,15 +700,18 @@ __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, co
   }
 }
 
-// M tiles of kMT pairs for every active expert, in expert order.
-__global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int* tile_a, int* tile_r0) {
+// M tiles of `rows` pairs (kMT for the GEMMs) for every active expert, in
+// expert order; with `units`, also each tile as {expert, first grouped pair,
+// pairs, 0}.
+__global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int rows, int* tile_a, int* tile_r0,
+                                                             int4* units) {
   __shared__ int scan[kTileThreads];
   const int tid = threadIdx.x;
   const int n_active = g.meta[0];
   const int per = (n_active + kTileThreads - 1) / kTileThreads;
   const int a0 = min(n_active, tid * per), a1 = min(n_active, a0 + per);
   int mine = 0;
-  for (int a = a0; a < a1; ++a) mine += (g.act_count[a] + kMT - 1) / kMT;
+  for (int a = a0; a < a1; ++a) mine += (g.act_count[a] + rows - 1) / rows;
   scan[tid] = mine;
   __syncthreads();
   for (int off = 1; off < kTileThreads; off <<= 1) {
@@ -714,9 +722,10 @@ __global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int* ti
   }
   int t = scan[tid] - mine;
   for (int a = a0; a < a1; ++a) {
-    for (int r = 0; r < g.act_count[a]; r += kMT) {
+    for (int r = 0; r < g.act_count[a]; r += rows) {
       tile_a[t] = a;
       tile_r0[t] = r;
+      if (units) units[t] = make_int4(g.act_expert[a], g.act_start[a] + r, min(rows, g.act_count[a] - r), 0);
       ++t;
     }
   }
@@ -726,9 +735,19 @@ __global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int* ti
 
 size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
 
-int64_t max_tiles(const latent_moe_args& a) {
+// The streaming-tile engine takes the call where the layer has a tile layout
+// it can stream; LATENT_PREFILL_ENGINE=gemm keeps the grouped GEMMs.
+bool use_bulk(const latent_moe_args& a) {
+  const char* env = std::getenv("LATENT_PREFILL_ENGINE");
+  if (env && !std::strcmp(env, "gemm")) return false;
+  return stream::bulk_supported(a);
+}
+
+// M tiles (units of the streaming-tile engine) of `rows` pairs: at most
+// ceil(n_e / rows) per active expert.
+int64_t max_tiles(const latent_moe_args& a, int rows) {
   const int64_t P = a.n_tokens * a.n_expert_used;
-  return (P + kMT - 1) / kMT + std::min<int64_t>(a.n_expert, P);
+  return (P + rows - 1) / rows + std::min<int64_t>(a.n_expert, P);
 }
 
 // Column tiles per work item: about 32 K slices of work per item, so short-K
@@ -767,7 +786,8 @@ bool supported(const latent_moe_args& a) {
 }
 
 Layout layout_for(const latent_moe_args& a) {
-  const int64_t P = a.n_tokens * a.n_expert_used, R = a.max_rank, T = max_tiles(a);
+  const bool bulk = use_bulk(a);
+  const int64_t P = a.n_tokens * a.n_expert_used, R = a.max_rank, T = max_tiles(a, bulk ? stream::kBulkM : kMT);
   Layout L{};
   size_t off = 0;
   L.tile_a = off;  off = align_up(off + T * sizeof(int));
@@ -777,20 +797,25 @@ Layout layout_for(const latent_moe_args& a) {
   L.xh = off;      off = align_up(off + a.n_tokens * a.n_embd * sizeof(_Float16));
   L.gu = off;      off = align_up(off + P * 2 * R * sizeof(_Float16));
   L.gu_exp = off;  off = align_up(off + P * 2 * rb * sizeof(int));
+  // The streaming-tile engine keeps finer exponent blocks: 32 h and 64 y columns.
+  const int64_t hb = bulk ? a.n_ff / 32 : fb, yb = bulk ? a.n_embd / 64 : db;
   L.h = off;       off = align_up(off + P * a.n_ff * sizeof(_Float16));
-  L.h_exp = off;   off = align_up(off + P * fb * sizeof(int));
+  L.h_exp = off;   off = align_up(off + P * hb * sizeof(int));
   L.dl = off;      off = align_up(off + P * R * sizeof(_Float16));
   L.dl_exp = off;  off = align_up(off + P * rb * sizeof(int));
   L.pos_of = off;  off = align_up(off + P * sizeof(int));
   L.y = off;       off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * a.n_embd * sizeof(_Float16) : 0));
-  L.y_exp = off;   off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * db * sizeof(int) : 0));
+  L.y_exp = off;   off = align_up(off + (a.out_mode == LATENT_OUT_REDUCED ? P * yb * sizeof(int) : 0));
+  L.units = off;   off = align_up(off + (bulk ? T * sizeof(int4) : 0));
+  L.part = off;    off = align_up(off + (bulk ? stream::bulk_part_bytes(a, T) : 0));
   L.total = off;
   return L;
 }
 
 int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char* scratch, hipStream_t s) {
   const Layout L = layout_for(a);
-  const int64_t tiles = max_tiles(a);
+  const bool bulk = use_bulk(a);
+  const int64_t tiles = max_tiles(a, bulk ? stream::kBulkM : kMT);
   int* tile_a = reinterpret_cast<int*>(scratch + L.tile_a);
   int* tile_r0 = reinterpret_cast<int*>(scratch + L.tile_r0);
   _Float16* gu = reinterpret_cast<_Float16*>(scratch + L.gu);
@@ -812,11 +837,41 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
                      xh, xexp, pos_of, K, a.ids, static_cast<int>(a.n_expert),
                      a.out_mode == LATENT_OUT_PER_SLOT ? static_cast<float*>(a.out) : nullptr);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
-  hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, tile_a, tile_r0);
+  int4* units = reinterpret_cast<int4*>(scratch + L.units);
+  hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, bulk ? stream::kBulkM : kMT, tile_a, tile_r0,
+                     bulk ? units : nullptr);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   hipLaunchKernelGGL(slots_kernel, dim3(static_cast<unsigned>((P + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g,
                      pos_of, P, K);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
+
+  if (bulk) {
+    // The streaming tile layout with 128-pair units: x -> latents -> h ->
+    // d latent -> y (or the per-slot rows), then the per-token combine.
+    stream::BulkArgs bk{};
+    bk.nunits = g.meta + 2;
+    bk.units = units;
+    bk.pair_tok = g.pair_tok;
+    bk.pair_slot = g.pair_slot;
+    bk.pair_w = g.pair_w;
+    bk.xh = xh;
+    bk.xexp = xexp;
+    bk.lat = gu;       // [2][P][256]: the gu buffer's size at rank 256
+    bk.lexp = gu_exp;
+    bk.hh = h;
+    bk.hexp = h_exp;
+    bk.dlat = dl;
+    bk.dexp = dl_exp;
+    bk.y = y;
+    bk.yexp = y_exp;
+    bk.part = reinterpret_cast<float*>(scratch + L.part);
+    const int st = stream::bulk_forward(a, bk, tiles, s);
+    if (st != LATENT_OK || a.out_mode == LATENT_OUT_PER_SLOT) return st;
+    // The router weight is applied here in both weighting modes (y is linear in h).
+    hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, y, y_exp, d / 64, 6,
+                       pos_of, g.pair_w, K, d, 0, static_cast<float*>(a.out));
+    return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+  }
 
   Params p{};
   p.g = g;
@@ -893,8 +948,8 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   p.dst_exp_ld = db;
   st = launch<kFromPairs, kStoreHalf>(p, tiles, s);
   if (st != LATENT_OK) return st;
-  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, y, y_exp, db, pos_of,
-                     g.pair_w, K, d, p.wbd, static_cast<float*>(a.out));
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, y, y_exp, db, 7,
+                     pos_of, g.pair_w, K, d, p.wbd, static_cast<float*>(a.out));
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 

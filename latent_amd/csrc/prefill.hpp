@@ -23,7 +23,7 @@ struct Grouping {
 
 // Scratch of the prefill path inside the caller's workspace.
 struct Layout {
-  size_t tile_a, tile_r0, xexp, xh, gu, gu_exp, h, h_exp, dl, dl_exp, pos_of, y, y_exp, total;
+  size_t tile_a, tile_r0, xexp, xh, gu, gu_exp, h, h_exp, dl, dl_exp, pos_of, y, y_exp, units, part, total;
 };
 
 // Routed pairs per active expert needed before the MFMA path pays off.

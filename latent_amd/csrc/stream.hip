@@ -81,6 +81,7 @@ constexpr int kGroupsPerCU = 2;                       // resident workgroups per
 constexpr int64_t kFlowSpinTicks = 100000000;         // bounded waits: 1 s of s_memrealtime (100 MHz)
 constexpr int kCombineBatch = 8;                      // slots' rows in flight per output float4 (combine)
 constexpr int kFlowMaxKTiles = 64;                    // one-launch chain: d / 256 at most
+constexpr int kRedLoads = 8;                          // partial rows in flight per reduce step
 enum Phase { kPhaseA = 0, kPhaseB, kPhaseC, kPhaseD };
 enum { T_GATE_A = 0, T_UP_A, T_GU_B, T_DOWN_A, T_DOWN_B, kTileArrays };
 enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
@@ -123,6 +124,10 @@ struct Params {
   int* err;               // set when a bounded wait times out
   int maxu;               // units bound (counter stride)
   int maxj;               // partial-sum slots per workgroup in phase A
+  // Bulk (prefill) launches only.
+  const int* nunits;      // number of units (reduce kernels; the decode launches set meta + 4)
+  _Float16* yh;           // reduced output: [P][d] fp16 y rows * 2^yexp
+  int* yexp;              // [P][d / 128]
 };
 
 // LDS byte address of a __shared__ object and raw LDS loads.
@@ -576,30 +581,42 @@ __device__ __forceinline__ void finish_row(float4 s, _Float16* dst, int* dexp, i
 }
 
 // lat (phase A) / dlat (phase C) rows: the partial sums of each (unit,
-// factor, row) added in workgroup order.  One wave per (key, row).
-template <int kPhase>
+// factor, row) added in workgroup order.  One wave per (key, row); units of
+// at most kRows pairs (partial blocks of kRows rows).
+template <int kPhase, int kRows>
 __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
   const int keys_per_unit = per_unit / per_key;
-  const int U = p.meta[4];
+  const int U = *p.nunits;
   const int total = U * per_unit;
   const int chunk = (total + p.G - 1) / p.G;
   const int maxj = (chunk + per_key - 1) / per_key + 1;
   const float* part = kPhase == kPhaseA ? p.partA : p.partC;
-  const int nrows = U * keys_per_unit * kMaxM;
+  const int nrows = U * keys_per_unit * kRows;
   for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nrows;
        w += gridDim.x * (kT / kWave)) {
-    const int key = w / kMaxM, row = w % kMaxM;
+    const int key = w / kRows, row = w % kRows;
     const int u = key / keys_per_unit, f = key - u * keys_per_unit;
     const int4 info = p.unit_info[u];
     if (row >= info.z) continue;
     const int b0 = (key * per_key) / chunk, b1 = (key * per_key + per_key - 1) / chunk;
+    // Batches of kRedLoads partials in flight, summed in workgroup order.
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int bb = b0; bb <= b1; ++bb) {
-      const float4 v = reinterpret_cast<const float4*>(
-          part + (static_cast<int64_t>(part_slot(bb, key, chunk, per_key, maxj)) * kMaxM + row) * kN)[lane];
-      s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+    for (int bb = b0; bb <= b1; bb += kRedLoads) {
+      float4 v[kRedLoads];
+#pragma unroll
+      for (int q = 0; q < kRedLoads; ++q) {
+        const int b = min(bb + q, b1);
+        v[q] = reinterpret_cast<const float4*>(
+            part + (static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kRows + row) * kN)[lane];
+      }
+#pragma unroll
+      for (int q = 0; q < kRedLoads; ++q) {
+        if (bb + q <= b1) {
+          s.x += v[q].x; s.y += v[q].y; s.z += v[q].z; s.w += v[q].w;
+        }
+      }
     }
     const int64_t pair = info.y + row;
     if (kPhase == kPhaseA)
@@ -612,21 +629,37 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
 // out from the y rows of the routed slots, in slot order: reduced mode sums
 // w * y over the token's slots; per-slot mode writes y (times w when the weight
 // goes before the down projection: y is linear in h) and zero for a dropped slot.
+// d % 256 == 0, so the 64 float4 columns of a wave lie in one output row: the
+// slot's id, weight and grouped position are wave-uniform (scalar loads), and
+// the y rows of kCombineBatch slots are loaded before any is added.
 __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
   const int64_t d4 = p.d / 4;
   const int64_t rows = p.out_mode == LATENT_OUT_REDUCED ? p.T : static_cast<int64_t>(p.T) * p.K;
   const int64_t n4 = rows * d4;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; i < n4; i += static_cast<int64_t>(gridDim.x) * kT) {
-    const int64_t r = i / d4, c4 = i - r * d4;
+    const int r = uniform(static_cast<int>(i / d4));
+    const int64_t c4 = i - static_cast<int64_t>(r) * d4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (p.out_mode == LATENT_OUT_REDUCED) {
-      for (int k = 0; k < p.K; ++k) {
-        const int64_t slot = r * p.K + k;
-        const int e = p.ids[slot];
-        if (e < 0 || e >= p.E) continue;
-        const float w = load_act(p.weights, p.w_dtype, slot);
-        const float4 v = reinterpret_cast<const float4*>(p.ybuf + static_cast<int64_t>(p.pos_of[slot]) * p.d)[c4];
-        s.x += w * v.x; s.y += w * v.y; s.z += w * v.z; s.w += w * v.w;
+      for (int k0 = 0; k0 < p.K; k0 += kCombineBatch) {
+        float4 v[kCombineBatch];
+        float w[kCombineBatch];
+        bool ok[kCombineBatch];
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q) {
+          const int slot = r * p.K + min(k0 + q, p.K - 1);
+          const int e = p.ids[slot];
+          ok[q] = k0 + q < p.K && e >= 0 && e < p.E;
+          w[q] = load_act(p.weights, p.w_dtype, slot);
+          const int pos = ok[q] ? p.pos_of[slot] : 0;
+          v[q] = reinterpret_cast<const float4*>(p.ybuf + static_cast<int64_t>(pos) * p.d)[c4];
+        }
+#pragma unroll
+        for (int q = 0; q < kCombineBatch; ++q) {
+          if (ok[q]) {
+            s.x += w[q] * v[q].x; s.y += w[q] * v[q].y; s.z += w[q] * v[q].z; s.w += w[q] * v[q].w;
+          }
+        }
       }
     } else {
       const int e = p.ids[r];
@@ -1324,6 +1357,448 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
+// Prefill-sized batches: bulk units of up to 128 pairs (bulk_kernel)
+// ---------------------------------------------------------------------------
+// The same tile layout and phases as the decode launches, with units of up
+// to kBulkM = 64 grouped pairs of one expert: a decoded B operand feeds four
+// 16-row MFMA blocks (the unit's blocks, rounded up to 1, 2 or 4), so an
+// expert's factor stream is read ceil(n_e / 64) times instead of
+// ceil(n_e / 16).  An expert with fewer than 16 pairs runs one 16-row block
+// per tile, the work shape of the decode path.  Two workgroups per CU, so a
+// SIMD holds two waves and one's decode and LDS waits overlap the other's
+// MFMAs; the unit's activation rows sit in LDS, 33 KB per 64 x 256 block
+// (phase B: the gate and up latents).  Phases A and C load the next tile's
+// block into registers while a tile is computed (their K slice changes every
+// tile); phases B and D load a unit's block once, when the unit changes.
+//
+// Exponents: A's rows are x rows (one exponent per token), B's the gate and
+// up latents and D's the d latent (one per row).  B writes h with one
+// exponent per row and 32 columns (a wave's columns of a tile, so no wave
+// waits for another).  C's K slices are eight such blocks: a unit's rows are
+// rescaled while they are staged to the smallest exponent c of the row's
+// blocks (exact powers of two; only the row's smaller blocks lose low bits),
+// and the partial sums are scaled by 2^-c.  Reduced output stores y in fp16
+// with one exponent per row and 64 columns (again a wave's own) for the
+// per-token combine; per-slot output stores fp32 rows.
+
+constexpr int kBulkBlocks = kBulkM / 16;
+constexpr int kBulkRing = 2;  // code ring depth (tiles)
+constexpr int kBulkHBlock = 32;  // h columns per exponent (phase B: a wave's columns of a tile)
+constexpr int kBulkYBlock = 64;  // y columns per exponent (phase D: a wave's columns of a tile)
+constexpr int kBulkRounds = kBulkM * kActChunks / kT;  // 16-byte activation chunks per thread and block
+constexpr uint32_t kNoRow = 0x80000000u;               // offset of a padding row: beyond every buffer range
+// Activation rows in LDS are 33 chunks apart: the 16 rows x 4 chunks of one
+// MFMA operand read fall on distinct banks, and every fragment address of a
+// tile is one base register plus an immediate offset.
+constexpr int kBulkStride = kActChunks + 1;
+__device__ __forceinline__ int bulk_slot(int row, int chunk) { return row * kBulkStride + chunk; }
+
+template <int kPhase>
+struct BulkShape {
+  static constexpr int kActBlocks = kPhase == kPhaseB ? 2 : 1;
+  // Level table copies: B keeps two activation blocks in LDS, and two
+  // workgroups share a CU's 160 KB.
+  static constexpr int kLut = kPhase == kPhaseB ? 8 : 32;
+  static constexpr int kLutShift = kPhase == kPhaseB ? 5 : 7;
+  static constexpr bool kStaged = kPhase == kPhaseA || kPhase == kPhaseC;
+};
+
+template <int kPhase>
+struct alignas(16) BulkSmem {
+  uint32_t lut[256 * BulkShape<kPhase>::kLut];                    // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[kScaleBytes / 16];                                 // the tile's scale block
+  u32x4 act[BulkShape<kPhase>::kActBlocks][kBulkM * kBulkStride];  // [block][row * 33 + chunk]
+  int rexp[2][kBulkM];     // A: x exponent, C: row exponent c (by unit parity); B: gate / up latent; D: d latent
+  uint32_t rowoff[2][kBulkM];  // A: byte offset of each row's x row (by unit parity); D: output row
+  int texp[kPhase == kPhaseC ? kK / kBulkHBlock : 1][kBulkM];  // C: the staged tile's h block exponents of each row
+  float pw[kBulkM];        // D, per-slot output: router weight of each row
+};
+
+// MFMA steps of a tile over the unit's first kRb 16-row blocks: per 32-row
+// step the four B operands of the wave's columns are decoded once and
+// multiplied into every block.  Rows past the unit's pairs hold zeros.
+template <int kPhase, int kRb>
+__device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32x4 (&cb)[kSteps], int n, int kq,
+                                           int wave, uint32_t lut_lane, float4v (&acc)[kBulkBlocks][4]) {
+  const uint32_t sbase = lds_addr(const_cast<BulkSmem<kPhase>&>(sm).scales[0]);
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int chunk = s * 4 + kq;
+    const int P0 = s * 16 + kq * 4;
+    u32x4 sc0, sc1;
+    if constexpr (kPhase == kPhaseB) {
+      const int Gg = wave, Gu = 4 + wave;
+      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
+      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+    } else {
+      const int G = 2 * wave + (n >> 3);
+      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc1 = sc0;
+    }
+    half8 bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = cb[s][j];
+      const u32x4 sc = j < 2 ? sc0 : sc1;
+      uint32_t f[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << BulkShape<kPhase>::kLutShift));
+        const uint32_t sq = sc[q];
+        f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
+      }
+      bf[j] = __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3]));
+    }
+#pragma unroll
+    for (int rb = 0; rb < kRb; ++rb) {
+      const int row = rb * 16 + n;
+      const half8 a0 = __builtin_bit_cast(half8, sm.act[0][bulk_slot(row, chunk)]);
+      const half8 a1 =
+          kPhase == kPhaseB ? __builtin_bit_cast(half8, sm.act[BulkShape<kPhase>::kActBlocks - 1][bulk_slot(row, chunk)]) : a0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1, bf[j], acc[rb][j], 0, 0, 0);
+    }
+  }
+}
+
+// Per-unit tables of the bulk phases (all threads; a barrier must follow).
+//   A: rowoff[buf][r] = byte offset of the row's x row, rexp[buf][r] = its exponent;
+//   C: rexp[buf][r] = smallest exponent of the row's h blocks.
+template <int kPhase>
+__device__ __forceinline__ void bulk_unit_tables(const Params& p, BulkSmem<kPhase>& sm, const TileRef& tr, int buf,
+                                                 int tid) {
+  if (tid >= kBulkM) return;
+  const bool live = tid < tr.m;
+  const int pair = tr.start + min(tid, tr.m - 1);
+  if constexpr (kPhase == kPhaseA) {
+    const int tok = p.pair_tok[pair];
+    sm.rowoff[buf][tid] = live ? static_cast<uint32_t>(tok) * p.d * 2u : kNoRow;
+    sm.rexp[buf][tid] = live ? p.xexp[tok] : 0;
+  } else if constexpr (kPhase == kPhaseC) {
+    const int nh = p.ff / kBulkHBlock;
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.hexp, static_cast<uint32_t>(p.P) * nh * 4);
+    int c = 0x7FFFFFFF;
+    for (int b0 = 0; b0 < nh; b0 += 8) {  // eight loads in flight
+      int e[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) e[q] = static_cast<int>(ld32(re, (static_cast<uint32_t>(pair) * nh + min(b0 + q, nh - 1)) * 4));
+#pragma unroll
+      for (int q = 0; q < 8; ++q) c = min(c, e[q]);
+    }
+    sm.rexp[buf][tid] = live ? c : 0;
+  }
+}
+
+// Phases B and D: the unit's activation block(s) into LDS (blocking), with
+// their row exponents and, for D's per-slot output, each row's output row and
+// weight.  Runs between barriers.
+template <int kPhase>
+__device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>& sm, const TileRef& tr, int tid,
+                                              u32x4 (&st)[kBulkRounds]) {
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+  constexpr int nblk = BulkShape<kPhase>::kActBlocks;
+#pragma unroll
+  for (int blk = 0; blk < nblk; ++blk) {
+    const _Float16* src = kPhase == kPhaseB ? p.lat + static_cast<int64_t>(blk) * p.P * kK : p.dlat;
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(src, static_cast<uint32_t>(p.P) * kK * 2);
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) {
+      const int r = r0 + 8 * h;
+      const uint32_t off = r < tr.m ? static_cast<uint32_t>(tr.start + r) * kK * 2 + chunk * 16 : kNoRow;
+      st[h] = ld128(rl, off, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) sm.act[blk][bulk_slot(r0 + 8 * h, chunk)] = st[h];
+  }
+  if (tid < nblk * kBulkM) {
+    const int blk = tid / kBulkM, r = tid % kBulkM;
+    const int pair = tr.start + min(r, tr.m - 1);
+    sm.rexp[blk][r] = kPhase == kPhaseB ? p.lexp[blk * p.P + pair] : p.dexp[pair];
+    if constexpr (kPhase == kPhaseD) {
+      sm.rowoff[0][r] = static_cast<uint32_t>(p.pair_tok[pair] * p.K + p.pair_slot[pair]);
+      sm.pw[r] = p.pair_w[pair];
+    }
+  }
+}
+
+// Phases A and C: issue the loads of a tile's activation block (and C's block
+// exponents) into registers.
+constexpr int kBulkTex = kK / kBulkHBlock * kBulkM / kT;  // C: h block exponents per thread and tile
+
+template <int kPhase>
+__device__ __forceinline__ void bulk_issue_act(const Params& p, BulkSmem<kPhase>& sm, const TileRef& tr, int ubuf,
+                                               int tid, bool valid, u32x4 (&st)[kBulkRounds], int (&tex)[kBulkTex]) {
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+  if constexpr (kPhase == kPhaseA) {
+    const int ks = tr.r >= p.nka ? tr.r - p.nka : tr.r;
+    const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.xh, valid ? static_cast<uint32_t>(p.T) * p.d * 2 : 0u);
+    const uint32_t col = ks * kK * 2 + chunk * 16;
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) st[h] = ld128(rx, sm.rowoff[ubuf][r0 + 8 * h] + col, 0);
+  } else {
+    const int ks = tr.r;
+    const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(p.hh, valid ? static_cast<uint32_t>(p.P) * p.ff * 2 : 0u);
+    const uint32_t col = ks * kK * 2 + chunk * 16;
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) {
+      const int r = r0 + 8 * h;
+      st[h] = ld128(rh, r < tr.m ? static_cast<uint32_t>(tr.start + r) * p.ff * 2 + col : kNoRow, 0);
+    }
+    // Exponent of h block q of row r: thread tid loads block tid % 8 of rows
+    // tid / 8 + 32 j.
+    const int nh = p.ff / kBulkHBlock, nq = kK / kBulkHBlock;
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.hexp, valid ? static_cast<uint32_t>(p.P) * nh * 4 : 0u);
+#pragma unroll
+    for (int j = 0; j < kBulkTex; ++j) {
+      const int r = tid / nq + (kT / nq) * j;
+      tex[j] = static_cast<int>(
+          ld32(re, r < tr.m ? (static_cast<uint32_t>(tr.start + r) * nh + ks * nq + tid % nq) * 4 : kNoRow));
+    }
+  }
+}
+
+// Phases A and C: store a staged activation block (C: rescaled to the unit's
+// row exponents; the block exponents go through LDS, so this takes one more
+// barrier).
+template <int kPhase>
+__device__ __forceinline__ void bulk_store_act(BulkSmem<kPhase>& sm, int ubuf, int tid, const u32x4 (&st)[kBulkRounds],
+                                               const int (&tex)[kBulkTex]) {
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+  if constexpr (kPhase == kPhaseC) {
+    constexpr int nq = kK / kBulkHBlock;
+#pragma unroll
+    for (int j = 0; j < kBulkTex; ++j) sm.texp[tid % nq][tid / nq + (kT / nq) * j] = tex[j];
+    lds_barrier();
+    const int q = chunk / (kBulkHBlock / 8);  // the chunk's h block within the tile
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) {
+      const int r = r0 + 8 * h;
+      const int sh = max(-30, sm.rexp[ubuf][r] - sm.texp[q][r]);
+      const _Float16 m = static_cast<_Float16>(ldexpf(1.0f, sh));
+      const half2v m2 = {m, m};
+      u32x4 v = st[h];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t vq = v[q];  // through a scalar: a bit_cast of a vector element reads element 0
+        v[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, vq) * m2);
+      }
+      sm.act[0][bulk_slot(r, chunk)] = v;
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) sm.act[0][bulk_slot(r0 + 8 * h, chunk)] = st[h];
+  }
+}
+
+template <int kPhase>
+__global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
+  using BS = BulkShape<kPhase>;
+  __shared__ BulkSmem<kPhase> sm;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = uniform(tid >> 6);
+  const int n = lane & 15, kq = lane >> 4;
+  const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
+  const int U = uniform(sload(p.nunits));
+  const int total = U * per_unit;
+  const int b = blockIdx.x;
+  const int chunk = (total + p.G - 1) / p.G;
+  const int lo = b * chunk, hi = min(total, lo + chunk);
+  if (lo >= hi) return;
+  const int ntile = hi - lo;
+  const int maxj = (chunk + per_key - 1) / per_key + 1;
+
+  {
+    const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
+    const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
+    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * BS::kLut]);
+#pragma unroll
+    for (int j = 0; j < BS::kLut / 4; ++j) dstv[(j + tid) & (BS::kLut / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+  }
+  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (BS::kLut - 1)) << 2);
+
+  // Code ring of kBulkRing tiles: tile i + kBulkRing - 1's loads are issued
+  // while tile i is computed.
+  u32x4 cb[kBulkRing][kSteps];
+  u32x4 sc[kBulkRing];
+  TileRef ref[kBulkRing];
+  u32x4 st[kBulkRounds];
+  int tex[kBulkTex] = {};
+  float4v acc[kBulkBlocks][4];
+#pragma unroll
+  for (int rb = 0; rb < kBulkBlocks; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[rb][j] = float4v{0.f, 0.f, 0.f, 0.f};
+  auto unit_of = [&](int t) { return uniform(t / per_unit); };
+
+  // Prologue: per-unit tables of tiles 0 and 1 (A, C) or the first unit's
+  // activations (B, D); tile 0's activations and scales in LDS; the ring's
+  // first tiles in flight.
+#pragma unroll
+  for (int r = 0; r + 1 < kBulkRing; ++r) ref[r] = tile_ref<kPhase>(p, min(lo + r, hi - 1));
+  const TileRef ref1 = tile_ref<kPhase>(p, min(lo + 1, hi - 1));
+  if constexpr (BS::kStaged) {
+    bulk_unit_tables<kPhase>(p, sm, ref[0], unit_of(lo) & 1, tid);
+    if (ntile > 1 && unit_of(lo + 1) != unit_of(lo)) bulk_unit_tables<kPhase>(p, sm, ref1, unit_of(lo + 1) & 1, tid);
+    lds_barrier();
+    bulk_issue_act<kPhase>(p, sm, ref[0], unit_of(lo) & 1, tid, true, st, tex);
+  } else {
+    bulk_unit_act<kPhase>(p, sm, ref[0], tid, st);
+  }
+#pragma unroll
+  for (int r = 0; r + 1 < kBulkRing; ++r) issue_codes<kPhase>(p, ref[r], tid, lane, wave, r < ntile, sc[r], cb[r]);
+  if constexpr (BS::kStaged) bulk_store_act<kPhase>(sm, unit_of(lo) & 1, tid, st, tex);
+  sm.scales[tid] = sc[0];
+
+  auto step = [&](int i, auto cs) __attribute__((always_inline)) {
+    // Slots: c holds tile i, c1 tile i + 1, cl the tile issued now (i + kBulkRing - 1).
+    constexpr int c = decltype(cs)::value, c1 = (c + 1) % kBulkRing, cl = (c + kBulkRing - 1) % kBulkRing;
+    const int t = lo + i;
+    const int ut = unit_of(t), ubuf = ut & 1;
+    lds_barrier();  // tile i's activations and scales are in LDS
+    // Tile i + 1's activations first (A, C), then tile i + 2's codes: loads
+    // complete in order, so the wait for the activations at the end of this
+    // step leaves the codes in flight.
+    ref[cl] = tile_ref<kPhase>(p, min(t + kBulkRing - 1, hi - 1));
+    if constexpr (BS::kStaged)
+      bulk_issue_act<kPhase>(p, sm, ref[c1], unit_of(min(t + 1, hi - 1)) & 1, tid, i + 1 < ntile, st, tex);
+    issue_codes<kPhase>(p, ref[cl], tid, lane, wave, i + kBulkRing - 1 < ntile, sc[cl], cb[cl]);
+    const TileRef& tr = ref[c];
+    const int nrb = (tr.m + 15) >> 4;
+    // Row tables from the lane's first row (kq * 4): entry rb * 16 + v is the
+    // lane's row v of block rb (immediate offsets).
+    const int* rx0 = &sm.rexp[0][kq * 4];
+    const int* rx1 = &sm.rexp[1][kq * 4];
+    // Branch-free MFMA sections for 1, 2 or 4 blocks (the unit's blocks
+    // rounded up): a branch per block would expose every operand read.
+    if (nrb > 2)
+      bulk_steps<kPhase, 4>(sm, cb[c], n, kq, wave, lut_lane, acc);
+    else if (nrb > 1)
+      bulk_steps<kPhase, 2>(sm, cb[c], n, kq, wave, lut_lane, acc);
+    else
+      bulk_steps<kPhase, 1>(sm, cb[c], n, kq, wave, lut_lane, acc);
+
+    if constexpr (Shape<kPhase>::kSliceK) {
+      if (i + 1 == ntile || (t + 1) % per_key == 0) {
+        const int key = t / per_key;
+        float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
+                      static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kBulkM * kN;
+#pragma unroll
+        for (int rb = 0; rb < kBulkBlocks; ++rb) {
+          if (rb < nrb) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int row = rb * 16 + kq * 4 + v;
+              if (row < tr.m) {
+                const float s = ldexpf(1.0f, -(ubuf ? rx1 : rx0)[rb * 16 + v]);
+                *reinterpret_cast<float4*>(part + row * kN + wave * 64 + n * 4) =
+                    make_float4(acc[rb][0][v] * s, acc[rb][1][v] * s, acc[rb][2][v] * s, acc[rb][3][v] * s);
+              }
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[rb][j] = float4v{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    } else if constexpr (kPhase == kPhaseB) {
+      // h = SiLU(g) * u of the wave's 32 h columns, fp16 with one exponent
+      // per row and 32-column block (the wave's own: no exchange).
+      const int nh = p.ff / kBulkHBlock;
+#pragma unroll
+      for (int rb = 0; rb < kBulkBlocks; ++rb) {
+        if (rb < nrb) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = rb * 16 + kq * 4 + v;
+            const float sg = ldexpf(1.0f, -rx0[rb * 16 + v]), su = ldexpf(1.0f, -rx1[rb * 16 + v]);
+            const float h0 = silu(acc[rb][0][v] * sg) * (acc[rb][2][v] * su);
+            const float h1 = silu(acc[rb][1][v] * sg) * (acc[rb][3][v] * su);
+            const int ex = pow2_row_exponent(op_over(fmaxf(fabsf(h0), fabsf(h1)), 1, 16, OpMax{}));
+            if (row < tr.m) {
+              half2v hb;
+              hb[0] = static_cast<_Float16>(ldexpf(h0, ex));
+              hb[1] = static_cast<_Float16>(ldexpf(h1, ex));
+              const int64_t prow = tr.start + row;
+              *reinterpret_cast<half2v*>(p.hh + prow * p.ff + tr.r * kHBlock + wave * 32 + n * 2) = hb;
+              if (n == 0) p.hexp[prow * nh + tr.r * 4 + wave] = ex;
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rb][j] = float4v{0.f, 0.f, 0.f, 0.f};
+      }
+    } else {
+      // D: y rows of the tile's 256 columns; reduced output in fp16 with one
+      // exponent per row and 64-column block (the wave's own).
+      const bool reduced = p.out_mode == LATENT_OUT_REDUCED;
+      const int ny = p.d / kBulkYBlock;
+#pragma unroll
+      for (int rb = 0; rb < kBulkBlocks; ++rb) {
+        if (rb < nrb) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = rb * 16 + kq * 4 + v;
+            const float s = ldexpf(1.0f, -rx0[rb * 16 + v]);
+            const int64_t prow = tr.start + row;
+            const int col = tr.r * kN + wave * 64 + n * 4;
+            if (reduced) {
+              float y[4], mx = 0.f;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                y[j] = acc[rb][j][v] * s;
+                mx = fmaxf(mx, fabsf(y[j]));
+              }
+              const int ex = pow2_row_exponent(op_over(mx, 1, 16, OpMax{}));
+              if (row < tr.m) {
+                half4v hv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) hv[j] = static_cast<_Float16>(ldexpf(y[j], ex));
+                *reinterpret_cast<half4v*>(p.yh + prow * p.d + col) = hv;
+                if (n == 0) p.yexp[prow * ny + tr.r * 4 + wave] = ex;
+              }
+            } else if (row < tr.m) {
+              const float w = s * (p.wbd ? (&sm.pw[kq * 4])[rb * 16 + v] : 1.0f);
+              *reinterpret_cast<float4*>(p.out + static_cast<int64_t>((&sm.rowoff[0][kq * 4])[rb * 16 + v]) * p.d + col) =
+                  make_float4(acc[rb][0][v] * w, acc[rb][1][v] * w, acc[rb][2][v] * w, acc[rb][3][v] * w);
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[rb][j] = float4v{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+
+    lds_barrier();  // every wave is done with tile i's activations and scales
+    if constexpr (BS::kStaged) {
+      bulk_store_act<kPhase>(sm, unit_of(min(t + 1, hi - 1)) & 1, tid, st, tex);
+      // Tables of tile i + 2's unit, when it starts one (tile i + 1's unit,
+      // of the other parity, is the one in use).
+      if (i + 2 < ntile && unit_of(t + 2) != unit_of(t + 1))
+        bulk_unit_tables<kPhase>(p, sm, tile_ref<kPhase>(p, t + 2), unit_of(t + 2) & 1, tid);
+    } else {
+      if (i + 1 < ntile && unit_of(t + 1) != ut) bulk_unit_act<kPhase>(p, sm, ref[c1], tid, st);
+    }
+    sm.scales[tid] = sc[c1];
+  };
+  int i = 0;
+  if constexpr (kBulkRing == 2) {
+    for (; i + 2 <= ntile; i += 2) {
+      step(i, std::integral_constant<int, 0>{});
+      step(i + 1, std::integral_constant<int, 1>{});
+    }
+    if (i < ntile) step(i, std::integral_constant<int, 0>{});
+  } else {
+    for (; i + 3 <= ntile; i += 3) {
+      step(i, std::integral_constant<int, 0>{});
+      step(i + 1, std::integral_constant<int, 1>{});
+      step(i + 2, std::integral_constant<int, 2>{});
+    }
+    if (i < ntile) step(i, std::integral_constant<int, 0>{});
+    if (i + 1 < ntile) step(i + 1, std::integral_constant<int, 1>{});
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Tile layout (latent_stream_tiles_pack)
 // ---------------------------------------------------------------------------
 struct PackParams {
@@ -1511,6 +1986,68 @@ static int flow_maxj(int64_t units, int nka, int G) {
   return static_cast<int>((chunk + nka - 1) / nka + 1);
 }
 
+bool bulk_supported(const latent_moe_args& a) {
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  // 32-bit byte offsets into x, h and the latents.
+  return a.stream_tiles != nullptr && aligned16(a.stream_tiles) && tiles_shape_ok(a) && P >= 1 &&
+         a.n_tokens * a.n_embd * 2 < (1ll << 31) && P * a.n_ff * 2 < (1ll << 31) && P * kK * 4 < (1ll << 31);
+}
+
+size_t bulk_part_bytes(const latent_moe_args& a, int64_t max_units) {
+  const int G = grid_size();
+  const int nka = static_cast<int>(a.n_embd / kK), nkc = static_cast<int>(a.n_ff / kK);
+  const int64_t slots = std::max(part_slots(max_units, 2 * nka, nka, G), part_slots(max_units, nkc, nkc, G));
+  return static_cast<size_t>(slots) * kBulkM * kN * 4;
+}
+
+int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units, hipStream_t s) {
+  const TileSizes ts = tile_sizes(a);
+  Params p{};
+  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  p.nunits = bk.nunits;
+  p.unit_info = bk.units;
+  p.pair_tok = bk.pair_tok;
+  p.pair_slot = bk.pair_slot;
+  p.pair_w = bk.pair_w;
+  p.xh = bk.xh;
+  p.xexp = bk.xexp;
+  p.partA = p.partC = bk.part;  // A's partials are summed before C writes its own
+  p.lat = bk.lat;
+  p.lexp = bk.lexp;
+  p.hh = bk.hh;
+  p.hexp = bk.hexp;
+  p.dlat = bk.dlat;
+  p.dexp = bk.dexp;
+  p.yh = bk.y;
+  p.yexp = bk.yexp;
+  p.out = static_cast<float*>(a.out);
+  p.T = static_cast<int>(a.n_tokens);
+  p.K = static_cast<int>(a.n_expert_used);
+  p.E = static_cast<int>(a.n_expert);
+  p.d = static_cast<int>(a.n_embd);
+  p.ff = static_cast<int>(a.n_ff);
+  p.P = p.T * p.K;
+  p.wbd = a.weight_before_down ? 1 : 0;
+  p.out_mode = a.out_mode;
+  p.nka = p.d / kK;
+  p.nb = p.ff / kHBlock;
+  p.nkc = p.ff / kK;
+  p.nd = p.d / kN;
+  p.G = grid_size();
+  const int64_t U = max_units;
+  auto grid = [&](int64_t per_unit) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(p.G, U * per_unit))); };
+  auto rblocks = [](int64_t rows) {
+    return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(2048, (rows + kT / kWave - 1) / (kT / kWave))));
+  };
+  hipLaunchKernelGGL(bulk_kernel<kPhaseA>, dim3(grid(2 * p.nka)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM>), dim3(rblocks(U * 2 * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseB>, dim3(grid(p.nb)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(grid(p.nkc)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM>), dim3(rblocks(U * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseD>, dim3(grid(p.nd)), dim3(kT), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}
+
 bool one_launch(const latent_moe_args& a) {
   const char* env = std::getenv("LATENT_STREAM_LAUNCH");
   if (!(env && !std::strcmp(env, "one"))) return false;
@@ -1553,6 +2090,7 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   Params p{};
   for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
   p.meta = g.meta;
+  p.nunits = g.meta + 4;
   p.unit_info = g.unit_info;
   p.unit_tok = g.unit_tok;
   p.pos_of = reinterpret_cast<const int*>(scratch + L.pos_of);
@@ -1605,11 +2143,11 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   }
   const int rows_per_block = kT / kWave;
   hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nka)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(reduce_kernel<kPhaseA>, dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),
+  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kMaxM>), dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),
                      dim3(kT), 0, s, p);
   hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(item_grid(p.nb)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(item_grid(p.nkc)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(reduce_kernel<kPhaseC>, dim3(blocks((U * kMaxM + rows_per_block - 1) / rows_per_block)), dim3(kT),
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kMaxM>), dim3(blocks((U * kMaxM + rows_per_block - 1) / rows_per_block)), dim3(kT),
                      0, s, p);
   hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(item_grid(p.nd)), dim3(kT), 0, s, p);
   const int64_t out4 = (a.out_mode == LATENT_OUT_REDUCED ? p.T : static_cast<int64_t>(p.P)) * p.d / 4;

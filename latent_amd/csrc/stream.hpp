@@ -43,5 +43,36 @@ int64_t max_units(int64_t pairs, int64_t experts);
 Layout layout_for(const latent_moe_args& a);
 int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStream_t s);
 
+// Prefill-sized batches on the same tile layout: units of up to kBulkM
+// grouped pairs of one expert, two workgroups per CU.
+constexpr int kBulkM = 64;
+
+// Inputs and intermediates of the bulk chain, all device pointers.
+struct BulkArgs {
+  const int* nunits;     // number of units
+  const int4* units;     // [units] {expert, first grouped pair, pairs (1..kBulkM), 0}
+  const int* pair_tok;   // [P] token, slot and router weight of each grouped pair
+  const int* pair_slot;
+  const float* pair_w;
+  const _Float16* xh;    // [T][d] x as fp16 rows * 2^xexp
+  const int* xexp;       // [T]
+  _Float16* lat;         // [2][P][256] gate / up latents * 2^lexp
+  int* lexp;             // [2][P]
+  _Float16* hh;          // [P][ff] h * 2^hexp
+  int* hexp;             // [P][ff / 32]: one exponent per 32 columns
+  _Float16* dlat;        // [P][256] down latent * 2^dexp
+  int* dexp;             // [P]
+  _Float16* y;           // reduced output: [P][d] y * 2^yexp (the caller's combine sums w * y per token)
+  int* yexp;             // [P][d / 64]: one exponent per 64 columns
+  float* part;           // partial sums, bulk_part_bytes
+};
+
+// The layer has a tile layout this chain can stream (rank 256, pure NF4).
+bool bulk_supported(const latent_moe_args& a);
+size_t bulk_part_bytes(const latent_moe_args& a, int64_t max_units);
+// Per-slot output: writes out's routed rows (times w when the weight goes
+// before the down projection); reduced output: writes y and yexp.
+int bulk_forward(const latent_moe_args& a, const BulkArgs& b, int64_t max_units, hipStream_t s);
+
 }  // namespace stream
 }  // namespace latent
