@@ -185,9 +185,11 @@ int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t st
 /*
  * Which implementation latent_moe_ffn_forward uses for these arguments, the
  * first that supports the call in this order:
- *   2 = grouped fp16-MFMA prefill: on average at least 16 routed pairs per
- *       active expert, no INT8 groups, n_embd / n_ff / max_rank multiples of
- *       128 with n_ff and max_rank <= 2048, 16-byte aligned x and codes;
+ *   2 = fp16-MFMA prefill: on average at least 16 routed pairs per active
+ *       expert, no INT8 groups, n_embd / n_ff / max_rank multiples of 128
+ *       with n_ff and max_rank <= 2048, 16-byte aligned x and codes; it runs
+ *       on the stream_tiles layout when one is given (64-pair units),
+ *       otherwise as grouped GEMMs (LATENT_PREFILL_ENGINE=gemm selects those);
  *   3 = streaming fp16-MFMA decode: a stream_tiles layout is given (pure NF4,
  *       max_rank 256, n_embd and n_ff multiples of 256), 1 to 4096 routed
  *       pairs, 16-byte aligned x;
