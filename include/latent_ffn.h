@@ -204,6 +204,19 @@ int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t st
 int latent_moe_path(const latent_moe_args* args);
 
 /*
+ * Launch style of a call that takes the streaming path (latent_moe_path 3):
+ *   2 = small-batch chain: one launch for at most 16 routed pairs, every
+ *       workgroup's tiles loaded first, grouping and combine inside (taken by
+ *       default wherever each workgroup's tiles fit its registers);
+ *   1 = one-launch chain for any batch (LATENT_STREAM_LAUNCH=one);
+ *   0 = one launch per phase (the default otherwise; LATENT_STREAM_LAUNCH=phases
+ *       also for small batches).
+ * LATENT_E_UNSUPPORTED when the call does not take the streaming path.
+ * Diagnostic only; no counterpart in the reference.
+ */
+int latent_stream_launch(const latent_moe_args* args);
+
+/*
  * Dequantize expert `expert` of one stacked factor into f32 [rows][cols]
  * (out, device).  Bit-exact restatement of dequantize_nf4 / dequantize_int8
  * (loader/latent_loader.py:133-145, 161-170): one fp32 multiply per element.

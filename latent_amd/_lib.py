@@ -38,6 +38,7 @@ EXPORTED = (
     "latent_moe_ffn_forward",
     "latent_moe_ffn_forward_noalloc",
     "latent_moe_path",
+    "latent_stream_launch",
     "latent_moe_check",
     "latent_unpack",
     "latent_pack_nf4",
@@ -178,6 +179,8 @@ def _load() -> ctypes.CDLL:
     lib.latent_moe_ffn_forward_noalloc.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p]
     lib.latent_moe_path.restype = ctypes.c_int
     lib.latent_moe_path.argtypes = [ctypes.POINTER(LatentMoeArgs)]
+    lib.latent_stream_launch.restype = ctypes.c_int
+    lib.latent_stream_launch.argtypes = [ctypes.POINTER(LatentMoeArgs)]
     lib.latent_unpack.restype = ctypes.c_int
     lib.latent_unpack.argtypes = [ctypes.POINTER(LatentFactor), ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
     lib.latent_pack_nf4.restype = ctypes.c_int

@@ -1022,6 +1022,16 @@ extern "C" int latent_moe_path(const latent_moe_args* args) {
   return choose_path(*args, pl);
 }
 
+extern "C" int latent_stream_launch(const latent_moe_args* args) {
+  if (!args) return LATENT_E_INVALID;
+  const int st = validate(*args);
+  if (st != LATENT_OK) return st;
+  fused::Plan pl;
+  if (choose_path(*args, pl) != kPathStream) return LATENT_E_UNSUPPORTED;
+  if (stream::lite_applies(*args)) return 2;
+  return stream::one_launch(*args) ? 1 : 0;
+}
+
 extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
   if (!args) return LATENT_E_INVALID;
   const latent_moe_args& a = *args;
@@ -1084,6 +1094,11 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   p.a_max = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P)));
   const bool use_prefill = path == kPathPrefill;
   const bool use_stream = path == kPathStream;
+  if (use_stream && stream::lite_applies(a)) {
+    static_assert(stream::kLiteCtrlOffset + stream::kLiteCtrlBytes <= fused::kReserved, "control block");
+    return stream::lite_forward(a, static_cast<char*>(a.workspace), ws + L.gu,
+                                reinterpret_cast<int*>(static_cast<char*>(a.workspace) + fused::kErrorOffset), s);
+  }
   if (use_stream) {
     const int64_t mu = stream::max_units(P, a.n_expert);
     p.unit_info = reinterpret_cast<int4*>(ws + L.units);

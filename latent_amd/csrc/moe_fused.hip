@@ -27,6 +27,7 @@
 // The group scale is folded into the activation: acc += (x * s) * level, fp32.
 #include "common.hpp"
 #include "fused.hpp"
+#include "stream.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -1269,7 +1270,7 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   off = align256(off + A * sizeof(ExpertSync));
   pl.off_ycnt = off;
   off = align256(off + T * pl.ncd * sizeof(int));
-  if (off > kReserved) return false;
+  if (off > stream::kLiteCtrlOffset) return false;  // the small-batch chain's counters follow
   off = 0;
   pl.off_partA = off; off = align256(off + 2ull * pl.nca * P * R * 4);
   pl.off_glat = off;  off = align256(off + P * 2 * R * 4);

@@ -81,6 +81,7 @@ constexpr int kGroupsPerCU = 2;                       // resident workgroups per
 constexpr int64_t kFlowSpinTicks = 100000000;         // bounded waits: 1 s of s_memrealtime (100 MHz)
 constexpr int kCombineBatch = 8;                      // slots' rows in flight per output float4 (combine)
 constexpr int kFlowMaxKTiles = 64;                    // one-launch chain: d / 256 at most
+constexpr int kFlowCntStride = 32;                    // ints between the one-launch chain's counters (128 B)
 constexpr int kRedLoads = 8;                          // partial rows in flight per reduce step
 enum Phase { kPhaseA = 0, kPhaseB, kPhaseC, kPhaseD };
 enum { T_GATE_A = 0, T_UP_A, T_GU_B, T_DOWN_A, T_DOWN_B, kTileArrays };
@@ -120,7 +121,8 @@ struct Params {
   const int* pair_tok;    // [P] token of each grouped pair
   const int* pair_slot;   // [P] slot of each grouped pair
   const float* pair_w;    // [P] router weight of each grouped pair
-  int* cnt;               // [maxu] A tiles done, [maxu] BC items done, [1] workgroups done (zeroed by prep)
+  int* cnt;               // [2 maxu + 1][kFlowCntStride]: A tiles done, BC items done per unit, workgroups done
+                          // (zeroed by prep; one cache line per counter)
   int* err;               // set when a bounded wait times out
   int maxu;               // units bound (counter stride)
   int maxj;               // partial-sum slots per workgroup in phase A
@@ -1035,8 +1037,8 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
   fl.vd = fl.va + (2 * fl.nbc + 2) / 3 * 3;
   fl.total = fl.vd + fl.ndd;
   int* const cntA = p.cnt;
-  int* const cntC = p.cnt + p.maxu;
-  int* const done = p.cnt + 2 * p.maxu;
+  int* const cntC = p.cnt + p.maxu * kFlowCntStride;
+  int* const done = p.cnt + 2 * p.maxu * kFlowCntStride;
 
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
@@ -1140,7 +1142,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
         if (tid <= u1 - u0) {
           const int u = u0 + tid;
           const int lo = max(fl.a0, u * per), hi = min(fl.a0 + fl.na, (u + 1) * per);
-          __hip_atomic_fetch_add(cntA + u, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(cntA + u * kFlowCntStride, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       stage_next(i, act1, cs);
@@ -1173,7 +1175,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
             sm.segslot[k][s] = ob * p.maxj + key - range_lo(fl.NA, ob, G) / p.nka;
           }
         }
-        flow_wait(p, cntA + d.u, 2 * p.nka);
+        flow_wait(p, cntA + d.u * kFlowCntStride, 2 * p.nka);
         auto src = [&](int k, int s) { return p.partA + static_cast<int64_t>(sm.segslot[k][s]) * kMaxM * kN; };
         flow_reduce(sm, 2, d.m, S0, S1, src, lane, wave);
         lds_barrier();
@@ -1242,7 +1244,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
         if (tid <= u1 - u0) {
           const int u = u0 + tid;
           const int lo = max(fl.b0, u * p.nb), hi = min(fl.b0 + fl.nbc, (u + 1) * p.nb);
-          __hip_atomic_fetch_add(cntC + u, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(cntC + u * kFlowCntStride, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       stage_next(i, act1, cs);
@@ -1264,7 +1266,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
           sm.pw[tid] = p.pair_w[pair];
           sm.prow[tid] = p.pair_tok[pair] * p.K + p.pair_slot[pair];
         }
-        flow_wait(p, cntC + d.u, p.nb);
+        flow_wait(p, cntC + d.u * kFlowCntStride, p.nb);
         auto src = [&](int, int s) { return p.partC + (static_cast<int64_t>(d.u) * p.nb + s) * kMaxM * kN; };
         flow_reduce(sm, 1, d.m, p.nb, 0, src, lane, wave);
         lds_barrier();
@@ -1353,6 +1355,559 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
       }
       reinterpret_cast<float4*>(p.out)[i] = s;
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Batches of a few routed pairs: one launch with every tile in flight from the
+// start (lite_kernel)
+// ---------------------------------------------------------------------------
+// For at most kLiteMaxP routed pairs.  Every workgroup groups the pairs itself
+// (wave 0: units are the distinct experts in order of first appearance, a
+// unit's pairs in index order), then takes one role by its index:
+//   [0, gA)          A:  up to kLiteSlots K tiles (unit, gate/up, k): x . A
+//   [gA, gA + gB)    BC: one item (unit, 128-column h block): its B tile and
+//                        the matching half of a C tile
+//   [gA + gB, G)     D:  up to kLiteSlots column tiles (unit, n): d_lat . B_d
+// and issues the loads of all its tiles (codes and scales into registers, an A
+// tile's x slices too) before anything else, so the whole factor stream is in
+// flight at once.  Dependencies point to lower workgroup indices only (BC waits
+// for A, D for BC), so the chain completes even when not every workgroup is
+// resident.
+//   * A writes one partial per tile ([gate/up][k][pair][256] fp32, coherent
+//     stores) and, once they are drained, adds one per tile to cntA[u];
+//   * BC waits for cntA[u] == 2 nka, sums the partials in k order into the gate
+//     and up latents (fp16 rows * 2^e in LDS), forms h for its 128 columns in
+//     LDS and writes its C half tile's partial ([nb][pair][256]); cntC[u] += 1;
+//   * D waits for cntC[u] == nb, sums the nb partials into the down latent and
+//     writes y rows: per-slot output straight to out; reduced output to ybuf,
+//     and each (token, column tile) counts its routed rows: the workgroup whose
+//     row completes the count sums the token's rows in slot order into out.
+// Counters are reset by their last user (cntA[u] by the workgroup holding D
+// tile (u, 0), after cntC[u] is complete; cntC[u] and cntD[u] by the unit's
+// last D tile; a (token, tile) count by its last arriver), so they are zero
+// again when the kernel ends.  x enters A as fp16 with one power-of-two
+// exponent per (token, 256-column slice), taken from the slice itself.
+
+constexpr int kLiteMaxP = 16;  // routed pairs the small-batch chain takes
+constexpr int kLiteSlots = 3;  // tiles a workgroup holds in registers
+constexpr int kLiteRed = 16;   // partial rows in flight per lane in the latent sums
+// Counters sit on their own cache lines (a line shared by every unit's
+// counter serialises all publishes and polls: ~5 us per dependency step).
+constexpr int kLiteUnitStride = 32;  // ints between per-unit counters (128 B)
+constexpr int kLiteKeyStride = 16;   // ints between (token, tile) counters (64 B)
+// B, C and D tiles are needed only after A's results: their workgroups issue
+// their loads this long after grouping, so A's tiles come first from HBM.
+constexpr int64_t kLiteLateTicks = 150;  // 1.5 us of s_memrealtime (100 MHz)
+
+struct LiteParams {
+  const uint8_t* tiles[kTileArrays];
+  const void* x;
+  int x_dtype;
+  const int32_t* ids;
+  const void* weights;
+  int w_dtype;
+  float* out;
+  float* partA;  // [2][nka][P][256]
+  float* partC;  // [nb][P][256]
+  float* ybuf;   // [P][d] (reduced output)
+  int* cntA;     // [kLiteMaxP][kLiteUnitStride] A tiles done per unit
+  int* cntC;     // [kLiteMaxP][kLiteUnitStride] BC items done per unit
+  int* cntD;     // [kLiteMaxP][kLiteUnitStride] D tiles done per unit
+  int* cntY;     // [T][nd][kLiteKeyStride] routed rows stored per (token, column tile)
+  int* err;      // set when a bounded wait times out
+  int T, K, E, d, P, wbd;
+  int nka, nb, nkc, nd;
+};
+
+// Workgroups per role: gB = the BC items, the rest split between A and D in
+// proportion to their tiles.
+struct LiteSplit {
+  int gA, gB, gD;
+};
+__host__ __device__ inline LiteSplit lite_split(int U, int nka, int nb, int nd, int G) {
+  const int64_t NA = 2ll * U * nka, ND = static_cast<int64_t>(U) * nd;
+  const int gB = U * nb, R = G - gB;
+  int gA = NA + ND > 0 ? static_cast<int>(R * NA / (NA + ND)) : 1;
+  gA = gA < 1 ? 1 : (gA > R - 1 ? R - 1 : gA);
+  return LiteSplit{gA, gB, R - gA};
+}
+// Every workgroup's tiles fit its registers (at most kLiteSlots A or D tiles).
+__host__ __device__ inline bool lite_fits(int U, int nka, int nb, int nd, int G) {
+  if (U < 1) return true;
+  if (G - U * nb < 2) return false;
+  const LiteSplit s = lite_split(U, nka, nb, nd, G);
+  const int64_t NA = 2ll * U * nka, ND = static_cast<int64_t>(U) * nd;
+  return (NA + s.gA - 1) / s.gA <= kLiteSlots && (ND + s.gD - 1) / s.gD <= kLiteSlots;
+}
+
+struct alignas(16) LiteSmem {
+  uint32_t lut[256 * kLutCopies];       // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[kScaleBytes / 16];       // the current tile's scale block
+  u32x4 act[2][kMaxM * kActChunks];     // A: x rows; BC: gate / up latents; D: down latent (block 0)
+  u32x4 hb[kMaxM * kActChunks];         // BC: h rows (128 columns)
+  float4 red[4][4][kWave];              // latent sums: [row of 4][wave][lane]
+  int rexp[2][kMaxM];                   // exponents of act's rows
+  int hexp[kMaxM];                      // h exponents
+  float hmax[4][kMaxM];                 // per-wave row maxima of h
+  int ue[kLiteMaxP], ustart[kLiteMaxP], um[kLiteMaxP];  // units: expert, first grouped pair, pairs
+  int pos_pair[kLiteMaxP];              // routed pair (token * K + slot) at each grouped position
+  int pos_of[kLiteMaxP];                // grouped position of each routed pair (-1: dropped)
+  float w[kLiteMaxP];                   // router weight of each routed pair
+  int last[kLiteSlots * kMaxM];         // D: (token, tile) sums this workgroup completes
+  int nunits, nlast;
+};
+
+__device__ __forceinline__ void lut_fill(uint32_t* lut, int tid) {
+  const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
+  const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
+  uint4* dstv = reinterpret_cast<uint4*>(&lut[tid * kLutCopies]);
+#pragma unroll
+  for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+}
+
+// Wave 0: the grouping of the call's routed pairs (lane i holds pair i).
+__device__ __forceinline__ void lite_group(const LiteParams& p, LiteSmem& sm, int lane) {
+  const bool in = lane < p.P;
+  const int e = in ? p.ids[lane] : -1;
+  const bool valid = e >= 0 && e < p.E;
+  if (in) sm.w[lane] = load_act(p.weights, p.w_dtype, lane);
+  uint64_t todo = __ballot(valid);
+  int u = 0, start = 0, pos = -1;
+  while (todo) {
+    const int leader = __ffsll(static_cast<unsigned long long>(todo)) - 1;
+    const int el = __shfl(e, leader, kWave);
+    const uint64_t same = __ballot(valid && e == el);
+    if (valid && e == el) pos = start + __popcll(same & ((1ull << lane) - 1ull));
+    const int c = __popcll(same);
+    if (lane == 0) {
+      sm.ue[u] = el;
+      sm.ustart[u] = start;
+      sm.um[u] = c;
+    }
+    start += c;
+    ++u;
+    todo &= ~same;
+  }
+  if (in) sm.pos_of[lane] = pos;
+  if (pos >= 0) sm.pos_pair[pos] = lane;
+  if (lane == 0) {
+    sm.nunits = u;
+    sm.nlast = 0;
+  }
+}
+
+// Routed slots of token t with a valid expert.
+__device__ __forceinline__ int lite_routed(const LiteParams& p, const LiteSmem& sm, int t) {
+  int c = 0;
+  for (int q = 0; q < p.K; ++q) c += sm.pos_of[t * p.K + q] >= 0;
+  return c;
+}
+
+// Bounded wait (thread 0) until *c >= target, then a workgroup barrier.
+__device__ __forceinline__ void lite_wait(int* err, const int* c, int target) {
+  if (threadIdx.x == 0) {
+    const int64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kFlowSpinTicks) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  lds_barrier();
+}
+
+// Sleep until `ticks` of s_memrealtime have passed since t0.
+__device__ __forceinline__ void lite_sleep_until(int64_t t0, int64_t ticks) {
+  while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
+// 8 x elements (dtype f32: a then b; f16 / bf16: a) as floats.
+__device__ __forceinline__ void lite_x8(const u32x4& a, const u32x4& b, int dtype, float v[8]) {
+  if (dtype == LATENT_F32) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = __uint_as_float(a[j]);
+      v[4 + j] = __uint_as_float(b[j]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (dtype == LATENT_F16) {
+      v[2 * j] = half_bits_to_float(static_cast<uint16_t>(a[j] & 0xFFFFu));
+      v[2 * j + 1] = half_bits_to_float(static_cast<uint16_t>(a[j] >> 16));
+    } else {
+      v[2 * j] = __uint_as_float(a[j] << 16);
+      v[2 * j + 1] = __uint_as_float(a[j] & 0xFFFF0000u);
+    }
+  }
+}
+
+// Codes and scales of one tile: steps [s0, s0 + ns) into cb[0 .. ns) and the
+// scale dwords of the threads `sc_on` selects (zeros elsewhere).
+template <int ns>
+__device__ __forceinline__ void lite_codes(const uint8_t* tile, bool valid, bool sc_on, int s0, int tid, int lane,
+                                           int wave, u32x4& sc, u32x4 (&cb)[kSteps]) {
+  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, valid ? kTileBytes : 0);
+  sc = ld128(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
+  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
+#pragma unroll
+  for (int s = 0; s < ns; ++s) cb[s] = ld128(rt, cbase, (s0 + s) * kWave * 16);
+}
+
+
+// Sums of partial rows into fp16 latent rows (act block k, exponents rexp[k])
+// for the rows [0, m) of a unit whose first grouped pair is `start`.  Block i
+// of key k holds P rows of 256 floats at byte ((k * nblocks + i) * P) * 1 KB of
+// `base`.  kKeys = 2 (gate and up latents, two chains per key) or 1 (down
+// latent, four chains): wave w runs chain c = w % chains of key w / chains,
+// adding blocks c, c + chains, ... in order; a row is the chains' sums added
+// in chain order.
+template <int kKeys>
+__device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, int P, int nblocks, int start, int m,
+                                             int lane, int wave) {
+  constexpr int kChains = 4 / kKeys;
+  const int key = wave / kChains, chain = wave % kChains;
+  const int nk = (nblocks - chain + kChains - 1) / kChains;
+  for (int r0 = 0; r0 < m; r0 += 4) {
+    const int rows = min(4, m - r0);
+    for (int rr = 0; rr < rows; ++rr) {
+      const uint32_t roff = static_cast<uint32_t>(start + r0 + rr) * (kN * 4) + lane * 16;
+      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i0 = 0; i0 < nk; i0 += kLiteRed) {
+        float4 v[kLiteRed];
+#pragma unroll
+        for (int q = 0; q < kLiteRed; ++q) {
+          const uint32_t blk = static_cast<uint32_t>(key * nblocks + chain + kChains * (i0 + q));
+          v[q] = i0 + q < nk ? ld_coh4(base, blk * P * (kN * 4) + roff) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int q = 0; q < kLiteRed; ++q) add4(s, v[q]);
+      }
+      sm.red[rr][wave][lane] = s;
+    }
+    lds_barrier();
+    for (int c = wave; c < rows * kKeys; c += 4) {
+      const int rr = c / kKeys, k = c % kKeys;
+      float4 t = sm.red[rr][k * kChains][lane];
+#pragma unroll
+      for (int ch = 1; ch < kChains; ++ch) add4(t, sm.red[rr][k * kChains + ch][lane]);
+      flow_finish_row(t, sm.act[k], sm.rexp[k], r0 + rr, lane);
+    }
+    lds_barrier();
+  }
+}
+
+// Role A: K tiles [j0, j0 + nj) of the list (unit, gate/up, k).
+__device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, int j0, int nj, int tid, int lane,
+                                            int wave, uint32_t lut_lane) {
+  const int n = lane & 15, kq = lane >> 4;
+  const int r0 = tid / kActChunks, chunk = tid % kActChunks;
+  const int per = 2 * p.nka;
+  const uint32_t esz = p.x_dtype == LATENT_F32 ? 4u : 2u;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.x, static_cast<uint32_t>(p.T) * p.d * esz);
+  u32x4 cb[kLiteSlots][kSteps], sc[kLiteSlots], xr[kLiteSlots][2][2];
+  // Every tile's scales, codes and x slices, tile by tile.
+#pragma unroll
+  for (int j = 0; j < kLiteSlots; ++j) {
+    const bool valid = j < nj;
+    const int t = j0 + min(j, nj - 1);
+    const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
+    const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+    lite_codes<kSteps>(p.tiles[f ? T_UP_A : T_GATE_A] + static_cast<int64_t>(e * p.nka + k) * kTileBytes, valid, true,
+                       0, tid, lane, wave, sc[j], cb[j]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = r0 + 8 * h;
+      const bool live = valid && row < m;
+      const int tok = live ? sm.pos_pair[start + row] / p.K : 0;
+      const uint32_t off = (static_cast<uint32_t>(tok) * p.d + k * kK + chunk * 8) * esz;
+      xr[j][h][0] = ld128(rx, live ? off : 0x80000000u, 0);
+      xr[j][h][1] = ld128(rx, live && esz == 4 ? off + 16 : 0x80000000u, 0);
+    }
+  }
+  float4v acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < kLiteSlots; ++j) {
+    if (j < nj) {
+      const int t = j0 + j;
+      const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
+      const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+      lds_barrier();  // every wave is done with the previous tile's LDS
+      sm.scales[tid] = sc[j];
+      // x rows -> fp16 * 2^e, one exponent per row of this 256-column slice.
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = r0 + 8 * h;
+        float v[8];
+        lite_x8(xr[j][h][0], xr[j][h][1], p.x_dtype, v);
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+        mx = op_over(mx, 1, 32, OpMax{});
+        const int ex = pow2_row_exponent(mx);
+        half8 hv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(v[i], ex));
+        sm.act[0][act_slot(row, chunk)] = __builtin_bit_cast(u32x4, hv);
+        if (chunk == 0) sm.rexp[0][row] = ex;
+      }
+      lds_barrier();
+      flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0]), cb[j], 0, n, kq, wave, lut_lane, acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < m) {
+          const float s = ldexpf(1.0f, -sm.rexp[0][row]);
+          const uint32_t off =
+              ((static_cast<uint32_t>(f * p.nka + k) * p.P + start + row) * kN + wave * 64 + n * 4) * 4;
+          st_coh4(p.partA, off, make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // Publish once every partial is stored.
+  drain_barrier();
+  if (tid < nj)
+    __hip_atomic_fetch_add(p.cntA + (j0 + tid) / per * kLiteUnitStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Role BC: item (unit u, h block kb).
+__device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, int item, int64_t t0, int tid, int lane,
+                                             int wave, uint32_t lut_lane) {
+  const int n = lane & 15, kq = lane >> 4;
+  const int u = item / p.nb, kb = item - u * p.nb, hh = kb & 1;
+  const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+  u32x4 cbB[kSteps], cbC[kSteps], scB, scC;
+  lite_sleep_until(t0, kLiteLateTicks);
+  lite_codes<kSteps>(p.tiles[T_GU_B] + static_cast<int64_t>(e * p.nb + kb) * kTileBytes, true, true, 0, tid, lane,
+                     wave, scB, cbB);
+  // C tile kb / 2, K half hh: steps 4hh .. 4hh + 3 and the scales of row pairs 64hh .. 64hh + 63.
+  lite_codes<kSteps / 2>(p.tiles[T_DOWN_A] + static_cast<int64_t>(e * p.nkc + (kb >> 1)) * kTileBytes, true,
+                         ((tid & 31) >= 16) == (hh != 0), 4 * hh, tid, lane, wave, scC, cbC);
+  lite_wait(p.err, p.cntA + u * kLiteUnitStride, 2 * p.nka);
+  lite_latents<2>(sm, p.partA, p.P, p.nka, start, m, lane, wave);
+  sm.scales[tid] = scB;
+  lds_barrier();
+  float4v acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+  flow_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0]), cbB, 0, n, kq, wave, lut_lane, acc);
+  // h = SiLU(g) * u of columns 32w + 2n + jj of the block, fp16 with one exponent per row.
+  float hv[2][4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int row = kq * 4 + v;
+    const float sg = ldexpf(1.0f, -sm.rexp[0][row]), su = ldexpf(1.0f, -sm.rexp[1][row]);
+    float mx = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      hv[jj][v] = silu(acc[jj][v] * sg) * (acc[jj + 2][v] * su);
+      mx = fmaxf(mx, fabsf(hv[jj][v]));
+    }
+    mx = op_over(mx, 1, 16, OpMax{});
+    if (n == 0) sm.hmax[wave][row] = mx;
+  }
+  lds_barrier();  // every wave is past B's products: the scale buffer is free
+  sm.scales[tid] = scC;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int row = kq * 4 + v;
+    const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
+    const int ex = pow2_row_exponent(mx);
+    half2v h2;
+    h2[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
+    h2[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
+    reinterpret_cast<half2v*>(&sm.hb[act_slot(row, 4 * wave + (n >> 2))])[n & 3] = h2;
+    if (wave == 0 && n == 0) sm.hexp[row] = ex;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+  lds_barrier();
+  flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int row = kq * 4 + v;
+    if (row < m) {
+      const float s = ldexpf(1.0f, -sm.hexp[row]);
+      const uint32_t off = ((static_cast<uint32_t>(kb) * p.P + start + row) * kN + wave * 64 + n * 4) * 4;
+      st_coh4(p.partC, off, make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
+    }
+  }
+  drain_barrier();
+  if (tid == 0) __hip_atomic_fetch_add(p.cntC + u * kLiteUnitStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Role D: column tiles [j0, j0 + nj) of the list (unit, n).
+template <int kOutMode>
+__device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, int j0, int nj, int64_t t0, int tid,
+                                            int lane, int wave, uint32_t lut_lane) {
+  const int n = lane & 15, kq = lane >> 4;
+  u32x4 cb[kLiteSlots][kSteps], sc[kLiteSlots];
+  lite_sleep_until(t0, kLiteLateTicks);
+#pragma unroll
+  for (int j = 0; j < kLiteSlots; ++j) {
+    const int t = j0 + min(j, nj - 1);
+    const int u = t / p.nd, s = t - u * p.nd;
+    const int e = uniform(sm.ue[u]);
+    lite_codes<kSteps>(p.tiles[T_DOWN_B] + static_cast<int64_t>(e * p.nd + s) * kTileBytes, j < nj, true, 0, tid,
+                       lane, wave, sc[j], cb[j]);
+  }
+  float4v acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+  int cur = -1;
+#pragma unroll
+  for (int j = 0; j < kLiteSlots; ++j) {
+    if (j < nj) {
+      const int t = j0 + j;
+      const int u = t / p.nd, s = t - u * p.nd;
+      const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+      if (u != cur) {
+        cur = u;
+        lite_wait(p.err, p.cntC + u * kLiteUnitStride, p.nb);
+        // Every BC item of the unit is past its wait for cntA[u].
+        if (s == 0 && tid == 0)
+          __hip_atomic_store(p.cntA + u * kLiteUnitStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lite_latents<1>(sm, p.partC, p.P, p.nb, start, m, lane, wave);
+      }
+      lds_barrier();  // every wave is done with the previous tile's scales
+      sm.scales[tid] = sc[j];
+      lds_barrier();
+      flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0]), cb[j], 0, n, kq, wave, lut_lane, acc);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        if (row < m) {
+          const float sy = ldexpf(1.0f, -sm.rexp[0][row]);
+          const int pos = start + row, col = s * kN + wave * 64 + n * 4;
+          if constexpr (kOutMode == LATENT_OUT_PER_SLOT) {
+            const int i = sm.pos_pair[pos];
+            const float sw = p.wbd ? sy * sm.w[i] : sy;
+            *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(i) * p.d + col) =
+                make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw);
+          } else {
+            st_coh4(p.ybuf, (static_cast<uint32_t>(pos) * p.d + col) * 4,
+                    make_float4(acc[0][v] * sy, acc[1][v] * sy, acc[2][v] * sy, acc[3][v] * sy));
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  drain_barrier();
+  // The unit's last D tile resets its BC and D counts.
+  if (tid < nj) {
+    const int u = (j0 + tid) / p.nd * kLiteUnitStride;
+    if (__hip_atomic_fetch_add(p.cntD + u, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == p.nd) {
+      __hip_atomic_store(p.cntC + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(p.cntD + u, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if constexpr (kOutMode == LATENT_OUT_REDUCED) {
+    // Thread 64 + 16 j + r counts row r of tile j into its (token, tile).
+    const int q = tid - kWave;
+    if (q >= 0 && q < kLiteSlots * kMaxM && (q >> 4) < nj) {
+      const int t = j0 + (q >> 4), row = q & 15;
+      const int u = t / p.nd, s = t - u * p.nd;
+      if (row < sm.um[u]) {
+        const int tok = sm.pos_pair[sm.ustart[u] + row] / p.K;
+        const int key = tok * p.nd + s;
+        if (__hip_atomic_fetch_add(p.cntY + key * kLiteKeyStride, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 ==
+            lite_routed(p, sm, tok))
+          sm.last[atomicAdd(&sm.nlast, 1)] = key;
+      }
+    }
+    lds_barrier();
+    // Completed (token, tile)s: the token's y rows in slot order, times w.
+    const int nl = uniform(sm.nlast);
+    for (int c = wave; c < nl; c += 4) {
+      const int key = uniform(sm.last[c]);
+      const int tok = key / p.nd, s = key - tok * p.nd;
+      const uint32_t col = static_cast<uint32_t>(s * kN + lane * 4) * 4;
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k0 = 0; k0 < p.K; k0 += kCombineBatch) {
+        float4 v[kCombineBatch];
+        float w[kCombineBatch];
+        bool ok[kCombineBatch];
+#pragma unroll
+        for (int q2 = 0; q2 < kCombineBatch; ++q2) {
+          const int i = tok * p.K + min(k0 + q2, p.K - 1);
+          const int pos = k0 + q2 < p.K ? sm.pos_of[i] : -1;
+          ok[q2] = pos >= 0;
+          w[q2] = sm.w[i];
+          v[q2] = ok[q2] ? ld_coh4(p.ybuf, static_cast<uint32_t>(pos) * p.d * 4 + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int q2 = 0; q2 < kCombineBatch; ++q2) {
+          if (ok[q2]) {
+            sum.x += w[q2] * v[q2].x;
+            sum.y += w[q2] * v[q2].y;
+            sum.z += w[q2] * v[q2].z;
+            sum.w += w[q2] * v[q2].w;
+          }
+        }
+      }
+      *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(tok) * p.d + s * kN + lane * 4) = sum;
+      if (lane == 0) __hip_atomic_store(p.cntY + key * kLiteKeyStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+template <int kOutMode>
+__global__ void __launch_bounds__(kT, kGroupsPerCU) lite_kernel(LiteParams p) {
+  __shared__ LiteSmem sm;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = uniform(tid >> 6);
+  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  lut_fill(sm.lut, tid);
+  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+  if (wave == 0) lite_group(p, sm, lane);
+  lds_barrier();
+  const int64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const int U = uniform(sm.nunits);
+  // Rows no D tile writes (reduced output: tokens without a routed slot;
+  // per-slot output: dropped slots), one row per workgroup from the last.
+  {
+    const int z = G - 1 - b;
+    if constexpr (kOutMode == LATENT_OUT_REDUCED) {
+      if (z < p.T && lite_routed(p, sm, z) == 0)
+        for (int c = tid; c < p.d / 4; c += kT)
+          reinterpret_cast<float4*>(p.out + static_cast<int64_t>(z) * p.d)[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      if (z < p.P && sm.pos_of[z] < 0)
+        for (int c = tid; c < p.d / 4; c += kT)
+          reinterpret_cast<float4*>(p.out + static_cast<int64_t>(z) * p.d)[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  if (U == 0) return;
+  const LiteSplit sp = lite_split(U, p.nka, p.nb, p.nd, G);
+  if (b < sp.gA) {
+    const int N = 2 * U * p.nka;
+    const int j0 = range_lo(N, b, sp.gA), nj = range_lo(N, b + 1, sp.gA) - j0;
+    if (nj > kLiteSlots) {
+      if (tid == 0) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (nj > 0) lite_role_a(p, sm, j0, nj, tid, lane, wave, lut_lane);
+  } else if (b < sp.gA + sp.gB) {
+    lite_role_bc(p, sm, b - sp.gA, t0, tid, lane, wave, lut_lane);
+  } else {
+    const int N = U * p.nd, jd = b - sp.gA - sp.gB;
+    const int j0 = range_lo(N, jd, sp.gD), nj = range_lo(N, jd + 1, sp.gD) - j0;
+    if (nj > kLiteSlots) {
+      if (tid == 0) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (nj > 0) lite_role_d<kOutMode>(p, sm, j0, nj, t0, tid, lane, wave, lut_lane);
   }
 }
 
@@ -2048,6 +2603,65 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
+bool lite_applies(const latent_moe_args& a) {
+  const char* env = std::getenv("LATENT_STREAM_LAUNCH");
+  if (env && (!std::strcmp(env, "phases") || !std::strcmp(env, "one"))) return false;
+  if (!supported(a)) return false;
+  const int64_t P = a.n_tokens * a.n_expert_used;
+  if (P < 1 || P > kLiteMaxP || a.n_embd / kK > kFlowMaxKTiles) return false;
+  if (a.n_tokens * a.n_embd * 4 >= (1ll << 31)) return false;  // 32-bit byte offsets into x
+  const int nka = static_cast<int>(a.n_embd / kK), nb = static_cast<int>(a.n_ff / kHBlock);
+  const int nd = static_cast<int>(a.n_embd / kN);
+  if ((3 * kLiteMaxP * kLiteUnitStride + a.n_tokens * nd * kLiteKeyStride) * 4 > static_cast<int64_t>(kLiteCtrlBytes))
+    return false;
+  const int G = grid_size();
+  const int64_t umax = std::min<int64_t>(P, a.n_expert);
+  for (int U = 1; U <= umax; ++U)
+    if (!lite_fits(U, nka, nb, nd, G)) return false;
+  return true;
+}
+
+int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, hipStream_t s) {
+  const Layout L = layout_for(a);
+  const TileSizes ts = tile_sizes(a);
+  LiteParams p{};
+  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  p.x = a.x;
+  p.x_dtype = a.x_dtype;
+  p.ids = a.ids;
+  p.weights = a.weights;
+  p.w_dtype = a.weights_dtype;
+  p.out = static_cast<float*>(a.out);
+  // The partial sums fit the decode layout's partial regions: A's 2 nka
+  // blocks of P <= 16 rows and C's nb blocks are at most one 16-row slot per
+  // block there.
+  p.partA = reinterpret_cast<float*>(scratch + L.partA);
+  p.partC = reinterpret_cast<float*>(scratch + L.partC);
+  p.ybuf = reinterpret_cast<float*>(scratch + L.ybuf);
+  int* c = reinterpret_cast<int*>(ctrl + kLiteCtrlOffset);
+  p.cntA = c;
+  p.cntC = c + kLiteMaxP * kLiteUnitStride;
+  p.cntD = c + 2 * kLiteMaxP * kLiteUnitStride;
+  p.cntY = c + 3 * kLiteMaxP * kLiteUnitStride;
+  p.err = err;
+  p.T = static_cast<int>(a.n_tokens);
+  p.K = static_cast<int>(a.n_expert_used);
+  p.E = static_cast<int>(a.n_expert);
+  p.d = static_cast<int>(a.n_embd);
+  p.P = p.T * p.K;
+  p.wbd = a.weight_before_down ? 1 : 0;
+  p.nka = p.d / kK;
+  p.nb = static_cast<int>(a.n_ff / kHBlock);
+  p.nkc = static_cast<int>(a.n_ff / kK);
+  p.nd = p.d / kN;
+  const unsigned G = static_cast<unsigned>(grid_size());
+  if (a.out_mode == LATENT_OUT_REDUCED)
+    hipLaunchKernelGGL(lite_kernel<LATENT_OUT_REDUCED>, dim3(G), dim3(kT), 0, s, p);
+  else
+    hipLaunchKernelGGL(lite_kernel<LATENT_OUT_PER_SLOT>, dim3(G), dim3(kT), 0, s, p);
+  return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
+}
+
 bool one_launch(const latent_moe_args& a) {
   const char* env = std::getenv("LATENT_STREAM_LAUNCH");
   if (!(env && !std::strcmp(env, "one"))) return false;
@@ -2078,7 +2692,7 @@ Layout layout_for(const latent_moe_args& a) {
   L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
   L.ybuf = off;   off = al(off + static_cast<size_t>(P) * d * 4);
   L.pos_of = off; off = al(off + static_cast<size_t>(P) * 4);
-  L.cnt_ints = 2 * U + 1;
+  L.cnt_ints = (2 * U + 1) * kFlowCntStride;
   L.cnt = off;    off = al(off + static_cast<size_t>(L.cnt_ints) * 4);
   L.total = off;
   return L;

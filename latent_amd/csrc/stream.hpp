@@ -35,6 +35,18 @@ struct Layout {
 // launches are measured faster today and are the default).
 bool one_launch(const latent_moe_args& a);
 
+// Batches of at most 16 routed pairs: the whole chain in one launch in which
+// every workgroup issues all its tile loads first (lite_kernel), grouping and
+// x conversion included, so the prep kernel is not launched.  Taken by default
+// wherever every workgroup's tiles fit its registers; LATENT_STREAM_LAUNCH=phases
+// or =one selects the other launch styles.  Its counters live in the
+// workspace control block at kLiteCtrlOffset (zero between calls).
+constexpr size_t kLiteCtrlOffset = 192 * 1024;
+constexpr size_t kLiteCtrlBytes = 64 * 1024;
+bool lite_applies(const latent_moe_args& a);
+// ctrl: the workspace's control block; scratch: the decode layout (layout_for).
+int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, hipStream_t s);
+
 // The call can take this path: a tile layout is given (latent_stream_tiles_pack)
 // and the batch has at most 4096 routed pairs.
 bool supported(const latent_moe_args& a);

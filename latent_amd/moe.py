@@ -284,6 +284,22 @@ def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
     return {1: "fused", 2: "prefill", 3: "stream"}.get(r, "general")
 
 
+def stream_launch(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> Optional[str]:
+    """Launch style of a streaming-path call: 'lite' (small-batch chain in one
+    launch), 'one' (one-launch chain) or 'phases' (one launch per phase); None
+    when the call does not take the streaming path."""
+    a = layer.args()
+    a.x = x.data_ptr()
+    a.n_tokens, a.n_expert_used = int(x.shape[0]), int(n_expert_used)
+    a.x_dtype, a.weights_dtype, a.out_mode = _DTYPE_CODE[x.dtype], _lib.LATENT_F32, _lib.LATENT_OUT_REDUCED
+    r = lib.latent_stream_launch(ctypes.byref(a))
+    if r == _lib.LATENT_E_UNSUPPORTED:
+        return None
+    if r < 0:
+        check(r, "latent_stream_launch")
+    return {0: "phases", 1: "one", 2: "lite"}[r]
+
+
 def moe_forward(
     x: torch.Tensor,
     ids: torch.Tensor,

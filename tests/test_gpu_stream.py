@@ -1,8 +1,9 @@
 """Streaming MFMA decode path (stream.hip) against the oracle.
 
-The path is selected with LATENT_MOE_PATH=stream for every call here, in both
-launch styles (LATENT_STREAM_LAUNCH=phases: one launch per phase;
-LATENT_STREAM_LAUNCH=one: the whole chain in one persistent launch).  Bar:
+The path is selected with LATENT_MOE_PATH=stream for every call here, in each
+launch styles (LATENT_STREAM_LAUNCH=auto: the default, which takes the
+small-batch chain for at most 16 routed pairs; =phases: one launch per phase;
+=one: the whole chain in one persistent launch).  Bar:
 rel-L2 <= 2e-3 against the oracle's fp32 result on the same packed factors
 (fp16 operands, fp32 accumulation), bit-identical results on a repeated call.
 """
@@ -19,9 +20,10 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.fixture(params=["phases", "one"])
+@pytest.fixture(params=["auto", "phases", "one"])
 def stream_path(monkeypatch, request):
-    # Per-phase launches (the default) and the one-launch chain (flow_kernel).
+    # The default launch style (the small-batch chain up to 16 routed pairs,
+    # per-phase launches above), per-phase launches and the one-launch chain.
     monkeypatch.setenv("LATENT_MOE_PATH", "stream")
     monkeypatch.setenv("LATENT_STREAM_LAUNCH", request.param)
 
