@@ -40,18 +40,20 @@
 // Every activation a phase reads is an fp16 row with a power-of-two exponent
 // (row maximum in [2^14, 2^15)): the prep kernel writes x that way (one
 // exponent per token), the reduce kernels the latents (one per row) and
-// phase B h (one per row and 128-column block), so the small latents of a
-// LATENT chain keep fp16's full precision.
+// phase B h (one per row and 128-column block, in LDS), so the small latents
+// of a LATENT chain keep fp16's full precision.
 //
-// Work split: each phase is one persistent launch of two workgroups per CU;
-// workgroup b takes the contiguous tile range [b*chunk, (b+1)*chunk) of the
-// phase's tile list (unit-major), so every workgroup streams the same number
+// Work split: phase A, phases B and C together (bc_kernel: h never leaves
+// LDS) and phase D are each one persistent launch of two workgroups per CU;
+// workgroup b takes the contiguous range [b*chunk, (b+1)*chunk) of the
+// launch's work list (unit-major), so every workgroup streams the same number
 // of tiles.  Tile i + 2's loads are issued while tile i is computed: its codes
 // into registers, its scales, activations and exponents into registers that
 // are stored to LDS at the end of tile i + 1.  All are ordinary buffer loads,
-// so the compiler places every wait.  K-tiled phases (A, C) accumulate
-// consecutive tiles of one (unit, factor) in registers and write one partial
-// sum per segment; the reduce kernels add a row's partials in workgroup order.
+// so the compiler places every wait.  Phase A accumulates consecutive tiles
+// of one (unit, factor) in registers and writes one partial sum per segment;
+// phase C writes one per item; the reduce kernels add a row's partials in
+// workgroup (item) order.
 //
 // Arithmetic: fp16 operands (levels and scales exact in fp16 up to one
 // rounding of level * scale and of the scaled activation), fp32 accumulation.
@@ -108,8 +110,8 @@ struct Params {
   float* partA;        // [slots][16][256]
   _Float16* lat;       // [2][P][256]
   int* lexp;           // [2][P]
-  _Float16* hh;        // [P][ff]
-  int* hexp;           // [P][ff/128]
+  _Float16* hh;        // bulk launches: [P][ff] h * 2^hexp
+  int* hexp;           // bulk launches: [P][ff/32]
   float* partC;        // [slots][16][256]
   _Float16* dlat;      // [P][256]
   int* dexp;           // [P]
@@ -201,13 +203,13 @@ __device__ __forceinline__ int tiles_per_key(const Params& p) {
   return kPhase == kPhaseA ? p.nka : kPhase == kPhaseC ? p.nkc : 1;
 }
 
+// LDS of the per-phase item kernel (phases A and D: one activation block).
 template <int kPhase>
 struct alignas(16) Smem {
   uint32_t lut[256 * kLutCopies];                              // [byte][copy]: half2(level(lo), level(hi))
   u32x4 scales[2][kScaleBytes / 16];                           // [buffer]: the tile's scale block
   u32x4 act[2][Shape<kPhase>::kActBlocks][kMaxM * kActChunks];  // [buffer][block][row][chunk ^ row]
-  int rexp[2][32];                                             // row exponents of act[buffer]
-  float hmax[4][kMaxM];                                        // phase B: row maxima of h per wave
+  int rexp[2][Shape<kPhase>::kExps];                           // row exponents of act[buffer]
 };
 
 // Registers a tile's non-code loads land in before they are stored to LDS.
@@ -216,14 +218,6 @@ struct StageAct {
   u32x4 act[Shape<kPhase>::kActLoads];
   int ex;
 };
-
-// Phase B issues a tile's activation loads one step later than its codes
-// (from the latents in L2, into one staging slot), which keeps its registers
-// within two waves per SIMD; the others issue them with the codes.
-template <int kPhase>
-constexpr bool late_act() {
-  return kPhase == kPhaseB;
-}
 
 // Phase A's per-lane token rows of a tile: the rows of the thread's two
 // activation chunks and of exponent row lane & 15.
@@ -290,35 +284,18 @@ __device__ __forceinline__ void issue_codes(const Params& p, const TileRef& tr, 
 template <int kPhase>
 __device__ __forceinline__ void issue_act(const Params& p, const TileRef& tr, const Toks& tk, int tid, int lane,
                                           bool valid, StageAct<kPhase>& st) {
+  static_assert(kPhase == kPhaseA || kPhase == kPhaseD, "phases B and C run in bc_kernel");
   const uint32_t live = valid ? 0xFFFFFFFFu : 0u;  // masks every buffer range
-  int ks = 0;
-  if constexpr (kPhase == kPhaseA) ks = tr.r >= p.nka ? tr.r - p.nka : tr.r;
-  if constexpr (kPhase == kPhaseC) ks = tr.r;
   auto pair_of = [&](int r) { return tr.start + min(r, tr.m - 1); };
   const int r0 = tid / kActChunks, chunk = tid % kActChunks;
   if constexpr (kPhase == kPhaseA) {
+    const int ks = tr.r >= p.nka ? tr.r - p.nka : tr.r;
     const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.xh, (static_cast<uint32_t>(p.T) * p.d * 2) & live);
     const uint32_t col = ks * kK * 2 + chunk * 16;
     st.act[0] = ld128(rx, static_cast<uint32_t>(tk.a0) * p.d * 2 + col, 0);
     st.act[1] = ld128(rx, static_cast<uint32_t>(tk.a1) * p.d * 2 + col, 0);
     const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.xexp, (p.T * 4) & live);
     st.ex = static_cast<int>(ld32(re, tk.e * 4));
-  } else if constexpr (kPhase == kPhaseB) {
-    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.lat, (2u * p.P * kK * 2) & live);
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int row = (r0 + 8 * h) % kMaxM, f = h / 2;
-      st.act[h] = ld128(rl, (static_cast<uint32_t>(f) * p.P + pair_of(row)) * kK * 2 + chunk * 16, 0);
-    }
-    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.lexp, (2u * p.P * 4) & live);
-    st.ex = static_cast<int>(ld32(re, (((lane >> 4) & 1) * p.P + pair_of(lane & 15)) * 4));
-  } else if constexpr (kPhase == kPhaseC) {
-    const __amdgpu_buffer_rsrc_t rh = buffer_rsrc(p.hh, (static_cast<uint32_t>(p.P) * p.ff * 2) & live);
-    const uint32_t col = ks * kK * 2 + chunk * 16;
-    st.act[0] = ld128(rh, static_cast<uint32_t>(pair_of(r0)) * p.ff * 2 + col, 0);
-    st.act[1] = ld128(rh, static_cast<uint32_t>(pair_of(r0 + 8)) * p.ff * 2 + col, 0);
-    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.hexp, (static_cast<uint32_t>(p.P) * p.nb * 4) & live);
-    st.ex = static_cast<int>(ld32(re, (pair_of(lane & 15) * p.nb + 2 * ks + ((lane >> 4) & 1)) * 4));
   } else {
     const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.dlat, (static_cast<uint32_t>(p.P) * kK * 2) & live);
     st.act[0] = ld128(rl, static_cast<uint32_t>(pair_of(r0)) * kK * 2 + chunk * 16, 0);
@@ -352,23 +329,11 @@ __device__ __forceinline__ void mfma_steps(const Smem<kPhase>& sm, int buf, cons
     const int chunk = s * 4 + kq;
     const half8 a0 = __builtin_bit_cast(half8, sm.act[buf][0][act_slot(n, chunk)]);
     const int P0 = s * 16 + kq * 4;
-    u32x4 sc0, sc1;
-    half8 a1;
-    if constexpr (kPhase == kPhaseB) {
-      a1 = __builtin_bit_cast(half8, sm.act[buf][1][act_slot(n, chunk)]);
-      const int Gg = wave, Gu = 4 + wave;
-      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
-      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
-    } else {
-      const int G = 2 * wave + (n >> 3);
-      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
-      sc1 = sc0;
-      a1 = a0;
-    }
+    const int G = 2 * wave + (n >> 3);
+    const u32x4 sc = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t x = cb[s][j];
-      const u32x4 sc = j < 2 ? sc0 : sc1;
       uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -377,8 +342,7 @@ __device__ __forceinline__ void mfma_steps(const Smem<kPhase>& sm, int buf, cons
         const uint32_t sq = sc[q];
         f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
       }
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1,
-                                                      __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3])),
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3])),
                                                       acc[j], 0, 0, 0);
     }
   }
@@ -391,7 +355,7 @@ __device__ __forceinline__ int part_slot(int b, int key, int chunk, int per_key,
 
 template <int kPhase>
 __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
-  using S = Shape<kPhase>;
+  static_assert(kPhase == kPhaseA || kPhase == kPhaseD, "phases B and C run in bc_kernel");
   __shared__ Smem<kPhase> sm;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = uniform(tid >> 6);
@@ -429,10 +393,9 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
     }
   };
 
-  constexpr bool kLate = late_act<kPhase>();
   u32x4 cb[3][kSteps];
   u32x4 sc[3];
-  StageAct<kPhase> sa[kLate ? 1 : 3];
+  StageAct<kPhase> sa[3];
   Toks tk[3] = {};
   TileRef ref[3];
   float4v acc[4];
@@ -448,7 +411,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
   ref[1] = tile_ref<kPhase>(p, min(lo + 1, hi - 1));
   issue_act<kPhase>(p, ref[0], tk[0], tid, lane, true, sa[0]);
   issue_codes<kPhase>(p, ref[0], tid, lane, wave, true, sc[0], cb[0]);
-  if constexpr (!kLate) issue_act<kPhase>(p, ref[1], tk[1], tid, lane, ntile > 1, sa[1]);
+  issue_act<kPhase>(p, ref[1], tk[1], tid, lane, ntile > 1, sa[1]);
   issue_codes<kPhase>(p, ref[1], tid, lane, wave, ntile > 1, sc[1], cb[1]);
   store_stage<kPhase>(sm, 0, sc[0], sa[0], tid, lane, wave);
 
@@ -457,48 +420,25 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
     constexpr int c = decltype(cs)::value, c1 = (c + 1) % 3, c2 = (c + 2) % 3;
     const int buf = i & 1;
     lds_barrier();  // LDS buffer `buf` holds tile i; every wave is done with tile i - 1
-    // Loads of tile i + 2 (and, late, tile i + 1's activations first: loads
-    // complete in order, so the wait for them at the end of this step leaves
-    // tile i + 2's in flight).
-    if constexpr (kLate) issue_act<kPhase>(p, ref[c1], tk[c1], tid, lane, i + 1 < ntile, sa[0]);
+    // Loads of tile i + 2.
     load_toks(lo + i + 3, i + 3 < ntile, tk[c]);
     ref[c2] = tile_ref<kPhase>(p, min(lo + i + 2, hi - 1));
-    if constexpr (!kLate) issue_act<kPhase>(p, ref[c2], tk[c2], tid, lane, i + 2 < ntile, sa[c2]);
+    issue_act<kPhase>(p, ref[c2], tk[c2], tid, lane, i + 2 < ntile, sa[c2]);
     issue_codes<kPhase>(p, ref[c2], tid, lane, wave, i + 2 < ntile, sc[c2], cb[c2]);
     const TileRef& tr = ref[c];
-    if constexpr (kPhase == kPhaseC) {
-      // Two exponent blocks per tile (rows 0..127 and 128..255 of h's
-      // columns): each half's products are scaled back before they join the
-      // running sum, which holds true values.
-      float4v part[4];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) part[j] = float4v{0.f, 0.f, 0.f, 0.f};
-        mfma_steps<kPhase>(sm, buf, cb[c], half * kSteps / 2, (half + 1) * kSteps / 2, n, kq, wave, lut_lane, part);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float sc = ldexpf(1.0f, -sm.rexp[buf][half * 16 + kq * 4 + v]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[j][v] = fmaf(part[j][v], sc, acc[j][v]);
-        }
-      }
-    } else {
-      mfma_steps<kPhase>(sm, buf, cb[c], 0, kSteps, n, kq, wave, lut_lane, acc);
-    }
+    mfma_steps<kPhase>(sm, buf, cb[c], 0, kSteps, n, kq, wave, lut_lane, acc);
     const int t = lo + i;
-    if constexpr (S::kSliceK) {
+    if constexpr (kPhase == kPhaseA) {
       // End of a segment (last tile of the range or of this key): one partial.
       if (i + 1 == ntile || (t + 1) % per_key == 0) {
         const int key = t / per_key;
-        float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
-                      static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kMaxM * kN;
+        float* part = p.partA + static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kMaxM * kN;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int row = kq * 4 + v;
           if (row < tr.m) {
-            // A: x's one exponent per token is the same in every tile.
-            const float sc = kPhase == kPhaseA ? ldexpf(1.0f, -sm.rexp[buf][row]) : 1.0f;
+            // x's one exponent per token is the same in every tile.
+            const float sc = ldexpf(1.0f, -sm.rexp[buf][row]);
             *reinterpret_cast<float4*>(part + row * kN + wave * 64 + n * 4) =
                 make_float4(acc[0][v] * sc, acc[1][v] * sc, acc[2][v] * sc, acc[3][v] * sc);
           }
@@ -506,40 +446,6 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
       }
-    } else if constexpr (kPhase == kPhaseB) {
-      // h = SiLU(g) * u of columns 32w + 2n + jj of the tile's 128, fp16 with
-      // one exponent per row over the 128 columns (maximum across the waves).
-      float hv[2][4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        const float sg = ldexpf(1.0f, -sm.rexp[buf][row]), su = ldexpf(1.0f, -sm.rexp[buf][16 + row]);
-        float mx = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          hv[jj][v] = silu(acc[jj][v] * sg) * (acc[jj + 2][v] * su);
-          mx = fmaxf(mx, fabsf(hv[jj][v]));
-        }
-        mx = op_over(mx, 1, 16, OpMax{});
-        if (n == 0) sm.hmax[wave][row] = mx;
-      }
-      lds_barrier();
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        if (row < tr.m) {
-          const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
-          const int ex = pow2_row_exponent(mx);
-          half2v hb;
-          hb[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
-          hb[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
-          const int64_t prow = tr.start + row;
-          *reinterpret_cast<half2v*>(p.hh + prow * p.ff + tr.r * kHBlock + wave * 32 + n * 2) = hb;
-          if (wave == 0 && n == 0) p.hexp[prow * p.nb + tr.r] = ex;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
     } else {
       // D: the y rows of the tile's 256 columns, by grouped pair.
 #pragma unroll
@@ -556,7 +462,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
     }
     // Tile i + 1's scales and activations into the other LDS buffer (last
     // read by tile i - 1, which every wave finished before this step's barrier).
-    store_stage<kPhase>(sm, buf ^ 1, sc[c1], sa[kLate ? 0 : c1], tid, lane, wave);
+    store_stage<kPhase>(sm, buf ^ 1, sc[c1], sa[c1], tid, lane, wave);
   };
   // Whole triples without branches between the steps, then the last one or two.
   int i = 0;
@@ -567,6 +473,212 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
   }
   if (i < ntile) step(i, std::integral_constant<int, 0>{});
   if (i + 1 < ntile) step(i + 1, std::integral_constant<int, 1>{});
+}
+
+// ---------------------------------------------------------------------------
+// Phases B and C in one launch (bc_kernel)
+// ---------------------------------------------------------------------------
+// Item (unit, j), j < ff / 256: B tiles 2j and 2j + 1 (h for ff columns
+// 256 j .. 256 j + 255, two 128-column blocks with one exponent per row each,
+// kept in LDS) and C tile j (those h columns times A_d's rows 256 j ..).  A
+// workgroup's range is whole items, so its tile sequence is B, B, C, B, B, C,
+// ...: tile i sits in register slot i % 3 and its kind is i % 3 (0, 1: the
+// item's B tiles, 2: its C tile).  The gate / up latents of an item's unit are
+// staged during the previous item's C tile.  Every C tile writes its own
+// partial d latent (slot = item), which reduce_kernel<kPhaseC, .., true> sums
+// in item order.
+struct alignas(16) BcSmem {
+  uint32_t lut[256 * kLutCopies];      // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[2][kScaleBytes / 16];   // [buffer]: the tile's scale block
+  u32x4 act[2][kMaxM * kActChunks];    // gate / up latents of the current item's unit
+  u32x4 hb[2][kMaxM * kActChunks];     // h of the item's two 128-column blocks (16 chunks a row)
+  int lexp[2][kMaxM];                  // latent exponents
+  int hexp[2][kMaxM];                  // h exponents per block
+  float hmax[4][kMaxM];                // per-wave row maxima of h
+};
+
+// MFMA steps [s0, s0 + ns) of a register tile: activation chunk 4 (s - s0) + kq
+// of act0 (and act1 for the up columns of a B tile), scale rows of step s.
+template <bool kTwo, int s0, int ns>
+__device__ __forceinline__ void bc_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
+                                        const u32x4 (&cb)[kSteps], int n, int kq, int wave, uint32_t lut_lane,
+                                        float4v (&acc)[4]) {
+#pragma unroll
+  for (int r = 0; r < ns; ++r) {
+    const int s = s0 + r;
+    const int chunk = r * 4 + kq;
+    const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
+    const int P0 = s * 16 + kq * 4;
+    u32x4 sc0, sc1;
+    half8 a1;
+    if constexpr (kTwo) {
+      a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
+      const int Gg = wave, Gu = 4 + wave;
+      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
+      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+    } else {
+      const int G = 2 * wave + (n >> 3);
+      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc1 = sc0;
+      a1 = a0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x = cb[s][j];
+      const u32x4 sc = j < 2 ? sc0 : sc1;
+      uint32_t f[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        const uint32_t sq = sc[q];  // through a scalar: a bit_cast of a vector element reads element 0
+        f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
+      }
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1,
+                                                      __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3])),
+                                                      acc[j], 0, 0, 0);
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
+  __shared__ BcSmem sm;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = uniform(tid >> 6);
+  const int n = lane & 15, kq = lane >> 4;
+  const int U = uniform(sload(p.meta + 4));
+  const int total = U * p.nkc;
+  const int b = blockIdx.x;
+  const int chunk = (total + p.G - 1) / p.G;
+  const int lo = b * chunk, hi = min(total, lo + chunk);
+  if (lo >= hi) return;
+  const int ntile = 3 * (hi - lo);
+  {
+    const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
+    const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
+    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
+#pragma unroll
+    for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+  }
+  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
+  const int r0 = tid / kActChunks, ch = tid % kActChunks;
+
+  // Codes and scales of tile t of the range (loads past the range fetch nothing).
+  auto issue_codes = [&](int t, u32x4& sc, u32x4 (&cb)[kSteps]) __attribute__((always_inline)) {
+    const int tt = min(t, ntile - 1);
+    const int it = lo + tt / 3, kind = tt % 3;
+    const int u = it / p.nkc, j = it - u * p.nkc;
+    const int e = uniform(sload4(p.unit_info + u)[0]);
+    const uint8_t* tile = kind < 2 ? p.tiles[T_GU_B] + static_cast<int64_t>(e * p.nb + 2 * j + kind) * kTileBytes
+                                   : p.tiles[T_DOWN_A] + static_cast<int64_t>(e * p.nkc + j) * kTileBytes;
+    const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, t < ntile ? kTileBytes : 0);
+    sc = ld128(rt, tid * 16, kCodeBytes);
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) cb[s] = ld128(rt, cbase, s * kWave * 16);
+  };
+  // Gate / up latent rows (rows past the unit's pairs repeat its last pair)
+  // and exponents of item it's unit.
+  u32x4 st[4];
+  int stex = 0;
+  auto issue_lat = [&](int it, bool valid) __attribute__((always_inline)) {
+    const int u = min(it, hi - 1) / p.nkc;
+    const i32x4 info = sload4(p.unit_info + u);
+    const int start = uniform(info[1]), m = uniform(info[2]);
+    const uint32_t live = valid ? 0xFFFFFFFFu : 0u;
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.lat, (2u * p.P * kK * 2) & live);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int row = (r0 + 8 * h) % kMaxM, f = h / 2;
+      st[h] = ld128(rl, (static_cast<uint32_t>(f) * p.P + start + min(row, m - 1)) * kK * 2 + ch * 16, 0);
+    }
+    const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.lexp, (2u * p.P * 4) & live);
+    stex = static_cast<int>(ld32(re, (((lane >> 4) & 1) * p.P + start + min(lane & 15, m - 1)) * 4));
+  };
+  auto store_lat = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) sm.act[h / 2][act_slot((r0 + 8 * h) % kMaxM, ch)] = st[h];
+    if (wave == 0 && lane < 32) sm.lexp[lane >> 4][lane & 15] = stex;
+  };
+
+  u32x4 cb[3][kSteps], sc[3];
+  issue_lat(lo, true);
+  issue_codes(0, sc[0], cb[0]);
+  issue_codes(1, sc[1], cb[1]);
+  sm.scales[0][tid] = sc[0];
+  store_lat();
+
+  auto step = [&](int i, auto cs) __attribute__((always_inline)) {
+    constexpr int c = decltype(cs)::value, c1 = (c + 1) % 3, c2 = (c + 2) % 3;
+    const int buf = i & 1;
+    const int it = lo + i / 3;
+    const int m = uniform(sload4(p.unit_info + it / p.nkc)[2]);
+    lds_barrier();  // LDS buffer `buf` holds tile i; every wave is done with tile i - 1
+    // C tile: the next item's latents first (loads complete in order, so the
+    // wait for them at the end of this step leaves tile i + 2's in flight).
+    if constexpr (c == 2) issue_lat(it + 1, i + 1 < ntile);
+    issue_codes(i + 2, sc[c2], cb[c2]);
+    const uint32_t sbase = lds_addr(sm.scales[buf][0]);
+    if constexpr (c < 2) {
+      float4v accB[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) accB[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      bc_mfma<true, 0, kSteps>(sm.act[0], sm.act[1], sbase, cb[c], n, kq, wave, lut_lane, accB);
+      // h = SiLU(g) * u of columns 32w + 2n + jj of block c, fp16 with one exponent per row.
+      float hv[2][4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float sg = ldexpf(1.0f, -sm.lexp[0][row]), su = ldexpf(1.0f, -sm.lexp[1][row]);
+        float mx = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          hv[jj][v] = silu(accB[jj][v] * sg) * (accB[jj + 2][v] * su);
+          mx = fmaxf(mx, fabsf(hv[jj][v]));
+        }
+        mx = op_over(mx, 1, 16, OpMax{});
+        if (n == 0) sm.hmax[wave][row] = mx;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
+        const int ex = pow2_row_exponent(mx);
+        half2v h2;
+        h2[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
+        h2[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
+        reinterpret_cast<half2v*>(&sm.hb[c][act_slot(row, 4 * wave + (n >> 2))])[n & 3] = h2;
+        if (wave == 0 && n == 0) sm.hexp[c][row] = ex;
+      }
+    } else {
+      // K rows 0..127 of the C tile take h block 0, rows 128..255 block 1;
+      // each half's products are scaled back before they join the sum.
+      float4v accC[4], part[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) accC[j] = part[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      bc_mfma<false, 0, kSteps / 2>(sm.hb[0], sm.hb[0], sbase, cb[c], n, kq, wave, lut_lane, accC);
+      bc_mfma<false, kSteps / 2, kSteps / 2>(sm.hb[1], sm.hb[1], sbase, cb[c], n, kq, wave, lut_lane, part);
+      float* dst = p.partC + static_cast<int64_t>(it) * kMaxM * kN;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = kq * 4 + v;
+        const float s0 = ldexpf(1.0f, -sm.hexp[0][row]), s1 = ldexpf(1.0f, -sm.hexp[1][row]);
+        if (row < m)
+          *reinterpret_cast<float4*>(dst + row * kN + wave * 64 + n * 4) =
+              make_float4(fmaf(part[0][v], s1, accC[0][v] * s0), fmaf(part[1][v], s1, accC[1][v] * s0),
+                          fmaf(part[2][v], s1, accC[2][v] * s0), fmaf(part[3][v], s1, accC[3][v] * s0));
+      }
+      // The next item's latents (the B tiles that read the old ones are done).
+      store_lat();
+    }
+    // Tile i + 1's scales into the other buffer (last read by tile i - 1).
+    sm.scales[buf ^ 1][tid] = sc[c1];
+  };
+  for (int i = 0; i < ntile; i += 3) {
+    step(i, std::integral_constant<int, 0>{});
+    step(i + 1, std::integral_constant<int, 1>{});
+    step(i + 2, std::integral_constant<int, 2>{});
+  }
 }
 
 // A row of 256 sums -> fp16 row * 2^e and e (one wave, 4 columns per lane).
@@ -585,7 +697,9 @@ __device__ __forceinline__ void finish_row(float4 s, _Float16* dst, int* dexp, i
 // lat (phase A) / dlat (phase C) rows: the partial sums of each (unit,
 // factor, row) added in workgroup order.  One wave per (key, row); units of
 // at most kRows pairs (partial blocks of kRows rows).
-template <int kPhase, int kRows>
+// kPerItem: phase C's partials are one per item (slot u * nkc + j, bc_kernel),
+// summed in item order.
+template <int kPhase, int kRows, bool kPerItem = false>
 __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
@@ -602,16 +716,17 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
     const int u = key / keys_per_unit, f = key - u * keys_per_unit;
     const int4 info = p.unit_info[u];
     if (row >= info.z) continue;
-    const int b0 = (key * per_key) / chunk, b1 = (key * per_key + per_key - 1) / chunk;
-    // Batches of kRedLoads partials in flight, summed in workgroup order.
+    const int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
+    const int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
+    // Batches of kRedLoads partials in flight, summed in workgroup (item) order.
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int bb = b0; bb <= b1; bb += kRedLoads) {
       float4 v[kRedLoads];
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
         const int b = min(bb + q, b1);
-        v[q] = reinterpret_cast<const float4*>(
-            part + (static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kRows + row) * kN)[lane];
+        const int64_t slot = kPerItem ? b : part_slot(b, key, chunk, per_key, maxj);
+        v[q] = reinterpret_cast<const float4*>(part + (slot * kRows + row) * kN)[lane];
       }
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
@@ -2673,11 +2788,12 @@ Layout layout_for(const latent_moe_args& a) {
   const int64_t T = a.n_tokens, P = a.n_tokens * a.n_expert_used, d = a.n_embd, ff = a.n_ff;
   const int64_t U = max_units(P, a.n_expert);
   const int G = grid_size();
-  const int nka = static_cast<int>(d / kK), nkc = static_cast<int>(ff / kK);
-  // Partial blocks: per-phase launches (slots per workgroup range) or the
-  // one-launch chain (A: maxj slots per workgroup; C: one per BC item, nb per unit).
+  const int nka = static_cast<int>(d / kK);
+  // Partial blocks: A per workgroup range (per-phase launches) or maxj per
+  // workgroup (one-launch chain); C one per item (bc_kernel: nkc per unit) or
+  // per BC item of the one-launch chain (nb per unit).
   const int64_t blocksA = std::max<int64_t>(part_slots(U, 2 * nka, nka, G), static_cast<int64_t>(G) * flow_maxj(U, nka, G));
-  const int64_t blocksC = std::max<int64_t>(part_slots(U, nkc, nkc, G), U * (ff / kHBlock));
+  const int64_t blocksC = U * (ff / kHBlock);
   Layout L{};
   size_t off = 0;
   L.xh = off;     off = al(off + static_cast<size_t>(T) * d * 2);
@@ -2685,8 +2801,6 @@ Layout layout_for(const latent_moe_args& a) {
   L.partA = off;  off = al(off + static_cast<size_t>(blocksA) * kMaxM * kN * 4);
   L.lath = off;   off = al(off + 2ull * P * kK * 2);
   L.lexp = off;   off = al(off + 2ull * P * 4);
-  L.hh = off;     off = al(off + static_cast<size_t>(P) * ff * 2);
-  L.hexp = off;   off = al(off + static_cast<size_t>(P) * (ff / kHBlock) * 4);
   L.partC = off;  off = al(off + static_cast<size_t>(blocksC) * kMaxM * kN * 4);
   L.dlath = off;  off = al(off + static_cast<size_t>(P) * kK * 2);
   L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
@@ -2717,8 +2831,6 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   p.partA = reinterpret_cast<float*>(scratch + L.partA);
   p.lat = reinterpret_cast<_Float16*>(scratch + L.lath);
   p.lexp = reinterpret_cast<int*>(scratch + L.lexp);
-  p.hh = reinterpret_cast<_Float16*>(scratch + L.hh);
-  p.hexp = reinterpret_cast<int*>(scratch + L.hexp);
   p.partC = reinterpret_cast<float*>(scratch + L.partC);
   p.dlat = reinterpret_cast<_Float16*>(scratch + L.dlath);
   p.dexp = reinterpret_cast<int*>(scratch + L.dexp);
@@ -2759,10 +2871,9 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nka)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL((reduce_kernel<kPhaseA, kMaxM>), dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),
                      dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseB>, dim3(item_grid(p.nb)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(item_kernel<kPhaseC>, dim3(item_grid(p.nkc)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kMaxM>), dim3(blocks((U * kMaxM + rows_per_block - 1) / rows_per_block)), dim3(kT),
-                     0, s, p);
+  hipLaunchKernelGGL(bc_kernel, dim3(item_grid(p.nkc)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kMaxM, true>), dim3(blocks((U * kMaxM + rows_per_block - 1) / rows_per_block)),
+                     dim3(kT), 0, s, p);
   hipLaunchKernelGGL(item_kernel<kPhaseD>, dim3(item_grid(p.nd)), dim3(kT), 0, s, p);
   const int64_t out4 = (a.out_mode == LATENT_OUT_REDUCED ? p.T : static_cast<int64_t>(p.P)) * p.d / 4;
   hipLaunchKernelGGL(combine_kernel, dim3(blocks((out4 + kT - 1) / kT)), dim3(kT), 0, s, p);

@@ -26,7 +26,7 @@ struct Grouping {
 // routed slot) are written by the prep kernel, which also clears cnt (the
 // one-launch chain's counters, cnt_ints of them).
 struct Layout {
-  size_t xh, xexp, partA, lath, lexp, hh, hexp, partC, dlath, dexp, ybuf, pos_of, cnt, total;
+  size_t xh, xexp, partA, lath, lexp, partC, dlath, dexp, ybuf, pos_of, cnt, total;
   int64_t cnt_ints;
 };
 
