@@ -1513,7 +1513,7 @@ constexpr int kLiteUnitStride = 32;  // ints between per-unit counters (128 B)
 constexpr int kLiteKeyStride = 16;   // ints between (token, tile) counters (64 B)
 // B, C and D tiles are needed only after A's results: their workgroups issue
 // their loads this long after grouping, so A's tiles come first from HBM.
-constexpr int64_t kLiteLateTicks = 150;  // 1.5 us of s_memrealtime (100 MHz)
+constexpr int64_t kLiteLateTicks = 300;  // 3 us of s_memrealtime (100 MHz)
 
 struct LiteParams {
   const uint8_t* tiles[kTileArrays];
@@ -1558,10 +1558,10 @@ __host__ __device__ inline bool lite_fits(int U, int nka, int nb, int nd, int G)
 
 struct alignas(16) LiteSmem {
   uint32_t lut[256 * kLutCopies];       // [byte][copy]: half2(level(lo), level(hi))
-  u32x4 scales[kScaleBytes / 16];       // the current tile's scale block
+  u32x4 scales[2][kScaleBytes / 16];    // scale blocks of the one or two tiles being computed
   u32x4 act[2][kMaxM * kActChunks];     // A: x rows; BC: gate / up latents; D: down latent (block 0)
   u32x4 hb[kMaxM * kActChunks];         // BC: h rows (128 columns)
-  float4 red[4][4][kWave];              // latent sums: [row of 4][wave][lane]
+  float4 red[2][4][kWave];              // latent sums: [row of 2][wave][lane]
   int rexp[2][kMaxM];                   // exponents of act's rows
   int hexp[kMaxM];                      // h exponents
   float hmax[4][kMaxM];                 // per-wave row maxima of h
@@ -1687,8 +1687,8 @@ __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, in
   constexpr int kChains = 4 / kKeys;
   const int key = wave / kChains, chain = wave % kChains;
   const int nk = (nblocks - chain + kChains - 1) / kChains;
-  for (int r0 = 0; r0 < m; r0 += 4) {
-    const int rows = min(4, m - r0);
+  for (int r0 = 0; r0 < m; r0 += 2) {
+    const int rows = min(2, m - r0);
     for (int rr = 0; rr < rows; ++rr) {
       const uint32_t roff = static_cast<uint32_t>(start + r0 + rr) * (kN * 4) + lane * 16;
       float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1716,6 +1716,42 @@ __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, in
   }
 }
 
+// Two register tiles' MFMA steps interleaved (two independent chains per
+// wave): accA += actA . tile A, accB += actB . tile B (non-interleaved
+// columns: phases A and D).
+__device__ __forceinline__ void lite_mfma2(const u32x4* actA, const u32x4* actB, uint32_t sbaseA, uint32_t sbaseB,
+                                           const u32x4 (&cbA)[kSteps], const u32x4 (&cbB)[kSteps], int n, int kq,
+                                           int wave, uint32_t lut_lane, float4v (&accA)[4], float4v (&accB)[4]) {
+  const int G = 2 * wave + (n >> 3);
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int chunk = s * 4 + kq;
+    const int sd = (G * 128 + ((s * 16 + kq * 4) ^ ((G & 1) << 3))) * 4;
+    const half8 a[2] = {__builtin_bit_cast(half8, actA[act_slot(n, chunk)]),
+                        __builtin_bit_cast(half8, actB[act_slot(n, chunk)])};
+    const u32x4 sc[2] = {lds_ld<u32x4>(sbaseA + sd), lds_ld<u32x4>(sbaseB + sd)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const uint32_t x = tt ? cbB[s][j] : cbA[s][j];
+        uint32_t f[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+          const uint32_t sq = sc[tt][q];  // through a scalar: a bit_cast of a vector element reads element 0
+          f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
+        }
+        const half8 b = __builtin_bit_cast(half8, make_uint4(f[0], f[1], f[2], f[3]));
+        if (tt)
+          accB[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], b, accB[j], 0, 0, 0);
+        else
+          accA[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], b, accA[j], 0, 0, 0);
+      }
+    }
+  }
+}
+
 // Role A: K tiles [j0, j0 + nj) of the list (unit, gate/up, k).
 __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, int j0, int nj, int tid, int lane,
                                             int wave, uint32_t lut_lane) {
@@ -1724,8 +1760,23 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
   const int per = 2 * p.nka;
   const uint32_t esz = p.x_dtype == LATENT_F32 ? 4u : 2u;
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.x, static_cast<uint32_t>(p.T) * p.d * esz);
-  u32x4 cb[kLiteSlots][kSteps], sc[kLiteSlots], xr[kLiteSlots][2][2];
-  // Every tile's scales, codes and x slices, tile by tile.
+  u32x4 cb[kLiteSlots][kSteps], sc[kLiteSlots], xr[2][2][2];
+  // x slices of tile j (rows r0, r0 + 8 of its unit; f32 x takes both dwords of a chunk pair).
+  auto load_x = [&](int j, bool valid, u32x4 (&xj)[2][2]) __attribute__((always_inline)) {
+    const int t = j0 + min(j, nj - 1);
+    const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
+    const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = r0 + 8 * h;
+      const bool live = valid && row < m;
+      const int tok = live ? sm.pos_pair[start + row] / p.K : 0;
+      const uint32_t off = (static_cast<uint32_t>(tok) * p.d + k * kK + chunk * 8) * esz;
+      xj[h][0] = ld128(rx, live ? off : 0x80000000u, 0);
+      xj[h][1] = ld128(rx, live && esz == 4 ? off + 16 : 0x80000000u, 0);
+    }
+  };
+  // Every tile's scales and codes, tile by tile, with the x slices of tiles 0 and 1.
 #pragma unroll
   for (int j = 0; j < kLiteSlots; ++j) {
     const bool valid = j < nj;
@@ -1734,59 +1785,68 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
     const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
     lite_codes<kSteps>(p.tiles[f ? T_UP_A : T_GATE_A] + static_cast<int64_t>(e * p.nka + k) * kTileBytes, valid, true,
                        0, tid, lane, wave, sc[j], cb[j]);
+    if (j < 2) load_x(j, valid, xr[j]);
+  }
+  // Tile j into LDS buffer `buf`: its scales, and its x rows as fp16 * 2^e
+  // with one exponent per row of this 256-column slice.
+  auto stage = [&](int j, int buf, const u32x4 (&xj)[2][2]) __attribute__((always_inline)) {
+    sm.scales[buf][tid] = sc[j];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int row = r0 + 8 * h;
-      const bool live = valid && row < m;
-      const int tok = live ? sm.pos_pair[start + row] / p.K : 0;
-      const uint32_t off = (static_cast<uint32_t>(tok) * p.d + k * kK + chunk * 8) * esz;
-      xr[j][h][0] = ld128(rx, live ? off : 0x80000000u, 0);
-      xr[j][h][1] = ld128(rx, live && esz == 4 ? off + 16 : 0x80000000u, 0);
+      float v[8];
+      lite_x8(xj[h][0], xj[h][1], p.x_dtype, v);
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+      mx = op_over(mx, 1, 32, OpMax{});
+      const int ex = pow2_row_exponent(mx);
+      half8 hv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(v[i], ex));
+      sm.act[buf][act_slot(row, chunk)] = __builtin_bit_cast(u32x4, hv);
+      if (chunk == 0) sm.rexp[buf][row] = ex;
     }
+  };
+  // Tile j's partial rows (the products of buffer buf's rows, scaled back).
+  auto store_part = [&](int j, int buf, float4v (&acc)[4]) __attribute__((always_inline)) {
+    const int t = j0 + j;
+    const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
+    const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = kq * 4 + v;
+      if (row < m) {
+        const float s = ldexpf(1.0f, -sm.rexp[buf][row]);
+        const uint32_t off = ((static_cast<uint32_t>(f * p.nka + k) * p.P + start + row) * kN + wave * 64 + n * 4) * 4;
+        st_coh4(p.partA, off, make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
+      }
+    }
+  };
+  float4v acc0[4], acc1[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc0[j] = acc1[j] = float4v{0.f, 0.f, 0.f, 0.f};
+  // Tiles 0 and 1 together (two independent MFMA chains per wave), then tile 2.
+  stage(0, 0, xr[0]);
+  if (nj > 1) stage(1, 1, xr[1]);
+  lds_barrier();
+  if (nj > 1) {
+    lite_mfma2(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq, wave,
+               lut_lane, acc0, acc1);
+    store_part(1, 1, acc1);
+  } else {
+    flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[0], 0, n, kq, wave, lut_lane, acc0);
   }
-  float4v acc[4];
+  store_part(0, 0, acc0);
+  if (nj > 2) {
+    lds_barrier();  // every wave is done with buffer 0
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < kLiteSlots; ++j) {
-    if (j < nj) {
-      const int t = j0 + j;
-      const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
-      const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
-      lds_barrier();  // every wave is done with the previous tile's LDS
-      sm.scales[tid] = sc[j];
-      // x rows -> fp16 * 2^e, one exponent per row of this 256-column slice.
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int row = r0 + 8 * h;
-        float v[8];
-        lite_x8(xr[j][h][0], xr[j][h][1], p.x_dtype, v);
-        float mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
-        mx = op_over(mx, 1, 32, OpMax{});
-        const int ex = pow2_row_exponent(mx);
-        half8 hv;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(v[i], ex));
-        sm.act[0][act_slot(row, chunk)] = __builtin_bit_cast(u32x4, hv);
-        if (chunk == 0) sm.rexp[0][row] = ex;
-      }
-      lds_barrier();
-      flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0]), cb[j], 0, n, kq, wave, lut_lane, acc);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        if (row < m) {
-          const float s = ldexpf(1.0f, -sm.rexp[0][row]);
-          const uint32_t off =
-              ((static_cast<uint32_t>(f * p.nka + k) * p.P + start + row) * kN + wave * 64 + n * 4) * 4;
-          st_coh4(p.partA, off, make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int j = 0; j < 4; ++j) acc0[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    load_x(2, true, xr[0]);  // only workgroups with three tiles get here
+    stage(2, 0, xr[0]);
+    lds_barrier();
+    flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[2], 0, n, kq, wave, lut_lane, acc0);
+    store_part(2, 0, acc0);
   }
   // Publish once every partial is stored.
   drain_barrier();
@@ -1809,12 +1869,13 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
                          ((tid & 31) >= 16) == (hh != 0), 4 * hh, tid, lane, wave, scC, cbC);
   lite_wait(p.err, p.cntA + u * kLiteUnitStride, 2 * p.nka);
   lite_latents<2>(sm, p.partA, p.P, p.nka, start, m, lane, wave);
-  sm.scales[tid] = scB;
+  sm.scales[0][tid] = scB;
+  sm.scales[1][tid] = scC;
   lds_barrier();
   float4v acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-  flow_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0]), cbB, 0, n, kq, wave, lut_lane, acc);
+  flow_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), cbB, 0, n, kq, wave, lut_lane, acc);
   // h = SiLU(g) * u of columns 32w + 2n + jj of the block, fp16 with one exponent per row.
   float hv[2][4];
 #pragma unroll
@@ -1830,8 +1891,7 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
     mx = op_over(mx, 1, 16, OpMax{});
     if (n == 0) sm.hmax[wave][row] = mx;
   }
-  lds_barrier();  // every wave is past B's products: the scale buffer is free
-  sm.scales[tid] = scC;
+  lds_barrier();
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int row = kq * 4 + v;
@@ -1846,7 +1906,7 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
   lds_barrier();
-  flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
+  flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[1][0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int row = kq * 4 + v;
@@ -1875,47 +1935,72 @@ __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, i
     lite_codes<kSteps>(p.tiles[T_DOWN_B] + static_cast<int64_t>(e * p.nd + s) * kTileBytes, j < nj, true, 0, tid,
                        lane, wave, sc[j], cb[j]);
   }
-  float4v acc[4];
+  // Wait for unit u's C partials and sum them into the down latent (act
+  // block 0); the workgroup holding D tile (u, 0) resets cntA[u] (every BC
+  // item of the unit is past its wait for it).
+  auto unit_latent = [&](int u, int s) __attribute__((always_inline)) {
+    lite_wait(p.err, p.cntC + u * kLiteUnitStride, p.nb);
+    if (s == 0 && tid == 0) __hip_atomic_store(p.cntA + u * kLiteUnitStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lite_latents<1>(sm, p.partC, p.P, p.nb, uniform(sm.ustart[u]), uniform(sm.um[u]), lane, wave);
+  };
+  // Tile j's y rows (the products of the down latent's rows, scaled back).
+  auto store_y = [&](int j, float4v (&acc)[4]) __attribute__((always_inline)) {
+    const int t = j0 + j;
+    const int u = t / p.nd, s = t - u * p.nd;
+    const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-  int cur = -1;
-#pragma unroll
-  for (int j = 0; j < kLiteSlots; ++j) {
-    if (j < nj) {
-      const int t = j0 + j;
-      const int u = t / p.nd, s = t - u * p.nd;
-      const int start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
-      if (u != cur) {
-        cur = u;
-        lite_wait(p.err, p.cntC + u * kLiteUnitStride, p.nb);
-        // Every BC item of the unit is past its wait for cntA[u].
-        if (s == 0 && tid == 0)
-          __hip_atomic_store(p.cntA + u * kLiteUnitStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        lite_latents<1>(sm, p.partC, p.P, p.nb, start, m, lane, wave);
-      }
-      lds_barrier();  // every wave is done with the previous tile's scales
-      sm.scales[tid] = sc[j];
-      lds_barrier();
-      flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0]), cb[j], 0, n, kq, wave, lut_lane, acc);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        if (row < m) {
-          const float sy = ldexpf(1.0f, -sm.rexp[0][row]);
-          const int pos = start + row, col = s * kN + wave * 64 + n * 4;
-          if constexpr (kOutMode == LATENT_OUT_PER_SLOT) {
-            const int i = sm.pos_pair[pos];
-            const float sw = p.wbd ? sy * sm.w[i] : sy;
-            *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(i) * p.d + col) =
-                make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw);
-          } else {
-            st_coh4(p.ybuf, (static_cast<uint32_t>(pos) * p.d + col) * 4,
-                    make_float4(acc[0][v] * sy, acc[1][v] * sy, acc[2][v] * sy, acc[3][v] * sy));
-          }
+    for (int v = 0; v < 4; ++v) {
+      const int row = kq * 4 + v;
+      if (row < m) {
+        const float sy = ldexpf(1.0f, -sm.rexp[0][row]);
+        const int pos = start + row, col = s * kN + wave * 64 + n * 4;
+        if constexpr (kOutMode == LATENT_OUT_PER_SLOT) {
+          const int i = sm.pos_pair[pos];
+          const float sw = p.wbd ? sy * sm.w[i] : sy;
+          *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(i) * p.d + col) =
+              make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw);
+        } else {
+          st_coh4(p.ybuf, (static_cast<uint32_t>(pos) * p.d + col) * 4,
+                  make_float4(acc[0][v] * sy, acc[1][v] * sy, acc[2][v] * sy, acc[3][v] * sy));
         }
       }
+    }
+  };
+  const int u0 = j0 / p.nd;
+  if (nj == 2 && (j0 + 1) / p.nd == u0) {
+    // Two tiles of one unit together (two independent MFMA chains per wave).
+    unit_latent(u0, j0 - u0 * p.nd);
+    float4v acc0[4], acc1[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc0[j] = acc1[j] = float4v{0.f, 0.f, 0.f, 0.f};
+    sm.scales[0][tid] = sc[0];
+    sm.scales[1][tid] = sc[1];
+    lds_barrier();
+    lite_mfma2(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq, wave,
+               lut_lane, acc0, acc1);
+    store_y(0, acc0);
+    store_y(1, acc1);
+  } else {
+    // One tile at a time, each after its unit's latent.
+    int cur = -1;
+#pragma unroll
+    for (int j = 0; j < kLiteSlots; ++j) {
+      if (j < nj) {
+        const int t = j0 + j;
+        const int u = t / p.nd;
+        lds_barrier();  // every wave is done with the previous tile's LDS
+        if (u != cur) {
+          cur = u;
+          unit_latent(u, t - u * p.nd);
+        }
+        sm.scales[0][tid] = sc[j];
+        lds_barrier();
+        float4v acc[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
+        flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[j], 0, n, kq, wave, lut_lane, acc);
+        store_y(j, acc);
+      }
     }
   }
   drain_barrier();
