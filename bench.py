@@ -118,6 +118,7 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
     return {
         "batch": batch,
         "path": latent.moe_path(layers[0], xs[0], K),
+        "launch": latent.moe.stream_launch(layers[0], xs[0], K),
         "ms_per_step": ms,
         "tokens_per_s": batch / (ms * 1e-3),
         "hbm_gbps": gbps,
@@ -480,8 +481,8 @@ def main():
             "traffic": measured_traffic(head["path"]) if args.batch == 64 else None,
             "traffic_source": "profiles/%s (rocprofv3 --pmc)" % TRAFFIC_PROFILE.get(head["path"], ("none",))[0],
             "kernel": {
-                "stream": "latent_moe_ffn_forward, streaming MFMA path: prep + 4 item kernels + 2 reductions + combine "
-                          "(8 launches per step; the step is the unit)",
+                "stream": "latent_moe_ffn_forward, streaming MFMA path: prep + 3 item kernels (A, B+C, D) + 2 "
+                          "reductions + combine (7 launches per step; the step is the unit)",
                 "fused": "fused_kernel (one launch per step)",
             }.get(head["path"], "latent_moe_ffn_forward (prep + 3 phase kernels per step)"),
             "bytes_per_launch": head["bytes_per_step"],
