@@ -161,6 +161,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 __device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+// Factor tile loads: non-temporal (nt), since a decode step streams each tile
+// once; the caches then favour the rows, latents and partial sums that are
+// read again (measured: batch 64 250 -> 242 us, batch 8 96 -> 92 us).
+constexpr int kTilePolicy = 2;  // cache-policy operand: nt
+__device__ __forceinline__ u32x4 ld128_tile(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kTilePolicy);
+}
 __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0);
 }
@@ -272,10 +279,10 @@ __device__ __forceinline__ void issue_codes(const Params& p, const TileRef& tr, 
                                             u32x4& sc, u32x4 (&cb)[kSteps]) {
   int ks;
   const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile_ptr<kPhase>(p, tr, ks), valid ? kTileBytes : 0);
-  sc = ld128(rt, tid * 16, kCodeBytes);
+  sc = ld128_tile(rt, tid * 16, kCodeBytes);
   const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) cb[s] = ld128(rt, cbase, s * kWave * 16);
+  for (int s = 0; s < kSteps; ++s) cb[s] = ld128_tile(rt, cbase, s * kWave * 16);
 }
 
 // A tile's activation chunks and row exponents.  Chunk tid + 256 h is 16-byte
@@ -572,9 +579,9 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
     const uint8_t* tile = kind < 2 ? p.tiles[T_GU_B] + static_cast<int64_t>(e * p.nb + 2 * j + kind) * kTileBytes
                                    : p.tiles[T_DOWN_A] + static_cast<int64_t>(e * p.nkc + j) * kTileBytes;
     const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, t < ntile ? kTileBytes : 0);
-    sc = ld128(rt, tid * 16, kCodeBytes);
+    sc = ld128_tile(rt, tid * 16, kCodeBytes);
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) cb[s] = ld128(rt, cbase, s * kWave * 16);
+    for (int s = 0; s < kSteps; ++s) cb[s] = ld128_tile(rt, cbase, s * kWave * 16);
   };
   // Gate / up latent rows (rows past the unit's pairs repeat its last pair)
   // and exponents of item it's unit.
@@ -945,13 +952,13 @@ __device__ __forceinline__ void flow_codes(const Params& p, const FTile& d, int 
   // Half h's scales: row pairs 64h .. 64h + 63, the dwords of the threads with
   // (tid % 32 >= 16) == h.
   const bool sc_on = !half || (((tid & 31) >= 16) == (h != 0));
-  sc = ld128(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
+  sc = ld128_tile(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
   const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
   const int s0 = half ? 4 * h : 0;
 #pragma unroll
-  for (int s = 0; s < kSteps / 2; ++s) cb[s] = ld128(rt, cbase, (s0 + s) * kWave * 16);
+  for (int s = 0; s < kSteps / 2; ++s) cb[s] = ld128_tile(rt, cbase, (s0 + s) * kWave * 16);
 #pragma unroll
-  for (int s = kSteps / 2; s < kSteps; ++s) cb[s] = ld128(rhi, cbase, s * kWave * 16);
+  for (int s = kSteps / 2; s < kSteps; ++s) cb[s] = ld128_tile(rhi, cbase, s * kWave * 16);
 }
 
 // Tokens of an A tile's rows (the thread's two activation chunks and
@@ -1667,10 +1674,10 @@ template <int ns>
 __device__ __forceinline__ void lite_codes(const uint8_t* tile, bool valid, bool sc_on, int s0, int tid, int lane,
                                            int wave, u32x4& sc, u32x4 (&cb)[kSteps]) {
   const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, valid ? kTileBytes : 0);
-  sc = ld128(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
+  sc = ld128_tile(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
   const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
 #pragma unroll
-  for (int s = 0; s < ns; ++s) cb[s] = ld128(rt, cbase, (s0 + s) * kWave * 16);
+  for (int s = 0; s < ns; ++s) cb[s] = ld128_tile(rt, cbase, (s0 + s) * kWave * 16);
 }
 
 
