@@ -189,6 +189,14 @@ __device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcp
 // Chunk c of activation row r sits at chunk (c ^ (r & 15)) of the row.
 __device__ __forceinline__ int act_slot(int row, int chunk) { return row * kActChunks + (chunk ^ (row & 15)); }
 
+// LDS byte offset of the lane's scale dwords of K step 0 in scale group G of a
+// tile's scale block; K step s adds 64 s.  (Row pair P of group G sits at
+// dword G * 128 + (P ^ 8 (G & 1)), the lane's first pair of step s is
+// P = 16 s + 4 kq, and the xor only touches bit 3, below 16 s.)
+__device__ __forceinline__ uint32_t scale_lane(int G, int kq) {
+  return static_cast<uint32_t>(G * 128 + ((kq * 4) ^ ((G & 1) << 3))) * 4;
+}
+
 // ---------------------------------------------------------------------------
 // Per-phase shape of the work
 // ---------------------------------------------------------------------------
@@ -335,9 +343,8 @@ __device__ __forceinline__ void mfma_steps(const Smem<kPhase>& sm, int buf, cons
   for (int s = s0; s < s1; ++s) {
     const int chunk = s * 4 + kq;
     const half8 a0 = __builtin_bit_cast(half8, sm.act[buf][0][act_slot(n, chunk)]);
-    const int P0 = s * 16 + kq * 4;
     const int G = 2 * wave + (n >> 3);
-    const u32x4 sc = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+    const u32x4 sc = lds_ld<u32x4>(sbase + scale_lane(G, kq) + s * 64);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t x = cb[s][j];
@@ -515,17 +522,17 @@ __device__ __forceinline__ void bc_mfma(const u32x4* act0, const u32x4* act1, ui
     const int s = s0 + r;
     const int chunk = r * 4 + kq;
     const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
-    const int P0 = s * 16 + kq * 4;
+    const int S0 = s;  // K step (scale rows)
     u32x4 sc0, sc1;
     half8 a1;
     if constexpr (kTwo) {
       a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
       const int Gg = wave, Gu = 4 + wave;
-      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
-      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+      sc0 = lds_ld<u32x4>(sbase + scale_lane(Gg, kq) + S0 * 64);
+      sc1 = lds_ld<u32x4>(sbase + scale_lane(Gu, kq) + S0 * 64);
     } else {
       const int G = 2 * wave + (n >> 3);
-      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc0 = lds_ld<u32x4>(sbase + scale_lane(G, kq) + S0 * 64);
       sc1 = sc0;
       a1 = a0;
     }
@@ -996,17 +1003,17 @@ __device__ __forceinline__ void flow_mfma(const u32x4* act0, const u32x4* act1, 
   for (int r = 0; r < ns; ++r) {
     const int chunk = r * 4 + kq;
     const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
-    const int P0 = (srow0 + r) * 16 + kq * 4;
+    const int S0 = srow0 + r;  // K step (scale rows)
     u32x4 sc0, sc1;
     half8 a1;
     if constexpr (kTwo) {
       a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
       const int Gg = wave, Gu = 4 + wave;
-      sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
-      sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+      sc0 = lds_ld<u32x4>(sbase + scale_lane(Gg, kq) + S0 * 64);
+      sc1 = lds_ld<u32x4>(sbase + scale_lane(Gu, kq) + S0 * 64);
     } else {
       const int G = 2 * wave + (n >> 3);
-      sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
+      sc0 = lds_ld<u32x4>(sbase + scale_lane(G, kq) + S0 * 64);
       sc1 = sc0;
       a1 = a0;
     }
@@ -1733,7 +1740,7 @@ __device__ __forceinline__ void lite_mfma2(const u32x4* actA, const u32x4* actB,
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int chunk = s * 4 + kq;
-    const int sd = (G * 128 + ((s * 16 + kq * 4) ^ ((G & 1) << 3))) * 4;
+    const uint32_t sd = scale_lane(G, kq) + s * 64;
     const half8 a[2] = {__builtin_bit_cast(half8, actA[act_slot(n, chunk)]),
                         __builtin_bit_cast(half8, actB[act_slot(n, chunk)])};
     const u32x4 sc[2] = {lds_ld<u32x4>(sbaseA + sd), lds_ld<u32x4>(sbaseB + sd)};
@@ -2443,8 +2450,13 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
     if constexpr (Shape<kPhase>::kSliceK) {
       if (i + 1 == ntile || (t + 1) % per_key == 0) {
         const int key = t / per_key;
-        float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
-                      static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kBulkM * kN;
+        // Through a buffer resource: one lane offset, and each row's offset a
+        // constant in the scalar operand (no per-row 64-bit addresses to keep
+        // live across the loop).
+        const float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
+                            static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kBulkM * kN;
+        const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(part, kBulkM * kN * 4);
+        const uint32_t lane_off = static_cast<uint32_t>(kq * 4 * kN + wave * 64 + n * 4) * 4;
 #pragma unroll
         for (int rb = 0; rb < kBulkBlocks; ++rb) {
           if (rb < nrb) {
@@ -2453,8 +2465,9 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
               const int row = rb * 16 + kq * 4 + v;
               if (row < tr.m) {
                 const float s = ldexpf(1.0f, -(ubuf ? rx1 : rx0)[rb * 16 + v]);
-                *reinterpret_cast<float4*>(part + row * kN + wave * 64 + n * 4) =
-                    make_float4(acc[rb][0][v] * s, acc[rb][1][v] * s, acc[rb][2][v] * s, acc[rb][3][v] * s);
+                const u32x4 w = {__float_as_uint(acc[rb][0][v] * s), __float_as_uint(acc[rb][1][v] * s),
+                                 __float_as_uint(acc[rb][2][v] * s), __float_as_uint(acc[rb][3][v] * s)};
+                __builtin_amdgcn_raw_buffer_store_b128(w, rp, lane_off, (rb * 16 + v) * kN * 4, 0);
               }
             }
           }
