@@ -2190,6 +2190,11 @@ template <int kPhase, int kRb>
 __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32x4 (&cb)[kSteps], int n, int kq,
                                            int wave, uint32_t lut_lane, float4v (&acc)[kBulkBlocks][4]) {
   const uint32_t sbase = lds_addr(const_cast<BulkSmem<kPhase>&>(sm).scales[0]);
+  // Phase C: the lane base of the scale rows, of which each step takes an
+  // opaque copy, so the compiler neither keeps eight per-step addresses live
+  // across the tile loop (they spilled, and every reload waited for the tile
+  // loads in flight) nor hoists later steps' scale reads.
+  const uint32_t slc = kPhase == kPhaseC ? sbase + scale_lane(2 * wave + (n >> 3), kq) : 0u;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int chunk = s * 4 + kq;
@@ -2199,6 +2204,11 @@ __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32
       const int Gg = wave, Gu = 4 + wave;
       sc0 = lds_ld<u32x4>(sbase + (Gg * 128 + (P0 ^ ((Gg & 1) << 3))) * 4);
       sc1 = lds_ld<u32x4>(sbase + (Gu * 128 + (P0 ^ ((Gu & 1) << 3))) * 4);
+    } else if constexpr (kPhase == kPhaseC) {
+      uint32_t a0 = slc;
+      asm volatile("" : "+v"(a0));
+      sc0 = lds_ld<u32x4>(a0 + s * 64);
+      sc1 = sc0;
     } else {
       const int G = 2 * wave + (n >> 3);
       sc0 = lds_ld<u32x4>(sbase + (G * 128 + (P0 ^ ((G & 1) << 3))) * 4);
