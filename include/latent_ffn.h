@@ -175,7 +175,12 @@ int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t ti
  * Reads and clears the error word of a workspace.  A decode kernel whose
  * bounded wait for another workgroup expires sets it and finishes its work
  * on whatever data it has, so it always terminates; the output of that call
- * is undefined.  Synchronises `stream`.  Returns LATENT_OK when no call on
+ * is undefined, and a late counter update may leave the workspace's control
+ * block non-zero.  When the word is set this call therefore re-zeros the
+ * whole control block (the first LATENT_NOALLOC_CONTROL_BYTES), after which
+ * the workspace serves later calls correctly.  workspace == NULL (with
+ * workspace_bytes == 0) checks the calling device's latent_moe_ffn_forward_noalloc
+ * array instead.  Synchronises `stream`.  Returns LATENT_OK when no call on
  * this workspace timed out since the last check, LATENT_E_TIMEOUT when one
  * did.  No counterpart in the reference, whose kernels never wait on each
  * other.

@@ -26,6 +26,7 @@ from .moe import (  # noqa: F401
     pack_int8,
     pack_nf4,
     unpack,
+    workspace_error,
     workspace_size,
 )
 from .router import Router, route  # noqa: F401

@@ -996,20 +996,41 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
 }
 
 namespace latent {
+// The calling device's noalloc scratch array (noalloc.hip), set up on first use.
+int noalloc_scratch(hipStream_t s, void** out);
 namespace {
-__global__ void clear_word_kernel(int* word) { *word = 0; }
+__global__ void clear_control_kernel(uint4* p, size_t n16) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
 }  // namespace
 }  // namespace latent
 
+// A set error word means a bounded wait expired: the chain that timed out
+// finished on whatever data it had, and a producer's late counter update may
+// have landed after its consumer reset that counter.  Once the stream has
+// drained, every kernel of that call has ended, so re-zeroing the whole
+// control block (counters, tickets and the error word) restores the state
+// every call expects on entry.
 extern "C" int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t stream) {
-  if (!workspace || workspace_bytes < fused::kReserved) return LATENT_E_WORKSPACE;
-  int* word = reinterpret_cast<int*>(static_cast<char*>(workspace) + fused::kErrorOffset);
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (!workspace) {
+    if (workspace_bytes != 0) return LATENT_E_WORKSPACE;
+    (void)hipGetLastError();
+    const int st = noalloc_scratch(s, &workspace);
+    if (st != LATENT_OK) return st;
+  } else if (workspace_bytes < fused::kReserved) {
+    return LATENT_E_WORKSPACE;
+  }
+  int* word = reinterpret_cast<int*>(static_cast<char*>(workspace) + fused::kErrorOffset);
   int h = 0;
   if (hipMemcpyAsync(&h, word, sizeof h, hipMemcpyDeviceToHost, s) != hipSuccess) return LATENT_E_HIP;
   if (hipStreamSynchronize(s) != hipSuccess) return LATENT_E_HIP;
   if (h == 0) return LATENT_OK;
-  hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, word);
+  const size_t n16 = fused::kReserved / 16;
+  hipLaunchKernelGGL(clear_control_kernel, dim3(static_cast<unsigned>((n16 + 255) / 256)), dim3(256), 0, s,
+                     static_cast<uint4*>(workspace), n16);
   if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return LATENT_E_HIP;
   return LATENT_E_TIMEOUT;
 }

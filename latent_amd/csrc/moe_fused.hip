@@ -1233,10 +1233,24 @@ static_assert(sizeof(SmemLayout) <= 80 * 1024, "two workgroups per CU");
 
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
+// INT8 groups are read through a buffer resource of kFbufBytes with a 32-bit
+// byte offset (group index * 32): a factor qualifies only when even an
+// all-INT8 side buffer (every group of every expert) stays below that range.
+bool int8_fits(const latent_moe_args& a) {
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  for (const latent_factor* f : fs) {
+    if (!f->int8_bitmap) continue;
+    const int64_t groups = a.n_expert * f->rows * (f->cols / kGroup);
+    if (groups * kGroup >= static_cast<int64_t>(kFbufBytes)) return false;
+  }
+  return true;
+}
+
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
   const bool x_aligned = (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0;  // 16-byte vector staging of x
-  return P >= kMinPairs && P <= kMaxPairs && a.n_expert <= kMaxE && 2 * a.max_rank <= kVMax && x_aligned;
+  return P >= kMinPairs && P <= kMaxPairs && a.n_expert <= kMaxE && 2 * a.max_rank <= kVMax && x_aligned &&
+         int8_fits(a);
 }
 
 static int pick_cols(int64_t extent, double per_xcd, int target, int lo, int hi) {

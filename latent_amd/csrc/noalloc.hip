@@ -7,8 +7,9 @@
 // per device with hipGetSymbolAddress and that pointer is used everywhere.
 // The first LATENT_NOALLOC_CONTROL_BYTES are the workspace control block,
 // whose counters every call leaves zero; it is cleared once per device, by a
-// fill kernel, before the first call uses it.  (Its error word, set only by a
-// timed-out bounded wait, is read by no call.)  All calls on one GPU share the
+// fill kernel, before the first call uses it.  Its error word, set only by a
+// timed-out bounded wait, is read (and after a timeout the whole control block
+// re-zeroed) by latent_moe_check with a NULL workspace.  All calls on one GPU share the
 // array, so calls that overlap on one GPU (several streams or host threads)
 // race; calls issued in order on one stream do not.
 #include "common.hpp"
@@ -34,9 +35,11 @@ __global__ void clear_kernel(uint4* p, size_t n16) {
 std::mutex g_mutex;
 void* g_ptr[kMaxDevices] = {};
 
+}  // namespace
+
 // The device address of `scratch` on the current device, set up on the first
 // call there (symbol lookup, control block cleared on `s`).
-int scratch_ptr(hipStream_t s, void** out) {
+int noalloc_scratch(hipStream_t s, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return LATENT_E_HIP;
   if (dev < 0 || dev >= kMaxDevices) return LATENT_E_UNSUPPORTED;
@@ -45,6 +48,7 @@ int scratch_ptr(hipStream_t s, void** out) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return LATENT_E_HIP;
     const size_t n16 = LATENT_NOALLOC_CONTROL_BYTES / 16;
+    (void)hipGetLastError();  // clear a stale error so the check below sees only this launch's
     hipLaunchKernelGGL(clear_kernel, dim3(static_cast<unsigned>((n16 + 255) / 256)), dim3(256), 0, s,
                        static_cast<uint4*>(p), n16);
     if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
@@ -54,7 +58,6 @@ int scratch_ptr(hipStream_t s, void** out) {
   return LATENT_OK;
 }
 
-}  // namespace
 }  // namespace latent
 
 extern "C" int latent_moe_ffn_forward_noalloc(const latent_moe_args* args, latent_stream_t stream) {
@@ -68,7 +71,7 @@ extern "C" int latent_moe_ffn_forward_noalloc(const latent_moe_args* args, laten
   if (need > LATENT_NOALLOC_SCRATCH_BYTES) return LATENT_E_WORKSPACE;
   if (a.n_tokens == 0) return LATENT_OK;
   void* p = nullptr;
-  const int sp = latent::scratch_ptr(reinterpret_cast<hipStream_t>(stream), &p);
+  const int sp = latent::noalloc_scratch(reinterpret_cast<hipStream_t>(stream), &p);
   if (sp != LATENT_OK) return sp;
   a.workspace = p;
   a.workspace_bytes = LATENT_NOALLOC_SCRATCH_BYTES;

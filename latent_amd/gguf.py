@@ -103,7 +103,15 @@ class LatentGGUF:
                 # per_expert_ranks.T (loader/write_latent_gguf.py:262-265,
                 # 432-436), so the bytes are kind-major [3][E] under recorded
                 # dims (E, 3).  Ranks of 256 or more wrapped modulo 256 when
-                # the reference wrote them.
+                # the reference wrote them, so beside factors padded to a
+                # max_rank above 255 the table is ambiguous (a stored 0 may be
+                # 256 or 512).  The reference never reads it: its factors are
+                # zero-padded to max_rank (loader/write_latent_gguf.py:101-123),
+                # so computing every expert at max_rank is exact, and such a
+                # table is dropped.
+                max_rank = 2 * int(self.arrays[tensor_name(layer, "gate_a")].shape[-1])
+                if max_rank > 255:
+                    return out
                 n_expert = int(self.tensors[rk].dims[0])
                 r = r.reshape(-1).view(np.uint8).reshape(3, n_expert).T
             out[rk] = np.ascontiguousarray(r, dtype=np.int32)

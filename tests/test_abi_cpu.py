@@ -202,7 +202,9 @@ def test_expert_workspace_and_argument_checks(L):
 
 
 def test_check_rejects_missing_workspace(L):
-    assert L.lib.latent_moe_check(None, 0, None) == L.LATENT_E_WORKSPACE
+    buf = np.zeros(64, np.uint8)
+    assert L.lib.latent_moe_check(buf.ctypes.data, 64, None) == L.LATENT_E_WORKSPACE  # below the control block
+    assert L.lib.latent_moe_check(None, 64, None) == L.LATENT_E_WORKSPACE  # NULL names the noalloc array: bytes 0
     assert L.status_string(L.LATENT_E_TIMEOUT) != "unknown status"
 
 

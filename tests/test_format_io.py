@@ -192,6 +192,38 @@ def test_reference_written_rank_table(tmp_path):
     assert np.array_equal(ref.moe_forward(x, ids, w, host), want)
 
 
+def _with_reference_rank_table(g, layer_idx: int, per_expert_ranks: np.ndarray) -> None:
+    """Replace a read file's rank table by the bytes the reference's writer
+    produces: per_expert_ranks.T as uint8 recorded as I8 with dims (E, 3)."""
+    E = per_expert_ranks.shape[0]
+    name = f"blk.{layer_idx}.ffn_latent_ranks"
+    file_bytes = per_expert_ranks.T.astype(np.uint8).tobytes(order="C")
+    g.tensors[name] = gguf.TensorInfo(name, (E, 3), gguf.GGML_I8, 0)
+    g.arrays[name] = np.frombuffer(file_bytes, np.int8).reshape(E, 3)
+
+
+def test_reference_rank_table_dropped_above_255(tmp_path):
+    # At max_rank 256 the reference's uint8 table stores a rank of 256 as 0:
+    # the table is ambiguous there, so the reader drops it (the factors are
+    # zero-padded to max_rank, so max_rank is exact); at max_rank 32 it is kept.
+    layer = synth.make_layer(seed=11, n_expert=3, d=256, ff=256, max_rank=256)
+    p = tmp_path / "wide.gguf"
+    arrays = _host_arrays(layer)
+    gguf.write_latent_gguf(p, {0: arrays}, max_rank=256)
+    g = gguf.read_latent_gguf(p)
+    _with_reference_rank_table(g, 0, np.array([[256, 256, 256], [128, 64, 256], [256, 200, 32]]))
+    got = g.layer_arrays(0)
+    assert "blk.0.ffn_latent_ranks" not in got
+    assert np.array_equal(got["blk.0.ffn_latent_gate_a"], arrays["gate_a"])
+
+    small = synth.make_layer(seed=12, n_expert=2, d=64, ff=64, max_rank=32)
+    p2 = tmp_path / "narrow.gguf"
+    gguf.write_latent_gguf(p2, {0: _host_arrays(small)}, max_rank=32)
+    g2 = gguf.read_latent_gguf(p2)
+    _with_reference_rank_table(g2, 0, np.array([[32, 16, 8], [0, 32, 32]]))
+    assert g2.layer_arrays(0)["blk.0.ffn_latent_ranks"].tolist() == [[32, 16, 8], [0, 32, 32]]
+
+
 def test_writer_rejects_bad_operands(tmp_path):
     layer = synth.make_layer(seed=9, n_expert=2, d=64, ff=64, max_rank=32)
     arrays = _host_arrays(layer)

@@ -180,3 +180,43 @@ def test_lite_dsv3_shape(gpu):
         err = ref.rel_l2(want, out.cpu().numpy())
         print(f"lite dsv3 B={B} experts={experts.size} rel_l2={err:.3e}")
         assert err <= TOL
+
+
+def test_check_after_timeout_rezeros_control_block(gpu, layer, dev):
+    """A timed-out chain leaves the error word set and may leave a counter
+    non-zero.  Both are seeded here from the host (no kernel is made to time
+    out): latent_moe_check reports LATENT_E_TIMEOUT, leaves the whole control
+    block zero, and the next call on that workspace matches the oracle."""
+    import torch
+
+    from latent_amd import _lib
+
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((1, D)).astype(np.float32)
+    ids, w = routing.softmax_topk(rng.standard_normal((1, E)), 8)
+    ws = torch.zeros(gpu.workspace_size(dev, 1, 8), dtype=torch.uint8, device="cuda")
+    ctrl = _lib.LATENT_NOALLOC_CONTROL_BYTES
+    ws[36:40] = torch.tensor([1, 0, 0, 0], dtype=torch.uint8)  # the error word
+    ws[192 * 1024 + 4] = 3                                     # a small-batch chain counter
+    ws[4096] = 9                                               # a persistent-kernel ticket
+    assert gpu.workspace_error(ws) == _lib.LATENT_E_TIMEOUT
+    assert int(ws[:ctrl].count_nonzero()) == 0
+    assert gpu.workspace_error(ws) == _lib.LATENT_OK
+    got, xq = _call(gpu, dev, x, ids, w, ws=ws)
+    torch.cuda.synchronize()
+    assert int(ws[:ctrl].count_nonzero()) == 0
+    err = ref.rel_l2(ref.moe_forward(xq, ids, w, layer), got.cpu().numpy())
+    assert err <= TOL
+
+
+def test_check_noalloc_array(gpu):
+    """latent_moe_check with a NULL workspace reads the calling device's
+    noalloc array: no call has timed out, so it reports LATENT_OK."""
+    import ctypes
+
+    import torch
+
+    from latent_amd import _lib
+
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert _lib.lib.latent_moe_check(None, 0, s) == _lib.LATENT_OK

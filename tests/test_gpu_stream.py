@@ -143,6 +143,43 @@ def test_stream_dsv3_decode(gpu, stream_path, dsv3, B):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("path", ["general", "fused"])
+def test_reference_rank_table_at_max_rank_256(gpu, tmp_path, monkeypatch, path):
+    """A file whose rank table the reference wrote (uint8 as I8, a rank of 256
+    stored as 0) beside factors padded to 256 is read without the table, and
+    the fp32 paths that honour ranks then match the oracle at max_rank."""
+    import torch
+
+    from latent_amd import StackedLayer, gguf
+
+    layer = synth.make_layer(seed=21, n_expert=4, d=256, ff=256, max_rank=256)
+    arrays = {}
+    for name in ref.FACTOR_NAMES:
+        arrays[name] = layer.factors[name].codes
+        arrays[name + "_s"] = layer.factors[name].scales.astype(np.float16)
+    p = tmp_path / "refranks256.gguf"
+    gguf.write_latent_gguf(p, {0: arrays}, max_rank=256)
+    g = gguf.read_latent_gguf(p)
+    name = "blk.0.ffn_latent_ranks"
+    per_expert = np.array([[256, 256, 256], [128, 256, 64], [256, 32, 256], [256, 256, 256]])
+    g.tensors[name] = gguf.TensorInfo(name, (4, 3), gguf.GGML_I8, 0)
+    g.arrays[name] = np.frombuffer(per_expert.T.astype(np.uint8).tobytes(), np.int8).reshape(4, 3)
+    dev = StackedLayer.from_arrays(g.layer_arrays(0), layer=0, stream_tiles=False)
+    assert dev.ranks is None
+    monkeypatch.setenv("LATENT_MOE_PATH", path)
+    rng = np.random.default_rng(5)
+    T = 40 if path == "fused" else 5  # the persistent kernel takes 32..512 routed pairs
+    x = rng.standard_normal((T, 256)).astype(np.float32)
+    ids, w = routing.softmax_topk(rng.standard_normal((T, 4)), 2)
+    xt = torch.from_numpy(x).cuda()
+    assert gpu.moe_path(dev, xt, 2) == path
+    out = gpu.moe_forward(xt, torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda(), dev)
+    want = ref.moe_forward(x, ids, w, layer)
+    err = ref.rel_l2(want, out.cpu().numpy())
+    print(f"reference rank table, path {path}: rel_l2={err:.3e}")
+    assert err <= 1e-5
+
+
 def test_gguf_round_trip_layer_gives_identical_outputs(gpu, small_dev, tmp_path):
     """A device layer written to GGUF and read back computes bit-identical outputs."""
     import torch

@@ -114,3 +114,58 @@ def test_noalloc_rejects_calls_beyond_its_scratch(gpu):
     got = _noalloc(dl, xt, torch.from_numpy(i2).cuda(), torch.from_numpy(w2).cuda())
     torch.cuda.synchronize()
     assert ref.rel_l2(ref.moe_forward(xs, i2, w2, hl), got.cpu().numpy()) <= 2e-3
+
+
+def test_noalloc_small_batch_chain_calls_in_a_row(gpu):
+    """Batch 1 at top-8 takes the small-batch chain, whose counters live in the
+    noalloc array's control block: several calls in a row with different
+    routings (and a per-slot call between) equal the workspace entry bit for bit."""
+    import torch
+
+    from latent_amd import synth as gsynth
+    from latent_amd.moe import stream_launch
+
+    layer = gsynth.make_layer(seed=17, n_expert=64, d=1024, ff=1024, max_rank=256)
+    x = gsynth.bf16_input(seed=3, n_tokens=1, d=1024)
+    assert stream_launch(layer, x, 8) == "lite"
+    for seed, mode in ((31, 0), (32, 0), (33, 1), (34, 0)):
+        _compare(gpu, layer, 1, 8, seed=seed, mode=mode, exact=True)
+    torch.cuda.synchronize()
+
+
+def test_noalloc_graph_capture_replays(gpu):
+    """A noalloc call captured in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed several times, with eager work and synchronisations between the
+    replays, gives the eager result on every replay."""
+    import torch
+
+    from latent_amd import synth as gsynth
+
+    layer = gsynth.make_layer(seed=18, n_expert=64, d=1024, ff=1024, max_rank=256)
+    T, k = 2, 8
+    ids, w = gsynth.route(seed=41, n_tokens=T, n_expert=64, k=k)
+    x = gsynth.bf16_input(seed=42, n_tokens=T, d=1024)
+    eager = _noalloc(layer, x, ids, w)  # first call on the device: sets up the array outside the capture
+    torch.cuda.synchronize()
+    out = torch.zeros((T, 1024), dtype=torch.float32, device="cuda")
+    a = _args(layer, x, ids, w, out)
+    a.workspace, a.workspace_bytes = None, 0
+    from latent_amd import _lib
+
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            st = _lib.lib.latent_moe_ffn_forward_noalloc(ctypes.byref(a), ctypes.c_void_p(cap.cuda_stream))
+    torch.cuda.current_stream().wait_stream(cap)
+    _lib.check(st, "latent_moe_ffn_forward_noalloc (captured)")
+    for i in range(3):
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager call"
+        # eager work on the same array between the replays
+        other = _noalloc(layer, gsynth.bf16_input(seed=50 + i, n_tokens=1, d=1024), ids[:1], w[:1])
+        torch.cuda.synchronize()
+        assert not torch.isnan(other).any()
