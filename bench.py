@@ -217,11 +217,10 @@ def _host_subset(torch, layer, ids, ref):
     lut = -np.ones(E, np.int64)
     lut[experts] = np.arange(experts.size)
     local = np.where(ids >= 0, lut[np.clip(ids, 0, E - 1)], -1).astype(np.int32)
-    sel = torch.as_tensor(experts, device="cuda")
     facs = {}
-    for name, f in layer.factors().items():
-        facs[name] = ref.StackedFactor(f.codes.index_select(0, sel).cpu().numpy(),
-                                       f.scales.index_select(0, sel).cpu().numpy().view(np.float16))
+    for name in layer.factors():
+        f = layer.factor_rows(name, experts)  # the routed experts, back in the row layout
+        facs[name] = ref.StackedFactor(f.codes.cpu().numpy(), f.scales.cpu().numpy().view(np.float16))
     return ref.StackedLayer(factors=facs, d=D, ff=FF, max_rank=R), local, experts.size
 
 

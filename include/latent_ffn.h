@@ -65,6 +65,22 @@ typedef struct ihipStream_t* latent_stream_t;
 #define LATENT_F16 1
 #define LATENT_BF16 2
 
+/* ---- factor layouts ----------------------------------------------------- */
+/* The stacked row layout above (loader/write_latent_gguf.py's). */
+#define LATENT_LAYOUT_ROWS 0
+/* The tile layout of the MFMA paths: every factor tensor, codes and scales
+ * alike, reordered in place of the row layout by latent_tiles_repack (same
+ * tensors, same sizes, each expert's bytes where its rows were). */
+#define LATENT_LAYOUT_TILES 1
+
+/* ---- factors, in the operand order (src3..src14 in code/scale pairs) ---- */
+#define LATENT_GATE_A 0
+#define LATENT_GATE_B 1
+#define LATENT_UP_A 2
+#define LATENT_UP_B 3
+#define LATENT_DOWN_A 4
+#define LATENT_DOWN_B 5
+
 /* ---- output modes ------------------------------------------------------- */
 /* f32 [T][d]: sum over slots of w*y (y when weight_before_down). */
 #define LATENT_OUT_REDUCED 0
@@ -119,10 +135,7 @@ typedef struct latent_moe_args {
   void* out;                /* f32, shape per out_mode */
   void* workspace;          /* device scratch, >= latent_moe_workspace_size() */
   size_t workspace_bytes;
-  /* Optional: the layer's factors in the streaming tile layout
-   * (latent_stream_tiles_pack), read by the streaming decode path instead of
-   * the six factors above; NULL => that path is not used. */
-  const void* stream_tiles;
+  int32_t layout;           /* LATENT_LAYOUT_ROWS | LATENT_LAYOUT_TILES: how the 12 factor tensors are ordered */
 } latent_moe_args;
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -157,19 +170,30 @@ int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream);
 int latent_moe_ffn_forward_noalloc(const latent_moe_args* args, latent_stream_t stream);
 
 /*
- * The layer's six factors in the streaming tile layout of the decode path:
- * every 256x256 block of a factor as 32 KB of NF4 codes in MFMA-operand order
- * followed by its 4 KB of scales, so the path reads each block as one
- * contiguous stream (no reference counterpart; a backend builds it once when
- * it loads the layer's tensors, as ggml backends repack weights for their
- * kernels).  Applies to pure-NF4 layers with max_rank == 256 and n_embd,
- * n_ff multiples of 256; for any other layer *bytes is 0.  The size equals
- * the packed factors' (the layout only reorders them).
+ * 1 when this layer's factors can take LATENT_LAYOUT_TILES (pure NF4,
+ * max_rank 256, n_embd and n_ff multiples of 256), 0 when not; reads only the
+ * dimensions and the INT8 pointers.  No reference counterpart.
  */
-int latent_stream_tiles_size(const latent_moe_args* args, size_t* bytes);
-/* Writes the tile layout of args' factors to `tiles` (16-byte aligned,
- * >= latent_stream_tiles_size bytes); stream ordered. */
-int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t tiles_bytes, latent_stream_t stream);
+int latent_tiles_supported(const latent_moe_args* args);
+
+/*
+ * Reorders one factor tensor pair between the row layout and the tile layout,
+ * as a ggml backend repacks weights when it loads them (no reference
+ * counterpart: the reference's kernels read the row layout,
+ * kernels/latent_fused_expert_ffn.cu:17-18).  `factor` is LATENT_GATE_A ..
+ * LATENT_DOWN_B; src and dst describe the same [n_expert][rows][cols] factor
+ * (rows, cols as in the row layout; INT8 pointers NULL), src in the row
+ * layout and dst in the tile layout when to_tiles != 0, the other way round
+ * when 0.  Codes are repacked when both codes pointers are set, scales when
+ * both scales pointers are (so a code tensor and its scale tensor can be
+ * repacked on their own); the tile side must be 16-byte aligned and the two
+ * sides must not overlap.  Shapes: gate_a, up_a, down_a rows % 256 == 0 and
+ * cols == 256; gate_b, up_b rows == 256, cols % 128 == 0; down_b rows == 256,
+ * cols % 256 == 0.  Expert e's bytes stay in expert e's byte range, so a
+ * slice of experts repacks on its own.  Stream ordered; allocates nothing.
+ */
+int latent_tiles_repack(int32_t factor, const latent_factor* src, latent_factor* dst, int64_t n_expert,
+                        int32_t to_tiles, latent_stream_t stream);
 
 /*
  * Reads and clears the error word of a workspace.  A decode kernel whose
@@ -191,16 +215,18 @@ int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t st
  * Which implementation latent_moe_ffn_forward uses for these arguments, the
  * first that supports the call in this order:
  *   2 = fp16-MFMA prefill: on average at least 16 routed pairs per active
- *       expert, no INT8 groups, n_embd / n_ff / max_rank multiples of 128
- *       with n_ff and max_rank <= 2048, 16-byte aligned x and codes; it runs
- *       on the stream_tiles layout when one is given (64-pair units),
- *       otherwise as grouped GEMMs (LATENT_PREFILL_ENGINE=gemm selects those);
- *   3 = streaming fp16-MFMA decode: a stream_tiles layout is given (pure NF4,
- *       max_rank 256, n_embd and n_ff multiples of 256), 1 to 4096 routed
- *       pairs, 16-byte aligned x;
- *   1 = single persistent fp32 decode kernel: 32 to 512 routed pairs,
- *       2 * max_rank <= 1024, 16-byte aligned x (INT8 groups allowed);
- *   0 = multi-kernel fp32 GEMV path: any call.
+ *       expert (or, for a layer in the tile layout, more routed pairs than
+ *       path 3 takes), no INT8 groups, 16-byte aligned x; on the tile layout
+ *       it streams 64-pair units of one expert, on the row layout (n_embd /
+ *       n_ff / max_rank multiples of 128, n_ff and max_rank <= 2048, 16-byte
+ *       aligned codes) it runs grouped GEMMs;
+ *   3 = streaming fp16-MFMA decode: the factors are in the tile layout, 1 to
+ *       4096 routed pairs, 16-byte aligned x;
+ *   1 = single persistent fp32 decode kernel: row layout, 32 to 512 routed
+ *       pairs, 2 * max_rank <= 1024, 16-byte aligned x (INT8 groups allowed);
+ *   0 = multi-kernel fp32 GEMV path: any call on the row layout.
+ * A call in the tile layout that neither path 2 nor 3 takes is
+ * LATENT_E_UNSUPPORTED.
  * < 0 = LATENT_E_* for bad arguments.  The environment variable
  * LATENT_MOE_PATH (general | fused | prefill | stream) selects another path
  * that supports the call, for comparisons.
@@ -213,7 +239,6 @@ int latent_moe_path(const latent_moe_args* args);
  *   2 = small-batch chain: one launch for at most 16 routed pairs, every
  *       workgroup's tiles loaded first, grouping and combine inside (taken by
  *       default wherever each workgroup's tiles fit its registers);
- *   1 = one-launch chain for any batch (LATENT_STREAM_LAUNCH=one);
  *   0 = one launch per phase (the default otherwise; LATENT_STREAM_LAUNCH=phases
  *       also for small batches).
  * LATENT_E_UNSUPPORTED when the call does not take the streaming path.

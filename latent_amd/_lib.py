@@ -31,6 +31,12 @@ LATENT_BF16 = 2
 LATENT_OUT_REDUCED = 0
 LATENT_OUT_PER_SLOT = 1
 
+LATENT_LAYOUT_ROWS = 0
+LATENT_LAYOUT_TILES = 1
+
+# Factor indices of latent_tiles_repack, in the operand order.
+LATENT_GATE_A, LATENT_GATE_B, LATENT_UP_A, LATENT_UP_B, LATENT_DOWN_A, LATENT_DOWN_B = range(6)
+
 EXPORTED = (
     "latent_version",
     "latent_status_string",
@@ -47,11 +53,12 @@ EXPORTED = (
     "latent_route",
     "latent_expert_workspace_size",
     "latent_expert_forward",
-    "latent_stream_tiles_size",
-    "latent_stream_tiles_pack",
+    "latent_tiles_supported",
+    "latent_tiles_repack",
 )
 
 LATENT_NOALLOC_SCRATCH_BYTES = 64 << 20
+LATENT_NOALLOC_CONTROL_BYTES = 256 << 10
 
 LATENT_Q_NF4 = 0
 LATENT_Q_INT8 = 1
@@ -98,7 +105,7 @@ class LatentMoeArgs(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
-        ("stream_tiles", ctypes.c_void_p),
+        ("layout", ctypes.c_int32),
     ]
 
 
@@ -197,10 +204,13 @@ def _load() -> ctypes.CDLL:
     lib.latent_expert_workspace_size.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.POINTER(ctypes.c_size_t)]
     lib.latent_expert_forward.restype = ctypes.c_int
     lib.latent_expert_forward.argtypes = [ctypes.POINTER(LatentExpertArgs), ctypes.c_void_p]
-    lib.latent_stream_tiles_size.restype = ctypes.c_int
-    lib.latent_stream_tiles_size.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.POINTER(ctypes.c_size_t)]
-    lib.latent_stream_tiles_pack.restype = ctypes.c_int
-    lib.latent_stream_tiles_pack.argtypes = [ctypes.POINTER(LatentMoeArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.latent_tiles_supported.restype = ctypes.c_int
+    lib.latent_tiles_supported.argtypes = [ctypes.POINTER(LatentMoeArgs)]
+    lib.latent_tiles_repack.restype = ctypes.c_int
+    lib.latent_tiles_repack.argtypes = [
+        ctypes.c_int32, ctypes.POINTER(LatentFactor), ctypes.POINTER(LatentFactor), ctypes.c_int64, ctypes.c_int32,
+        ctypes.c_void_p,
+    ]
     return lib
 
 

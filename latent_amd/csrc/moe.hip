@@ -71,8 +71,6 @@ struct MoeParams {
   int* pos_of;      // [T*K] grouped position of each routed slot (streaming path)
   _Float16* xh;     // streaming path: x as fp16 rows * 2^xexp (NULL: not converted)
   int* xexp;        // [T] row exponents
-  int* flow_cnt;    // streaming path in one launch: counters cleared here (NULL: none)
-  int64_t flow_cnt_n;
   int x_dtype, w_dtype;
   int T, d, ff, E, K, R;
   int wbd, out_mode;
@@ -475,20 +473,6 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
       }
       if (threadIdx.x == 0) p.xexp[t] = ex;
     }
-    if (p.flow_cnt) {
-      // One-launch chain: its counters start at zero, and in per-slot mode the
-      // rows of dropped slots are zero (no tile writes them).
-      for (int64_t i = t0; i < p.flow_cnt_n; i += stride) p.flow_cnt[i] = 0;
-      if (p.out_mode == LATENT_OUT_PER_SLOT) {
-        const int64_t rows = static_cast<int64_t>(p.T) * p.K;
-        for (int64_t r = blockIdx.x - 1; r < rows; r += nblk) {
-          const int e = p.ids[r];
-          if (e >= 0 && e < p.E) continue;
-          float4* o4 = reinterpret_cast<float4*>(p.out + r * p.d);
-          for (int c = threadIdx.x; c < p.d / 4; c += kRouteThreads) o4[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-    }
     return;  // otherwise the streaming path clears nothing: its kernels write every output
   }
   // Accumulators gu and dl are contiguous: zero_floats covers both.
@@ -849,6 +833,7 @@ int validate(const latent_moe_args& a) {
   if (a.x_dtype < LATENT_F32 || a.x_dtype > LATENT_BF16) return LATENT_E_INVALID;
   if (a.weights_dtype != LATENT_F32 && a.weights_dtype != LATENT_F16) return LATENT_E_INVALID;
   if (a.out_mode != LATENT_OUT_REDUCED && a.out_mode != LATENT_OUT_PER_SLOT) return LATENT_E_INVALID;
+  if (a.layout != LATENT_LAYOUT_ROWS && a.layout != LATENT_LAYOUT_TILES) return LATENT_E_INVALID;
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   const int64_t rows[6] = {a.n_embd, a.max_rank, a.n_embd, a.max_rank, a.n_ff, a.max_rank};
   const int64_t cols[6] = {a.max_rank, a.n_ff, a.max_rank, a.n_ff, a.max_rank, a.n_embd};
@@ -860,6 +845,7 @@ int validate(const latent_moe_args& a) {
   if (a.n_expert > kMaxExperts || a.max_rank > kMaxRank || a.n_expert_used > kMaxExpertUsed) return LATENT_E_UNSUPPORTED;
   const int64_t P = a.n_tokens * a.n_expert_used;
   if (a.n_tokens > (1 << 24) || P > (1 << 26) || a.n_embd > (1 << 20) || a.n_ff > (1 << 20)) return LATENT_E_UNSUPPORTED;
+  if (a.layout == LATENT_LAYOUT_TILES && !stream::tiles_shape_ok(a)) return LATENT_E_UNSUPPORTED;
   return LATENT_OK;
 }
 
@@ -873,8 +859,18 @@ enum { kPathGeneral = 0, kPathFused = 1, kPathPrefill = 2, kPathStream = 3 };
 
 // The implementation for one call shape.  LATENT_MOE_PATH (general | fused |
 // prefill | stream) selects another path that supports the call, for
-// comparisons; the default is the measured fastest supported path.
+// comparisons; the default is the measured fastest supported path.  A layer
+// in the tile layout has only the two MFMA paths (LATENT_E_UNSUPPORTED when
+// neither takes the call).
 int choose_path(const latent_moe_args& a, fused::Plan& pl) {
+  if (a.layout == LATENT_LAYOUT_TILES) {
+    const bool prefill_ok = prefill::supported(a), stream_ok = stream::supported(a);
+    const char* env = std::getenv("LATENT_MOE_PATH");
+    if (env && !std::strcmp(env, "stream") && stream_ok) return kPathStream;
+    if (prefill_ok) return kPathPrefill;
+    if (stream_ok) return kPathStream;
+    return LATENT_E_UNSUPPORTED;
+  }
   const bool fused_ok = fused::supported(a) && fused::make_plan(a, pl);
   const bool prefill_ok = prefill::supported(a);
   const bool stream_ok = stream::supported(a);
@@ -989,7 +985,8 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   size_t scratch = L.total;
   if (prefill::supported(*args)) scratch = std::max(scratch, L.gu + prefill::layout_for(*args).total);
   fused::Plan pl;
-  if (fused::supported(*args) && fused::make_plan(*args, pl)) scratch = std::max(scratch, pl.scratch_bytes);
+  if (args->layout == LATENT_LAYOUT_ROWS && fused::supported(*args) && fused::make_plan(*args, pl))
+    scratch = std::max(scratch, pl.scratch_bytes);
   if (stream::supported(*args)) scratch = std::max(scratch, L.gu + stream::layout_for(*args).total);
   *bytes = fused::kReserved + align_up(scratch) + int8_word_offset_bytes(*args);
   return LATENT_OK;
@@ -1049,8 +1046,7 @@ extern "C" int latent_stream_launch(const latent_moe_args* args) {
   if (st != LATENT_OK) return st;
   fused::Plan pl;
   if (choose_path(*args, pl) != kPathStream) return LATENT_E_UNSUPPORTED;
-  if (stream::lite_applies(*args)) return 2;
-  return stream::one_launch(*args) ? 1 : 0;
+  return stream::lite_applies(*args) ? 2 : 0;
 }
 
 extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream_t stream) {
@@ -1069,6 +1065,7 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
   (void)hipGetLastError();  // clear a stale error so the checks below see only ours
   fused::Plan pl;
   const int path = choose_path(a, pl);
+  if (path < 0) return path;
   MoeParams p{};
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   bool any_int8 = false;
@@ -1128,10 +1125,6 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.pos_of = reinterpret_cast<int*>(ws + L.gu + SL.pos_of);
     p.xh = reinterpret_cast<_Float16*>(ws + L.gu + SL.xh);
     p.xexp = reinterpret_cast<int*>(ws + L.gu + SL.xexp);
-    if (stream::one_launch(a)) {
-      p.flow_cnt = reinterpret_cast<int*>(ws + L.gu + SL.cnt);
-      p.flow_cnt_n = SL.cnt_ints;
-    }
   }
   // The MFMA paths write their intermediates whole, and every output row (per-token combine).
   p.zero_floats = use_prefill || use_stream ? 0 : P * 3 * a.max_rank;

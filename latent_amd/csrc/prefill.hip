@@ -735,13 +735,9 @@ __global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int row
 
 size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
 
-// The streaming-tile engine takes the call where the layer has a tile layout
-// it can stream; LATENT_PREFILL_ENGINE=gemm keeps the grouped GEMMs.
-bool use_bulk(const latent_moe_args& a) {
-  const char* env = std::getenv("LATENT_PREFILL_ENGINE");
-  if (env && !std::strcmp(env, "gemm")) return false;
-  return stream::bulk_supported(a);
-}
+// A layer in the tile layout runs the streaming-tile engine; one in the row
+// layout the grouped GEMMs.
+bool use_bulk(const latent_moe_args& a) { return a.layout == LATENT_LAYOUT_TILES; }
 
 // M tiles (units of the streaming-tile engine) of `rows` pairs: at most
 // ceil(n_e / rows) per active expert.
@@ -770,11 +766,15 @@ int launch(Params p, int64_t tiles, hipStream_t s) {
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
   const int64_t active = std::max<int64_t>(1, std::min<int64_t>(a.n_expert, P));
-  if (P < static_cast<int64_t>(kMinPairsPerExpert) * active) return false;
+  // In the tile layout, calls beyond the decode launches' pairs come here at
+  // any number of pairs per expert (the row-layout paths cannot read tiles).
+  const bool beyond_decode = a.layout == LATENT_LAYOUT_TILES && P > stream::kMaxPairs;
+  if (P < static_cast<int64_t>(kMinPairsPerExpert) * active && !beyond_decode) return false;
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   for (const latent_factor* f : fs)
     if (f->int8_bitmap != nullptr) return false;  // per-group INT8 layers take the general path
   if ((reinterpret_cast<uintptr_t>(a.x) & 15u) != 0) return false;
+  if (a.layout == LATENT_LAYOUT_TILES) return stream::bulk_supported(a);
   // Whole 128-column halves and exponent blocks, whole 4-slice groups of K;
   // at most kMaxBlocks exponent blocks in a K range; 16-byte code rows and
   // 4-byte scale pairs for the direct loads.

@@ -14,11 +14,12 @@
 //   C   h . A_d                    K tiles of 256 rows -> partial d latent (reduce C)
 //   D   d_lat . B_d                N tiles of 256 columns -> y rows, then the combine
 //
-// The factors are read from a tile layout built once per layer
-// (latent_stream_tiles_pack): every 256 x 256 block of a factor is 32 KB of
-// NF4 codes followed by 4 KB of fp16 scales, in the order the lanes consume
-// them, so each lane reads its MFMA operand bytes with one 128-bit load per
-// 32-row step and every tile is one contiguous 36 KB stream:
+// The factors are read in the tile layout (latent_tiles_repack, which
+// reorders each of the twelve factor tensors in place of the row layout at
+// load time): every 256 x 256 block of a factor is 32 KB of NF4 codes in the
+// order the lanes consume them, plus its 4 KB of fp16 scales in the factor's
+// scale tensor, so each lane reads its MFMA operand bytes with one 128-bit
+// load per 32-row step and every tile is one contiguous stream:
 //   * wave w owns tile columns 64w .. 64w+63 over all 256 rows; lane
 //     (n = lane & 15, kq = lane >> 4) holds, per 32-row step s, the code
 //     pairs of rows s*32 + kq*8 + (2q, 2q+1), q = 0..3, for columns
@@ -28,11 +29,12 @@
 //   * scales: half2 (scale(2P, G), scale(2P + 1, G)) for group G = 0..7 and
 //     row pair P at dword G * 128 + (P ^ 8 (G & 1)) (the xor spreads the
 //     lanes of one LDS read over all banks);
-//   * phase B's tiles interleave the two factors: for lane n of wave w the
-//     columns j = 0, 1 are gate columns 32w + 2n + j of the 128-column block
-//     and j = 2, 3 the up columns of the same outputs, so each lane forms
-//     h = SiLU(g) * u of its two columns itself; groups 0..3 are the gate
-//     groups of waves 0..3, groups 4..7 the up groups.
+//   * a phase-B tile is a 128-column half tile of gate_b and the same columns
+//     of up_b: for lane n of wave w the columns j = 0, 1 are gate columns
+//     32w + 2n + j of the 128-column block and j = 2, 3 the up columns of the
+//     same outputs, so each lane forms h = SiLU(g) * u of its two columns
+//     itself; each half tile keeps a lane's 16 bytes per K step pair, and its
+//     four scale groups become groups 0..3 (gate) and 4..7 (up) in LDS.
 // A byte (two rows of one column) is looked up in a 256-entry table of
 // (level, level) fp16 pairs in LDS, one copy per LDS bank, and one
 // v_pk_mul_f16 by the two rows' scales gives one K pair of the B operand.
@@ -73,21 +75,21 @@ constexpr int kT = 256;                               // threads per workgroup
 constexpr int kK = 256;                               // rows of a tile
 constexpr int kN = 256;                               // columns of a tile
 constexpr int kSteps = kK / 32;                       // MFMA K steps per tile
-constexpr int kCodeBytes = kK * kN / 2;               // 32 KB
-constexpr int kScaleBytes = kK * kN / kGroup * 2;     // 4 KB
-constexpr int kTileBytes = kCodeBytes + kScaleBytes;  // 36 KB
+constexpr int kCodeBytes = kK * kN / 2;               // 32 KB of a 256 x 256 tile's codes
+constexpr int kScaleBytes = kK * kN / kGroup * 2;     // 4 KB of its scales
 constexpr int kHBlock = kN / 2;                       // h columns of a phase-B tile
+constexpr int kHalfCodeBytes = kCodeBytes / 2;        // a gate_b / up_b half tile: 256 x 128
+constexpr int kHalfScaleBytes = kScaleBytes / 2;
 constexpr int kLutCopies = 32;                        // one table copy per LDS bank
 constexpr int kActChunks = kK / 8;                    // 16-byte chunks of an fp16 activation row
 constexpr int kGroupsPerCU = 2;                       // resident workgroups per CU of the item kernels
-constexpr int64_t kFlowSpinTicks = 100000000;         // bounded waits: 1 s of s_memrealtime (100 MHz)
+constexpr int64_t kSpinTicks = 100000000;             // bounded waits: 1 s of s_memrealtime (100 MHz)
 constexpr int kCombineBatch = 8;                      // slots' rows in flight per output float4 (combine)
-constexpr int kFlowMaxKTiles = 64;                    // one-launch chain: d / 256 at most
-constexpr int kFlowCntStride = 32;                    // ints between the one-launch chain's counters (128 B)
+constexpr int kMaxKTiles = 64;                        // small-batch chain: d / 256 at most
 constexpr int kRedLoads = 8;                          // partial rows in flight per reduce step
 enum Phase { kPhaseA = 0, kPhaseB, kPhaseC, kPhaseD };
-enum { T_GATE_A = 0, T_UP_A, T_GU_B, T_DOWN_A, T_DOWN_B, kTileArrays };
-enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B };
+// Factor order of latent_moe_args (src3..src14 of the ggml op).
+enum { F_GATE_A = 0, F_GATE_B, F_UP_A, F_UP_B, F_DOWN_A, F_DOWN_B, kFactors };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4v __attribute__((ext_vector_type(4)));
@@ -96,7 +98,8 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct Params {
-  const uint8_t* tiles[kTileArrays];
+  const uint8_t* codes[kFactors];   // the six factors' codes in the tile layout
+  const uint8_t* scales[kFactors];  // and their scales (fp16 bits), same order
   const int* meta;        // [4] work units
   const int4* unit_info;  // [units] {expert, first grouped pair, pairs, 0}
   const int* unit_tok;    // [units][16] token of each row
@@ -119,16 +122,10 @@ struct Params {
   int T, K, E, d, ff, P, wbd, out_mode;
   int nka, nb, nkc, nd;  // tiles per unit and factor: A (d/256), B (ff/128), C (ff/256), D (d/256)
   int G;                 // workgroups the tile ranges are cut for
-  // One-launch chain (flow_kernel) only.
+  // Bulk (prefill) launches only.
   const int* pair_tok;    // [P] token of each grouped pair
   const int* pair_slot;   // [P] slot of each grouped pair
   const float* pair_w;    // [P] router weight of each grouped pair
-  int* cnt;               // [2 maxu + 1][kFlowCntStride]: A tiles done, BC items done per unit, workgroups done
-                          // (zeroed by prep; one cache line per counter)
-  int* err;               // set when a bounded wait times out
-  int maxu;               // units bound (counter stride)
-  int maxj;               // partial-sum slots per workgroup in phase A
-  // Bulk (prefill) launches only.
   const int* nunits;      // number of units (reduce kernels; the decode launches set meta + 4)
   _Float16* yh;           // reduced output: [P][d] fp16 y rows * 2^yexp
   int* yexp;              // [P][d / 128]
@@ -253,44 +250,72 @@ __device__ __forceinline__ TileRef tile_ref(const Params& p, int t) {
   return TileRef{uniform(info[0]), uniform(info[1]), uniform(info[2]), t - u * per};
 }
 
-// Tile array, tile index and K tile of a tile.
-template <int kPhase>
-__device__ __forceinline__ const uint8_t* tile_ptr(const Params& p, const TileRef& tr, int& ks) {
-  int arr, idx;
-  ks = 0;
-  if constexpr (kPhase == kPhaseA) {
-    const int f = tr.r >= p.nka;
-    ks = tr.r - f * p.nka;
-    arr = f ? T_UP_A : T_GATE_A;
-    idx = tr.e * p.nka + ks;
-  } else if constexpr (kPhase == kPhaseB) {
-    arr = T_GU_B;
-    idx = tr.e * p.nb + tr.r;
-  } else if constexpr (kPhase == kPhaseC) {
-    ks = tr.r;
-    arr = T_DOWN_A;
-    idx = tr.e * p.nkc + ks;
-  } else {
-    arr = T_DOWN_B;
-    idx = tr.e * p.nd + tr.r;
-  }
-  return p.tiles[arr] + static_cast<int64_t>(idx) * kTileBytes;
-}
-
 // The loads below take `valid`: when false they are issued against empty
 // buffer ranges, fetch nothing and return zeros, so every step issues the same
 // loads and the compiler's wait counts hold on every path.
+
+// Scales and codes of tile idx of factor f (a 256 x 256 tile of gate_a, up_a,
+// down_a or down_b): the scale block into `sc` (the dwords of the threads
+// `sc_on` selects, zeros elsewhere), K steps [s0, s0 + ns) into cb[0 .. ns).
+template <int ns, typename Prm>
+__device__ __forceinline__ void load_full(const Prm& p, int f, int idx, bool valid, bool sc_on, int s0, int tid,
+                                          int lane, int wave, u32x4& sc, u32x4 (&cb)[kSteps]) {
+  const __amdgpu_buffer_rsrc_t rs =
+      buffer_rsrc(p.scales[f] + static_cast<int64_t>(idx) * kScaleBytes, valid ? kScaleBytes : 0);
+  sc = ld128_tile(rs, sc_on ? tid * 16 : 0x40000000u, 0);
+  const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(p.codes[f] + static_cast<int64_t>(idx) * kCodeBytes, valid ? kCodeBytes : 0);
+  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
+#pragma unroll
+  for (int s = 0; s < ns; ++s) cb[s] = ld128_tile(rc, cbase, (s0 + s) * kWave * 16);
+}
+
+// A phase-B tile, h block idx (expert-major): gate_b's and up_b's half tiles
+// of those 128 columns.  Waves 0 and 1 load the gate half tile's 2 KB of
+// scales, waves 2 and 3 the up half tile's, so the block in LDS is the gate
+// groups 0..3 followed by the up groups 4..7.  cb[0..3] hold the gate half
+// tile's K step pairs, cb[4..7] the up half tile's (see code_dword).
+template <typename Prm>
+__device__ __forceinline__ void load_btile(const Prm& p, int idx, bool valid, int tid, int lane, int wave, u32x4& sc,
+                                           u32x4 (&cb)[kSteps]) {
+  const int64_t so = static_cast<int64_t>(idx) * kHalfScaleBytes, co = static_cast<int64_t>(idx) * kHalfCodeBytes;
+  const __amdgpu_buffer_rsrc_t rs =
+      buffer_rsrc((wave < 2 ? p.scales[F_GATE_B] : p.scales[F_UP_B]) + so, valid ? kHalfScaleBytes : 0);
+  sc = ld128_tile(rs, (tid & 127) * 16, 0);
+  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(p.codes[F_GATE_B] + co, valid ? kHalfCodeBytes : 0);
+  const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(p.codes[F_UP_B] + co, valid ? kHalfCodeBytes : 0);
+  const uint32_t cbase = wave * (kSteps / 2 * kWave * 16) + lane * 16;
+#pragma unroll
+  for (int sp = 0; sp < kSteps / 2; ++sp) {
+    cb[sp] = ld128_tile(rg, cbase, sp * kWave * 16);
+    cb[kSteps / 2 + sp] = ld128_tile(ru, cbase, sp * kWave * 16);
+  }
+}
+
+// Code dword j (the B operand of MFMA j) of K step s of a register tile.  A
+// phase-B tile (kB) keeps, per lane, 16 bytes per K step pair of each half
+// tile: dwords (s even, j), (s even, j + 1), (s odd, j), (s odd, j + 1) of the
+// gate columns (j = 0, 1) in cb[s / 2] and of the up columns (j = 2, 3) in
+// cb[4 + s / 2].  Compile-time indices: no register moves.
+template <bool kB>
+__device__ __forceinline__ uint32_t code_dword(const u32x4 (&cb)[kSteps], int s, int j) {
+  if constexpr (kB) return j < 2 ? cb[s >> 1][(s & 1) * 2 + j] : cb[kSteps / 2 + (s >> 1)][(s & 1) * 2 + j - 2];
+  else return cb[s][j];
+}
 
 // A tile's scale block into `sc`, then its codes into `cb`.
 template <int kPhase>
 __device__ __forceinline__ void issue_codes(const Params& p, const TileRef& tr, int tid, int lane, int wave, bool valid,
                                             u32x4& sc, u32x4 (&cb)[kSteps]) {
-  int ks;
-  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile_ptr<kPhase>(p, tr, ks), valid ? kTileBytes : 0);
-  sc = ld128_tile(rt, tid * 16, kCodeBytes);
-  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) cb[s] = ld128_tile(rt, cbase, s * kWave * 16);
+  if constexpr (kPhase == kPhaseA) {
+    const int f = tr.r >= p.nka;
+    load_full<kSteps>(p, f ? F_UP_A : F_GATE_A, tr.e * p.nka + tr.r - f * p.nka, valid, true, 0, tid, lane, wave, sc, cb);
+  } else if constexpr (kPhase == kPhaseB) {
+    load_btile(p, tr.e * p.nb + tr.r, valid, tid, lane, wave, sc, cb);
+  } else if constexpr (kPhase == kPhaseC) {
+    load_full<kSteps>(p, F_DOWN_A, tr.e * p.nkc + tr.r, valid, true, 0, tid, lane, wave, sc, cb);
+  } else {
+    load_full<kSteps>(p, F_DOWN_B, tr.e * p.nd + tr.r, valid, true, 0, tid, lane, wave, sc, cb);
+  }
 }
 
 // A tile's activation chunks and row exponents.  Chunk tid + 256 h is 16-byte
@@ -538,7 +563,7 @@ __device__ __forceinline__ void bc_mfma(const u32x4* act0, const u32x4* act1, ui
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t x = cb[s][j];
+      const uint32_t x = code_dword<kTwo>(cb, s, j);
       const u32x4 sc = j < 2 ? sc0 : sc1;
       uint32_t f[4];
 #pragma unroll
@@ -574,7 +599,6 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
     for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
   }
   const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
-  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
   const int r0 = tid / kActChunks, ch = tid % kActChunks;
 
   // Codes and scales of tile t of the range (loads past the range fetch nothing).
@@ -583,12 +607,10 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
     const int it = lo + tt / 3, kind = tt % 3;
     const int u = it / p.nkc, j = it - u * p.nkc;
     const int e = uniform(sload4(p.unit_info + u)[0]);
-    const uint8_t* tile = kind < 2 ? p.tiles[T_GU_B] + static_cast<int64_t>(e * p.nb + 2 * j + kind) * kTileBytes
-                                   : p.tiles[T_DOWN_A] + static_cast<int64_t>(e * p.nkc + j) * kTileBytes;
-    const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, t < ntile ? kTileBytes : 0);
-    sc = ld128_tile(rt, tid * 16, kCodeBytes);
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) cb[s] = ld128_tile(rt, cbase, s * kWave * 16);
+    if (kind < 2)
+      load_btile(p, e * p.nb + 2 * j + kind, t < ntile, tid, lane, wave, sc, cb);
+    else
+      load_full<kSteps>(p, F_DOWN_A, e * p.nkc + j, t < ntile, true, 0, tid, lane, wave, sc, cb);
   };
   // Gate / up latent rows (rows past the unit's pairs repeat its last pair)
   // and exponents of item it's unit.
@@ -807,53 +829,8 @@ __global__ void __launch_bounds__(kT) combine_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// The whole chain in one persistent launch (flow_kernel)
+// Helpers of the small-batch chain (lite_kernel)
 // ---------------------------------------------------------------------------
-// Workgroup b takes, in each phase, the balanced range [N*b/G, N*(b+1)/G) of
-// that phase's work list, and streams its three ranges in order through one
-// load pipeline:
-//   A   tiles (unit, gate/up, K tile)                      N = U * 2 * nka
-//   BC  items (unit, nb): B tile nb (h for ff columns 128 nb .. 128 nb + 127,
-//       kept in LDS) and the matching 128-row half of C tile nb / 2 (those h
-//       columns times A_d's rows)                          N = U * nb
-//   D   tiles (unit, 256-column tile)                      N = U * nd
-// A tile's codes and scales are issued two tiles ahead whatever its phase,
-// so the factor stream runs on through the phase changes.
-//
-// Dependencies between workgroups:
-//   * a B tile needs the A sums of its unit: every workgroup adds, at the end
-//     of its A range, the tiles it computed of each unit to cnt[u]
-//     (2 * nka when complete) once its partial stores are drained;
-//   * a D tile needs the nb BC partials of its unit (cnt[maxu + u]), added at
-//     the end of each workgroup's BC range.
-// The consumer waits for the count, then sums the partials itself in a fixed
-// order (segment order for A, item order for BC) into fp16 rows with a
-// power-of-two exponent per row in LDS, once per unit it meets.  Partial sums
-// move through coherent (sc1) stores and loads, so no L2 write-back or
-// invalidate is needed.  Every wait is bounded and sets `err` on a timeout.
-// A workgroup never waits before it has published everything the phases
-// before the awaited one need from it (A never waits; BC waits only for A; D
-// only for BC), so with every workgroup resident (two per CU) the chain always
-// completes.
-//
-// Reduced mode ends with a grid-wide arrival count, after which every
-// workgroup sums its share of the output rows from the weighted y rows in slot
-// order; per-slot mode writes the output in phase D.
-
-struct alignas(16) FlowSmem {
-  uint32_t lut[256 * kLutCopies];     // [byte][copy]: half2(level(lo), level(hi))
-  u32x4 scales[2][kScaleBytes / 16];  // [buffer]: the tile's scale block
-  u32x4 xa[2][kMaxM * kActChunks];    // A: x rows of buffer 0 / 1; BC: gate / up latents; D: d latent (block 0)
-  u32x4 hb[kMaxM * kActChunks];       // the BC item's h rows (128 columns); reduction scratch
-  int xexp[2][kMaxM];                 // A: token exponents of buffer 0 / 1
-  int lexp[2][kMaxM];                 // latent exponents (gate / up; D: block 0)
-  int hexp[kMaxM];                    // h exponents
-  float hmax[4][kMaxM];               // per-wave row maxima of h
-  float pw[kMaxM];                    // D: router weight of each row's pair
-  int prow[kMaxM];                    // D: output row (token * k + slot) of each row's pair
-  int segslot[2][kFlowMaxKTiles];     // BC: partial-sum slots of the unit's gate / up A segments
-};
-
 // Coherent (sc1) 128-bit load and store: agent-scope, seen across XCDs.
 __device__ __forceinline__ float4 ld_coh4(const float* base, uint32_t voff) {
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(buffer_rsrc(base, 0x7FFFFFFF), voff, 0, 16);
@@ -870,125 +847,9 @@ __device__ __forceinline__ void add4(float4& a, const float4& b) {
   a.w += b.w;
 }
 
-// Balanced split of N items over G workgroups, and the workgroup owning item
-// t (N * G < 2^32 for the work lists; range_lo64 for the output rows).
+// Balanced split of N items over G workgroups (N * G < 2^32).
 __device__ __forceinline__ int range_lo(int N, int b, int G) {
   return static_cast<int>(static_cast<uint32_t>(N) * static_cast<uint32_t>(b) / static_cast<uint32_t>(G));
-}
-__device__ __forceinline__ int range_lo64(int N, int b, int G) {
-  return static_cast<int>(static_cast<int64_t>(N) * b / G);
-}
-__device__ __forceinline__ int owner_of(int t, int N, int G) {
-  return static_cast<int>((static_cast<uint32_t>(t + 1) * static_cast<uint32_t>(G) - 1u) / static_cast<uint32_t>(N));
-}
-
-// Workgroup's ranges: A tiles [a0, a0 + na), BC items [b0, b0 + nbc), D tiles
-// [d0, d0 + ndd).  Its tile sequence: the A tiles, empty tiles up to va (na
-// rounded up to a multiple of 3), the BC items' two tiles each, empty tiles up
-// to vd (a multiple of 3), then the D tiles; so every phase starts in load-ring
-// slot 0.
-struct Flow {
-  int NA, a0, na, va, NB, b0, nbc, vd, ND, d0, ndd, total;
-};
-
-// Scalar description of the workgroup's tile i (0 <= i < total).
-struct FTile {
-  int ph;     // kPhaseA .. kPhaseD (phase B and C tiles are the parts of a BC item); -1: empty
-  int u;      // unit
-  int e, start, m;
-  int k;      // A: K tile; B, C: the item's ff block nb; D: column tile
-  int key;    // A: segment key 2u + f
-  int arr, idx;
-};
-
-__device__ __forceinline__ FTile describe(const Params& p, const Flow& fl, int i) {
-  FTile d{};
-  int u;
-  if (i < fl.na) {
-    const int t = fl.a0 + i;
-    const int per = 2 * p.nka;
-    u = t / per;
-    const int r = t - u * per;
-    const int f = r >= p.nka ? 1 : 0;
-    d.ph = kPhaseA;
-    d.k = r - f * p.nka;
-    d.key = t / p.nka;
-    d.arr = f ? T_UP_A : T_GATE_A;
-  } else if (i < fl.va || (i >= fl.va + 2 * fl.nbc && i < fl.vd)) {
-    FTile z{};
-    z.ph = -1;
-    z.arr = T_GATE_A;
-    return z;
-  } else if (i < fl.va + 2 * fl.nbc) {
-    const int j = i - fl.va;
-    const int item = fl.b0 + (j >> 1);
-    u = item / p.nb;
-    d.k = item - u * p.nb;
-    d.ph = (j & 1) ? kPhaseC : kPhaseB;
-    d.arr = (j & 1) ? T_DOWN_A : T_GU_B;
-  } else {
-    const int t = fl.d0 + (i - fl.vd);
-    u = t / p.nd;
-    d.k = t - u * p.nd;
-    d.ph = kPhaseD;
-    d.arr = T_DOWN_B;
-  }
-  const i32x4 info = sload4(p.unit_info + u);
-  d.u = u;
-  d.e = uniform(info[0]);
-  d.start = uniform(info[1]);
-  d.m = uniform(info[2]);
-  if (d.ph == kPhaseA) d.idx = d.e * p.nka + d.k;
-  else if (d.ph == kPhaseB) d.idx = d.e * p.nb + d.k;
-  else if (d.ph == kPhaseC) d.idx = d.e * p.nkc + (d.k >> 1);
-  else d.idx = d.e * p.nd + d.k;
-  return d;
-}
-
-// Codes of tile d into cb (a C tile: its half k & 1, K steps 4h .. 4h + 3, into
-// cb[0..3]), its scale block into sc.  Every tile issues the same nine loads
-// (those it does not need fetch nothing: an empty buffer range, or an offset
-// past it), so the compiler's wait counts hold whatever tiles are in flight.
-__device__ __forceinline__ void flow_codes(const Params& p, const FTile& d, int tid, int lane, int wave, bool valid,
-                                           u32x4& sc, u32x4 (&cb)[kSteps]) {
-  const uint8_t* base = p.tiles[d.arr] + static_cast<int64_t>(d.idx) * kTileBytes;
-  const bool half = d.ph == kPhaseC;
-  const int h = d.k & 1;
-  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(base, valid ? kTileBytes : 0);
-  const __amdgpu_buffer_rsrc_t rhi = buffer_rsrc(base, valid && !half ? kTileBytes : 0);
-  // Half h's scales: row pairs 64h .. 64h + 63, the dwords of the threads with
-  // (tid % 32 >= 16) == h.
-  const bool sc_on = !half || (((tid & 31) >= 16) == (h != 0));
-  sc = ld128_tile(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
-  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
-  const int s0 = half ? 4 * h : 0;
-#pragma unroll
-  for (int s = 0; s < kSteps / 2; ++s) cb[s] = ld128_tile(rt, cbase, (s0 + s) * kWave * 16);
-#pragma unroll
-  for (int s = kSteps / 2; s < kSteps; ++s) cb[s] = ld128_tile(rhi, cbase, s * kWave * 16);
-}
-
-// Tokens of an A tile's rows (the thread's two activation chunks and
-// exponent row lane & 15); rows past the unit's pairs hold token 0.
-__device__ __forceinline__ void flow_toks(const Params& p, const FTile& d, int tid, int lane, bool valid, Toks& tk) {
-  const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(p.unit_tok + static_cast<int64_t>(d.u) * kMaxM, valid ? kMaxM * 4 : 0);
-  const int r0 = tid / kActChunks;
-  tk.a0 = static_cast<int>(ld32(ru, r0 * 4));
-  tk.a1 = static_cast<int>(ld32(ru, (r0 + 8) * 4));
-  tk.e = static_cast<int>(ld32(ru, (lane & 15) * 4));
-}
-
-// An A tile's activation chunks (x rows of K tile d.k) and token exponents.
-__device__ __forceinline__ void flow_act(const Params& p, const FTile& d, const Toks& tk, int tid, bool valid,
-                                         StageAct<kPhaseA>& st) {
-  const uint32_t live = valid ? 0xFFFFFFFFu : 0u;
-  const int chunk = tid % kActChunks;
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(p.xh, (static_cast<uint32_t>(p.T) * p.d * 2) & live);
-  const uint32_t col = d.k * kK * 2 + chunk * 16;
-  st.act[0] = ld128(rx, static_cast<uint32_t>(tk.a0) * p.d * 2 + col, 0);
-  st.act[1] = ld128(rx, static_cast<uint32_t>(tk.a1) * p.d * 2 + col, 0);
-  const __amdgpu_buffer_rsrc_t re = buffer_rsrc(p.xexp, (p.T * 4) & live);
-  st.ex = static_cast<int>(ld32(re, tk.e * 4));
 }
 
 // MFMA steps over code registers cb[0 .. ns): register step r is K step
@@ -996,7 +857,7 @@ __device__ __forceinline__ void flow_act(const Params& p, const FTile& d, const 
 // acc[j] += act . (codes dword j, decoded and scaled); act1 feeds the up
 // columns of a B tile (kTwo).
 template <bool kTwo, int ns>
-__device__ __forceinline__ void flow_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
+__device__ __forceinline__ void reg_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
                                           const u32x4 (&cb)[kSteps], int srow0, int n, int kq, int wave,
                                           uint32_t lut_lane, float4v (&acc)[4]) {
 #pragma unroll
@@ -1019,7 +880,7 @@ __device__ __forceinline__ void flow_mfma(const u32x4* act0, const u32x4* act1, 
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t x = cb[r][j];
+      const uint32_t x = code_dword<kTwo>(cb, r, j);
       const u32x4 sc = j < 2 ? sc0 : sc1;
       uint32_t f[4];
 #pragma unroll
@@ -1037,7 +898,7 @@ __device__ __forceinline__ void flow_mfma(const u32x4* act0, const u32x4* act1, 
 
 // A row of 256 sums (four per lane) -> fp16 row * 2^e in an LDS activation
 // block (chunk layout of act_slot) and its exponent.
-__device__ __forceinline__ void flow_finish_row(float4 s, u32x4* blk, int* exps, int r, int lane) {
+__device__ __forceinline__ void finish_row_lds(float4 s, u32x4* blk, int* exps, int r, int lane) {
   const float mx = op_over(fmaxf(fmaxf(fabsf(s.x), fabsf(s.y)), fmaxf(fabsf(s.z), fabsf(s.w))), 1, kWave, OpMax{});
   const int ex = pow2_row_exponent(mx);
   half4v h;
@@ -1049,21 +910,6 @@ __device__ __forceinline__ void flow_finish_row(float4 s, u32x4* blk, int* exps,
   if (lane == 0) exps[r] = ex;
 }
 
-// Bounded wait (thread 0) until *c >= target, then a workgroup barrier.
-__device__ __forceinline__ void flow_wait(const Params& p, const int* c, int target) {
-  if (threadIdx.x == 0) {
-    const int64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      __builtin_amdgcn_s_sleep(1);
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kFlowSpinTicks) {
-        __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-  }
-  lds_barrier();
-}
-
 // Every wave's stores (and loads) complete, then a barrier: the workgroup's
 // partial sums are visible before its counter adds.
 __device__ __forceinline__ void drain_barrier() {
@@ -1072,451 +918,6 @@ __device__ __forceinline__ void drain_barrier() {
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
-
-constexpr int kRedBatch = 4;  // partial blocks in flight per lane and row
-
-// Sums of fp32 partial rows into fp16 LDS rows.  Row q < nkeys * m is row
-// q % m of key q / m; key k has S[k] partial blocks ([16][256] fp32) at
-// src(k, s).  A row's sum is the same however many rows there are: the blocks
-// s = j, j + 4, j + 8, ... are summed in order for each j, then the four sums
-// in j order.  With one or two rows wave j takes residue j of both rows (the
-// waves' sums meet in LDS); with more rows each wave takes rows q = wave,
-// wave + 4, ... whole.
-template <typename Src>
-__device__ __forceinline__ void flow_reduce(FlowSmem& sm, int nkeys, int m, int S0, int S1, Src src, int lane,
-                                            int wave) {
-  const int R = nkeys * m;
-  if (R <= 2) {
-    const int k1 = R == 2 ? (nkeys == 2 ? 1 : 0) : 0, r1 = R == 2 ? (nkeys == 2 ? 0 : 1) : 0;
-    const int S1r = k1 ? S1 : S0;
-    float4 acc0 = make_float4(0.f, 0.f, 0.f, 0.f), acc1 = acc0;
-    const uint32_t o0 = static_cast<uint32_t>(lane * 4) * 4, o1 = static_cast<uint32_t>(r1 * kN + lane * 4) * 4;
-    for (int s = wave; s < max(S0, R == 2 ? S1r : 0); s += 4 * kRedBatch) {
-      float4 v0[kRedBatch], v1[kRedBatch];
-#pragma unroll
-      for (int j = 0; j < kRedBatch; ++j) {
-        const int ss = s + 4 * j;
-        v0[j] = ss < S0 ? ld_coh4(src(0, ss), o0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        v1[j] = R == 2 && ss < S1r ? ld_coh4(src(k1, ss), o1) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int j = 0; j < kRedBatch; ++j) {
-        add4(acc0, v0[j]);
-        add4(acc1, v1[j]);
-      }
-    }
-    float4* scratch = reinterpret_cast<float4*>(sm.hb);
-    scratch[(wave * 2) * kWave + lane] = acc0;
-    scratch[(wave * 2 + 1) * kWave + lane] = acc1;
-    lds_barrier();
-    if (wave < R) {
-      float4 t = scratch[wave * kWave + lane];
-      for (int w = 1; w < 4; ++w) add4(t, scratch[(w * 2 + wave) * kWave + lane]);
-      if (wave == 0)
-        flow_finish_row(t, sm.xa[0], sm.lexp[0], 0, lane);
-      else
-        flow_finish_row(t, sm.xa[k1], sm.lexp[k1], r1, lane);
-    }
-    return;
-  }
-  // The same order as above: blocks s = j, j + 4, ... summed per j, then j = 0..3.
-  static_assert(kRedBatch == 4, "one accumulator per block residue mod 4");
-  for (int q = wave; q < R; q += 4) {
-    const int k = q / m, r = q - k * m, S = k ? S1 : S0;
-    const uint32_t off = static_cast<uint32_t>(r * kN + lane * 4) * 4;
-    float4 acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < S; s += 4) {
-      float4 v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = s + j < S ? ld_coh4(src(k, s + j), off) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) add4(acc[j], v[j]);
-    }
-    add4(acc[0], acc[1]);
-    add4(acc[0], acc[2]);
-    add4(acc[0], acc[3]);
-    flow_finish_row(acc[0], sm.xa[k], sm.lexp[k], r, lane);
-  }
-}
-
-template <int kOutMode>
-__global__ void __launch_bounds__(kT, kGroupsPerCU) flow_kernel(Params p) {
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  __shared__ FlowSmem sm;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int wave = uniform(tid >> 6);
-  const int n = lane & 15, kq = lane >> 4;
-  const int U = uniform(sload(p.meta + 4));
-  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
-  Flow fl;
-  fl.NA = U * 2 * p.nka;
-  fl.a0 = range_lo(fl.NA, b, G);
-  fl.na = range_lo(fl.NA, b + 1, G) - fl.a0;
-  fl.NB = U * p.nb;
-  fl.b0 = range_lo(fl.NB, b, G);
-  fl.nbc = range_lo(fl.NB, b + 1, G) - fl.b0;
-  fl.ND = U * p.nd;
-  fl.d0 = range_lo(fl.ND, b, G);
-  fl.ndd = range_lo(fl.ND, b + 1, G) - fl.d0;
-  fl.va = (fl.na + 2) / 3 * 3;
-  fl.vd = fl.va + (2 * fl.nbc + 2) / 3 * 3;
-  fl.total = fl.vd + fl.ndd;
-  int* const cntA = p.cnt;
-  int* const cntC = p.cnt + p.maxu * kFlowCntStride;
-  int* const done = p.cnt + 2 * p.maxu * kFlowCntStride;
-
-  {
-    const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
-    const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
-    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
-#pragma unroll
-    for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
-  }
-  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
-
-  if (fl.total > 0) {
-    const int ntile = fl.total;
-    // Tile j's codes and scales sit in ring slot j % 3 (cb, sc), its A tokens
-    // in tk[j % 3]; tile i + 1's A activations in sa.
-    u32x4 cb[3][kSteps];
-    u32x4 sc[3];
-    StageAct<kPhaseA> sa;
-    Toks tk[3] = {};
-    float4v acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-    int bunit = -1, dunit = -1;  // units whose latents xa holds (BC) / whose d latent xa[0] holds (D)
-
-    auto stage_act = [&](int buf) __attribute__((always_inline)) {
-      const int r0 = tid / kActChunks, chunk = tid % kActChunks;
-      sm.xa[buf][act_slot(r0, chunk)] = sa.act[0];
-      sm.xa[buf][act_slot(r0 + 8, chunk)] = sa.act[1];
-      if (wave == 0 && lane < kMaxM) sm.xexp[buf][lane] = sa.ex;
-    };
-
-    // Prologue: tile 0's scales (and A activations) staged, tiles 0 and 1 in flight.
-    {
-      const FTile d0 = describe(p, fl, 0);
-      const FTile d1 = describe(p, fl, min(1, ntile - 1));
-      const bool a0 = d0.ph == kPhaseA;
-      flow_toks(p, d0, tid, lane, a0, tk[0]);
-      flow_act(p, d0, tk[0], tid, a0, sa);
-      flow_toks(p, d1, tid, lane, ntile > 1 && d1.ph == kPhaseA, tk[1]);
-      flow_codes(p, d0, tid, lane, wave, d0.ph >= 0, sc[0], cb[0]);
-      flow_codes(p, d1, tid, lane, wave, ntile > 1 && d1.ph >= 0, sc[1], cb[1]);
-      sm.scales[0][tid] = sc[0];
-      if (a0) stage_act(0);
-    }
-
-    // Loads issued by step i, after its waits: tile i + 1's activations (A),
-    // tile i + 2's tokens (A), codes and scales.  Returns whether tile i + 1
-    // is an A tile.  (Only steps of the A range can have an A tile next.)
-    auto issue = [&](int i, auto cs, auto may_a) __attribute__((always_inline)) {
-      constexpr int c1 = (decltype(cs)::value + 1) % 3, c2 = (decltype(cs)::value + 2) % 3;
-      const FTile d2 = describe(p, fl, min(i + 2, ntile - 1));
-      bool act1 = false;
-      if constexpr (decltype(may_a)::value) {
-        const FTile d1 = describe(p, fl, min(i + 1, ntile - 1));
-        act1 = i + 1 < ntile && d1.ph == kPhaseA;
-        flow_act(p, d1, tk[c1], tid, act1, sa);
-        flow_toks(p, d2, tid, lane, i + 2 < ntile && d2.ph == kPhaseA, tk[c2]);
-      }
-      flow_codes(p, d2, tid, lane, wave, i + 2 < ntile && d2.ph >= 0, sc[c2], cb[c2]);
-      return act1;
-    };
-    // End of step i: tile i + 1's scales (and A activations) into the other LDS buffer.
-    auto stage_next = [&](int i, bool act1, auto cs) __attribute__((always_inline)) {
-      constexpr int c1 = (decltype(cs)::value + 1) % 3;
-      sm.scales[(i & 1) ^ 1][tid] = sc[c1];
-      if (act1) stage_act((i & 1) ^ 1);
-    };
-
-    auto stepA = [&](int i, auto cs) __attribute__((always_inline)) {
-      constexpr int c = decltype(cs)::value;
-      const int buf = i & 1;
-      lds_barrier();  // LDS buffer `buf` holds tile i; every wave is done with tile i - 1
-      const bool act1 = issue(i, cs, std::true_type{});
-      if (i >= fl.na) {  // empty tile: only the loads above
-        stage_next(i, act1, cs);
-        return;
-      }
-      const FTile d = describe(p, fl, i);
-      flow_mfma<false, kSteps>(sm.xa[buf], sm.xa[buf], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane,
-                               acc);
-      // End of a segment (last A tile of the range, or of this key): one partial.
-      if (i + 1 == fl.na || (fl.a0 + i + 1) % p.nka == 0) {
-        const int slot = b * p.maxj + d.key - fl.a0 / p.nka;
-        float* part = p.partA + static_cast<int64_t>(slot) * kMaxM * kN;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = kq * 4 + v;
-          if (row < d.m) {
-            const float s = ldexpf(1.0f, -sm.xexp[buf][row]);
-            st_coh4(part, static_cast<uint32_t>(row * kN + wave * 64 + n * 4) * 4,
-                    make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      }
-      if (i + 1 == fl.na) {
-        // Publish: the tiles of each unit this range computed.
-        drain_barrier();
-        const int per = 2 * p.nka;
-        const int u0 = fl.a0 / per, u1 = (fl.a0 + fl.na - 1) / per;
-        if (tid <= u1 - u0) {
-          const int u = u0 + tid;
-          const int lo = max(fl.a0, u * per), hi = min(fl.a0 + fl.na, (u + 1) * per);
-          __hip_atomic_fetch_add(cntA + u * kFlowCntStride, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      stage_next(i, act1, cs);
-    };
-
-    // B tile of a BC item; the first of each unit waits for the unit's A sums
-    // and reduces them into the gate / up latents.
-    auto stepB = [&](int i, auto cs) __attribute__((always_inline)) {
-      constexpr int c = decltype(cs)::value;
-      const int buf = i & 1;
-      lds_barrier();
-      const FTile d = describe(p, fl, i);
-      if (d.u != bunit) {
-        bunit = d.u;
-        // Segments of key 2u + k: the workgroups whose A ranges meet its tiles
-        // (consecutive workgroups when every range is non-empty, else one
-        // workgroup per tile); thread k * 64 + s finds segment s's slot.
-        const bool full = fl.NA >= G;
-        auto nseg = [&](int key) {
-          const int t0 = key * p.nka;
-          return full ? owner_of(t0 + p.nka - 1, fl.NA, G) - owner_of(t0, fl.NA, G) + 1 : p.nka;
-        };
-        const int key0 = 2 * d.u;
-        const int S0 = nseg(key0), S1 = nseg(key0 + 1);
-        {
-          const int k = tid >> 6, s = tid & 63;
-          if (k < 2 && s < (k ? S1 : S0)) {
-            const int key = key0 + k, t0 = key * p.nka;
-            const int ob = full ? owner_of(t0, fl.NA, G) + s : owner_of(t0 + s, fl.NA, G);
-            sm.segslot[k][s] = ob * p.maxj + key - range_lo(fl.NA, ob, G) / p.nka;
-          }
-        }
-        flow_wait(p, cntA + d.u * kFlowCntStride, 2 * p.nka);
-        auto src = [&](int k, int s) { return p.partA + static_cast<int64_t>(sm.segslot[k][s]) * kMaxM * kN; };
-        flow_reduce(sm, 2, d.m, S0, S1, src, lane, wave);
-        lds_barrier();
-      }
-      const bool act1 = issue(i, cs, std::false_type{});
-      flow_mfma<true, kSteps>(sm.xa[0], sm.xa[1], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane, acc);
-      // h = SiLU(g) * u of columns 32w + 2n + jj of the item's 128 into the h
-      // rows, fp16 with one exponent per row.
-      float hv[2][4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        const float sg = ldexpf(1.0f, -sm.lexp[0][row]), su = ldexpf(1.0f, -sm.lexp[1][row]);
-        float mx = 0.f;
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          hv[jj][v] = silu(acc[jj][v] * sg) * (acc[jj + 2][v] * su);
-          mx = fmaxf(mx, fabsf(hv[jj][v]));
-        }
-        mx = op_over(mx, 1, 16, OpMax{});
-        if (n == 0) sm.hmax[wave][row] = mx;
-      }
-      lds_barrier();
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        const float mx = fmaxf(fmaxf(sm.hmax[0][row], sm.hmax[1][row]), fmaxf(sm.hmax[2][row], sm.hmax[3][row]));
-        const int ex = pow2_row_exponent(mx);
-        half2v hh;
-        hh[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
-        hh[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
-        reinterpret_cast<half2v*>(&sm.hb[act_slot(row, 4 * wave + (n >> 2))])[n & 3] = hh;
-        if (wave == 0 && n == 0) sm.hexp[row] = ex;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      stage_next(i, act1, cs);
-    };
-
-    // C half tile of a BC item: the item's h rows times A_d's 128 rows ->
-    // the item's partial d latent.
-    auto stepC = [&](int i, auto cs) __attribute__((always_inline)) {
-      constexpr int c = decltype(cs)::value;
-      const int buf = i & 1;
-      lds_barrier();
-      const FTile d = describe(p, fl, i);
-      const bool act1 = issue(i, cs, std::false_type{});
-      flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[buf][0]), cb[c], 4 * (d.k & 1), n, kq, wave,
-                                   lut_lane, acc);
-      float* part = p.partC + (static_cast<int64_t>(d.u) * p.nb + d.k) * kMaxM * kN;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        if (row < d.m) {
-          const float s = ldexpf(1.0f, -sm.hexp[row]);
-          st_coh4(part, static_cast<uint32_t>(row * kN + wave * 64 + n * 4) * 4,
-                  make_float4(acc[0][v] * s, acc[1][v] * s, acc[2][v] * s, acc[3][v] * s));
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      if (i + 1 == fl.va + 2 * fl.nbc) {
-        // Publish: the BC items of each unit this range computed.
-        drain_barrier();
-        const int u0 = fl.b0 / p.nb, u1 = (fl.b0 + fl.nbc - 1) / p.nb;
-        if (tid <= u1 - u0) {
-          const int u = u0 + tid;
-          const int lo = max(fl.b0, u * p.nb), hi = min(fl.b0 + fl.nbc, (u + 1) * p.nb);
-          __hip_atomic_fetch_add(cntC + u * kFlowCntStride, hi - lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      stage_next(i, act1, cs);
-    };
-
-    // D tile: the first of each unit waits for its BC partials and reduces
-    // them into the d latent; then y for 256 output columns.
-    auto stepD = [&](int i, auto cs) __attribute__((always_inline)) {
-      constexpr int c = decltype(cs)::value;
-      const int buf = i & 1;
-      lds_barrier();
-      const FTile d = describe(p, fl, i);
-      if (d.u != dunit) {
-        dunit = d.u;
-        // The unit's pair weights and output rows, read here (the wait below
-        // drains the loads anyway) rather than behind the tile's code loads.
-        if (tid < d.m) {
-          const int pair = d.start + tid;
-          sm.pw[tid] = p.pair_w[pair];
-          sm.prow[tid] = p.pair_tok[pair] * p.K + p.pair_slot[pair];
-        }
-        flow_wait(p, cntC + d.u * kFlowCntStride, p.nb);
-        auto src = [&](int, int s) { return p.partC + (static_cast<int64_t>(d.u) * p.nb + s) * kMaxM * kN; };
-        flow_reduce(sm, 1, d.m, p.nb, 0, src, lane, wave);
-        lds_barrier();
-      }
-      const bool act1 = issue(i, cs, std::false_type{});
-      flow_mfma<false, kSteps>(sm.xa[0], sm.xa[0], lds_addr(sm.scales[buf][0]), cb[c], 0, n, kq, wave, lut_lane, acc);
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = kq * 4 + v;
-        if (row < d.m) {
-          const int pair = d.start + row;
-          const float w = sm.pw[row];
-          const float s = ldexpf(1.0f, -sm.lexp[0][row]);
-          const int col = d.k * kN + wave * 64 + n * 4;
-          if constexpr (kOutMode == LATENT_OUT_PER_SLOT) {
-            const float sw = p.wbd ? s * w : s;
-            const int64_t orow = sm.prow[row];
-            *reinterpret_cast<float4*>(p.out + orow * p.d + col) =
-                make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw);
-          } else {
-            const float sw = s * w;
-            st_coh4(p.ybuf, static_cast<uint32_t>(static_cast<int64_t>(pair) * p.d + col) * 4,
-                    make_float4(acc[0][v] * sw, acc[1][v] * sw, acc[2][v] * sw, acc[3][v] * sw));
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      stage_next(i, act1, cs);
-    };
-
-    // An empty tile: only the loads of later tiles.
-    auto stepE = [&](int i, auto cs) __attribute__((always_inline)) {
-      lds_barrier();
-      stage_next(i, issue(i, cs, std::false_type{}), cs);
-    };
-    // Tile i sits in ring slot i % 3; every phase starts at a multiple of 3.
-    for (int i = 0; i < fl.va; i += 3) {
-      stepA(i, I0{});
-      stepA(i + 1, I1{});
-      stepA(i + 2, I2{});
-    }
-    // BC: three items (six tiles) per pass; positions past the last item up
-    // to vd are empty tiles.
-    for (int i = fl.va; i < fl.vd; i += 6) {
-      const int left = fl.va + 2 * fl.nbc - i;  // BC tiles from i on
-      stepB(i, I0{});
-      stepC(i + 1, I1{});
-      if (left > 2) stepB(i + 2, I2{}); else stepE(i + 2, I2{});
-      if (i + 3 >= fl.vd) break;
-      if (left > 3) stepC(i + 3, I0{}); else stepE(i + 3, I0{});
-      if (left > 4) stepB(i + 4, I1{}); else stepE(i + 4, I1{});
-      if (left > 5) stepC(i + 5, I2{}); else stepE(i + 5, I2{});
-    }
-    for (int i = fl.vd; i < ntile; i += 3) {
-      stepD(i, I0{});
-      if (i + 1 < ntile) stepD(i + 1, I1{});
-      if (i + 2 < ntile) stepD(i + 2, I2{});
-    }
-  }
-
-  if constexpr (kOutMode == LATENT_OUT_REDUCED) {
-    // Every workgroup's y rows are stored: then out rows by slot-order sums.
-    drain_barrier();
-    if (tid == 0) __hip_atomic_fetch_add(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flow_wait(p, done, G);
-    const int d4 = p.d / 4;
-    const int total4 = p.T * d4;
-    const int lo = range_lo64(total4, b, G), hi = range_lo64(total4, b + 1, G);
-    for (int i = lo + tid; i < hi; i += kT) {
-      const int t = i / d4, c4 = i - t * d4;
-      float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int k0 = 0; k0 < p.K; k0 += kCombineBatch) {
-        // A batch of slots' rows in flight, then their sum in slot order.
-        float4 v[kCombineBatch];
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) {
-          const int slot = t * p.K + k0 + j;
-          const int e = k0 + j < p.K ? p.ids[slot] : -1;
-          v[j] = e >= 0 && e < p.E
-                     ? ld_coh4(p.ybuf, static_cast<uint32_t>(static_cast<int64_t>(p.pos_of[slot]) * p.d + c4 * 4) * 4)
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < kCombineBatch; ++j) add4(s, v[j]);
-      }
-      reinterpret_cast<float4*>(p.out)[i] = s;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Batches of a few routed pairs: one launch with every tile in flight from the
-// start (lite_kernel)
-// ---------------------------------------------------------------------------
-// For at most kLiteMaxP routed pairs.  Every workgroup groups the pairs itself
-// (wave 0: units are the distinct experts in order of first appearance, a
-// unit's pairs in index order), then takes one role by its index:
-//   [0, gA)          A:  up to kLiteSlots K tiles (unit, gate/up, k): x . A
-//   [gA, gA + gB)    BC: one item (unit, 128-column h block): its B tile and
-//                        the matching half of a C tile
-//   [gA + gB, G)     D:  up to kLiteSlots column tiles (unit, n): d_lat . B_d
-// and issues the loads of all its tiles (codes and scales into registers, an A
-// tile's x slices too) before anything else, so the whole factor stream is in
-// flight at once.  Dependencies point to lower workgroup indices only (BC waits
-// for A, D for BC), so the chain completes even when not every workgroup is
-// resident.
-//   * A writes one partial per tile ([gate/up][k][pair][256] fp32, coherent
-//     stores) and, once they are drained, adds one per tile to cntA[u];
-//   * BC waits for cntA[u] == 2 nka, sums the partials in k order into the gate
-//     and up latents (fp16 rows * 2^e in LDS), forms h for its 128 columns in
-//     LDS and writes its C half tile's partial ([nb][pair][256]); cntC[u] += 1;
-//   * D waits for cntC[u] == nb, sums the nb partials into the down latent and
-//     writes y rows: per-slot output straight to out; reduced output to ybuf,
-//     and each (token, column tile) counts its routed rows: the workgroup whose
-//     row completes the count sums the token's rows in slot order into out.
-// Counters are reset by their last user (cntA[u] by the workgroup holding D
-// tile (u, 0), after cntC[u] is complete; cntC[u] and cntD[u] by the unit's
-// last D tile; a (token, tile) count by its last arriver), so they are zero
-// again when the kernel ends.  x enters A as fp16 with one power-of-two
-// exponent per (token, 256-column slice), taken from the slice itself.
 
 constexpr int kLiteMaxP = 16;  // routed pairs the small-batch chain takes
 constexpr int kLiteSlots = 3;  // tiles a workgroup holds in registers
@@ -1530,7 +931,8 @@ constexpr int kLiteKeyStride = 16;   // ints between (token, tile) counters (64 
 constexpr int64_t kLiteLateTicks = 300;  // 3 us of s_memrealtime (100 MHz)
 
 struct LiteParams {
-  const uint8_t* tiles[kTileArrays];
+  const uint8_t* codes[kFactors];   // the six factors in the tile layout (Params' order)
+  const uint8_t* scales[kFactors];
   const void* x;
   int x_dtype;
   const int32_t* ids;
@@ -1639,7 +1041,7 @@ __device__ __forceinline__ void lite_wait(int* err, const int* c, int target) {
     const int64_t t0 = __builtin_amdgcn_s_memrealtime();
     while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(2);
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kFlowSpinTicks) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kSpinTicks) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
@@ -1675,17 +1077,6 @@ __device__ __forceinline__ void lite_x8(const u32x4& a, const u32x4& b, int dtyp
   }
 }
 
-// Codes and scales of one tile: steps [s0, s0 + ns) into cb[0 .. ns) and the
-// scale dwords of the threads `sc_on` selects (zeros elsewhere).
-template <int ns>
-__device__ __forceinline__ void lite_codes(const uint8_t* tile, bool valid, bool sc_on, int s0, int tid, int lane,
-                                           int wave, u32x4& sc, u32x4 (&cb)[kSteps]) {
-  const __amdgpu_buffer_rsrc_t rt = buffer_rsrc(tile, valid ? kTileBytes : 0);
-  sc = ld128_tile(rt, sc_on ? tid * 16 : 0x40000000u, kCodeBytes);
-  const uint32_t cbase = wave * (kSteps * kWave * 16) + lane * 16;
-#pragma unroll
-  for (int s = 0; s < ns; ++s) cb[s] = ld128_tile(rt, cbase, (s0 + s) * kWave * 16);
-}
 
 
 // Sums of partial rows into fp16 latent rows (act block k, exponents rexp[k])
@@ -1724,7 +1115,7 @@ __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, in
       float4 t = sm.red[rr][k * kChains][lane];
 #pragma unroll
       for (int ch = 1; ch < kChains; ++ch) add4(t, sm.red[rr][k * kChains + ch][lane]);
-      flow_finish_row(t, sm.act[k], sm.rexp[k], r0 + rr, lane);
+      finish_row_lds(t, sm.act[k], sm.rexp[k], r0 + rr, lane);
     }
     lds_barrier();
   }
@@ -1797,8 +1188,7 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
     const int t = j0 + min(j, nj - 1);
     const int u = t / per, r = t - u * per, f = r >= p.nka ? 1 : 0, k = r - f * p.nka;
     const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
-    lite_codes<kSteps>(p.tiles[f ? T_UP_A : T_GATE_A] + static_cast<int64_t>(e * p.nka + k) * kTileBytes, valid, true,
-                       0, tid, lane, wave, sc[j], cb[j]);
+    load_full<kSteps>(p, f ? F_UP_A : F_GATE_A, e * p.nka + k, valid, true, 0, tid, lane, wave, sc[j], cb[j]);
     if (j < 2) load_x(j, valid, xr[j]);
   }
   // Tile j into LDS buffer `buf`: its scales, and its x rows as fp16 * 2^e
@@ -1849,7 +1239,7 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
                lut_lane, acc0, acc1);
     store_part(1, 1, acc1);
   } else {
-    flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[0], 0, n, kq, wave, lut_lane, acc0);
+    reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[0], 0, n, kq, wave, lut_lane, acc0);
   }
   store_part(0, 0, acc0);
   if (nj > 2) {
@@ -1859,7 +1249,7 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
     load_x(2, true, xr[0]);  // only workgroups with three tiles get here
     stage(2, 0, xr[0]);
     lds_barrier();
-    flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[2], 0, n, kq, wave, lut_lane, acc0);
+    reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[2], 0, n, kq, wave, lut_lane, acc0);
     store_part(2, 0, acc0);
   }
   // Publish once every partial is stored.
@@ -1876,11 +1266,10 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
   const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
   u32x4 cbB[kSteps], cbC[kSteps], scB, scC;
   lite_sleep_until(t0, kLiteLateTicks);
-  lite_codes<kSteps>(p.tiles[T_GU_B] + static_cast<int64_t>(e * p.nb + kb) * kTileBytes, true, true, 0, tid, lane,
-                     wave, scB, cbB);
+  load_btile(p, e * p.nb + kb, true, tid, lane, wave, scB, cbB);
   // C tile kb / 2, K half hh: steps 4hh .. 4hh + 3 and the scales of row pairs 64hh .. 64hh + 63.
-  lite_codes<kSteps / 2>(p.tiles[T_DOWN_A] + static_cast<int64_t>(e * p.nkc + (kb >> 1)) * kTileBytes, true,
-                         ((tid & 31) >= 16) == (hh != 0), 4 * hh, tid, lane, wave, scC, cbC);
+  load_full<kSteps / 2>(p, F_DOWN_A, e * p.nkc + (kb >> 1), true, ((tid & 31) >= 16) == (hh != 0), 4 * hh, tid, lane,
+                        wave, scC, cbC);
   lite_wait(p.err, p.cntA + u * kLiteUnitStride, 2 * p.nka);
   lite_latents<2>(sm, p.partA, p.P, p.nka, start, m, lane, wave);
   sm.scales[0][tid] = scB;
@@ -1889,7 +1278,7 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
   float4v acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-  flow_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), cbB, 0, n, kq, wave, lut_lane, acc);
+  reg_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), cbB, 0, n, kq, wave, lut_lane, acc);
   // h = SiLU(g) * u of columns 32w + 2n + jj of the block, fp16 with one exponent per row.
   float hv[2][4];
 #pragma unroll
@@ -1920,7 +1309,7 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
   lds_barrier();
-  flow_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[1][0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
+  reg_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[1][0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int row = kq * 4 + v;
@@ -1946,8 +1335,7 @@ __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, i
     const int t = j0 + min(j, nj - 1);
     const int u = t / p.nd, s = t - u * p.nd;
     const int e = uniform(sm.ue[u]);
-    lite_codes<kSteps>(p.tiles[T_DOWN_B] + static_cast<int64_t>(e * p.nd + s) * kTileBytes, j < nj, true, 0, tid,
-                       lane, wave, sc[j], cb[j]);
+    load_full<kSteps>(p, F_DOWN_B, e * p.nd + s, j < nj, true, 0, tid, lane, wave, sc[j], cb[j]);
   }
   // Wait for unit u's C partials and sum them into the down latent (act
   // block 0); the workgroup holding D tile (u, 0) resets cntA[u] (every BC
@@ -2012,7 +1400,7 @@ __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, i
         float4v acc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
-        flow_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[j], 0, n, kq, wave, lut_lane, acc);
+        reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[j], 0, n, kq, wave, lut_lane, acc);
         store_y(j, acc);
       }
     }
@@ -2217,7 +1605,7 @@ __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32
     half8 bf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t x = cb[s][j];
+      const uint32_t x = code_dword<kPhase == kPhaseB>(cb, s, j);
       const u32x4 sc = j < 2 ? sc0 : sc1;
       uint32_t f[4];
 #pragma unroll
@@ -2584,102 +1972,128 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile layout (latent_stream_tiles_pack)
+// Tile layout (latent_tiles_repack)
 // ---------------------------------------------------------------------------
-struct PackParams {
-  Factor fac[6];  // gate_a, gate_b, up_a, up_b, down_a, down_b
-  uint8_t* dst[kTileArrays];
-  int64_t ntiles[kTileArrays];  // tiles of each array (all experts)
-  int per_expert[kTileArrays];
-  int64_t total16;              // 16-byte units over all arrays
+// Each factor tensor holds its own tiles, expert-major (expert e's tiles are
+// the same byte range of the tensor as its rows in the row layout):
+//   K tiles  gate_a, up_a, down_a: 256-row K slices (all 256 columns), tile t
+//            = rows 256 t ..; 32 KB of codes, 4 KB of scales;
+//   N tiles  down_b: 256-column slices (all 256 rows), tile t = columns 256 t ..;
+//   H tiles  gate_b, up_b: 128-column half tiles (all 256 rows), 16 KB + 2 KB.
+// A tile's codes are 16-byte units, one per (wave w, K step s or step pair
+// sp, lane): unit (w * 8 + s) * 64 + lane of a K / N tile holds, in dword j,
+// the code pairs of rows 32 s + 8 kq + (2q, 2q + 1) (byte q, low nibble = even
+// row) of column 64 w + 4 n + j (n = lane & 15, kq = lane >> 4); unit
+// (w * 4 + sp) * 64 + lane of an H tile holds in dword 2 h + jj the code pairs
+// of K step s = 2 sp + h, column 32 w + 2 n + jj.  Scales: dword G * 128 + (P
+// ^ 8 (G & 1)) holds the fp16 scales of rows 2P and 2P + 1 of the tile's
+// 32-column group G (8 groups in a K / N tile, 4 in an H tile).
+enum TileKind { kKindK = 0, kKindN, kKindH };
+
+__host__ __device__ inline int tile_kind(int f) {
+  return f == F_GATE_B || f == F_UP_B ? kKindH : f == F_DOWN_B ? kKindN : kKindK;
+}
+
+struct RepackParams {
+  uint8_t* rcodes;    // row layout: u8 [E][rows][cols / 2]
+  uint16_t* rscales;  //             u16 [E][rows][cols / 32]
+  uint8_t* tcodes;    // tile layout, same sizes
+  uint16_t* tscales;
+  int kind;
+  int64_t rows, cols;
+  int64_t code_units;    // 16-byte units over all experts (0: codes not repacked)
+  int64_t scale_dwords;  // scale dwords over all experts (0: scales not repacked)
 };
 
-__device__ __forceinline__ int nibble(const Factor& f, int64_t e, int64_t row, int64_t col) {
-  const uint8_t v = f.codes[(e * f.rows + row) * f.code_stride() + col / 2];
-  return (v >> ((col & 1) * 4)) & 15;
+// Row base and column (within the expert) of dword dw of code unit u of an
+// expert's tile-layout codes: byte q of the dword holds rows rbase + 2q
+// (low nibble) and rbase + 2q + 1 of that column.
+__device__ __forceinline__ void unit_coords(int kind, int64_t u, int dw, int64_t& rbase, int64_t& col) {
+  const int per = kind == kKindH ? kHalfCodeBytes / 16 : kCodeBytes / 16;
+  const int64_t t = u / per;
+  const int k16 = static_cast<int>(u - t * per);
+  const int lane = k16 % kWave, nn = lane & 15, kq = lane >> 4;
+  if (kind == kKindH) {
+    const int w = k16 / (kSteps / 2 * kWave), sp = (k16 / kWave) % (kSteps / 2);
+    rbase = (2 * sp + (dw >> 1)) * 32 + kq * 8;
+    col = t * kHBlock + 32 * w + 2 * nn + (dw & 1);
+  } else {
+    const int w = k16 / (kSteps * kWave), s = (k16 / kWave) % kSteps;
+    rbase = (kind == kKindK ? t * kK : 0) + s * 32 + kq * 8;
+    col = (kind == kKindN ? t * kN : 0) + 64 * w + 4 * nn + dw;
+  }
 }
 
-// Source factor, first row and column of tile column c of tile t of array arr.
-__device__ __forceinline__ const Factor& src_col(const PackParams& pp, int arr, int t, int c, int64_t& row0,
-                                                 int64_t& col) {
-  if (arr == T_GU_B) {
-    const int w = c >> 6, nn = (c >> 2) & 15, j = c & 3;
-    row0 = 0;
-    col = static_cast<int64_t>(t) * kHBlock + 32 * w + 2 * nn + (j & 1);
-    return pp.fac[j < 2 ? F_GATE_B : F_UP_B];
-  }
-  if (arr == T_DOWN_B) {
-    row0 = 0;
-    col = static_cast<int64_t>(t) * kN + c;
-    return pp.fac[F_DOWN_B];
-  }
-  row0 = static_cast<int64_t>(t) * kK;
-  col = c;
-  return pp.fac[arr == T_GATE_A ? F_GATE_A : arr == T_UP_A ? F_UP_A : F_DOWN_A];
+// Row pair and group (within the expert) of scale dword i of an expert's
+// tile-layout scales: the scales of rows `row` and row + 1.
+__device__ __forceinline__ void scale_coords(int kind, int64_t i, int64_t& row, int64_t& grp) {
+  const int per = kind == kKindH ? kHalfScaleBytes / 4 : kScaleBytes / 4;
+  const int64_t t = i / per;
+  const int dw = static_cast<int>(i - t * per);
+  const int G = dw / 128, P = (dw % 128) ^ ((G & 1) << 3);
+  row = (kind == kKindK ? t * kK : 0) + 2 * P;
+  grp = kind == kKindK ? G : t * (kind == kKindN ? kN / kGroup : kHBlock / kGroup) + G;
 }
 
-// Source factor, first row and scale group of tile group G of tile t of array arr.
-__device__ __forceinline__ const Factor& src_group(const PackParams& pp, int arr, int t, int G, int64_t& row0,
-                                                   int64_t& grp) {
-  if (arr == T_GU_B) {
-    row0 = 0;
-    grp = static_cast<int64_t>(t) * (kHBlock / kGroup) + (G & 3);
-    return pp.fac[G < 4 ? F_GATE_B : F_UP_B];
-  }
-  if (arr == T_DOWN_B) {
-    row0 = 0;
-    grp = static_cast<int64_t>(t) * (kN / kGroup) + G;
-    return pp.fac[F_DOWN_B];
-  }
-  row0 = static_cast<int64_t>(t) * kK;
-  grp = G;
-  return pp.fac[arr == T_GATE_A ? F_GATE_A : arr == T_UP_A ? F_UP_A : F_DOWN_A];
-}
-
-__global__ void __launch_bounds__(kT) pack_kernel(PackParams pp) {
-  constexpr int kUnits = kTileBytes / 16;  // 16-byte units per tile
-  for (int64_t g = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; g < pp.total16;
-       g += static_cast<int64_t>(gridDim.x) * kT) {
-    int arr = 0;
-    int64_t rem = g;
-    while (arr < kTileArrays - 1 && rem >= pp.ntiles[arr] * kUnits) {
-      rem -= pp.ntiles[arr] * kUnits;
-      ++arr;
-    }
-    const int64_t tile = rem / kUnits;
-    const int k16 = static_cast<int>(rem - tile * kUnits);
-    const int64_t e = tile / pp.per_expert[arr];
-    const int t = static_cast<int>(tile - e * pp.per_expert[arr]);
-    uint32_t out[4];
-    if (k16 < kCodeBytes / 16) {
-      const int w = k16 / (kSteps * kWave), s = (k16 / kWave) % kSteps, lane = k16 % kWave;
-      const int nn = lane & 15, kq = lane >> 4;
-      const int r0 = s * 32 + kq * 8;
+// One direction of the repack, grid-stride over the code units, then the
+// scale dwords: kToTiles gathers each tile unit's 32 nibbles from the row
+// layout; the inverse scatters them back as whole row bytes (the columns of a
+// row byte, 2c and 2c + 1, are dwords (0, 1) or (2, 3) of one unit).
+template <bool kToTiles>
+__global__ void __launch_bounds__(kT) repack_kernel(RepackParams rp) {
+  const int64_t upe = rp.rows * rp.cols / 32;            // code units per expert
+  const int64_t dpe = rp.rows * rp.cols / kGroup / 2;    // scale dwords per expert
+  const int64_t rstride = rp.cols / 2, sstride = rp.cols / kGroup;
+  const int64_t n = rp.code_units + rp.scale_dwords;
+  for (int64_t g = blockIdx.x * static_cast<int64_t>(kT) + threadIdx.x; g < n; g += static_cast<int64_t>(gridDim.x) * kT) {
+    if (g < rp.code_units) {
+      const int64_t e = g / upe, u = g - e * upe;
+      uint8_t* rbytes = rp.rcodes + e * rp.rows * rstride;
+      uint4* tunit = reinterpret_cast<uint4*>(rp.tcodes) + g;
+      if constexpr (kToTiles) {
+        uint32_t out[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int64_t row0, col;
-        const Factor& f = src_col(pp, arr, t, 64 * w + 4 * nn + j, row0, col);
-        uint32_t word = 0;
+        for (int dw = 0; dw < 4; ++dw) {
+          int64_t rb, c;
+          unit_coords(rp.kind, u, dw, rb, c);
+          uint32_t word = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int lo = nibble(f, e, row0 + r0 + 2 * q, col), hi = nibble(f, e, row0 + r0 + 2 * q + 1, col);
-          word |= static_cast<uint32_t>(lo | (hi << 4)) << (8 * q);
+          for (int q = 0; q < 8; ++q) {
+            const uint8_t v = rbytes[(rb + q) * rstride + c / 2];
+            word |= static_cast<uint32_t>((v >> ((c & 1) * 4)) & 15u) << (4 * q);
+          }
+          out[dw] = word;
         }
-        out[j] = word;
+        *tunit = make_uint4(out[0], out[1], out[2], out[3]);
+      } else {
+        const uint4 in = *tunit;
+        const uint32_t w[4] = {in.x, in.y, in.z, in.w};
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          int64_t rb, c;
+          unit_coords(rp.kind, u, 2 * pr, rb, c);  // dword 2 pr + 1: column c + 1, same rows
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const uint32_t lo = (w[2 * pr] >> (4 * q)) & 15u, hi = (w[2 * pr + 1] >> (4 * q)) & 15u;
+            rbytes[(rb + q) * rstride + c / 2] = static_cast<uint8_t>(lo | (hi << 4));
+          }
+        }
       }
     } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dw = (k16 - kCodeBytes / 16) * 4 + i;
-        const int G = dw / 128, P = (dw % 128) ^ ((G & 1) << 3);
-        int64_t row0, grp;
-        const Factor& f = src_group(pp, arr, t, G, row0, grp);
-        const uint16_t s0 = f.scales[(e * f.rows + row0 + 2 * P) * f.scale_stride() + grp];
-        const uint16_t s1 = f.scales[(e * f.rows + row0 + 2 * P + 1) * f.scale_stride() + grp];
-        out[i] = static_cast<uint32_t>(s0) | (static_cast<uint32_t>(s1) << 16);
+      const int64_t i = g - rp.code_units;
+      const int64_t e = i / dpe, k = i - e * dpe;
+      int64_t row, grp;
+      scale_coords(rp.kind, k, row, grp);
+      uint16_t* rs = rp.rscales + e * rp.rows * sstride;
+      uint32_t* ts = reinterpret_cast<uint32_t*>(rp.tscales) + i;
+      if constexpr (kToTiles) {
+        *ts = static_cast<uint32_t>(rs[row * sstride + grp]) | (static_cast<uint32_t>(rs[(row + 1) * sstride + grp]) << 16);
+      } else {
+        const uint32_t v = *ts;
+        rs[row * sstride + grp] = static_cast<uint16_t>(v & 0xFFFFu);
+        rs[(row + 1) * sstride + grp] = static_cast<uint16_t>(v >> 16);
       }
     }
-    reinterpret_cast<uint4*>(pp.dst[arr] + tile * kTileBytes)[k16] = make_uint4(out[0], out[1], out[2], out[3]);
   }
 }
 
@@ -2699,43 +2113,36 @@ namespace stream {
 static bool aligned16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 // Layers the tile layout exists for: pure NF4, rank 256, d and ff multiples of 256.
-static bool tiles_shape_ok(const latent_moe_args& a) {
+bool tiles_shape_ok(const latent_moe_args& a) {
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
-  for (const latent_factor* f : fs) {
+  for (const latent_factor* f : fs)
     if (f->int8_bitmap || f->int8_row_offset || f->int8_data) return false;
-    if (!f->codes || !f->scales) return false;
-  }
   return a.max_rank == kK && a.n_embd % kK == 0 && a.n_ff % kK == 0 && a.n_expert >= 1 && a.n_expert <= 4096 &&
          a.n_embd <= (1 << 16) && a.n_ff <= (1 << 16);
 }
 
-struct TileSizes {
-  int64_t ntiles[kTileArrays];
-  int per_expert[kTileArrays];
-  size_t offset[kTileArrays];
-  size_t total;
-};
+// A call whose factors are in the tile layout: the shapes it exists for and
+// 16-byte aligned code and scale tensors (the kernels' 128-bit loads).
+static bool tiles_given(const latent_moe_args& a) {
+  if (a.layout != LATENT_LAYOUT_TILES || !tiles_shape_ok(a)) return false;
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  for (const latent_factor* f : fs)
+    if (!f->codes || !f->scales || !aligned16(f->codes) || !aligned16(f->scales)) return false;
+  return true;
+}
 
-static TileSizes tile_sizes(const latent_moe_args& a) {
-  TileSizes ts{};
-  const int nka = static_cast<int>(a.n_embd / kK), nb = static_cast<int>(a.n_ff / kHBlock);
-  const int nkc = static_cast<int>(a.n_ff / kK), nd = static_cast<int>(a.n_embd / kN);
-  const int per[kTileArrays] = {nka, nka, nb, nkc, nd};
-  size_t off = 0;
-  for (int i = 0; i < kTileArrays; ++i) {
-    ts.per_expert[i] = per[i];
-    ts.ntiles[i] = a.n_expert * per[i];
-    ts.offset[i] = off;
-    off += static_cast<size_t>(ts.ntiles[i]) * kTileBytes;
+template <typename Prm>
+static void set_tiles(const latent_moe_args& a, Prm& p) {
+  const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
+  for (int i = 0; i < kFactors; ++i) {
+    p.codes[i] = fs[i]->codes;
+    p.scales[i] = reinterpret_cast<const uint8_t*>(fs[i]->scales);
   }
-  ts.total = off;
-  return ts;
 }
 
 bool supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
-  return a.stream_tiles != nullptr && aligned16(a.stream_tiles) && tiles_shape_ok(a) && P >= 1 && P <= 4096 &&
-         aligned16(a.x);
+  return tiles_given(a) && P >= 1 && P <= kMaxPairs && aligned16(a.x);
 }
 
 int64_t max_units(int64_t pairs, int64_t experts) { return std::min(pairs, experts) + pairs / kMaxM; }
@@ -2764,18 +2171,11 @@ static int64_t part_slots(int64_t units, int per_unit, int per_key, int G) {
   return static_cast<int64_t>(G) * maxj;
 }
 
-// Phase-A partial slots per workgroup of the one-launch chain: the keys
-// (unit, gate/up) a balanced range of at most ceil(N/G) tiles can meet.
-static int flow_maxj(int64_t units, int nka, int G) {
-  const int64_t chunk = (units * 2 * nka + G - 1) / G;
-  return static_cast<int>((chunk + nka - 1) / nka + 1);
-}
-
 bool bulk_supported(const latent_moe_args& a) {
   const int64_t P = a.n_tokens * a.n_expert_used;
   // 32-bit byte offsets into x, h and the latents.
-  return a.stream_tiles != nullptr && aligned16(a.stream_tiles) && tiles_shape_ok(a) && P >= 1 &&
-         a.n_tokens * a.n_embd * 2 < (1ll << 31) && P * a.n_ff * 2 < (1ll << 31) && P * kK * 4 < (1ll << 31);
+  return tiles_given(a) && P >= 1 && a.n_tokens * a.n_embd * 2 < (1ll << 31) && P * a.n_ff * 2 < (1ll << 31) &&
+         P * kK * 4 < (1ll << 31);
 }
 
 size_t bulk_part_bytes(const latent_moe_args& a, int64_t max_units) {
@@ -2786,9 +2186,8 @@ size_t bulk_part_bytes(const latent_moe_args& a, int64_t max_units) {
 }
 
 int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units, hipStream_t s) {
-  const TileSizes ts = tile_sizes(a);
   Params p{};
-  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  set_tiles(a, p);
   p.nunits = bk.nunits;
   p.unit_info = bk.units;
   p.pair_tok = bk.pair_tok;
@@ -2835,10 +2234,10 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
 
 bool lite_applies(const latent_moe_args& a) {
   const char* env = std::getenv("LATENT_STREAM_LAUNCH");
-  if (env && (!std::strcmp(env, "phases") || !std::strcmp(env, "one"))) return false;
+  if (env && !std::strcmp(env, "phases")) return false;
   if (!supported(a)) return false;
   const int64_t P = a.n_tokens * a.n_expert_used;
-  if (P < 1 || P > kLiteMaxP || a.n_embd / kK > kFlowMaxKTiles) return false;
+  if (P < 1 || P > kLiteMaxP || a.n_embd / kK > kMaxKTiles) return false;
   if (a.n_tokens * a.n_embd * 4 >= (1ll << 31)) return false;  // 32-bit byte offsets into x
   const int nka = static_cast<int>(a.n_embd / kK), nb = static_cast<int>(a.n_ff / kHBlock);
   const int nd = static_cast<int>(a.n_embd / kN);
@@ -2853,9 +2252,8 @@ bool lite_applies(const latent_moe_args& a) {
 
 int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, hipStream_t s) {
   const Layout L = layout_for(a);
-  const TileSizes ts = tile_sizes(a);
   LiteParams p{};
-  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  set_tiles(a, p);
   p.x = a.x;
   p.x_dtype = a.x_dtype;
   p.ids = a.ids;
@@ -2892,22 +2290,16 @@ int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, 
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
-bool one_launch(const latent_moe_args& a) {
-  const char* env = std::getenv("LATENT_STREAM_LAUNCH");
-  if (!(env && !std::strcmp(env, "one"))) return false;
-  return a.n_embd / kK <= kFlowMaxKTiles;
-}
-
 Layout layout_for(const latent_moe_args& a) {
   auto al = [](size_t v) { return (v + 255) / 256 * 256; };
   const int64_t T = a.n_tokens, P = a.n_tokens * a.n_expert_used, d = a.n_embd, ff = a.n_ff;
   const int64_t U = max_units(P, a.n_expert);
   const int G = grid_size();
   const int nka = static_cast<int>(d / kK);
-  // Partial blocks: A per workgroup range (per-phase launches) or maxj per
-  // workgroup (one-launch chain); C one per item (bc_kernel: nkc per unit) or
-  // per BC item of the one-launch chain (nb per unit).
-  const int64_t blocksA = std::max<int64_t>(part_slots(U, 2 * nka, nka, G), static_cast<int64_t>(G) * flow_maxj(U, nka, G));
+  // Partial blocks: A per workgroup range and segment; C one per item
+  // (bc_kernel: nkc per unit; the small-batch chain: nb per unit, in the
+  // same region).
+  const int64_t blocksA = part_slots(U, 2 * nka, nka, G);
   const int64_t blocksC = U * (ff / kHBlock);
   Layout L{};
   size_t off = 0;
@@ -2921,17 +2313,14 @@ Layout layout_for(const latent_moe_args& a) {
   L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
   L.ybuf = off;   off = al(off + static_cast<size_t>(P) * d * 4);
   L.pos_of = off; off = al(off + static_cast<size_t>(P) * 4);
-  L.cnt_ints = (2 * U + 1) * kFlowCntStride;
-  L.cnt = off;    off = al(off + static_cast<size_t>(L.cnt_ints) * 4);
   L.total = off;
   return L;
 }
 
 int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStream_t s) {
   const Layout L = layout_for(a);
-  const TileSizes ts = tile_sizes(a);
   Params p{};
-  for (int i = 0; i < kTileArrays; ++i) p.tiles[i] = static_cast<const uint8_t*>(a.stream_tiles) + ts.offset[i];
+  set_tiles(a, p);
   p.meta = g.meta;
   p.nunits = g.meta + 4;
   p.unit_info = g.unit_info;
@@ -2968,20 +2357,6 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
   // At most G workgroups; fewer when the phase has fewer tiles than that even
   // at the largest unit count (the others would find an empty range).
   auto item_grid = [&](int64_t per_unit) { return static_cast<unsigned>(std::min<int64_t>(p.G, U * per_unit)); };
-  if (one_launch(a)) {
-    p.pair_tok = g.pair_tok;
-    p.pair_slot = g.pair_slot;
-    p.pair_w = g.pair_w;
-    p.cnt = reinterpret_cast<int*>(scratch + L.cnt);
-    p.err = g.err;
-    p.maxu = static_cast<int>(U);
-    p.maxj = flow_maxj(U, p.nka, p.G);
-    if (a.out_mode == LATENT_OUT_REDUCED)
-      hipLaunchKernelGGL(flow_kernel<LATENT_OUT_REDUCED>, dim3(p.G), dim3(kT), 0, s, p);
-    else
-      hipLaunchKernelGGL(flow_kernel<LATENT_OUT_PER_SLOT>, dim3(p.G), dim3(kT), 0, s, p);
-    return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
-  }
   const int rows_per_block = kT / kWave;
   hipLaunchKernelGGL(item_kernel<kPhaseA>, dim3(item_grid(2 * p.nka)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL((reduce_kernel<kPhaseA, kMaxM>), dim3(blocks((U * 2 * kMaxM + rows_per_block - 1) / rows_per_block)),
@@ -2998,39 +2373,49 @@ int forward(const latent_moe_args& a, const Grouping& g, char* scratch, hipStrea
 }  // namespace stream
 }  // namespace latent
 
-extern "C" int latent_stream_tiles_size(const latent_moe_args* args, size_t* bytes) {
-  if (!args || !bytes) return LATENT_E_INVALID;
-  *bytes = 0;
-  if (!latent::stream::tiles_shape_ok(*args)) return LATENT_OK;
-  *bytes = latent::stream::tile_sizes(*args).total;
-  return LATENT_OK;
+extern "C" int latent_tiles_supported(const latent_moe_args* args) {
+  if (!args) return LATENT_E_INVALID;
+  return latent::stream::tiles_shape_ok(*args) ? 1 : 0;
 }
 
-extern "C" int latent_stream_tiles_pack(const latent_moe_args* args, void* tiles, size_t tiles_bytes,
-                                        latent_stream_t stream) {
+extern "C" int latent_tiles_repack(int32_t factor, const latent_factor* src, latent_factor* dst, int64_t n_expert,
+                                   int32_t to_tiles, latent_stream_t stream) {
   using namespace latent;
   using namespace latent::stream;
-  if (!args || !tiles) return LATENT_E_INVALID;
-  if (!tiles_shape_ok(*args)) return LATENT_E_UNSUPPORTED;
-  const TileSizes ts = tile_sizes(*args);
-  if (tiles_bytes < ts.total || !aligned16(tiles)) return LATENT_E_INVALID;
-  const latent_factor* fs[6] = {&args->gate_a, &args->gate_b, &args->up_a, &args->up_b, &args->down_a, &args->down_b};
-  const int64_t want[6][2] = {{args->n_embd, kK}, {kK, args->n_ff}, {args->n_embd, kK},
-                              {kK, args->n_ff},   {args->n_ff, kK}, {kK, args->n_embd}};
-  PackParams pp{};
-  for (int i = 0; i < 6; ++i) {
-    if (fs[i]->rows != want[i][0] || fs[i]->cols != want[i][1]) return LATENT_E_INVALID;
-    pp.fac[i] = make_factor(*fs[i]);
-  }
-  pp.total16 = 0;
-  for (int i = 0; i < kTileArrays; ++i) {
-    pp.dst[i] = static_cast<uint8_t*>(tiles) + ts.offset[i];
-    pp.ntiles[i] = ts.ntiles[i];
-    pp.per_expert[i] = ts.per_expert[i];
-    pp.total16 += ts.ntiles[i] * (kTileBytes / 16);
-  }
+  if (!src || !dst || factor < 0 || factor >= kFactors || n_expert < 1) return LATENT_E_INVALID;
+  if (src->rows != dst->rows || src->cols != dst->cols) return LATENT_E_INVALID;
+  if (src->int8_bitmap || src->int8_row_offset || src->int8_data || dst->int8_bitmap || dst->int8_row_offset ||
+      dst->int8_data)
+    return LATENT_E_UNSUPPORTED;  // the tile layout is pure NF4
+  if (!src->codes != !dst->codes || !src->scales != !dst->scales || (!src->codes && !src->scales))
+    return LATENT_E_INVALID;
+  const int kind = tile_kind(factor);
+  const int64_t rows = src->rows, cols = src->cols;
+  const bool ok = kind == kKindK ? cols == kN && rows > 0 && rows % kK == 0
+                : kind == kKindN ? rows == kK && cols > 0 && cols % kN == 0
+                                 : rows == kK && cols > 0 && cols % kHBlock == 0;
+  if (!ok) return LATENT_E_UNSUPPORTED;
+  const latent_factor* tile_side = to_tiles ? dst : src;
+  if ((tile_side->codes && !aligned16(tile_side->codes)) || (tile_side->scales && !aligned16(tile_side->scales)))
+    return LATENT_E_INVALID;
+  RepackParams rp{};
+  const latent_factor* rows_side = to_tiles ? src : dst;
+  rp.rcodes = const_cast<uint8_t*>(rows_side->codes);
+  rp.rscales = const_cast<uint16_t*>(rows_side->scales);
+  rp.tcodes = const_cast<uint8_t*>(tile_side->codes);
+  rp.tscales = const_cast<uint16_t*>(tile_side->scales);
+  rp.kind = kind;
+  rp.rows = rows;
+  rp.cols = cols;
+  rp.code_units = src->codes ? n_expert * rows * cols / 32 : 0;
+  rp.scale_dwords = src->scales ? n_expert * rows * cols / kGroup / 2 : 0;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(pack_kernel, dim3(4096), dim3(kT), 0, s, pp);
+  const int64_t n = rp.code_units + rp.scale_dwords;
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(8192, (n + kT - 1) / kT));
+  if (to_tiles)
+    hipLaunchKernelGGL(repack_kernel<true>, dim3(blocks), dim3(kT), 0, s, rp);
+  else
+    hipLaunchKernelGGL(repack_kernel<false>, dim3(blocks), dim3(kT), 0, s, rp);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }

@@ -7,6 +7,10 @@ namespace latent {
 namespace stream {
 
 constexpr int kMaxM = 16;  // routed pairs per work unit (the MFMA row count)
+constexpr int64_t kMaxPairs = 4096;  // routed pairs the decode launches take
+
+// The layer's shape and format can take the tile layout (latent_tiles_supported).
+bool tiles_shape_ok(const latent_moe_args& a);
 
 // Token grouping produced by the prep kernel (moe.hip), all device pointers.
 // Pairs are grouped by expert; a work unit is a run of at most kMaxM
@@ -18,28 +22,21 @@ struct Grouping {
   const int* pair_tok;     // [P] token, slot and router weight of each grouped pair
   const int* pair_slot;
   const float* pair_w;
-  int* err;                // word a timed-out bounded wait sets (one-launch chain)
+  int* err;                // word a timed-out bounded wait sets
 };
 
 // Scratch of the path inside the caller's workspace.  xh / xexp (x as fp16
 // rows * 2^xexp, one exponent per token) and pos_of (grouped pair of each
-// routed slot) are written by the prep kernel, which also clears cnt (the
-// one-launch chain's counters, cnt_ints of them).
+// routed slot) are written by the prep kernel.
 struct Layout {
-  size_t xh, xexp, partA, lath, lexp, partC, dlath, dexp, ybuf, pos_of, cnt, total;
-  int64_t cnt_ints;
+  size_t xh, xexp, partA, lath, lexp, partC, dlath, dexp, ybuf, pos_of, total;
 };
-
-// One launch for the whole chain (flow_kernel) rather than one per phase:
-// taken with LATENT_STREAM_LAUNCH=one where d <= 16384 (the per-phase
-// launches are measured faster today and are the default).
-bool one_launch(const latent_moe_args& a);
 
 // Batches of at most 16 routed pairs: the whole chain in one launch in which
 // every workgroup issues all its tile loads first (lite_kernel), grouping and
 // x conversion included, so the prep kernel is not launched.  Taken by default
 // wherever every workgroup's tiles fit its registers; LATENT_STREAM_LAUNCH=phases
-// or =one selects the other launch styles.  Its counters live in the
+// selects the per-phase launches instead.  Its counters live in the
 // workspace control block at kLiteCtrlOffset (zero between calls).
 constexpr size_t kLiteCtrlOffset = 192 * 1024;
 constexpr size_t kLiteCtrlBytes = 64 * 1024;
@@ -47,8 +44,8 @@ bool lite_applies(const latent_moe_args& a);
 // ctrl: the workspace's control block; scratch: the decode layout (layout_for).
 int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, hipStream_t s);
 
-// The call can take this path: a tile layout is given (latent_stream_tiles_pack)
-// and the batch has at most 4096 routed pairs.
+// The call can take this path: the factors are in the tile layout
+// (latent_tiles_repack) and the batch has at most kMaxPairs routed pairs.
 bool supported(const latent_moe_args& a);
 // Upper bound of work units: every active expert contributes ceil(n_e / kMaxM).
 int64_t max_units(int64_t pairs, int64_t experts);

@@ -296,10 +296,15 @@ def read_latent_gguf(path: Union[str, Path]) -> LatentGGUF:
 
 
 def layer_to_arrays(layer, experts: Optional[Iterable[int]] = None) -> Dict[str, np.ndarray]:
-    """Host copies of a device StackedLayer under the writer's short names
-    (input of write_latent_gguf)."""
+    """Host copies of a device StackedLayer (of `experts` only, when given)
+    under the writer's short names, in the row layout (input of
+    write_latent_gguf)."""
     out: Dict[str, np.ndarray] = {}
     for name, f in layer.factors().items():
+        if f.layout != "rows" or experts is not None:
+            if f.has_int8 and experts is not None:
+                raise ValueError("an expert subset of a layer with INT8 groups is not exported")
+            f = layer.factor_rows(name, None if experts is None else list(experts))
         out[name] = f.codes.cpu().numpy()
         out[name + "_s"] = f.scales.cpu().numpy().view(np.float16)
         if f.has_int8:
@@ -307,5 +312,6 @@ def layer_to_arrays(layer, experts: Optional[Iterable[int]] = None) -> Dict[str,
             out[name + "_i8off"] = f.int8_row_offset.cpu().numpy()
             out[name + "_i8"] = f.int8_data.cpu().numpy()
     if layer.ranks is not None:
-        out["ranks"] = layer.ranks.cpu().numpy()
+        ranks = layer.ranks.cpu().numpy()
+        out["ranks"] = ranks if experts is None else ranks[np.asarray(list(experts), dtype=np.int64)]
     return out

@@ -34,6 +34,9 @@ def _stream(stream: Optional[torch.cuda.Stream] = None) -> ctypes.c_void_p:
     return ctypes.c_void_p(s.cuda_stream)
 
 
+LAYOUTS = ("rows", "tiles")
+
+
 @dataclass
 class DeviceFactor:
     """One stacked factor in HBM: codes u8 [E, rows, cols/2], scales f16 [E, rows, cols/32].
@@ -41,6 +44,10 @@ class DeviceFactor:
     Optional per-group INT8 fallback (see include/latent_ffn.h): int8_bitmap
     int32 [E, rows, words] (bit patterns of u32), int8_row_offset int32
     [E, rows], int8_data int8 [n, 32].
+
+    layout "rows" is the writer's row order; "tiles" is the same tensors
+    reordered by latent_tiles_repack for the MFMA paths (each expert's bytes
+    stay in its own slice of the tensor, so expert selection works alike).
     """
 
     codes: torch.Tensor
@@ -48,6 +55,7 @@ class DeviceFactor:
     int8_bitmap: Optional[torch.Tensor] = None
     int8_row_offset: Optional[torch.Tensor] = None
     int8_data: Optional[torch.Tensor] = None
+    layout: str = "rows"
 
     def __post_init__(self) -> None:
         if self.codes.dtype != torch.uint8 or self.codes.dim() != 3:
@@ -63,6 +71,10 @@ class DeviceFactor:
         ext = (self.int8_bitmap, self.int8_row_offset, self.int8_data)
         if any(t is not None for t in ext) and not all(t is not None for t in ext):
             raise ValueError("INT8 extension needs bitmap, row_offset and data together")
+        if self.layout not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS}")
+        if self.layout == "tiles" and self.has_int8:
+            raise ValueError("the tile layout is pure NF4")
 
     @property
     def n_expert(self) -> int:
@@ -98,6 +110,29 @@ class DeviceFactor:
                 n += t.numel() * t.element_size()
         return n
 
+    def select(self, experts) -> "DeviceFactor":
+        """The factor of `experts` only (either layout; pure NF4)."""
+        if self.has_int8:
+            raise ValueError("select() keeps no INT8 side buffer")
+        sel = torch.as_tensor(np.asarray(experts, dtype=np.int64), device=self.codes.device)
+        return DeviceFactor(self.codes.index_select(0, sel).contiguous(), self.scales.index_select(0, sel).contiguous(),
+                            layout=self.layout)
+
+    def repacked(self, factor: int, layout: str, stream: Optional[torch.cuda.Stream] = None) -> "DeviceFactor":
+        """This factor in `layout` (a new pair of tensors; latent_tiles_repack).
+        `factor` is its operand index, LATENT_GATE_A .. LATENT_DOWN_B."""
+        if layout not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS}")
+        if layout == self.layout:
+            return self
+        codes = torch.empty_like(self.codes)
+        scales = torch.empty_like(self.scales)
+        src = self.c_struct()
+        dst = LatentFactor(codes=codes.data_ptr(), scales=scales.data_ptr(), rows=self.rows, cols=self.cols)
+        check(lib.latent_tiles_repack(int(factor), ctypes.byref(src), ctypes.byref(dst), self.n_expert,
+                                      1 if layout == "tiles" else 0, _stream(stream)), "latent_tiles_repack")
+        return DeviceFactor(codes, scales, layout=layout)
+
     @classmethod
     def from_numpy(
         cls,
@@ -131,6 +166,12 @@ class StackedLayer:
     Shapes (patches/002-latent-gguf-tensors.patch:135-148, packed code axis):
       gate_a, up_a [E, d, R/2]; gate_b, up_b [E, R, ff/2];
       down_a [E, ff, R/2]; down_b [E, R, d/2]; scales on a 1/16 axis.
+
+    layout: "tiles" holds the twelve tensors in the tile layout of the MFMA
+    paths (reordered in place of the row layout, factor by factor, so the
+    layer is held once); "rows" keeps the writer's row layout; None (the
+    default) takes "tiles" wherever latent_tiles_supported says the layer
+    can (pure NF4, rank 256, d and ff multiples of 256).
     """
 
     gate_a: DeviceFactor
@@ -140,9 +181,8 @@ class StackedLayer:
     down_a: DeviceFactor
     down_b: DeviceFactor
     ranks: Optional[torch.Tensor] = None  # int32 [E, 3] (gate, up, down)
-    stream_tiles: Optional[bool] = None  # build the streaming tile layout (None: when the layer qualifies)
+    layout: Optional[str] = None
     _workspace: Dict[int, torch.Tensor] = field(default_factory=dict, repr=False)
-    _tiles: Optional[torch.Tensor] = field(default=None, repr=False)
 
     def __post_init__(self) -> None:
         E, d, R = self.n_expert, self.d, self.max_rank
@@ -154,30 +194,49 @@ class StackedLayer:
             f = getattr(self, name)
             if f.n_expert != E or f.rows != rows or f.cols != cols:
                 raise ValueError(f"{name}: got [E={f.n_expert}, {f.rows}, {f.cols}], want [E={E}, {rows}, {cols}]")
+        given = {f.layout for f in self.factors().values()}
+        if len(given) != 1:
+            raise ValueError("all six factors must be in one layout")
         if self.ranks is not None:
             if self.ranks.dtype != torch.int32 or tuple(self.ranks.shape) != (E, 3) or not self.ranks.is_cuda:
                 raise ValueError("ranks must be a CUDA int32 [E, 3] tensor")
             self.ranks = self.ranks.contiguous()
-        if self.stream_tiles is not False:
-            self.build_stream_tiles(required=bool(self.stream_tiles))
+        target = self.layout
+        if target is None:
+            target = "tiles" if given == {"tiles"} or self.tiles_supported() else "rows"
+        if target not in LAYOUTS:
+            raise ValueError(f"layout must be one of {LAYOUTS} or None")
+        if target == "tiles" and given != {"tiles"} and not self.tiles_supported():
+            raise ValueError("this layer has no tile layout (needs pure NF4, rank 256, d and ff % 256 == 0)")
+        self.layout = next(iter(given))
+        self._convert(target)
 
-    def build_stream_tiles(self, required: bool = False) -> bool:
-        """Pack the factors into the streaming decode path's tile layout
-        (latent_stream_tiles_pack; same size as the packed factors).  Returns
-        False, or raises when `required`, for a layer the layout does not apply
-        to (INT8 groups, rank other than 256, d or ff not a multiple of 256)."""
+    def tiles_supported(self) -> bool:
+        """Whether the layer can take the tile layout (latent_tiles_supported)."""
         a = self.args()
-        n = ctypes.c_size_t(0)
-        check(lib.latent_stream_tiles_size(ctypes.byref(a), ctypes.byref(n)), "latent_stream_tiles_size")
-        if n.value == 0:
-            if required:
-                raise ValueError("this layer has no streaming tile layout (needs pure NF4, rank 256, d and ff % 256 == 0)")
-            return False
-        tiles = torch.empty(int(n.value), dtype=torch.uint8, device=self.gate_a.codes.device)
-        check(lib.latent_stream_tiles_pack(ctypes.byref(a), tiles.data_ptr(), int(n.value), _stream()),
-              "latent_stream_tiles_pack")
-        self._tiles = tiles
-        return True
+        r = lib.latent_tiles_supported(ctypes.byref(a))
+        if r < 0:
+            check(r, "latent_tiles_supported")
+        return r == 1
+
+    def _convert(self, layout: str) -> None:
+        # One factor at a time: the old pair is released before the next is
+        # repacked, so converting needs one factor's bytes beyond the layer.
+        for k, name in enumerate(FACTOR_NAMES):
+            setattr(self, name, getattr(self, name).repacked(k, layout))
+        self.layout = layout
+
+    def to_layout(self, layout: str) -> "StackedLayer":
+        """A copy of this layer in `layout` (this layer is left as it is)."""
+        facs = {k: v for k, v in self.factors().items()}
+        return StackedLayer(**facs, ranks=self.ranks, layout=layout)
+
+    def factor_rows(self, name: str, experts=None) -> DeviceFactor:
+        """Factor `name` (of `experts` only, when given) in the row layout."""
+        f = getattr(self, name)
+        if experts is not None:
+            f = f.select(experts)
+        return f.repacked(FACTOR_NAMES.index(name), "rows")
 
     @property
     def n_expert(self) -> int:
@@ -199,7 +258,8 @@ class StackedLayer:
         return {n: getattr(self, n) for n in FACTOR_NAMES}
 
     def nbytes(self) -> int:
-        """Bytes of the six factors (the tile layout, when built, holds the same bytes again)."""
+        """Bytes of the twelve factor tensors (plus INT8 side buffers): all the
+        layer holds in HBM, in either layout."""
         return sum(f.nbytes() for f in self.factors().values())
 
     @classmethod
@@ -208,6 +268,7 @@ class StackedLayer:
         arrays: Mapping[str, np.ndarray],
         layer: Optional[int] = None,
         device: str = "cuda",
+        layout: Optional[str] = None,
     ) -> "StackedLayer":
         """From the writer's tensor names (loader/write_latent_gguf.py:72-74, 256-265).
 
@@ -215,7 +276,8 @@ class StackedLayer:
         (scales), optional `..._{a,b}_i8map / _i8off / _i8` (per-group INT8
         extension), plus optional `blk.{layer}.ffn_latent_ranks`; with layer=None
         the `blk.N.ffn_latent_` prefix is omitted.  Ranks are widened to int32
-        (the writer's uint8 table cannot hold 256 or 512).
+        (the writer's uint8 table cannot hold 256 or 512).  The arrays are in
+        the row layout; `layout` is the layout the layer is held in.
         """
         prefix = "" if layer is None else f"blk.{layer}.ffn_latent_"
         facs = {}
@@ -227,7 +289,7 @@ class StackedLayer:
             facs[name] = DeviceFactor.from_numpy(arrays[key], arrays[key + "_s"], ext, device=device)
         ranks = arrays.get(prefix + "ranks")
         rt = None if ranks is None else torch.from_numpy(np.asarray(ranks).astype(np.int32)).to(device)
-        return cls(**facs, ranks=rt)
+        return cls(**facs, ranks=rt, layout=layout)
 
     def args(self) -> LatentMoeArgs:
         a = LatentMoeArgs()
@@ -235,7 +297,7 @@ class StackedLayer:
             setattr(a, name, getattr(self, name).c_struct())
         a.ranks = _ptr(self.ranks)
         a.n_embd, a.n_ff, a.n_expert, a.max_rank = self.d, self.ff, self.n_expert, self.max_rank
-        a.stream_tiles = _ptr(self._tiles)
+        a.layout = _lib.LATENT_LAYOUT_TILES if self.layout == "tiles" else _lib.LATENT_LAYOUT_ROWS
         return a
 
     def workspace(self, n_tokens: int, n_expert_used: int) -> torch.Tensor:
@@ -286,7 +348,7 @@ def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
 
 def stream_launch(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> Optional[str]:
     """Launch style of a streaming-path call: 'lite' (small-batch chain in one
-    launch), 'one' (one-launch chain) or 'phases' (one launch per phase); None
+    launch) or 'phases' (one launch per phase); None
     when the call does not take the streaming path."""
     a = layer.args()
     a.x = x.data_ptr()
@@ -297,7 +359,7 @@ def stream_launch(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> O
         return None
     if r < 0:
         check(r, "latent_stream_launch")
-    return {0: "phases", 1: "one", 2: "lite"}[r]
+    return {0: "phases", 2: "lite"}[r]
 
 
 def moe_forward(
@@ -358,10 +420,18 @@ def moe_forward(
     return out
 
 
-def unpack(factor: DeviceFactor, expert: int, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-    """Dequantized f32 [rows, cols] of one expert (bit-exact NF4 / INT8 decode)."""
+def unpack(factor: DeviceFactor, expert: int, stream: Optional[torch.cuda.Stream] = None,
+           kind: Optional[int] = None) -> torch.Tensor:
+    """Dequantized f32 [rows, cols] of one expert (bit-exact NF4 / INT8 decode).
+    A factor in the tile layout needs its operand index `kind`
+    (LATENT_GATE_A .. LATENT_DOWN_B): the expert is repacked to rows first."""
     if not 0 <= expert < factor.n_expert:
         raise IndexError(expert)
+    if factor.layout == "tiles":
+        if kind is None:
+            raise ValueError("unpack of a tile-layout factor needs its operand index `kind`")
+        factor = factor.select([expert]).repacked(kind, "rows", stream)
+        expert = 0
     out = torch.empty((factor.rows, factor.cols), dtype=torch.float32, device=factor.codes.device)
     c = factor.c_struct()
     check(lib.latent_unpack(ctypes.byref(c), int(expert), out.data_ptr(), _stream(stream)), "latent_unpack")

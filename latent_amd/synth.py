@@ -183,11 +183,10 @@ def bf16_input(seed: int, n_tokens: int, d: int, device: str = "cuda") -> torch.
 
 
 def layer_to_host(layer: StackedLayer, experts: Optional[Sequence[int]] = None) -> Dict[str, Tuple]:
-    """Copy (a subset of experts of) a layer's packed operands to host numpy arrays."""
-    sel = None if experts is None else torch.as_tensor(np.asarray(experts, dtype=np.int64), device=layer.gate_a.codes.device)
+    """Copy (a subset of experts of) a layer's packed operands to host numpy
+    arrays, in the row layout."""
     out = {}
-    for name, f in layer.factors().items():
-        codes = f.codes if sel is None else f.codes[sel]
-        scales = f.scales if sel is None else f.scales[sel]
-        out[name] = (codes.cpu().numpy(), scales.cpu().numpy().view(np.float16))
+    for name in layer.factors():
+        f = layer.factor_rows(name, None if experts is None else list(experts))
+        out[name] = (f.codes.cpu().numpy(), f.scales.cpu().numpy().view(np.float16))
     return out

@@ -47,15 +47,20 @@ def _int8_subset(f, experts: np.ndarray) -> ref.Int8Groups:
 
 
 def subset_to_host(dev_layer, experts: Sequence[int]) -> ref.StackedLayer:
-    """Oracle StackedLayer holding only `experts` of a device layer (INT8 groups included)."""
+    """Oracle StackedLayer holding only `experts` of a device layer (INT8
+    groups included; a tile-layout layer is read back in the row layout)."""
     import torch
 
     ex = np.asarray(experts, dtype=np.int64)
     sel = torch.as_tensor(ex, device=dev_layer.gate_a.codes.device)
     facs = {}
     for name, f in dev_layer.factors().items():
-        codes = f.codes.index_select(0, sel).cpu().numpy()
-        scales = f.scales.index_select(0, sel).cpu().numpy().view(np.float16)
+        if f.layout == "tiles":
+            rows = dev_layer.factor_rows(name, ex)
+            codes, scales = rows.codes.cpu().numpy(), rows.scales.cpu().numpy().view(np.float16)
+        else:
+            codes = f.codes.index_select(0, sel).cpu().numpy()
+            scales = f.scales.index_select(0, sel).cpu().numpy().view(np.float16)
         facs[name] = ref.StackedFactor(codes, scales, _int8_subset(f, ex) if f.has_int8 else None)
     ranks = None if dev_layer.ranks is None else dev_layer.ranks.index_select(0, sel).cpu().numpy()
     return ref.StackedLayer(factors=facs, d=dev_layer.d, ff=dev_layer.ff, max_rank=dev_layer.max_rank, ranks=ranks)

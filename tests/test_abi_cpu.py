@@ -225,3 +225,39 @@ def test_runtime_load_pair_keeps_artifacts_flat():
     bad["w.a.scales"] = bad["w.a.scales"][:-1]
     with pytest.raises(ValueError):
         runtime.load_pair(bad, "w")
+
+
+def test_layout_flag_and_tiles_queries(L):
+    # a DeepSeek-V3-like shape at rank 256 can take the tile layout; rank 64 cannot
+    a, keep = _args(L, d=512, ff=768, R=256)
+    assert L.lib.latent_tiles_supported(ctypes.byref(a)) == 1
+    b, keep2 = _args(L)
+    assert L.lib.latent_tiles_supported(ctypes.byref(b)) == 0
+    b.up_a.int8_bitmap = 4096
+    assert L.lib.latent_tiles_supported(ctypes.byref(b)) == 0
+    # the flag is checked, and a tile-layout call needs a shape the layout exists for
+    a.layout = 3
+    assert _ws(L, a)[0] == L.LATENT_E_INVALID
+    b, keep2 = _args(L)
+    b.layout = L.LATENT_LAYOUT_TILES
+    assert _ws(L, b)[0] == L.LATENT_E_UNSUPPORTED
+    assert L.lib.latent_moe_path(ctypes.byref(b)) == L.LATENT_E_UNSUPPORTED
+
+
+def test_tiles_repack_argument_checks(L):
+    f = L.LatentFactor(codes=16, scales=16, rows=512, cols=256)
+    g = L.LatentFactor(codes=32, scales=32, rows=512, cols=256)
+    bad = [
+        (L.LATENT_GATE_A, L.LatentFactor(codes=16, scales=16, rows=500, cols=256), g, L.LATENT_E_INVALID),  # rows differ
+        (L.LATENT_GATE_A, L.LatentFactor(codes=16, scales=16, rows=384, cols=256),
+         L.LatentFactor(codes=32, scales=32, rows=384, cols=256), L.LATENT_E_UNSUPPORTED),  # not whole K tiles
+        (L.LATENT_GATE_B, f, g, L.LATENT_E_UNSUPPORTED),  # gate_b has 256 rows
+        (6, f, g, L.LATENT_E_INVALID),
+        (L.LATENT_GATE_A, L.LatentFactor(codes=16, scales=None, rows=512, cols=256), g, L.LATENT_E_INVALID),
+        (L.LATENT_GATE_A, f, L.LatentFactor(codes=33, scales=32, rows=512, cols=256), L.LATENT_E_INVALID),  # unaligned
+        (L.LATENT_GATE_A, L.LatentFactor(codes=16, scales=16, int8_bitmap=64, rows=512, cols=256), g,
+         L.LATENT_E_UNSUPPORTED),
+    ]
+    for factor, src, dst, status in bad:
+        assert L.lib.latent_tiles_repack(factor, ctypes.byref(src), ctypes.byref(dst), 4, 1, None) == status
+    assert L.lib.latent_tiles_repack(0, None, ctypes.byref(g), 4, 1, None) == L.LATENT_E_INVALID

@@ -104,9 +104,9 @@ def test_gpu_factorize_matches_oracle_and_runs(gpu):
         assert layer.ranks.cpu().tolist() == [list(r) for r in ranks]
         assert all(f.has_int8 == (thr is not None) for f in layer.factors().values())
         host = _host_layer(gguf.layer_to_arrays(layer), d, ff, R)
-        for name, f in layer.factors().items():  # the built layout decodes bit-exactly as the oracle reads it
+        for k, (name, f) in enumerate(layer.factors().items()):  # the built layout decodes as the oracle reads it
             for e in range(E):
-                assert np.array_equal(gpu.unpack(f, e).cpu().numpy(), host.factors[name].expert(e))
+                assert np.array_equal(gpu.unpack(f, e, kind=k).cpu().numpy(), host.factors[name].expert(e))
         out = gpu.moe_forward(x, ids, w, layer)
         torch.cuda.synchronize()
         got = out.cpu().numpy()

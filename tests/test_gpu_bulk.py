@@ -1,9 +1,9 @@
-"""Prefill on the streaming tile layout (bulk units of up to 128 pairs) against
-the oracle.
+"""Prefill on the tile layout (bulk units of up to 64 pairs) against the
+oracle.
 
-Rank-256 layers with a tile layout take this engine for prefill-sized batches;
-LATENT_PREFILL_ENGINE=gemm selects the grouped GEMMs instead, which the last
-test uses as a second, independent implementation.  Bar: rel-L2 <= 2e-3
+Rank-256 layers held in the tile layout take this engine for prefill-sized
+batches; the same layer in the row layout takes the grouped GEMMs, which the
+last test uses as a second, independent implementation.  Bar: rel-L2 <= 2e-3
 against the oracle's fp32 result on the same packed factors, bit-identical
 results on a repeated call, exact zeros in dropped per-slot rows.
 """
@@ -29,7 +29,7 @@ def layer():
 @pytest.fixture(scope="module")
 def dev(gpu, layer):
     d = to_device(layer)
-    assert d._tiles is not None  # the layer has a tile layout, so prefill takes the bulk engine
+    assert d.layout == "tiles"  # the layer is held in the tile layout, so prefill takes the bulk engine
     return d
 
 
@@ -115,8 +115,9 @@ def test_bulk_matches_gemm_engine(gpu, layer, dev, monkeypatch):
     xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
     it, wt = torch.from_numpy(ids).cuda(), torch.from_numpy(w).cuda()
     bulk = gpu.moe_forward(xt, it, wt, dev)
-    monkeypatch.setenv("LATENT_PREFILL_ENGINE", "gemm")
-    gemm = gpu.moe_forward(xt, it, wt, dev)
+    rows = dev.to_layout("rows")
+    assert gpu.moe_path(rows, xt, k) == "prefill"
+    gemm = gpu.moe_forward(xt, it, wt, rows)
     torch.cuda.synchronize()
     assert not torch.equal(bulk, gemm), "both calls ran the same engine"
     assert ref.rel_l2(gemm.cpu().numpy(), bulk.cpu().numpy()) <= TOL

@@ -1,9 +1,9 @@
 """Streaming MFMA decode path (stream.hip) against the oracle.
 
-The path is selected with LATENT_MOE_PATH=stream for every call here, in each
+The path is selected with LATENT_MOE_PATH=stream for every call here, in both
 launch styles (LATENT_STREAM_LAUNCH=auto: the default, which takes the
-small-batch chain for at most 16 routed pairs; =phases: one launch per phase;
-=one: the whole chain in one persistent launch).  Bar:
+small-batch chain for at most 16 routed pairs; =phases: one launch per phase).
+Bar:
 rel-L2 <= 2e-3 against the oracle's fp32 result on the same packed factors
 (fp16 operands, fp32 accumulation), bit-identical results on a repeated call.
 """
@@ -20,10 +20,10 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-@pytest.fixture(params=["auto", "phases", "one"])
+@pytest.fixture(params=["auto", "phases"])
 def stream_path(monkeypatch, request):
     # The default launch style (the small-batch chain up to 16 routed pairs,
-    # per-phase launches above), per-phase launches and the one-launch chain.
+    # per-phase launches above) and per-phase launches throughout.
     monkeypatch.setenv("LATENT_MOE_PATH", "stream")
     monkeypatch.setenv("LATENT_STREAM_LAUNCH", request.param)
 
@@ -164,7 +164,7 @@ def test_reference_rank_table_at_max_rank_256(gpu, tmp_path, monkeypatch, path):
     per_expert = np.array([[256, 256, 256], [128, 256, 64], [256, 32, 256], [256, 256, 256]])
     g.tensors[name] = gguf.TensorInfo(name, (4, 3), gguf.GGML_I8, 0)
     g.arrays[name] = np.frombuffer(per_expert.T.astype(np.uint8).tobytes(), np.int8).reshape(4, 3)
-    dev = StackedLayer.from_arrays(g.layer_arrays(0), layer=0, stream_tiles=False)
+    dev = StackedLayer.from_arrays(g.layer_arrays(0), layer=0, layout="rows")
     assert dev.ranks is None
     monkeypatch.setenv("LATENT_MOE_PATH", path)
     rng = np.random.default_rng(5)
