@@ -56,7 +56,9 @@ def parse():
     p.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 to skip)")
     p.add_argument("--prefill-steps", type=int, default=5)
     p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
-    p.add_argument("--routings", type=int, default=8, help="distinct routings per batch size")
+    p.add_argument("--routings", type=int, default=16, help="distinct routings per batch size")
+    p.add_argument("--graph-steps", type=int, default=16,
+                   help="decode steps captured in one HIP graph for the graph-replay timing (0 to skip)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run one device-to-device copy of this many MiB first (counter calibration)")
@@ -98,7 +100,26 @@ def time_loop(fn, n_steps, warmup, torch):
     return start.elapsed_time(end) / n_steps  # ms per step
 
 
-def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings):
+def graph_time(torch, fn, n_in_graph, replays):
+    """ms per step of `n_in_graph` steps captured once in a HIP graph
+    (torch.cuda.CUDAGraph) and replayed `replays` times: the GPU time of the
+    steps without the host's per-call enqueue."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(n_in_graph):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_in_graph):
+            fn(i)
+    ms = time_loop(lambda i: g.replay(), replays, 2, torch)
+    del g
+    return ms / n_in_graph
+
+
+def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings, graph_steps=0):
     routes = [gsynth.route(seed=10_000 + 97 * batch + r, n_tokens=batch, n_expert=E, k=K) for r in range(n_routings)]
     xs = [gsynth.bf16_input(seed=20_000 + 89 * batch + r, n_tokens=batch, d=D) for r in range(n_routings)]
     outs = [torch.empty((batch, D), dtype=torch.float32, device="cuda") for _ in range(n_routings)]
@@ -112,6 +133,7 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
         latent.moe_forward(xs[r], ids, w, layers[i % len(layers)], out=outs[r], workspace=ws)
 
     ms = time_loop(step, steps, warmup, torch)
+    gms = graph_time(torch, step, graph_steps, max(4, steps // graph_steps)) if graph_steps else None
     ids_host = [routes[i % n_routings][0].cpu().numpy() for i in range(steps)]
     bytes_per_step = float(np.mean(realized_bytes(ids_host)))
     gbps = bytes_per_step / (ms * 1e-3) / 1e9
@@ -120,6 +142,7 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
         "path": latent.moe_path(layers[0], xs[0], K),
         "launch": latent.moe.stream_launch(layers[0], xs[0], K),
         "ms_per_step": ms,
+        "graph_ms_per_step": gms,
         "tokens_per_s": batch / (ms * 1e-3),
         "hbm_gbps": gbps,
         "roofline_frac": gbps / HBM_PEAK_GBPS,
@@ -166,7 +189,11 @@ def stack_point(torch, latent, gsynth, n_layers, batch, steps):
     """n_layers DeepSeek-V3-shaped LATENT MoE layers, each with its own seeded
     router (W_r ~ N(0, 1/d), fp32) and a residual add, decoded as one HIP graph."""
     t0 = time.time()
+    torch.cuda.synchronize()
+    alloc0 = torch.cuda.memory_allocated()
     layers = [gsynth.make_layer(seed=500_000 + 7919 * l, n_expert=E, d=D, ff=FF, max_rank=R) for l in range(n_layers)]
+    torch.cuda.synchronize()
+    resident_alloc = torch.cuda.memory_allocated() - alloc0  # what the process holds for the layers
     routers = []
     for l in range(n_layers):
         g = torch.Generator(device="cuda")
@@ -180,8 +207,14 @@ def stack_point(torch, latent, gsynth, n_layers, batch, steps):
     stack.load(x0)
     # Eager (one host call per kernel) for comparison, then the captured graph.
     eager_ms = time_loop(lambda i: stack.forward(), 3, 1, torch)
+    eager_out = stack.forward().clone()
     stack.capture()
     ms = time_loop(lambda i: stack.replay(), steps, 2, torch)
+    stack.load(x0)
+    replay_out = stack.replay().clone()
+    torch.cuda.synchronize()
+    replay_equal = bool(torch.equal(replay_out, eager_out))
+    replay_maxdiff = float((replay_out - eager_out).abs().max().item())
     ids = [t.cpu().numpy() for t in stack.layer_ids()]
     step_bytes = float(sum(realized_bytes(ids)))
     resident = stack.resident_bytes()
@@ -201,8 +234,11 @@ def stack_point(torch, latent, gsynth, n_layers, batch, steps):
         "roofline_frac": gbps / HBM_PEAK_GBPS,
         "router_bytes_per_step": stack.router_bytes(),
         "resident_bytes": resident,
+        "resident_allocated_bytes": resident_alloc,
         "dense_bf16_bytes": dense_bf16,
-        "compression_vs_dense_bf16": dense_bf16 / resident,
+        "compression_vs_dense_bf16": dense_bf16 / resident_alloc,
+        "replay_equals_eager": replay_equal,
+        "replay_max_abs_diff_vs_eager": replay_maxdiff,
         "generate_s": gen_s,
     }
     del stack, layers, routers
@@ -413,15 +449,20 @@ def main():
     print(f"# generated {args.layers} layers ({layers[0].nbytes() / 1e9:.3f} GB packed each) in {time.time() - t0:.1f} s",
           file=sys.stderr, flush=True)
 
-    head, routes, xs = decode_point(torch, latent, gsynth, layers, args.batch, args.steps, args.warmup, args.routings)
-    print(f"# decode B={args.batch}: {head['ms_per_step'] * 1e3:.1f} us/step, {head['hbm_gbps']:.0f} GB/s",
-          file=sys.stderr, flush=True)
+    def show(pt):
+        g = pt["graph_ms_per_step"]
+        return (f"# decode B={pt['batch']}: {pt['ms_per_step'] * 1e3:.1f} us/step, {pt['hbm_gbps']:.0f} GB/s"
+                + (f"; graph replay {g * 1e3:.1f} us/step" if g else ""))
+
+    head, routes, xs = decode_point(torch, latent, gsynth, layers, args.batch, args.steps, args.warmup, args.routings,
+                                    args.graph_steps)
+    print(show(head), file=sys.stderr, flush=True)
     sweep = []
     for b in [int(v) for v in args.sweep.split(",") if v.strip()]:
-        pt, _, _ = decode_point(torch, latent, gsynth, layers, b, args.steps, args.warmup, args.routings)
+        pt, _, _ = decode_point(torch, latent, gsynth, layers, b, args.steps, args.warmup, args.routings,
+                                args.graph_steps)
         sweep.append(pt)
-        print(f"# decode B={b}: {pt['ms_per_step'] * 1e3:.1f} us/step, {pt['hbm_gbps']:.0f} GB/s",
-              file=sys.stderr, flush=True)
+        print(show(pt), file=sys.stderr, flush=True)
     prefill, prefill_inputs = None, None
     if args.prefill:
         prefill, prefill_inputs = prefill_point(torch, latent, gsynth, layers, args.prefill, args.prefill_steps,
@@ -441,8 +482,9 @@ def main():
         stack = stack_point(torch, latent, gsynth, args.stack, args.stack_batch, args.stack_steps)
         print(f"# stack {args.stack} layers B={args.stack_batch}: {stack['ms_per_step']:.2f} ms/step "
               f"({stack['us_per_layer']:.1f} us/layer, {stack['hbm_gbps']:.0f} GB/s; eager "
-              f"{stack['eager_ms_per_step']:.2f} ms; generated in {stack['generate_s']:.1f} s)",
-              file=sys.stderr, flush=True)
+              f"{stack['eager_ms_per_step']:.2f} ms; generated in {stack['generate_s']:.1f} s; "
+              f"{stack['resident_allocated_bytes'] / 1e9:.2f} GB allocated; replay == eager: "
+              f"{stack['replay_equals_eager']})", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, layers[0], routes, xs, args.batch, args.cpu_steps,

@@ -365,15 +365,18 @@ __global__ void __launch_bounds__(kRouteThreads) group_scan_kernel(MoeParams p, 
   __shared__ int h[kHistInts];
   __shared__ int scan_c[kRouteThreads];
   __shared__ int scan_a[kRouteThreads];
-  const int tid = threadIdx.x, E = p.E, n = (E + 1) * nchunk;
-  for (int i = tid; i < n; i += kRouteThreads) h[i] = hist[i];
+  const int tid = threadIdx.x, E = p.E, n = (E + 1) * nchunk, E1 = E + 1;
+  // Chunk-major in LDS (h[k * E1 + e]): the threads of one expert range then
+  // read consecutive words (expert-major, a stride of nchunk words put a
+  // wave's reads on one bank).
+  for (int i = tid; i < n; i += kRouteThreads) h[(i % nchunk) * E1 + i / nchunk] = hist[i];
   __syncthreads();
   const int per = (E + kRouteThreads - 1) / kRouteThreads;
   const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
   int sc = 0, sa = 0;
   for (int e = e0; e < e1; ++e) {
     int c = 0;
-    for (int k = 0; k < nchunk; ++k) c += h[e * nchunk + k];
+    for (int k = 0; k < nchunk; ++k) c += h[k * E1 + e];
     sc += c;
     sa += c > 0;
   }
@@ -393,8 +396,8 @@ __global__ void __launch_bounds__(kRouteThreads) group_scan_kernel(MoeParams p, 
   for (int e = e0; e < e1; ++e) {
     const int s0 = start;
     for (int k = 0; k < nchunk; ++k) {  // chunk insert positions, in chunk order
-      const int c = h[e * nchunk + k];
-      h[e * nchunk + k] = start;
+      const int c = h[k * E1 + e];
+      h[k * E1 + e] = start;
       start += c;
     }
     if (start > s0) {
@@ -405,7 +408,7 @@ __global__ void __launch_bounds__(kRouteThreads) group_scan_kernel(MoeParams p, 
     }
   }
   __syncthreads();
-  for (int i = tid; i < E * nchunk; i += kRouteThreads) hist[i] = h[i];
+  for (int i = tid; i < E * nchunk; i += kRouteThreads) hist[i] = h[(i % nchunk) * E1 + i / nchunk];
   if (tid == kRouteThreads - 1) {
     int bad = 0;
     for (int k = 0; k < nchunk; ++k) bad += h[E * nchunk + k];

@@ -629,12 +629,29 @@ __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_d
       }
     }
   };
+  // Rows of up to kXRegs * 8 * kThreads values stay in registers between the
+  // maximum and the conversion; longer rows are read twice.
+  constexpr int kXRegs = 4;
+  float xv[kXRegs][8];
+  const bool cached = d <= kXRegs * 8 * kThreads;
   float m = 0.f;
-  for (int c = tid * 8; c < d; c += kThreads * 8) {
-    float v[8];
-    load8(c, v);
+  if (cached) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    for (int r = 0; r < kXRegs; ++r) {
+      const int c = (tid + r * kThreads) * 8;
+      if (c < d) {
+        load8(c, xv[r]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(xv[r][i]));
+      }
+    }
+  } else {
+    for (int c = tid * 8; c < d; c += kThreads * 8) {
+      float v[8];
+      load8(c, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+    }
   }
   m = op_over(m, 1, kWave, OpMax{});
   if ((tid & (kWave - 1)) == 0) red[tid / kWave] = m;
@@ -646,6 +663,19 @@ __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_d
   }
   __syncthreads();
   const int e = ex;
+  if (cached) {
+#pragma unroll
+    for (int r = 0; r < kXRegs; ++r) {
+      const int c = (tid + r * kThreads) * 8;
+      if (c < d) {
+        half8 h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(xv[r][i], e));
+        *reinterpret_cast<half8*>(xh + base + c) = h;
+      }
+    }
+    return;
+  }
   for (int c = tid * 8; c < d; c += kThreads * 8) {
     float v[8];
     load8(c, v);

@@ -214,6 +214,12 @@ template <int kPhase>
 __device__ __forceinline__ int tiles_per_key(const Params& p) {
   return kPhase == kPhaseA ? p.nka : kPhase == kPhaseC ? p.nkc : 1;
 }
+// Tiles of a key of the bulk (prefill) launches, the unit of work a
+// workgroup takes whole: A a (unit, factor), B, C and D a unit.
+template <int kPhase>
+__device__ __forceinline__ int bulk_key_tiles(const Params& p) {
+  return kPhase == kPhaseA ? p.nka : tiles_per_unit<kPhase>(p);
+}
 
 // LDS of the per-phase item kernel (phases A and D: one activation block).
 template <int kPhase>
@@ -730,12 +736,46 @@ __device__ __forceinline__ void finish_row(float4 s, _Float16* dst, int* dexp, i
   if (lane == 0) *dexp = ex;
 }
 
+// How a bulk launch deals its keys (runs of `per_key` consecutive tiles that
+// share activations: A a (unit, factor), B, C and D a unit) to workgroups.
+// Workgroup b runs on XCD x = b % 8 (workgroups go to the XCDs round robin),
+// as the j = b / 8-th of that XCD's J = G / 8.  XCD x takes the contiguous
+// block [K x / 8, K (x + 1) / 8) of the key list (unit-major, so an expert's
+// keys are neighbours, and a unit's gate and up keys too):
+//   * F = (its keys) / J full rounds: workgroup j takes keys j, j + J, ...
+//     whole, so the XCD's workgroups that run at the same time work on the
+//     keys of one expert, reading the same factor tile at the same K step
+//     and the same unit's activation slices: all but the first read of each
+//     hit that XCD's L2;
+//   * the rest (fewer than J keys) as even tile ranges of c tiles, so every
+//     workgroup ends within one tile of the others.
+// A partial sum of a K-tiled phase (A, C) belongs to a whole key (slot =
+// key) or to a piece of a rest key: slot 2 U + (x J + j) * kRemPieces + the
+// piece's key ordinal in workgroup j's range (a range of at most per_key
+// tiles meets at most two keys).
+struct Deal {
+  int kx0, F, J, rest0, T_rem, c;  // XCD's first key, full rounds, workgroups, first rest key, rest tiles, range
+};
+__host__ __device__ inline Deal deal_for(int nkey, int per_key, int G, int xcd) {
+  Deal d;
+  d.J = G >> 3;
+  d.kx0 = static_cast<int>(static_cast<int64_t>(nkey) * xcd / 8);
+  const int kx1 = static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8);
+  d.F = (kx1 - d.kx0) / d.J;
+  d.rest0 = d.kx0 + d.F * d.J;
+  d.T_rem = (kx1 - d.rest0) * per_key;
+  d.c = (d.T_rem + d.J - 1) / d.J;
+  return d;
+}
+constexpr int kRemPieces = 2;  // rest pieces per workgroup range (<= per_key tiles)
+
 // lat (phase A) / dlat (phase C) rows: the partial sums of each (unit,
 // factor, row) added in workgroup order.  One wave per (key, row); units of
 // at most kRows pairs (partial blocks of kRows rows).
 // kPerItem: phase C's partials are one per item (slot u * nkc + j, bc_kernel),
-// summed in item order.
-template <int kPhase, int kRows, bool kPerItem = false>
+// summed in item order.  kByKey: the bulk launches' slots (Deal): a whole
+// key's one partial, or a rest key's pieces in workgroup order.
+template <int kPhase, int kRows, bool kPerItem = false, bool kByKey = false>
 __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
@@ -752,8 +792,19 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
     const int u = key / keys_per_unit, f = key - u * keys_per_unit;
     const int4 info = p.unit_info[u];
     if (row >= info.z) continue;
-    const int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
-    const int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
+    int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
+    int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
+    Deal dl{};
+    int xcd = 0;
+    if constexpr (kByKey) {
+      const int nkey = U * keys_per_unit;
+      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
+      dl = deal_for(nkey, per_key, p.G, xcd);
+      // A whole key: b = -1 names its slot; a rest key: workgroups b0..b1 of the XCD.
+      const int rk = key - dl.rest0;
+      b0 = rk < 0 ? -1 : rk * per_key / dl.c;
+      b1 = rk < 0 ? -1 : ((rk + 1) * per_key - 1) / dl.c;
+    }
     // Batches of kRedLoads partials in flight, summed in workgroup (item) order.
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int bb = b0; bb <= b1; bb += kRedLoads) {
@@ -761,7 +812,11 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
         const int b = min(bb + q, b1);
-        const int64_t slot = kPerItem ? b : part_slot(b, key, chunk, per_key, maxj);
+        int64_t slot;
+        if constexpr (kByKey)
+          slot = b < 0 ? key : 2 * U + (xcd + 8 * b) * kRemPieces + key - (dl.rest0 * per_key + b * dl.c) / per_key;
+        else
+          slot = kPerItem ? b : part_slot(b, key, chunk, per_key, maxj);
         v[q] = reinterpret_cast<const float4*>(part + (slot * kRows + row) * kN)[lane];
       }
 #pragma unroll
@@ -1765,15 +1820,41 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = uniform(tid >> 6);
   const int n = lane & 15, kq = lane >> 4;
-  const int per_unit = tiles_per_unit<kPhase>(p), per_key = tiles_per_key<kPhase>(p);
+  const int per_unit = tiles_per_unit<kPhase>(p), per_key = bulk_key_tiles<kPhase>(p);
   const int U = uniform(sload(p.nunits));
-  const int total = U * per_unit;
-  const int b = blockIdx.x;
-  const int chunk = (total + p.G - 1) / p.G;
-  const int lo = b * chunk, hi = min(total, lo + chunk);
-  if (lo >= hi) return;
-  const int ntile = hi - lo;
-  const int maxj = (chunk + per_key - 1) / per_key + 1;
+  // Whole keys per workgroup, dealt XCD by XCD: workgroup b runs on XCD
+  // b % 8, which takes the contiguous block [K x / 8, K (x + 1) / 8) of the
+  // key list (unit-major, so an expert's keys are neighbours); its
+  // workgroups take the block's keys round robin.  Workgroups of one XCD
+  // that run at the same time then work on the keys of one expert, the same
+  // factor tile at the same K step, and the same unit's activation slices
+  // (gate and up keys of a unit are neighbours): all but the first read hit
+  // that XCD's L2.
+  const int nkey = U * (per_unit / per_key);
+  const int b = blockIdx.x, xcd = b & 7, jw = b >> 3;
+  const Deal dl = deal_for(nkey, per_key, p.G, xcd);
+  const int nfull = dl.F * per_key;                          // tiles of the whole keys
+  const int r0 = jw * dl.c;                                  // first rest tile of the range
+  const int nrest = max(0, min(dl.c, dl.T_rem - r0));
+  const int ntile = nfull + nrest;
+  if (ntile == 0) return;
+  // Flat tile index (unit-major, as tile_ref reads it) of the workgroup's tile i.
+  auto vt = [&](int i) __attribute__((always_inline)) {
+    if (i < nfull) {
+      const int r = i / per_key;
+      return (dl.kx0 + jw + r * dl.J) * per_key + (i - r * per_key);
+    }
+    return dl.rest0 * per_key + r0 + (i - nfull);
+  };
+  const int key_rest0 = (dl.rest0 * per_key + r0) / per_key;  // key of the first rest tile
+  // Segment (run of one key's tiles) ordinal of tile i in the workgroup, and
+  // the LDS table buffer it uses (segments alternate).
+  auto seg = [&](int i) __attribute__((always_inline)) {
+    return i < nfull ? i / per_key : dl.F + vt(i) / per_key - key_rest0;
+  };
+  auto kbuf = [&](int i) __attribute__((always_inline)) { return seg(i) & 1; };
+  // Tile i1 starts another segment than tile i1 - 1.
+  auto new_seg = [&](int i1) __attribute__((always_inline)) { return seg(i1) != seg(i1 - 1); };
 
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
@@ -1796,39 +1877,38 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
   for (int rb = 0; rb < kBulkBlocks; ++rb)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[rb][j] = float4v{0.f, 0.f, 0.f, 0.f};
-  auto unit_of = [&](int t) { return uniform(t / per_unit); };
 
   // Prologue: per-unit tables of tiles 0 and 1 (A, C) or the first unit's
   // activations (B, D); tile 0's activations and scales in LDS; the ring's
   // first tiles in flight.
 #pragma unroll
-  for (int r = 0; r + 1 < kBulkRing; ++r) ref[r] = tile_ref<kPhase>(p, min(lo + r, hi - 1));
-  const TileRef ref1 = tile_ref<kPhase>(p, min(lo + 1, hi - 1));
+  for (int r = 0; r + 1 < kBulkRing; ++r) ref[r] = tile_ref<kPhase>(p, vt(min(r, ntile - 1)));
+  const TileRef ref1 = tile_ref<kPhase>(p, vt(min(1, ntile - 1)));
   if constexpr (BS::kStaged) {
-    bulk_unit_tables<kPhase>(p, sm, ref[0], unit_of(lo) & 1, tid);
-    if (ntile > 1 && unit_of(lo + 1) != unit_of(lo)) bulk_unit_tables<kPhase>(p, sm, ref1, unit_of(lo + 1) & 1, tid);
+    bulk_unit_tables<kPhase>(p, sm, ref[0], 0, tid);
+    if (ntile > 1 && new_seg(1)) bulk_unit_tables<kPhase>(p, sm, ref1, 1, tid);
     lds_barrier();
-    bulk_issue_act<kPhase>(p, sm, ref[0], unit_of(lo) & 1, tid, true, st, tex);
+    bulk_issue_act<kPhase>(p, sm, ref[0], 0, tid, true, st, tex);
   } else {
     bulk_unit_act<kPhase>(p, sm, ref[0], tid, st);
   }
 #pragma unroll
   for (int r = 0; r + 1 < kBulkRing; ++r) issue_codes<kPhase>(p, ref[r], tid, lane, wave, r < ntile, sc[r], cb[r]);
-  if constexpr (BS::kStaged) bulk_store_act<kPhase>(sm, unit_of(lo) & 1, tid, st, tex);
+  if constexpr (BS::kStaged) bulk_store_act<kPhase>(sm, 0, tid, st, tex);
   sm.scales[tid] = sc[0];
 
   auto step = [&](int i, auto cs) __attribute__((always_inline)) {
     // Slots: c holds tile i, c1 tile i + 1, cl the tile issued now (i + kBulkRing - 1).
     constexpr int c = decltype(cs)::value, c1 = (c + 1) % kBulkRing, cl = (c + kBulkRing - 1) % kBulkRing;
-    const int t = lo + i;
-    const int ut = unit_of(t), ubuf = ut & 1;
+    const int t = vt(i);
+    const int ubuf = kbuf(i);
     lds_barrier();  // tile i's activations and scales are in LDS
     // Tile i + 1's activations first (A, C), then tile i + 2's codes: loads
     // complete in order, so the wait for the activations at the end of this
     // step leaves the codes in flight.
-    ref[cl] = tile_ref<kPhase>(p, min(t + kBulkRing - 1, hi - 1));
+    ref[cl] = tile_ref<kPhase>(p, vt(min(i + kBulkRing - 1, ntile - 1)));
     if constexpr (BS::kStaged)
-      bulk_issue_act<kPhase>(p, sm, ref[c1], unit_of(min(t + 1, hi - 1)) & 1, tid, i + 1 < ntile, st, tex);
+      bulk_issue_act<kPhase>(p, sm, ref[c1], kbuf(min(i + 1, ntile - 1)), tid, i + 1 < ntile, st, tex);
     issue_codes<kPhase>(p, ref[cl], tid, lane, wave, i + kBulkRing - 1 < ntile, sc[cl], cb[cl]);
     const TileRef& tr = ref[c];
     const int nrb = (tr.m + 15) >> 4;
@@ -1846,13 +1926,15 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
       bulk_steps<kPhase, 1>(sm, cb[c], n, kq, wave, lut_lane, acc);
 
     if constexpr (Shape<kPhase>::kSliceK) {
-      if (i + 1 == ntile || (t + 1) % per_key == 0) {
+      if (i + 1 == ntile || new_seg(i + 1)) {
+        // End of a segment: a whole key's sum (slot = key) or a rest piece
+        // (slot in the workgroup's rest range, see Deal).  Through a buffer
+        // resource: one lane offset, and each row's offset a constant in
+        // the scalar operand (no per-row 64-bit addresses to keep live
+        // across the loop).
         const int key = t / per_key;
-        // Through a buffer resource: one lane offset, and each row's offset a
-        // constant in the scalar operand (no per-row 64-bit addresses to keep
-        // live across the loop).
-        const float* part = (kPhase == kPhaseA ? p.partA : p.partC) +
-                            static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kBulkM * kN;
+        const int slot = i < nfull ? key : 2 * U + ((xcd + 8 * jw) * kRemPieces + key - key_rest0);
+        const float* part = (kPhase == kPhaseA ? p.partA : p.partC) + static_cast<int64_t>(slot) * kBulkM * kN;
         const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(part, kBulkM * kN * 4);
         const uint32_t lane_off = static_cast<uint32_t>(kq * 4 * kN + wave * 64 + n * 4) * 4;
 #pragma unroll
@@ -1943,13 +2025,13 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
 
     lds_barrier();  // every wave is done with tile i's activations and scales
     if constexpr (BS::kStaged) {
-      bulk_store_act<kPhase>(sm, unit_of(min(t + 1, hi - 1)) & 1, tid, st, tex);
-      // Tables of tile i + 2's unit, when it starts one (tile i + 1's unit,
-      // of the other parity, is the one in use).
-      if (i + 2 < ntile && unit_of(t + 2) != unit_of(t + 1))
-        bulk_unit_tables<kPhase>(p, sm, tile_ref<kPhase>(p, t + 2), unit_of(t + 2) & 1, tid);
+      bulk_store_act<kPhase>(sm, kbuf(min(i + 1, ntile - 1)), tid, st, tex);
+      // Tables of tile i + 2's segment, when it starts one (tile i + 1's
+      // segment, in the other buffer, is the one in use).
+      if (i + 2 < ntile && new_seg(i + 2))
+        bulk_unit_tables<kPhase>(p, sm, tile_ref<kPhase>(p, vt(i + 2)), kbuf(i + 2), tid);
     } else {
-      if (i + 1 < ntile && unit_of(t + 1) != ut) bulk_unit_act<kPhase>(p, sm, ref[c1], tid, st);
+      if (i + 1 < ntile && new_seg(i + 1)) bulk_unit_act<kPhase>(p, sm, ref[c1], tid, st);
     }
     sm.scales[tid] = sc[c1];
   };
@@ -2179,10 +2261,10 @@ bool bulk_supported(const latent_moe_args& a) {
 }
 
 size_t bulk_part_bytes(const latent_moe_args& a, int64_t max_units) {
-  const int G = grid_size();
-  const int nka = static_cast<int>(a.n_embd / kK), nkc = static_cast<int>(a.n_ff / kK);
-  const int64_t slots = std::max(part_slots(max_units, 2 * nka, nka, G), part_slots(max_units, nkc, nkc, G));
-  return static_cast<size_t>(slots) * kBulkM * kN * 4;
+  (void)a;
+  // One partial per whole key (A's (unit, factor) keys outnumber C's units)
+  // and kRemPieces per workgroup for the pieces of the rest keys (Deal).
+  return static_cast<size_t>(2 * max_units + kRemPieces * (grid_size() & ~7)) * kBulkM * kN * 4;
 }
 
 int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units, hipStream_t s) {
@@ -2217,18 +2299,19 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   p.nb = p.ff / kHBlock;
   p.nkc = p.ff / kK;
   p.nd = p.d / kN;
-  p.G = grid_size();
+  p.G = grid_size() & ~7;  // whole XCDs: the bulk kernels deal keys XCD by XCD (b % 8)
   const int64_t U = max_units;
-  auto grid = [&](int64_t per_unit) { return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(p.G, U * per_unit))); };
   auto rblocks = [](int64_t rows) {
     return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(2048, (rows + kT / kWave - 1) / (kT / kWave))));
   };
-  hipLaunchKernelGGL(bulk_kernel<kPhaseA>, dim3(grid(2 * p.nka)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM>), dim3(rblocks(U * 2 * kBulkM)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(bulk_kernel<kPhaseB>, dim3(grid(p.nb)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(grid(p.nkc)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM>), dim3(rblocks(U * kBulkM)), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL(bulk_kernel<kPhaseD>, dim3(grid(p.nd)), dim3(kT), 0, s, p);
+  // Every workgroup is launched (those the dealing leaves without a key
+  // return at once), so each XCD's block of keys is covered.
+  hipLaunchKernelGGL(bulk_kernel<kPhaseA>, dim3(p.G), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM, false, true>), dim3(rblocks(U * 2 * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseB>, dim3(p.G), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(p.G), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM, false, true>), dim3(rblocks(U * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL(bulk_kernel<kPhaseD>, dim3(p.G), dim3(kT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
