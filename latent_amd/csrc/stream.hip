@@ -115,7 +115,7 @@ struct Params {
   int* lexp;           // [2][P]
   _Float16* hh;        // bulk launches: [P][ff] h * 2^hexp
   int* hexp;           // bulk launches: [P][ff/32]
-  float* partC;        // [slots][16][256]
+  float* partC;        // decode: [P][nkc][256] by grouped pair; bulk launches: [slots][64][256]
   _Float16* dlat;      // [P][256]
   int* dexp;           // [P]
   float* ybuf;         // [P][d]
@@ -700,13 +700,16 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
       for (int j = 0; j < 4; ++j) accC[j] = part[j] = float4v{0.f, 0.f, 0.f, 0.f};
       bc_mfma<false, 0, kSteps / 2>(sm.hb[0], sm.hb[0], sbase, cb[c], n, kq, wave, lut_lane, accC);
       bc_mfma<false, kSteps / 2, kSteps / 2>(sm.hb[1], sm.hb[1], sbase, cb[c], n, kq, wave, lut_lane, part);
-      float* dst = p.partC + static_cast<int64_t>(it) * kMaxM * kN;
+      // The item's partial rows by grouped pair: row (pair * nkc + j).
+      const int iu = it / p.nkc, ij = it - iu * p.nkc;
+      const int istart = uniform(sload4(p.unit_info + iu)[1]);
+      float* dst = p.partC + (static_cast<int64_t>(istart) * p.nkc + ij) * kN;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = kq * 4 + v;
         const float s0 = ldexpf(1.0f, -sm.hexp[0][row]), s1 = ldexpf(1.0f, -sm.hexp[1][row]);
         if (row < m)
-          *reinterpret_cast<float4*>(dst + row * kN + wave * 64 + n * 4) =
+          *reinterpret_cast<float4*>(dst + static_cast<int64_t>(row) * p.nkc * kN + wave * 64 + n * 4) =
               make_float4(fmaf(part[0][v], s1, accC[0][v] * s0), fmaf(part[1][v], s1, accC[1][v] * s0),
                           fmaf(part[2][v], s1, accC[2][v] * s0), fmaf(part[3][v], s1, accC[3][v] * s0));
       }
@@ -772,8 +775,8 @@ constexpr int kRemPieces = 2;  // rest pieces per workgroup range (<= per_key ti
 // lat (phase A) / dlat (phase C) rows: the partial sums of each (unit,
 // factor, row) added in workgroup order.  One wave per (key, row); units of
 // at most kRows pairs (partial blocks of kRows rows).
-// kPerItem: phase C's partials are one per item (slot u * nkc + j, bc_kernel),
-// summed in item order.  kByKey: the bulk launches' slots (Deal): a whole
+// kPerItem: phase C's partials are one per item (bc_kernel), row (pair * nkc
+// + j) for item j of a unit, summed in item order.  kByKey: the bulk launches' slots (Deal): a whole
 // key's one partial, or a rest key's pieces in workgroup order.
 template <int kPhase, int kRows, bool kPerItem = false, bool kByKey = false>
 __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
@@ -812,12 +815,17 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
         const int b = min(bb + q, b1);
-        int64_t slot;
-        if constexpr (kByKey)
-          slot = b < 0 ? key : 2 * U + (xcd + 8 * b) * kRemPieces + key - (dl.rest0 * per_key + b * dl.c) / per_key;
-        else
-          slot = kPerItem ? b : part_slot(b, key, chunk, per_key, maxj);
-        v[q] = reinterpret_cast<const float4*>(part + (slot * kRows + row) * kN)[lane];
+        int64_t rowoff;  // float offset of the partial row
+        if constexpr (kByKey) {
+          const int64_t slot =
+              b < 0 ? key : 2 * U + (xcd + 8 * b) * kRemPieces + key - (dl.rest0 * per_key + b * dl.c) / per_key;
+          rowoff = (slot * kRows + row) * kN;
+        } else if constexpr (kPerItem) {
+          rowoff = (static_cast<int64_t>(info.y + row) * per_key + (b - key * per_key)) * kN;  // by grouped pair
+        } else {
+          rowoff = (static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kRows + row) * kN;
+        }
+        v[q] = reinterpret_cast<const float4*>(part + rowoff)[lane];
       }
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
@@ -2379,11 +2387,13 @@ Layout layout_for(const latent_moe_args& a) {
   const int64_t U = max_units(P, a.n_expert);
   const int G = grid_size();
   const int nka = static_cast<int>(d / kK);
-  // Partial blocks: A per workgroup range and segment; C one per item
-  // (bc_kernel: nkc per unit; the small-batch chain: nb per unit, in the
-  // same region).
+  // Partial blocks of 16 rows: A per workgroup range and segment.  C's
+  // partials are rows by grouped pair, nkc per pair (bc_kernel: one per item
+  // and row).  The small-batch chain (at most 16 routed pairs) keeps its
+  // partials in the same regions as [factor block][pair] rows: 2 nka blocks
+  // of A (fewer than A's slots here) and nb blocks of P rows of C.
   const int64_t blocksA = part_slots(U, 2 * nka, nka, G);
-  const int64_t blocksC = U * (ff / kHBlock);
+  const int64_t rowsC = P * (ff / kHBlock);
   Layout L{};
   size_t off = 0;
   L.xh = off;     off = al(off + static_cast<size_t>(T) * d * 2);
@@ -2391,7 +2401,7 @@ Layout layout_for(const latent_moe_args& a) {
   L.partA = off;  off = al(off + static_cast<size_t>(blocksA) * kMaxM * kN * 4);
   L.lath = off;   off = al(off + 2ull * P * kK * 2);
   L.lexp = off;   off = al(off + 2ull * P * 4);
-  L.partC = off;  off = al(off + static_cast<size_t>(blocksC) * kMaxM * kN * 4);
+  L.partC = off;  off = al(off + static_cast<size_t>(rowsC) * kN * 4);
   L.dlath = off;  off = al(off + static_cast<size_t>(P) * kK * 2);
   L.dexp = off;   off = al(off + static_cast<size_t>(P) * 4);
   L.ybuf = off;   off = al(off + static_cast<size_t>(P) * d * 4);

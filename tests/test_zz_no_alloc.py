@@ -73,8 +73,9 @@ def test_noalloc_matches_workspace_entry_dsv3(gpu):
     from latent_amd.moe import moe_path
 
     layer = gsynth.make_layer(seed=7, n_expert=256, d=7168, ff=2048, max_rank=256)
-    # two calls in a row, the second with a smaller input (streaming path, fixed-order sums)
-    for T in (16, 3):
+    # calls in a row, each with a smaller input (streaming path, fixed-order
+    # sums); batch 64 needs about 48 MiB of the 64 MiB array
+    for T in (64, 16, 3):
         x = gsynth.bf16_input(seed=1, n_tokens=T, d=7168)
         assert moe_path(layer, x, 8) == "stream"
         for mode in (0, 1):
