@@ -1130,8 +1130,14 @@ __device__ __forceinline__ void item_zero(const Params& p, int row, int chunk) {
   for (int col = threadIdx.x; col < ncol; col += kNT) dst[col] = 0.f;
 }
 
+// Waves per SIMD: two workgroups per CU (128 VGPRs) for pure-NF4 layers; one
+// workgroup per CU (256 VGPRs) with INT8 groups, whose second decode stage
+// spilled 321 VGPRs (372 bytes per lane) at 128.
 template <bool kInt8>
-__global__ void __launch_bounds__(kNT, 4) fused_kernel(Params p) {  // >= 4 waves per SIMD: two workgroups per CU
+constexpr int waves_per_simd() { return kInt8 ? 2 : 4; }
+
+template <bool kInt8>
+__global__ void __launch_bounds__(kNT, waves_per_simd<kInt8>()) fused_kernel(Params p) {
   __shared__ SmemLayout smem;
   const Smem s = carve(smem);
   const int tid = threadIdx.x;
@@ -1295,21 +1301,24 @@ bool make_plan(const latent_moe_args& a, Plan& pl) {
   return true;
 }
 
-static int grid_size() {
+// Workgroups that are resident at once: whole XCDs of CUs times the
+// workgroups per CU (fewer CUs when the kernel holds more registers).
+static int grid_size(int per_cu) {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (!cached[dev]) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = std::max(8, n / 8 * 8) * kWgPerCu;
+    cached[dev] = std::max(8, n / 8 * 8);
   }
-  return cached[dev];
+  return cached[dev] * per_cu;
 }
 
 template <bool kInt8>
 static int launch(const Params& p, hipStream_t s) {
-  const int grid = grid_size();
+  // 512 threads = 2 waves per SIMD per workgroup.
+  const int grid = grid_size(waves_per_simd<kInt8>() / 2);
   if (grid <= 0) return LATENT_E_HIP;
   hipLaunchKernelGGL(fused_kernel<kInt8>, dim3(grid), dim3(kNT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
