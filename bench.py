@@ -406,7 +406,6 @@ def hetero_point(torch, latent, gsynth, batches, steps, warmup):
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 TRAFFIC_PROFILE = {
     "stream": ("streaming_decode_b64_hbm_traffic.md", "traffic_bytes_per_step:"),
-    "fused": ("fused_kernel_decode_b64_hbm_traffic.md", "traffic_bytes_per_launch:"),
 }
 
 
@@ -524,7 +523,6 @@ def main():
             "kernel": {
                 "stream": "latent_moe_ffn_forward, streaming MFMA path: prep + 3 item kernels (A, B+C, D) + 2 "
                           "reductions + combine (7 launches per step; the step is the unit)",
-                "fused": "fused_kernel (one launch per step)",
             }.get(head["path"], "latent_moe_ffn_forward (prep + 3 phase kernels per step)"),
             "bytes_per_launch": head["bytes_per_step"],
         },
