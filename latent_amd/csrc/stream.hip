@@ -140,6 +140,10 @@ template <typename T>
 __device__ __forceinline__ T lds_ld(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
 }
+template <typename T>
+__device__ __forceinline__ void lds_st(uint32_t addr, const T& v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr)) = v;
+}
 
 // Loads through the scalar unit: the address must be the same in every lane.
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -221,14 +225,27 @@ __device__ __forceinline__ int bulk_key_tiles(const Params& p) {
   return kPhase == kPhaseA ? p.nka : tiles_per_unit<kPhase>(p);
 }
 
-// LDS of the per-phase item kernel (phases A and D: one activation block).
-template <int kPhase>
-struct alignas(16) Smem {
-  uint32_t lut[256 * kLutCopies];                              // [byte][copy]: half2(level(lo), level(hi))
-  u32x4 scales[2][kScaleBytes / 16];                           // [buffer]: the tile's scale block
-  u32x4 act[2][Shape<kPhase>::kActBlocks][kMaxM * kActChunks];  // [buffer][block][row][chunk ^ row]
-  int rexp[2][Shape<kPhase>::kExps];                           // row exponents of act[buffer]
+// LDS of the per-phase item kernels (phases A and D), 64 KB in 256 rows of
+// 256 bytes.  The first 128 bytes of row b hold the level pair of code byte b
+// in 32 copies (copy c at 4 c), so the table address of a code byte is one
+// byte permute of the byte and the lane's copy offset (row = byte << 8).  The
+// rows' other halves, 32 KB in all, hold the staging of a tile, addressed by
+// staging offset o (item_st): the scale blocks [2][4 KB], the activation rows
+// [2][16][32 chunks of 16 B] and the row exponents [2][16].  No 16-byte access
+// straddles a half row.
+struct alignas(16) ItemLds {
+  uint32_t w[256 * 64];
 };
+constexpr uint32_t kStScales = 0;
+constexpr uint32_t kStAct = kStScales + 2 * kScaleBytes;
+constexpr uint32_t kStExp = kStAct + 2 * kMaxM * kActChunks * 16;
+static_assert(kStExp + 2 * 16 * 4 <= 256 * 128, "a tile's staging fits the table rows' second halves");
+__device__ __forceinline__ uint32_t item_st(uint32_t o) { return o + (o & ~127u) + 128u; }
+// Table address of byte q of code dword x, for the lane's copy offset lc
+// (< 128): (byte << 8) | lc.
+__device__ __forceinline__ uint32_t lut_addr(uint32_t x, int q, uint32_t lc) {
+  return __builtin_amdgcn_perm(x, lc, 0x0C0C0000u | ((4u + q) << 8));
+}
 
 // Registers a tile's non-code loads land in before they are stored to LDS.
 template <int kPhase>
@@ -351,38 +368,40 @@ __device__ __forceinline__ void issue_act(const Params& p, const TileRef& tr, co
   }
 }
 
-// Store a staged tile into LDS buffer `buf`.
+// Store a staged tile into LDS buffer `buf` (L: the item kernel's LDS).
 template <int kPhase>
-__device__ __forceinline__ void store_stage(Smem<kPhase>& sm, int buf, const u32x4& sc, const StageAct<kPhase>& st,
-                                            int tid, int lane, int wave) {
-  sm.scales[buf][tid] = sc;
+__device__ __forceinline__ void store_stage(uint32_t L, int buf, const u32x4& sc, const StageAct<kPhase>& st, int tid,
+                                            int lane, int wave) {
+  static_assert(Shape<kPhase>::kActBlocks == 1 && Shape<kPhase>::kExps == 16, "phases A and D");
+  lds_st<u32x4>(L + item_st(kStScales + buf * kScaleBytes + tid * 16), sc);
   const int r0 = tid / kActChunks, chunk = tid % kActChunks;
 #pragma unroll
   for (int h = 0; h < Shape<kPhase>::kActLoads; ++h) {
     const int row = (r0 + 8 * h) % kMaxM;
-    sm.act[buf][h / 2][act_slot(row, chunk)] = st.act[h];
+    lds_st<u32x4>(L + item_st(kStAct + (buf * kMaxM * kActChunks + act_slot(row, chunk)) * 16), st.act[h]);
   }
-  if (wave == 0 && lane < Shape<kPhase>::kExps) sm.rexp[buf][lane] = st.ex;
+  if (wave == 0 && lane < 16) lds_st<int>(L + item_st(kStExp + (buf * 16 + lane) * 4), st.ex);
 }
 
-// MFMA steps [s0, s1) of a tile: acc[j] += act . (codes dword j, decoded and scaled).
-template <int kPhase>
-__device__ __forceinline__ void mfma_steps(const Smem<kPhase>& sm, int buf, const u32x4 (&cb)[kSteps], int s0, int s1,
-                                           int n, int kq, int wave, uint32_t lut_lane, float4v (&acc)[4]) {
-  const uint32_t sbase = lds_addr(const_cast<Smem<kPhase>&>(sm).scales[buf][0]);
+// The MFMA steps of a tile: acc[j] += act . (codes dword j, decoded and
+// scaled).  L: the item kernel's LDS; lc: the lane's table copy offset.
+__device__ __forceinline__ void mfma_steps(uint32_t L, int buf, const u32x4 (&cb)[kSteps], int n, int kq, int wave,
+                                           uint32_t lc, float4v (&acc)[4]) {
+  // The lane's scale dwords of step s sit 64 s bytes after those of step 0
+  // (fewer than 64 bytes into a half row), 128 more per step pair in LDS.
+  const uint32_t sc0 = L + item_st(kStScales + buf * kScaleBytes + scale_lane(2 * wave + (n >> 3), kq));
 #pragma unroll
-  for (int s = s0; s < s1; ++s) {
+  for (int s = 0; s < kSteps; ++s) {
     const int chunk = s * 4 + kq;
-    const half8 a0 = __builtin_bit_cast(half8, sm.act[buf][0][act_slot(n, chunk)]);
-    const int G = 2 * wave + (n >> 3);
-    const u32x4 sc = lds_ld<u32x4>(sbase + scale_lane(G, kq) + s * 64);
+    const half8 a0 = lds_ld<half8>(L + item_st(kStAct + (buf * kMaxM * kActChunks + act_slot(n, chunk)) * 16));
+    const u32x4 sc = lds_ld<u32x4>(sc0 + s * 64 + (s >> 1) * 128);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t x = cb[s][j];
       uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        const uint32_t pr = lds_ld<uint32_t>(L + lut_addr(x, q, lc));
         // Through a scalar: __builtin_bit_cast of a vector element reads element 0.
         const uint32_t sq = sc[q];
         f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
@@ -401,7 +420,8 @@ __device__ __forceinline__ int part_slot(int b, int key, int chunk, int per_key,
 template <int kPhase>
 __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
   static_assert(kPhase == kPhaseA || kPhase == kPhaseD, "phases B and C run in bc_kernel");
-  __shared__ Smem<kPhase> sm;
+  __shared__ ItemLds sm;
+  const uint32_t L = lds_addr(sm);
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = uniform(tid >> 6);
   const int n = lane & 15, kq = lane >> 4;
@@ -415,16 +435,16 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
   const int ntile = hi - lo;
   const int maxj = (chunk + per_key - 1) / per_key + 1;
 
-  // Level-pair table: thread tid fills entry tid's copies (rotated start, so
+  // Level-pair table: thread tid fills row tid's 32 copies (rotated start, so
   // the lanes of one store spread over the banks).
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
     const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
-    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
 #pragma unroll
-    for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+    for (int j = 0; j < 8; ++j) lds_st<u32x4>(L + tid * 256 + ((j + tid) & 7) * 16, u32x4{bits, bits, bits, bits});
   }
-  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+  static_assert(kLutCopies == 32, "one table copy per bank of a 32-lane half wave");
+  const uint32_t lc = (lane & 31) << 2;
 
   // Phase A's token rows of tile t (loaded one tile before the tile's loads).
   const int ar0 = tid / kActChunks, ar1 = ar0 + 8;
@@ -458,7 +478,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
   issue_codes<kPhase>(p, ref[0], tid, lane, wave, true, sc[0], cb[0]);
   issue_act<kPhase>(p, ref[1], tk[1], tid, lane, ntile > 1, sa[1]);
   issue_codes<kPhase>(p, ref[1], tid, lane, wave, ntile > 1, sc[1], cb[1]);
-  store_stage<kPhase>(sm, 0, sc[0], sa[0], tid, lane, wave);
+  store_stage<kPhase>(L, 0, sc[0], sa[0], tid, lane, wave);
 
   // Tile i sits in slot c = i % 3; tiles i + 1 and i + 2 in the other two.
   auto step = [&](int i, auto cs) __attribute__((always_inline)) {
@@ -471,7 +491,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
     issue_act<kPhase>(p, ref[c2], tk[c2], tid, lane, i + 2 < ntile, sa[c2]);
     issue_codes<kPhase>(p, ref[c2], tid, lane, wave, i + 2 < ntile, sc[c2], cb[c2]);
     const TileRef& tr = ref[c];
-    mfma_steps<kPhase>(sm, buf, cb[c], 0, kSteps, n, kq, wave, lut_lane, acc);
+    mfma_steps(L, buf, cb[c], n, kq, wave, lc, acc);
     const int t = lo + i;
     if constexpr (kPhase == kPhaseA) {
       // End of a segment (last tile of the range or of this key): one partial.
@@ -483,7 +503,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
           const int row = kq * 4 + v;
           if (row < tr.m) {
             // x's one exponent per token is the same in every tile.
-            const float sc = ldexpf(1.0f, -sm.rexp[buf][row]);
+            const float sc = ldexpf(1.0f, -lds_ld<int>(L + item_st(kStExp + (buf * 16 + row) * 4)));
             *reinterpret_cast<float4*>(part + row * kN + wave * 64 + n * 4) =
                 make_float4(acc[0][v] * sc, acc[1][v] * sc, acc[2][v] * sc, acc[3][v] * sc);
           }
@@ -497,7 +517,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
       for (int v = 0; v < 4; ++v) {
         const int row = kq * 4 + v;
         if (row < tr.m) {
-          const float sc = ldexpf(1.0f, -sm.rexp[buf][row]);
+          const float sc = ldexpf(1.0f, -lds_ld<int>(L + item_st(kStExp + (buf * 16 + row) * 4)));
           float* dst = p.ybuf + static_cast<int64_t>(tr.start + row) * p.d + tr.r * kN + wave * 64 + n * 4;
           *reinterpret_cast<float4*>(dst) = make_float4(acc[0][v] * sc, acc[1][v] * sc, acc[2][v] * sc, acc[3][v] * sc);
         }
@@ -507,7 +527,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
     }
     // Tile i + 1's scales and activations into the other LDS buffer (last
     // read by tile i - 1, which every wave finished before this step's barrier).
-    store_stage<kPhase>(sm, buf ^ 1, sc[c1], sa[c1], tid, lane, wave);
+    store_stage<kPhase>(L, buf ^ 1, sc[c1], sa[c1], tid, lane, wave);
   };
   // Whole triples without branches between the steps, then the last one or two.
   int i = 0;
@@ -532,32 +552,38 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) item_kernel(Params p) {
 // staged during the previous item's C tile.  Every C tile writes its own
 // partial d latent (slot = item), which reduce_kernel<kPhaseC, .., true> sums
 // in item order.
+// LDS: the item kernels' 64 KB of table rows (ItemLds) whose second halves
+// hold the gate / up latents of the current item's unit (staging offset
+// kBcAct, [2][16][32 chunks]) and h of the item's two 128-column blocks
+// (kBcHb, [2][16][16 chunks], a row's chunks at its first 16 slots), then the
+// scale blocks and the row exponents.
 struct alignas(16) BcSmem {
-  uint32_t lut[256 * kLutCopies];      // [byte][copy]: half2(level(lo), level(hi))
+  ItemLds rows;
   u32x4 scales[2][kScaleBytes / 16];   // [buffer]: the tile's scale block
-  u32x4 act[2][kMaxM * kActChunks];    // gate / up latents of the current item's unit
-  u32x4 hb[2][kMaxM * kActChunks];     // h of the item's two 128-column blocks (16 chunks a row)
   int lexp[2][kMaxM];                  // latent exponents
   int hexp[2][kMaxM];                  // h exponents per block
   float hmax[4][kMaxM];                // per-wave row maxima of h
 };
+constexpr uint32_t kBcAct = 0;
+constexpr uint32_t kBcHb = kBcAct + 2 * kMaxM * kActChunks * 16;
+static_assert(kBcHb + 2 * kMaxM * kActChunks * 16 <= 256 * 128, "latents and h fit the table rows' second halves");
 
 // MFMA steps [s0, s0 + ns) of a register tile: activation chunk 4 (s - s0) + kq
 // of act0 (and act1 for the up columns of a B tile), scale rows of step s.
 template <bool kTwo, int s0, int ns>
-__device__ __forceinline__ void bc_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
-                                        const u32x4 (&cb)[kSteps], int n, int kq, int wave, uint32_t lut_lane,
+__device__ __forceinline__ void bc_mfma(uint32_t L, uint32_t act0, uint32_t act1, uint32_t sbase,
+                                        const u32x4 (&cb)[kSteps], int n, int kq, int wave, uint32_t lc,
                                         float4v (&acc)[4]) {
 #pragma unroll
   for (int r = 0; r < ns; ++r) {
     const int s = s0 + r;
     const int chunk = r * 4 + kq;
-    const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
+    const half8 a0 = lds_ld<half8>(L + item_st(act0 + act_slot(n, chunk) * 16));
     const int S0 = s;  // K step (scale rows)
     u32x4 sc0, sc1;
     half8 a1;
     if constexpr (kTwo) {
-      a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
+      a1 = lds_ld<half8>(L + item_st(act1 + act_slot(n, chunk) * 16));
       const int Gg = wave, Gu = 4 + wave;
       sc0 = lds_ld<u32x4>(sbase + scale_lane(Gg, kq) + S0 * 64);
       sc1 = lds_ld<u32x4>(sbase + scale_lane(Gu, kq) + S0 * 64);
@@ -574,7 +600,7 @@ __device__ __forceinline__ void bc_mfma(const u32x4* act0, const u32x4* act1, ui
       uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        const uint32_t pr = lds_ld<uint32_t>(L + lut_addr(x, q, lc));
         const uint32_t sq = sc[q];  // through a scalar: a bit_cast of a vector element reads element 0
         f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
       }
@@ -597,26 +623,44 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
   const int lo = b * chunk, hi = min(total, lo + chunk);
   if (lo >= hi) return;
   const int ntile = 3 * (hi - lo);
+  const uint32_t L = lds_addr(sm.rows);
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
     const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
-    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * kLutCopies]);
 #pragma unroll
-    for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+    for (int j = 0; j < 8; ++j) lds_st<u32x4>(L + tid * 256 + ((j + tid) & 7) * 16, u32x4{bits, bits, bits, bits});
   }
-  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+  const uint32_t lc = (lane & 31) << 2;
   const int r0 = tid / kActChunks, ch = tid % kActChunks;
 
-  // Codes and scales of tile t of the range (loads past the range fetch nothing).
+  // Codes and scales of tile t of the range (loads past the range fetch
+  // nothing): a B tile (kind 0, 1) is the gate_b and up_b half tiles of h
+  // block 2 j + kind (as load_btile lays them out), a C tile (kind 2) down_a's
+  // tile j (as load_full).  Both kinds issue the same loads, one scale block
+  // and eight code quads, and the kind selects only their bases and offsets:
+  // with a branch between two load sequences the compiler's wait counts,
+  // merged over both paths, waited for every load, including those just
+  // issued for the tile two steps ahead.
   auto issue_codes = [&](int t, u32x4& sc, u32x4 (&cb)[kSteps]) __attribute__((always_inline)) {
     const int tt = min(t, ntile - 1);
     const int it = lo + tt / 3, kind = tt % 3;
     const int u = it / p.nkc, j = it - u * p.nkc;
     const int e = uniform(sload4(p.unit_info + u)[0]);
-    if (kind < 2)
-      load_btile(p, e * p.nb + 2 * j + kind, t < ntile, tid, lane, wave, sc, cb);
-    else
-      load_full<kSteps>(p, F_DOWN_A, e * p.nkc + j, t < ntile, true, 0, tid, lane, wave, sc, cb);
+    const bool bt = kind < 2, valid = t < ntile;
+    const int64_t hb = static_cast<int64_t>(e) * p.nb + 2 * j + kind;  // B: half tile of gate_b / up_b
+    const int64_t ct = static_cast<int64_t>(e) * p.nkc + j;            // C: tile of down_a
+    const uint8_t* sbase = bt ? (wave < 2 ? p.scales[F_GATE_B] : p.scales[F_UP_B]) + hb * kHalfScaleBytes
+                              : p.scales[F_DOWN_A] + ct * kScaleBytes;
+    const uint8_t* c0 = bt ? p.codes[F_GATE_B] + hb * kHalfCodeBytes : p.codes[F_DOWN_A] + ct * kCodeBytes;
+    const uint8_t* c1 = bt ? p.codes[F_UP_B] + hb * kHalfCodeBytes : c0;
+    const uint32_t cbytes = valid ? (bt ? kHalfCodeBytes : kCodeBytes) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sbase, valid ? (bt ? kHalfScaleBytes : kScaleBytes) : 0u);
+    sc = ld128_tile(rs, bt ? (tid & 127) * 16 : tid * 16, 0);
+    const __amdgpu_buffer_rsrc_t r0 = buffer_rsrc(c0, cbytes), r1 = buffer_rsrc(c1, cbytes);
+    const uint32_t cbase = (bt ? wave * (kSteps / 2 * kWave * 16) : wave * (kSteps * kWave * 16)) + lane * 16;
+#pragma unroll
+    for (int q = 0; q < kSteps; ++q)
+      cb[q] = ld128_tile(q < kSteps / 2 ? r0 : r1, cbase, (bt ? q % (kSteps / 2) : q) * kWave * 16);
   };
   // Gate / up latent rows (rows past the unit's pairs repeat its last pair)
   // and exponents of item it's unit.
@@ -638,7 +682,8 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
   };
   auto store_lat = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) sm.act[h / 2][act_slot((r0 + 8 * h) % kMaxM, ch)] = st[h];
+    for (int h = 0; h < 4; ++h)
+      lds_st<u32x4>(L + item_st(kBcAct + ((h / 2) * kMaxM * kActChunks + act_slot((r0 + 8 * h) % kMaxM, ch)) * 16), st[h]);
     if (wave == 0 && lane < 32) sm.lexp[lane >> 4][lane & 15] = stex;
   };
 
@@ -664,7 +709,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
       float4v accB[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) accB[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      bc_mfma<true, 0, kSteps>(sm.act[0], sm.act[1], sbase, cb[c], n, kq, wave, lut_lane, accB);
+      bc_mfma<true, 0, kSteps>(L, kBcAct, kBcAct + kMaxM * kActChunks * 16, sbase, cb[c], n, kq, wave, lc, accB);
       // h = SiLU(g) * u of columns 32w + 2n + jj of block c, fp16 with one exponent per row.
       float hv[2][4];
 #pragma unroll
@@ -689,7 +734,8 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
         half2v h2;
         h2[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
         h2[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
-        reinterpret_cast<half2v*>(&sm.hb[c][act_slot(row, 4 * wave + (n >> 2))])[n & 3] = h2;
+        lds_st<half2v>(L + item_st(kBcHb + (c * kMaxM * kActChunks + act_slot(row, 4 * wave + (n >> 2))) * 16 + (n & 3) * 4),
+                       h2);
         if (wave == 0 && n == 0) sm.hexp[c][row] = ex;
       }
     } else {
@@ -698,8 +744,9 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bc_kernel(Params p) {
       float4v accC[4], part[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) accC[j] = part[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      bc_mfma<false, 0, kSteps / 2>(sm.hb[0], sm.hb[0], sbase, cb[c], n, kq, wave, lut_lane, accC);
-      bc_mfma<false, kSteps / 2, kSteps / 2>(sm.hb[1], sm.hb[1], sbase, cb[c], n, kq, wave, lut_lane, part);
+      constexpr uint32_t kHb1 = kBcHb + kMaxM * kActChunks * 16;
+      bc_mfma<false, 0, kSteps / 2>(L, kBcHb, kBcHb, sbase, cb[c], n, kq, wave, lc, accC);
+      bc_mfma<false, kSteps / 2, kSteps / 2>(L, kHb1, kHb1, sbase, cb[c], n, kq, wave, lc, part);
       // The item's partial rows by grouped pair: row (pair * nkc + j).
       const int iu = it / p.nkc, ij = it - iu * p.nkc;
       const int istart = uniform(sload4(p.unit_info + iu)[1]);
