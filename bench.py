@@ -12,6 +12,14 @@ timed loop rotates over `--layers` independently generated layers (1 GB of
 packed factors each) and several routings; consecutive steps never touch the
 same layer.
 
+Timing of the decode points: W eager warmup steps, then exactly K steps
+captured in one HIP graph (torch.cuda.CUDAGraph) that is replayed once
+untimed and once timed, HIP events around the timed replay: the seven
+kernels of a step run back to back as in a graph-launched decode loop (the
+way the reference's llama.cpp backend launches decode).  The same K steps
+issued eagerly are timed too and reported as `eager_ms_per_step`
+(`--timing eager` makes them the figure).
+
 The headline `value` is tokens/s at batch 64; batches 1, 8 and 32, the
 4096-token prefill, the heterogeneous-rank layer (ranks 64..512, 10% INT8
 groups, drop below 0.05, batches 16 and 256) and the 58-layer graph-captured
@@ -57,8 +65,8 @@ def parse():
     p.add_argument("--prefill-steps", type=int, default=5)
     p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
     p.add_argument("--routings", type=int, default=16, help="distinct routings per batch size")
-    p.add_argument("--graph-steps", type=int, default=16,
-                   help="decode steps captured in one HIP graph for the graph-replay timing (0 to skip)")
+    p.add_argument("--timing", choices=("graph", "eager"), default="graph",
+                   help="decode points: K steps replayed from one HIP graph (default) or issued eagerly")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--copy-probe-mb", type=int, default=0,
                    help="run one device-to-device copy of this many MiB first (counter calibration)")
@@ -100,26 +108,24 @@ def time_loop(fn, n_steps, warmup, torch):
     return start.elapsed_time(end) / n_steps  # ms per step
 
 
-def graph_time(torch, fn, n_in_graph, replays):
-    """ms per step of `n_in_graph` steps captured once in a HIP graph
-    (torch.cuda.CUDAGraph) and replayed `replays` times: the GPU time of the
-    steps without the host's per-call enqueue."""
+def graph_time(torch, fn, n_steps):
+    """ms per step of exactly `n_steps` steps captured once in a HIP graph
+    (torch.cuda.CUDAGraph): one untimed replay, then one timed replay."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for i in range(n_in_graph):
-            fn(i)
+        fn(0)
     torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(n_in_graph):
+        for i in range(n_steps):
             fn(i)
-    ms = time_loop(lambda i: g.replay(), replays, 2, torch)
+    ms = time_loop(lambda i: g.replay(), 1, 1, torch)
     del g
-    return ms / n_in_graph
+    return ms / n_steps
 
 
-def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings, graph_steps=0):
+def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings, timing="graph"):
     routes = [gsynth.route(seed=10_000 + 97 * batch + r, n_tokens=batch, n_expert=E, k=K) for r in range(n_routings)]
     xs = [gsynth.bf16_input(seed=20_000 + 89 * batch + r, n_tokens=batch, d=D) for r in range(n_routings)]
     outs = [torch.empty((batch, D), dtype=torch.float32, device="cuda") for _ in range(n_routings)]
@@ -132,8 +138,9 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
         ids, w = routes[r]
         latent.moe_forward(xs[r], ids, w, layers[i % len(layers)], out=outs[r], workspace=ws)
 
-    ms = time_loop(step, steps, warmup, torch)
-    gms = graph_time(torch, step, graph_steps, max(4, steps // graph_steps)) if graph_steps else None
+    eager = time_loop(step, steps, warmup, torch)
+    gms = graph_time(torch, step, steps) if timing == "graph" else None
+    ms = gms if gms is not None else eager
     ids_host = [routes[i % n_routings][0].cpu().numpy() for i in range(steps)]
     bytes_per_step = float(np.mean(realized_bytes(ids_host)))
     gbps = bytes_per_step / (ms * 1e-3) / 1e9
@@ -142,7 +149,8 @@ def decode_point(torch, latent, gsynth, layers, batch, steps, warmup, n_routings
         "path": latent.moe_path(layers[0], xs[0], K),
         "launch": latent.moe.stream_launch(layers[0], xs[0], K),
         "ms_per_step": ms,
-        "graph_ms_per_step": gms,
+        "timing": timing,
+        "eager_ms_per_step": eager,
         "tokens_per_s": batch / (ms * 1e-3),
         "hbm_gbps": gbps,
         "roofline_frac": gbps / HBM_PEAK_GBPS,
@@ -449,17 +457,16 @@ def main():
           file=sys.stderr, flush=True)
 
     def show(pt):
-        g = pt["graph_ms_per_step"]
-        return (f"# decode B={pt['batch']}: {pt['ms_per_step'] * 1e3:.1f} us/step, {pt['hbm_gbps']:.0f} GB/s"
-                + (f"; graph replay {g * 1e3:.1f} us/step" if g else ""))
+        return (f"# decode B={pt['batch']}: {pt['ms_per_step'] * 1e3:.1f} us/step ({pt['timing']}), "
+                f"{pt['hbm_gbps']:.0f} GB/s; eager {pt['eager_ms_per_step'] * 1e3:.1f} us/step")
 
     head, routes, xs = decode_point(torch, latent, gsynth, layers, args.batch, args.steps, args.warmup, args.routings,
-                                    args.graph_steps)
+                                    args.timing)
     print(show(head), file=sys.stderr, flush=True)
     sweep = []
     for b in [int(v) for v in args.sweep.split(",") if v.strip()]:
         pt, _, _ = decode_point(torch, latent, gsynth, layers, b, args.steps, args.warmup, args.routings,
-                                args.graph_steps)
+                                args.timing)
         sweep.append(pt)
         print(show(pt), file=sys.stderr, flush=True)
     prefill, prefill_inputs = None, None
@@ -500,6 +507,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"],
+        "timing": head["timing"],
+        "eager_ms_per_step": head["eager_ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
