@@ -508,17 +508,74 @@ template <int MB, bool kInt8>
 __device__ __forceinline__ void accumulate_rows(const Factor& f, int64_t e, int row_begin, int row_end, int step, int g,
                                                 const float* lut, const float* vin, int vstride, int vbase, int m,
                                                 float (&acc)[MB][kGroup]) {
-  if constexpr (kInt8) {
-    for (int row = row_begin; row < row_end; row += step) {
-      float v[kGroup];
-      decode_group<true>(f, e, row, g, lut, v);
-      const float s = group_scale(f, e, row, g);
+  if (kInt8 && f.ext.bitmap != nullptr) {
+    // U rows per pass, every load of a row independent of the others: the
+    // codes, the scale, the group's bitmap word and its word offset (the
+    // side-buffer index of the word's first INT8 group), then, for the lanes
+    // whose group is INT8, its 32 bytes.  (One row at a time, the chain
+    // bitmap -> offset -> data paid three dependent round trips per row.)
+    constexpr int U = 2;
+    const int words = f.words(), wsel = g >> 5;
+    const uint32_t bit = 1u << (g & 31);
+    const int64_t cstride = f.code_stride(), sstride = f.scale_stride(), erow0 = e * f.rows;
+    for (int row = row_begin; row < row_end; row += U * step) {
+      uint4 c[U], q[U][2];
+      float s[U];
+      uint32_t wd[U];
+      int64_t wo[U];
 #pragma unroll
-      for (int t = 0; t < MB; ++t) {
-        if (t < m) {
-          const float xs = vin[t * vstride + row - vbase] * s;
+      for (int u = 0; u < U; ++u) {
+        const int r = min(row + u * step, row_end - 1);  // past the end: row_end - 1 again, never used
+        const int64_t er = erow0 + r;
+        c[u] = *reinterpret_cast<const uint4*>(f.codes + er * cstride + static_cast<int64_t>(g) * kGroupBytes);
+        s[u] = half_bits_to_float(f.scales[er * sstride + g]);
+        wd[u] = f.ext.bitmap[er * words + wsel];
+        wo[u] = words == 1 ? f.ext.row_offset[er]
+                           : (f.ext.word_offset ? f.ext.word_offset[er * words + wsel] : int64_t{-1});
+      }
 #pragma unroll
-          for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+      for (int u = 0; u < U; ++u) {
+        q[u][0] = q[u][1] = make_uint4(0u, 0u, 0u, 0u);
+        if (wd[u] & bit) {
+          int64_t idx = wo[u];
+          if (idx < 0) {  // no word offsets built: count the row's earlier words
+            const int r = min(row + u * step, row_end - 1);
+            const uint32_t* bm = f.ext.bitmap + (erow0 + r) * words;
+            idx = f.ext.row_offset[erow0 + r];
+            for (int w = 0; w < wsel; ++w) idx += popc(bm[w]);
+          }
+          idx += popc(wd[u] & (bit - 1u));
+          const uint4* qp = reinterpret_cast<const uint4*>(f.ext.data + idx * kGroup);
+          q[u][0] = qp[0];
+          q[u][1] = qp[1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = row + u * step;
+        if (r >= row_end) break;
+        float v[kGroup];
+        if (wd[u] & bit) {
+          const uint32_t qw[8] = {q[u][0].x, q[u][0].y, q[u][0].z, q[u][0].w,
+                                  q[u][1].x, q[u][1].y, q[u][1].z, q[u][1].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) v[i * 4 + b] = static_cast<float>(static_cast<int8_t>((qw[i] >> (8 * b)) & 0xFF));
+        } else {
+          const uint32_t cw[4] = {c[u].x, c[u].y, c[u].z, c[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int n = 0; n < 8; ++n) v[i * 8 + n] = lut[(cw[i] >> (4 * n)) & 15u];
+        }
+#pragma unroll
+        for (int t = 0; t < MB; ++t) {
+          if (t < m) {
+            const float xs = vin[t * vstride + r - vbase] * s[u];
+#pragma unroll
+            for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+          }
         }
       }
     }
