@@ -212,3 +212,36 @@ def test_int8_group_selection_matches_oracle(gpu):
               f"{int(borderline.sum())} borderline")
         assert 0 < want.sum() < want.size
         assert not ((got != want) & ~borderline).any()
+
+
+def _fake_int8_args(L, d, E=512, R=256, ff=512, T=8, k=8):
+    """Arguments whose pointers are never dereferenced (a path query only),
+    with INT8 groups on gate_a (d x R per expert)."""
+    def fac(rows, cols, int8=False):
+        f = L.LatentFactor(codes=1 << 20, scales=2 << 20, rows=rows, cols=cols)
+        if int8:
+            f.int8_bitmap, f.int8_row_offset, f.int8_data = 3 << 20, 4 << 20, 5 << 20
+        return f
+
+    a = L.LatentMoeArgs()
+    a.gate_a, a.gate_b = fac(d, R, True), fac(R, ff)
+    a.up_a, a.up_b = fac(d, R), fac(R, ff)
+    a.down_a, a.down_b = fac(ff, R), fac(R, d)
+    a.x, a.ids, a.weights, a.out = 6 << 20, 7 << 20, 8 << 20, 9 << 20
+    a.n_tokens, a.n_embd, a.n_ff, a.n_expert, a.n_expert_used, a.max_rank = T, d, ff, E, k, R
+    a.x_dtype, a.weights_dtype, a.out_mode = L.LATENT_BF16, L.LATENT_F32, L.LATENT_OUT_REDUCED
+    return a
+
+
+def test_int8_side_buffer_beyond_32_bit_offsets_leaves_the_persistent_kernel(gpu):
+    """The persistent kernel reads INT8 groups with 32-bit byte offsets: a
+    factor whose side buffer could reach 2^31 bytes (every group INT8) goes to
+    the multi-kernel path, one just below stays on the persistent kernel."""
+    import ctypes
+
+    from latent_amd import _lib as L
+
+    below = _fake_int8_args(L, d=8192)  # 512 x 8192 x 256 = 2^30 bytes of INT8 at most
+    beyond = _fake_int8_args(L, d=16384)  # 2^31 bytes
+    assert L.lib.latent_moe_path(ctypes.byref(below)) == 1
+    assert L.lib.latent_moe_path(ctypes.byref(beyond)) == 0

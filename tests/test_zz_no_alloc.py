@@ -170,3 +170,47 @@ def test_noalloc_graph_capture_replays(gpu):
         other = _noalloc(layer, gsynth.bf16_input(seed=50 + i, n_tokens=1, d=1024), ids[:1], w[:1])
         torch.cuda.synchronize()
         assert not torch.isnan(other).any()
+
+
+_FIRST_CALL = r'''
+import ctypes, sys
+sys.path.insert(0, sys.argv[1])
+import torch
+from latent_amd import _lib
+from oracle import synth
+from tests._layers import to_device
+from tests.test_zz_no_alloc import _args
+
+layer = to_device(synth.make_layer(seed=101, n_expert=16, d=256, ff=512, max_rank=64))
+from latent_amd import synth as gsynth
+ids, w = gsynth.route(seed=7, n_tokens=40, n_expert=16, k=4)
+x = gsynth.bf16_input(seed=8, n_tokens=40, d=256)
+import latent_amd
+want = latent_amd.moe_forward(x, ids, w, layer)
+out = torch.full((40, 256), float("nan"), dtype=torch.float32, device="cuda")
+a = _args(layer, x, ids, w, out)
+a.workspace, a.workspace_bytes = None, 0
+torch.cuda.synchronize()
+hip = ctypes.CDLL("libamdhip64.so")
+assert hip.hipSetDevice(ctypes.c_int(4096)) != 0  # an unrelated failed call, its error left pending
+st = _lib.lib.latent_moe_ffn_forward_noalloc(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+assert st == _lib.LATENT_OK, _lib.status_string(st)
+torch.cuda.synchronize()
+assert torch.equal(out, want)
+print("first call ok")
+'''
+
+
+def test_noalloc_first_call_after_an_unrelated_hip_error(gpu, tmp_path):
+    """The first allocation-free call of a process sets up the device's
+    scratch array; a HIP error that earlier, unrelated code left pending must
+    not fail it (checked in a fresh process, where that call is the first)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    script = tmp_path / "first_call.py"
+    script.write_text(_FIRST_CALL)
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, str(script), root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "first call ok" in r.stdout, r.stdout + r.stderr
