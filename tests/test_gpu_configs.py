@@ -72,6 +72,38 @@ def test_prefill_4096_skewed(gpu, dsv3):
     assert ref.rel_l2((s * w[..., None]).sum(1), red.cpu().numpy()) <= 1e-3
 
 
+def test_prefill_4096_with_empty_experts(gpu, dsv3):
+    # The same skewed routing with every 16th expert's slots moved to its
+    # neighbour: 16 experts receive no token (no unit, no tile of theirs may
+    # run), their neighbours twice the load.
+    import torch
+
+    from latent_amd import synth as gsynth
+
+    T = 4096
+    ids_t, w_t = gsynth.route(seed=30_000, n_tokens=T, n_expert=E, k=K, rank_beta=1.5)
+    ids = ids_t.cpu().numpy()
+    ids = np.where(ids % 16 == 0, ids + 1, ids).astype(np.int32)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    assert (counts == 0).sum() == 16
+    ids_t = torch.from_numpy(ids).cuda()
+    x_t = gsynth.bf16_input(seed=30_002, n_tokens=T, d=D)
+    assert gpu.moe_path(dsv3, x_t, K) == "prefill"
+    red = gpu.moe_forward(x_t, ids_t, w_t, dsv3, out_mode=0)
+    slot = gpu.moe_forward(x_t, ids_t, w_t, dsv3, out_mode=1)
+    torch.cuda.synchronize()
+    w, x = w_t.cpu().numpy(), x_t.float().cpu().numpy()
+    hot = int(np.argmax(counts))
+    tokens = np.array(sorted({int(np.nonzero((ids == hot).any(1))[0][0])} | set(range(7, T, T // 24))))[:28]
+    per_slot, reduced, n_exp = _oracle(dsv3, x, ids, w, tokens)
+    err_red = ref.rel_l2(reduced, red.cpu().numpy()[tokens])
+    err_slot = ref.rel_l2(per_slot, slot.cpu().numpy()[tokens])
+    print(f"prefill 4096, 16 empty experts: {tokens.size} tokens, {n_exp} experts: reduced {err_red:.3e} "
+          f"per-slot {err_slot:.3e}")
+    assert err_red <= TOL and err_slot <= TOL
+    assert not torch.isnan(red).any()
+
+
 def test_prefill_per_slot_zeroes_dropped_slots(gpu):
     # Per-slot output on the prefill path: dropped (-1) and out-of-range ids
     # give exact zero rows, routed rows match the oracle.
