@@ -966,19 +966,21 @@ __device__ __forceinline__ int range_lo(int N, int b, int G) {
 // srow0 + r of the tile (its scale rows) and activation chunk step r.
 // acc[j] += act . (codes dword j, decoded and scaled); act1 feeds the up
 // columns of a B tile (kTwo).
+// L: the workgroup's table rows (ItemLds); act0 / act1: staging offsets of
+// the activation blocks; lc: the lane's table copy offset.
 template <bool kTwo, int ns>
-__device__ __forceinline__ void reg_mfma(const u32x4* act0, const u32x4* act1, uint32_t sbase,
+__device__ __forceinline__ void reg_mfma(uint32_t L, uint32_t act0, uint32_t act1, uint32_t sbase,
                                           const u32x4 (&cb)[kSteps], int srow0, int n, int kq, int wave,
-                                          uint32_t lut_lane, float4v (&acc)[4]) {
+                                          uint32_t lc, float4v (&acc)[4]) {
 #pragma unroll
   for (int r = 0; r < ns; ++r) {
     const int chunk = r * 4 + kq;
-    const half8 a0 = __builtin_bit_cast(half8, act0[act_slot(n, chunk)]);
+    const half8 a0 = lds_ld<half8>(L + item_st(act0 + act_slot(n, chunk) * 16));
     const int S0 = srow0 + r;  // K step (scale rows)
     u32x4 sc0, sc1;
     half8 a1;
     if constexpr (kTwo) {
-      a1 = __builtin_bit_cast(half8, act1[act_slot(n, chunk)]);
+      a1 = lds_ld<half8>(L + item_st(act1 + act_slot(n, chunk) * 16));
       const int Gg = wave, Gu = 4 + wave;
       sc0 = lds_ld<u32x4>(sbase + scale_lane(Gg, kq) + S0 * 64);
       sc1 = lds_ld<u32x4>(sbase + scale_lane(Gu, kq) + S0 * 64);
@@ -995,7 +997,7 @@ __device__ __forceinline__ void reg_mfma(const u32x4* act0, const u32x4* act1, u
       uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+        const uint32_t pr = lds_ld<uint32_t>(L + lut_addr(x, q, lc));
         const uint32_t sq = sc[q];
         f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
       }
@@ -1007,8 +1009,9 @@ __device__ __forceinline__ void reg_mfma(const u32x4* act0, const u32x4* act1, u
 }
 
 // A row of 256 sums (four per lane) -> fp16 row * 2^e in an LDS activation
-// block (chunk layout of act_slot) and its exponent.
-__device__ __forceinline__ void finish_row_lds(float4 s, u32x4* blk, int* exps, int r, int lane) {
+// block (chunk layout of act_slot, at staging offset blk of the table rows L)
+// and its exponent.
+__device__ __forceinline__ void finish_row_lds(float4 s, uint32_t L, uint32_t blk, int* exps, int r, int lane) {
   const float mx = op_over(fmaxf(fmaxf(fabsf(s.x), fabsf(s.y)), fmaxf(fabsf(s.z), fabsf(s.w))), 1, kWave, OpMax{});
   const int ex = pow2_row_exponent(mx);
   half4v h;
@@ -1016,7 +1019,7 @@ __device__ __forceinline__ void finish_row_lds(float4 s, u32x4* blk, int* exps, 
   h[1] = static_cast<_Float16>(ldexpf(s.y, ex));
   h[2] = static_cast<_Float16>(ldexpf(s.z, ex));
   h[3] = static_cast<_Float16>(ldexpf(s.w, ex));
-  reinterpret_cast<half4v*>(&blk[act_slot(r, lane >> 1)])[lane & 1] = h;
+  lds_st<half4v>(L + item_st(blk + act_slot(r, lane >> 1) * 16 + (lane & 1) * 8), h);
   if (lane == 0) exps[r] = ex;
 }
 
@@ -1082,12 +1085,18 @@ __host__ __device__ inline bool lite_fits(int U, int nka, int nb, int nd, int G)
   return (NA + s.gA - 1) / s.gA <= kLiteSlots && (ND + s.gD - 1) / s.gD <= kLiteSlots;
 }
 
+// The table rows (ItemLds) hold in their second halves the activation
+// blocks (staging offset kLtAct, [2][16][32 chunks]; A: x rows; BC: gate / up
+// latents; D: down latent in block 0), h (kLtHb, [16][32 chunks], 128
+// columns) and the latent sums (kLtRed, [row of 2][wave][lane] float4).
+constexpr uint32_t kLtAct = 0;
+constexpr uint32_t kLtHb = kLtAct + 2 * kMaxM * kActChunks * 16;
+constexpr uint32_t kLtRed = kLtHb + kMaxM * kActChunks * 16;
+static_assert(kLtRed + 2 * 4 * kWave * 16 <= 256 * 128, "the chain's staging fits the table rows' second halves");
+constexpr uint32_t lt_act(int blk) { return kLtAct + blk * kMaxM * kActChunks * 16; }
 struct alignas(16) LiteSmem {
-  uint32_t lut[256 * kLutCopies];       // [byte][copy]: half2(level(lo), level(hi))
+  ItemLds rows;
   u32x4 scales[2][kScaleBytes / 16];    // scale blocks of the one or two tiles being computed
-  u32x4 act[2][kMaxM * kActChunks];     // A: x rows; BC: gate / up latents; D: down latent (block 0)
-  u32x4 hb[kMaxM * kActChunks];         // BC: h rows (128 columns)
-  float4 red[2][4][kWave];              // latent sums: [row of 2][wave][lane]
   int rexp[2][kMaxM];                   // exponents of act's rows
   int hexp[kMaxM];                      // h exponents
   float hmax[4][kMaxM];                 // per-wave row maxima of h
@@ -1099,12 +1108,13 @@ struct alignas(16) LiteSmem {
   int nunits, nlast;
 };
 
-__device__ __forceinline__ void lut_fill(uint32_t* lut, int tid) {
+// Level-pair table: thread tid fills row tid's 32 copies (rotated start, so
+// the lanes of one store spread over the banks).
+__device__ __forceinline__ void lut_fill(uint32_t L, int tid) {
   const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
   const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
-  uint4* dstv = reinterpret_cast<uint4*>(&lut[tid * kLutCopies]);
 #pragma unroll
-  for (int j = 0; j < kLutCopies / 4; ++j) dstv[(j + tid) & (kLutCopies / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+  for (int j = 0; j < 8; ++j) lds_st<u32x4>(L + tid * 256 + ((j + tid) & 7) * 16, u32x4{bits, bits, bits, bits});
 }
 
 // Wave 0: the grouping of the call's routed pairs (lane i holds pair i).
@@ -1199,6 +1209,7 @@ __device__ __forceinline__ void lite_x8(const u32x4& a, const u32x4& b, int dtyp
 template <int kKeys>
 __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, int P, int nblocks, int start, int m,
                                              int lane, int wave) {
+  const uint32_t L = lds_addr(sm.rows);
   constexpr int kChains = 4 / kKeys;
   const int key = wave / kChains, chain = wave % kChains;
   const int nk = (nblocks - chain + kChains - 1) / kChains;
@@ -1217,15 +1228,19 @@ __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, in
 #pragma unroll
         for (int q = 0; q < kLiteRed; ++q) add4(s, v[q]);
       }
-      sm.red[rr][wave][lane] = s;
+      lds_st<float4v>(L + item_st(kLtRed + ((rr * 4 + wave) * kWave + lane) * 16), float4v{s.x, s.y, s.z, s.w});
     }
     lds_barrier();
     for (int c = wave; c < rows * kKeys; c += 4) {
       const int rr = c / kKeys, k = c % kKeys;
-      float4 t = sm.red[rr][k * kChains][lane];
+      auto red = [&](int w) __attribute__((always_inline)) {
+        const float4v v = lds_ld<float4v>(L + item_st(kLtRed + ((rr * 4 + w) * kWave + lane) * 16));
+        return make_float4(v[0], v[1], v[2], v[3]);
+      };
+      float4 t = red(k * kChains);
 #pragma unroll
-      for (int ch = 1; ch < kChains; ++ch) add4(t, sm.red[rr][k * kChains + ch][lane]);
-      finish_row_lds(t, sm.act[k], sm.rexp[k], r0 + rr, lane);
+      for (int ch = 1; ch < kChains; ++ch) add4(t, red(k * kChains + ch));
+      finish_row_lds(t, L, lt_act(k), sm.rexp[k], r0 + rr, lane);
     }
     lds_barrier();
   }
@@ -1234,16 +1249,16 @@ __device__ __forceinline__ void lite_latents(LiteSmem& sm, const float* base, in
 // Two register tiles' MFMA steps interleaved (two independent chains per
 // wave): accA += actA . tile A, accB += actB . tile B (non-interleaved
 // columns: phases A and D).
-__device__ __forceinline__ void lite_mfma2(const u32x4* actA, const u32x4* actB, uint32_t sbaseA, uint32_t sbaseB,
+__device__ __forceinline__ void lite_mfma2(uint32_t L, uint32_t actA, uint32_t actB, uint32_t sbaseA, uint32_t sbaseB,
                                            const u32x4 (&cbA)[kSteps], const u32x4 (&cbB)[kSteps], int n, int kq,
-                                           int wave, uint32_t lut_lane, float4v (&accA)[4], float4v (&accB)[4]) {
+                                           int wave, uint32_t lc, float4v (&accA)[4], float4v (&accB)[4]) {
   const int G = 2 * wave + (n >> 3);
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int chunk = s * 4 + kq;
     const uint32_t sd = scale_lane(G, kq) + s * 64;
-    const half8 a[2] = {__builtin_bit_cast(half8, actA[act_slot(n, chunk)]),
-                        __builtin_bit_cast(half8, actB[act_slot(n, chunk)])};
+    const half8 a[2] = {lds_ld<half8>(L + item_st(actA + act_slot(n, chunk) * 16)),
+                        lds_ld<half8>(L + item_st(actB + act_slot(n, chunk) * 16))};
     const u32x4 sc[2] = {lds_ld<u32x4>(sbaseA + sd), lds_ld<u32x4>(sbaseB + sd)};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1253,7 +1268,7 @@ __device__ __forceinline__ void lite_mfma2(const u32x4* actA, const u32x4* actB,
         uint32_t f[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << 7));
+          const uint32_t pr = lds_ld<uint32_t>(L + lut_addr(x, q, lc));
           const uint32_t sq = sc[tt][q];  // through a scalar: a bit_cast of a vector element reads element 0
           f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
         }
@@ -1269,7 +1284,8 @@ __device__ __forceinline__ void lite_mfma2(const u32x4* actA, const u32x4* actB,
 
 // Role A: K tiles [j0, j0 + nj) of the list (unit, gate/up, k).
 __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, int j0, int nj, int tid, int lane,
-                                            int wave, uint32_t lut_lane) {
+                                            int wave, uint32_t lc) {
+  const uint32_t L = lds_addr(sm.rows);
   const int n = lane & 15, kq = lane >> 4;
   const int r0 = tid / kActChunks, chunk = tid % kActChunks;
   const int per = 2 * p.nka;
@@ -1318,7 +1334,7 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
       half8 hv;
 #pragma unroll
       for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(v[i], ex));
-      sm.act[buf][act_slot(row, chunk)] = __builtin_bit_cast(u32x4, hv);
+      lds_st<u32x4>(L + item_st(lt_act(buf) + act_slot(row, chunk) * 16), __builtin_bit_cast(u32x4, hv));
       if (chunk == 0) sm.rexp[buf][row] = ex;
     }
   };
@@ -1345,11 +1361,11 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
   if (nj > 1) stage(1, 1, xr[1]);
   lds_barrier();
   if (nj > 1) {
-    lite_mfma2(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq, wave,
-               lut_lane, acc0, acc1);
+    lite_mfma2(L, lt_act(0), lt_act(1), lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq,
+               wave, lc, acc0, acc1);
     store_part(1, 1, acc1);
   } else {
-    reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[0], 0, n, kq, wave, lut_lane, acc0);
+    reg_mfma<false, kSteps>(L, lt_act(0), lt_act(0), lds_addr(sm.scales[0][0]), cb[0], 0, n, kq, wave, lc, acc0);
   }
   store_part(0, 0, acc0);
   if (nj > 2) {
@@ -1359,7 +1375,7 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
     load_x(2, true, xr[0]);  // only workgroups with three tiles get here
     stage(2, 0, xr[0]);
     lds_barrier();
-    reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[2], 0, n, kq, wave, lut_lane, acc0);
+    reg_mfma<false, kSteps>(L, lt_act(0), lt_act(0), lds_addr(sm.scales[0][0]), cb[2], 0, n, kq, wave, lc, acc0);
     store_part(2, 0, acc0);
   }
   // Publish once every partial is stored.
@@ -1370,7 +1386,8 @@ __device__ __forceinline__ void lite_role_a(const LiteParams& p, LiteSmem& sm, i
 
 // Role BC: item (unit u, h block kb).
 __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, int item, int64_t t0, int tid, int lane,
-                                             int wave, uint32_t lut_lane) {
+                                             int wave, uint32_t lc) {
+  const uint32_t L = lds_addr(sm.rows);
   const int n = lane & 15, kq = lane >> 4;
   const int u = item / p.nb, kb = item - u * p.nb, hh = kb & 1;
   const int e = uniform(sm.ue[u]), start = uniform(sm.ustart[u]), m = uniform(sm.um[u]);
@@ -1388,7 +1405,7 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
   float4v acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-  reg_mfma<true, kSteps>(sm.act[0], sm.act[1], lds_addr(sm.scales[0][0]), cbB, 0, n, kq, wave, lut_lane, acc);
+  reg_mfma<true, kSteps>(L, lt_act(0), lt_act(1), lds_addr(sm.scales[0][0]), cbB, 0, n, kq, wave, lc, acc);
   // h = SiLU(g) * u of columns 32w + 2n + jj of the block, fp16 with one exponent per row.
   float hv[2][4];
 #pragma unroll
@@ -1413,13 +1430,13 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
     half2v h2;
     h2[0] = static_cast<_Float16>(ldexpf(hv[0][v], ex));
     h2[1] = static_cast<_Float16>(ldexpf(hv[1][v], ex));
-    reinterpret_cast<half2v*>(&sm.hb[act_slot(row, 4 * wave + (n >> 2))])[n & 3] = h2;
+    lds_st<half2v>(L + item_st(kLtHb + act_slot(row, 4 * wave + (n >> 2)) * 16 + (n & 3) * 4), h2);
     if (wave == 0 && n == 0) sm.hexp[row] = ex;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
   lds_barrier();
-  reg_mfma<false, kSteps / 2>(sm.hb, sm.hb, lds_addr(sm.scales[1][0]), cbC, 4 * hh, n, kq, wave, lut_lane, acc);
+  reg_mfma<false, kSteps / 2>(L, kLtHb, kLtHb, lds_addr(sm.scales[1][0]), cbC, 4 * hh, n, kq, wave, lc, acc);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int row = kq * 4 + v;
@@ -1436,7 +1453,8 @@ __device__ __forceinline__ void lite_role_bc(const LiteParams& p, LiteSmem& sm, 
 // Role D: column tiles [j0, j0 + nj) of the list (unit, n).
 template <int kOutMode>
 __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, int j0, int nj, int64_t t0, int tid,
-                                            int lane, int wave, uint32_t lut_lane) {
+                                            int lane, int wave, uint32_t lc) {
+  const uint32_t L = lds_addr(sm.rows);
   const int n = lane & 15, kq = lane >> 4;
   u32x4 cb[kLiteSlots][kSteps], sc[kLiteSlots];
   lite_sleep_until(t0, kLiteLateTicks);
@@ -1488,8 +1506,8 @@ __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, i
     sm.scales[0][tid] = sc[0];
     sm.scales[1][tid] = sc[1];
     lds_barrier();
-    lite_mfma2(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq, wave,
-               lut_lane, acc0, acc1);
+    lite_mfma2(L, lt_act(0), lt_act(0), lds_addr(sm.scales[0][0]), lds_addr(sm.scales[1][0]), cb[0], cb[1], n, kq,
+               wave, lc, acc0, acc1);
     store_y(0, acc0);
     store_y(1, acc1);
   } else {
@@ -1510,7 +1528,7 @@ __device__ __forceinline__ void lite_role_d(const LiteParams& p, LiteSmem& sm, i
         float4v acc[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) acc[q] = float4v{0.f, 0.f, 0.f, 0.f};
-        reg_mfma<false, kSteps>(sm.act[0], sm.act[0], lds_addr(sm.scales[0][0]), cb[j], 0, n, kq, wave, lut_lane, acc);
+        reg_mfma<false, kSteps>(L, lt_act(0), lt_act(0), lds_addr(sm.scales[0][0]), cb[j], 0, n, kq, wave, lc, acc);
         store_y(j, acc);
       }
     }
@@ -1580,8 +1598,8 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) lite_kernel(LiteParams p) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = uniform(tid >> 6);
   const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
-  lut_fill(sm.lut, tid);
-  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (kLutCopies - 1)) << 2);
+  lut_fill(lds_addr(sm.rows), tid);
+  const uint32_t lc = (lane & 31) << 2;  // the lane's table copy offset
   if (wave == 0) lite_group(p, sm, lane);
   lds_barrier();
   const int64_t t0 = __builtin_amdgcn_s_memrealtime();
@@ -1609,9 +1627,9 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) lite_kernel(LiteParams p) {
       if (tid == 0) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    if (nj > 0) lite_role_a(p, sm, j0, nj, tid, lane, wave, lut_lane);
+    if (nj > 0) lite_role_a(p, sm, j0, nj, tid, lane, wave, lc);
   } else if (b < sp.gA + sp.gB) {
-    lite_role_bc(p, sm, b - sp.gA, t0, tid, lane, wave, lut_lane);
+    lite_role_bc(p, sm, b - sp.gA, t0, tid, lane, wave, lc);
   } else {
     const int N = U * p.nd, jd = b - sp.gA - sp.gB;
     const int j0 = range_lo(N, jd, sp.gD), nj = range_lo(N, jd + 1, sp.gD) - j0;
@@ -1619,7 +1637,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) lite_kernel(LiteParams p) {
       if (tid == 0) __hip_atomic_store(p.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
-    if (nj > 0) lite_role_d<kOutMode>(p, sm, j0, nj, t0, tid, lane, wave, lut_lane);
+    if (nj > 0) lite_role_d<kOutMode>(p, sm, j0, nj, t0, tid, lane, wave, lc);
   }
 }
 
