@@ -504,17 +504,34 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
 // ---------------------------------------------------------------------------
 // acc[t][j] += sum over this lane's rows of vin[t][row] * scale(row, g) * level(code(row, g*32+j))
 // Rows: row_begin, row_begin + step, ... < row_end.  vin[t][row] = vin[t*vstride + row - vbase].
-template <int MB, bool kInt8>
+// kInt8Rows: rows per pass of a factor with INT8 groups, their loads in
+// flight together; 0: one row at a time through decode_group (phase BC, which
+// the prefetching form pushes to 256 VGPRs and one wave per SIMD).
+template <int MB, bool kInt8, int kInt8Rows = 2>
 __device__ __forceinline__ void accumulate_rows(const Factor& f, int64_t e, int row_begin, int row_end, int step, int g,
                                                 const float* lut, const float* vin, int vstride, int vbase, int m,
                                                 float (&acc)[MB][kGroup]) {
-  if (kInt8 && f.ext.bitmap != nullptr) {
+  if (kInt8 && kInt8Rows == 0) {
+    for (int row = row_begin; row < row_end; row += step) {
+      float v[kGroup];
+      decode_group<true>(f, e, row, g, lut, v);
+      const float s = group_scale(f, e, row, g);
+#pragma unroll
+      for (int t = 0; t < MB; ++t) {
+        if (t < m) {
+          const float xs = vin[t * vstride + row - vbase] * s;
+#pragma unroll
+          for (int j = 0; j < kGroup; ++j) acc[t][j] = fmaf(xs, v[j], acc[t][j]);
+        }
+      }
+    }
+  } else if (kInt8 && f.ext.bitmap != nullptr) {
     // U rows per pass, every load of a row independent of the others: the
     // codes, the scale, the group's bitmap word and its word offset (the
     // side-buffer index of the word's first INT8 group), then, for the lanes
-    // whose group is INT8, its 32 bytes.  (One row at a time, the chain
-    // bitmap -> offset -> data paid three dependent round trips per row.)
-    constexpr int U = 2;
+    // whose group is INT8, its 32 bytes.  (The chain bitmap -> offset ->
+    // data paid three dependent round trips per row.)
+    constexpr int U = kInt8Rows > 0 ? kInt8Rows : 1;
     const int words = f.words(), wsel = g >> 5;
     const uint32_t bit = 1u << (g & 31);
     const int64_t cstride = f.code_stride(), sstride = f.scale_stride(), erow0 = e * f.rows;
@@ -754,7 +771,7 @@ __global__ void __launch_bounds__(kThreads) phase_bc_kernel(MoeParams p) {
       float acc[MB][kGroup];
       zero_acc(acc);
       if (gb < gpc)
-        accumulate_rows<MB, kInt8>(f, e, wave * rpw_b + rob, rk, kWaves * rpw_b, c0 / kGroup + gb, lut,
+        accumulate_rows<MB, kInt8, 0>(f, e, wave * rpw_b + rob, rk, kWaves * rpw_b, c0 / kGroup + gb, lut,
                                    lat + kind * p.R, 2 * p.R, 0, m, acc);
       wave_reduce_store<MB>(acc, lpr_b, lane, wave, gpc, m, red, redw);
       __syncthreads();
@@ -779,7 +796,7 @@ __global__ void __launch_bounds__(kThreads) phase_bc_kernel(MoeParams p) {
       float acc[MB][kGroup];
       zero_acc(acc);
       if (gd < ngd)
-        accumulate_rows<MB, kInt8>(p.fac[F_DOWN_A], e, c0 + wave * rpw_d + rod, c0 + ncol, kWaves * rpw_d, gd, lut, hs,
+        accumulate_rows<MB, kInt8, 0>(p.fac[F_DOWN_A], e, c0 + wave * rpw_d + rod, c0 + ncol, kWaves * rpw_d, gd, lut, hs,
                                    p.cb, c0, m, acc);
       wave_reduce_store<MB>(acc, lpr_d, lane, wave, ngd, m, red, redw);
       __syncthreads();
