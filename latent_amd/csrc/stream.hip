@@ -1039,6 +1039,7 @@ constexpr int kLiteRed = 16;   // partial rows in flight per lane in the latent 
 // counter serialises all publishes and polls: ~5 us per dependency step).
 constexpr int kLiteUnitStride = 32;  // ints between per-unit counters (128 B)
 constexpr int kLiteKeyStride = 16;   // ints between (token, tile) counters (64 B)
+constexpr int kLiteTicketInts = 32;  // the start-order ticket's line (128 B) before the counters
 // B, C and D tiles are needed only after A's results: their workgroups issue
 // their loads this long after grouping, so A's tiles come first from HBM.
 constexpr int64_t kLiteLateTicks = 300;  // 3 us of s_memrealtime (100 MHz)
@@ -1059,9 +1060,11 @@ struct LiteParams {
   int* cntC;     // [kLiteMaxP][kLiteUnitStride] BC items done per unit
   int* cntD;     // [kLiteMaxP][kLiteUnitStride] D tiles done per unit
   int* cntY;     // [T][nd][kLiteKeyStride] routed rows stored per (token, column tile)
+  int* ticket;   // start-order ticket (grids beyond the resident workgroups), else null
   int* err;      // set when a bounded wait times out
   int T, K, E, d, P, wbd;
   int nka, nb, nkc, nd;
+  int resident;  // workgroups resident at once (two per CU)
 };
 
 // Workgroups per role: gB = the BC items, the rest split between A and D in
@@ -1105,7 +1108,7 @@ struct alignas(16) LiteSmem {
   int pos_of[kLiteMaxP];                // grouped position of each routed pair (-1: dropped)
   float w[kLiteMaxP];                   // router weight of each routed pair
   int last[kLiteSlots * kMaxM];         // D: (token, tile) sums this workgroup completes
-  int nunits, nlast;
+  int nunits, nlast, ticket;
 };
 
 // Level-pair table: thread tid fills row tid's 32 copies (rotated start, so
@@ -1597,12 +1600,23 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) lite_kernel(LiteParams p) {
   __shared__ LiteSmem sm;
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = uniform(tid >> 6);
-  const int G = static_cast<int>(gridDim.x), b = static_cast<int>(blockIdx.x);
+  const int G = static_cast<int>(gridDim.x);
+  // A grid larger than the resident workgroups takes roles in start order:
+  // every workgroup a role waits for holds a lower ticket, so it is already
+  // running.  The last ticket's holder resets the counter for the next call.
+  int tk = 0;
+  if (p.ticket && tid == 0) tk = __hip_atomic_fetch_add(p.ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   lut_fill(lds_addr(sm.rows), tid);
   const uint32_t lc = (lane & 31) << 2;  // the lane's table copy offset
   if (wave == 0) lite_group(p, sm, lane);
+  if (p.ticket && tid == 0) {
+    sm.ticket = tk;
+    if (tk == G - 1) __hip_atomic_store(p.ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   lds_barrier();
-  const int64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const int b = p.ticket ? uniform(sm.ticket) : static_cast<int>(blockIdx.x);
+  // Workgroups that start once others have finished skip the B, C and D load delay.
+  const int64_t t0 = __builtin_amdgcn_s_memrealtime() - (b < p.resident ? 0 : kLiteLateTicks);
   const int U = uniform(sm.nunits);
   // Rows no D tile writes (reduced output: tokens without a routed slot;
   // per-slot output: dropped slots), one row per workgroup from the last.
@@ -2388,23 +2402,42 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
 
-bool lite_applies(const latent_moe_args& a) {
+// Workgroups of the small-batch chain for a call: the resident count (two
+// per CU) when every unit count up to the call's maximum fits it, else the
+// fewest beyond it (a multiple of 8, at most twice the resident count) with
+// which they all fit; 0 when the call does not take the chain.
+static int lite_grid(const latent_moe_args& a) {
   const char* env = std::getenv("LATENT_STREAM_LAUNCH");
-  if (env && !std::strcmp(env, "phases")) return false;
-  if (!supported(a)) return false;
+  if (env && !std::strcmp(env, "phases")) return 0;
+  if (!supported(a)) return 0;
   const int64_t P = a.n_tokens * a.n_expert_used;
-  if (P < 1 || P > kLiteMaxP || a.n_embd / kK > kMaxKTiles) return false;
-  if (a.n_tokens * a.n_embd * 4 >= (1ll << 31)) return false;  // 32-bit byte offsets into x
+  if (P < 1 || P > kLiteMaxP || a.n_embd / kK > kMaxKTiles) return 0;
+  if (a.n_tokens * a.n_embd * 4 >= (1ll << 31)) return 0;  // 32-bit byte offsets into x
   const int nka = static_cast<int>(a.n_embd / kK), nb = static_cast<int>(a.n_ff / kHBlock);
   const int nd = static_cast<int>(a.n_embd / kN);
-  if ((3 * kLiteMaxP * kLiteUnitStride + a.n_tokens * nd * kLiteKeyStride) * 4 > static_cast<int64_t>(kLiteCtrlBytes))
-    return false;
-  const int G = grid_size();
-  const int64_t umax = std::min<int64_t>(P, a.n_expert);
-  for (int U = 1; U <= umax; ++U)
-    if (!lite_fits(U, nka, nb, nd, G)) return false;
-  return true;
+  if ((kLiteTicketInts + 3 * kLiteMaxP * kLiteUnitStride + a.n_tokens * nd * kLiteKeyStride) * 4 >
+      static_cast<int64_t>(kLiteCtrlBytes))
+    return 0;
+  const int G0 = grid_size();
+  const int umax = static_cast<int>(std::min<int64_t>(P, a.n_expert));
+  auto all_fit = [&](int G) {
+    for (int U = 1; U <= umax; ++U)
+      if (!lite_fits(U, nka, nb, nd, G)) return false;
+    return true;
+  };
+  if (all_fit(G0)) return G0;
+  // Lower bound: every unit's BC items plus A and D tiles in full slots.
+  int G = G0;
+  for (int U = 1; U <= umax; ++U) {
+    const int need = U * nb + (2 * U * nka + kLiteSlots - 1) / kLiteSlots + (U * nd + kLiteSlots - 1) / kLiteSlots;
+    G = std::max(G, (need + 7) / 8 * 8);
+  }
+  for (; G <= 2 * G0; G += 8)
+    if (all_fit(G)) return G;
+  return 0;
 }
+
+bool lite_applies(const latent_moe_args& a) { return lite_grid(a) > 0; }
 
 int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, hipStream_t s) {
   const Layout L = layout_for(a);
@@ -2422,7 +2455,12 @@ int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, 
   p.partA = reinterpret_cast<float*>(scratch + L.partA);
   p.partC = reinterpret_cast<float*>(scratch + L.partC);
   p.ybuf = reinterpret_cast<float*>(scratch + L.ybuf);
+  const int G = lite_grid(a);
+  if (G <= 0) return LATENT_E_UNSUPPORTED;
   int* c = reinterpret_cast<int*>(ctrl + kLiteCtrlOffset);
+  p.ticket = G > grid_size() ? c : nullptr;
+  p.resident = grid_size();
+  c += kLiteTicketInts;
   p.cntA = c;
   p.cntC = c + kLiteMaxP * kLiteUnitStride;
   p.cntD = c + 2 * kLiteMaxP * kLiteUnitStride;
@@ -2438,7 +2476,6 @@ int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, 
   p.nb = static_cast<int>(a.n_ff / kHBlock);
   p.nkc = static_cast<int>(a.n_ff / kK);
   p.nd = p.d / kN;
-  const unsigned G = static_cast<unsigned>(grid_size());
   if (a.out_mode == LATENT_OUT_REDUCED)
     hipLaunchKernelGGL(lite_kernel<LATENT_OUT_REDUCED>, dim3(G), dim3(kT), 0, s, p);
   else

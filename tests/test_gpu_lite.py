@@ -166,12 +166,15 @@ def test_lite_dsv3_shape(gpu):
     from latent_amd.moe import stream_launch
 
     layer = gsynth.make_layer(seed=9, n_expert=256, d=7168, ff=2048, max_rank=256)
-    for B, k in [(1, 8), (1, 11)]:
+    # Up to 11 units the chain's 512 workgroups are all resident; two tokens
+    # at top-8 (up to 16 units) take a larger grid whose roles follow the
+    # workgroups' start order.
+    for B, k in [(1, 8), (1, 11), (2, 8), (1, 16)]:
         ids_t, w_t = gsynth.route(seed=300 + B, n_tokens=B, n_expert=256, k=k)
         x_t = gsynth.bf16_input(seed=400 + B, n_tokens=B, d=7168)
         assert stream_launch(layer, x_t, k) == "lite"
-        out = gpu.moe_forward(x_t, ids_t, w_t, layer)
-        again = gpu.moe_forward(x_t, ids_t, w_t, layer)
+        out = gpu.moe_forward(x_t, ids_t, w_t, layer, check_timeout=True)
+        again = gpu.moe_forward(x_t, ids_t, w_t, layer, check_timeout=True)
         torch.cuda.synchronize()
         assert torch.equal(out, again)
         ids, w, x = ids_t.cpu().numpy(), w_t.cpu().numpy(), x_t.float().cpu().numpy()
