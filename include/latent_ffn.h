@@ -236,9 +236,10 @@ int latent_moe_path(const latent_moe_args* args);
 
 /*
  * Launch style of a call that takes the streaming path (latent_moe_path 3):
- *   2 = small-batch chain: one launch for at most 16 routed pairs, every
+ *   2 = small-batch chain: one launch for at most 32 routed pairs, every
  *       workgroup's tiles loaded first, grouping and combine inside (taken by
- *       default wherever each workgroup's tiles fit its registers);
+ *       default wherever a grid of at most four resident grids gives each
+ *       workgroup tiles that fit its registers);
  *   0 = one launch per phase (the default otherwise; LATENT_STREAM_LAUNCH=phases
  *       also for small batches).
  * LATENT_E_UNSUPPORTED when the call does not take the streaming path.

@@ -1032,7 +1032,7 @@ __device__ __forceinline__ void drain_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-constexpr int kLiteMaxP = 16;  // routed pairs the small-batch chain takes
+constexpr int kLiteMaxP = 32;  // routed pairs the small-batch chain takes
 constexpr int kLiteSlots = 3;  // tiles a workgroup holds in registers
 constexpr int kLiteRed = 16;   // partial rows in flight per lane in the latent sums
 // Counters sit on their own cache lines (a line shared by every unit's
@@ -1040,6 +1040,7 @@ constexpr int kLiteRed = 16;   // partial rows in flight per lane in the latent 
 constexpr int kLiteUnitStride = 32;  // ints between per-unit counters (128 B)
 constexpr int kLiteKeyStride = 16;   // ints between (token, tile) counters (64 B)
 constexpr int kLiteTicketInts = 32;  // the start-order ticket's line (128 B) before the counters
+constexpr int kLiteMaxGrid = 4;      // largest grid, in resident grids
 // B, C and D tiles are needed only after A's results: their workgroups issue
 // their loads this long after grouping, so A's tiles come first from HBM.
 constexpr int64_t kLiteLateTicks = 300;  // 3 us of s_memrealtime (100 MHz)
@@ -1134,13 +1135,15 @@ __device__ __forceinline__ void lite_group(const LiteParams& p, LiteSmem& sm, in
     const uint64_t same = __ballot(valid && e == el);
     if (valid && e == el) pos = start + __popcll(same & ((1ull << lane) - 1ull));
     const int c = __popcll(same);
-    if (lane == 0) {
-      sm.ue[u] = el;
-      sm.ustart[u] = start;
-      sm.um[u] = c;
+    // An expert's pairs beyond kMaxM start further units of the expert.
+    for (int q = 0; q < c; q += kMaxM, ++u) {
+      if (lane == 0) {
+        sm.ue[u] = el;
+        sm.ustart[u] = start + q;
+        sm.um[u] = min(kMaxM, c - q);
+      }
     }
     start += c;
-    ++u;
     todo &= ~same;
   }
   if (in) sm.pos_of[lane] = pos;
@@ -2404,7 +2407,7 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
 
 // Workgroups of the small-batch chain for a call: the resident count (two
 // per CU) when every unit count up to the call's maximum fits it, else the
-// fewest beyond it (a multiple of 8, at most twice the resident count) with
+// fewest beyond it (a multiple of 8, at most kLiteMaxGrid times the resident count) with
 // which they all fit; 0 when the call does not take the chain.
 static int lite_grid(const latent_moe_args& a) {
   const char* env = std::getenv("LATENT_STREAM_LAUNCH");
@@ -2418,8 +2421,10 @@ static int lite_grid(const latent_moe_args& a) {
   if ((kLiteTicketInts + 3 * kLiteMaxP * kLiteUnitStride + a.n_tokens * nd * kLiteKeyStride) * 4 >
       static_cast<int64_t>(kLiteCtrlBytes))
     return 0;
+  // Partial sums in the decode layout's regions: A's 2 nka blocks of P rows.
+  if (2ll * nka * P > part_slots(max_units(P, a.n_expert), 2 * nka, nka, grid_size()) * kMaxM) return 0;
   const int G0 = grid_size();
-  const int umax = static_cast<int>(std::min<int64_t>(P, a.n_expert));
+  const int umax = static_cast<int>(std::min<int64_t>(P, max_units(P, a.n_expert)));
   auto all_fit = [&](int G) {
     for (int U = 1; U <= umax; ++U)
       if (!lite_fits(U, nka, nb, nd, G)) return false;
@@ -2432,7 +2437,7 @@ static int lite_grid(const latent_moe_args& a) {
     const int need = U * nb + (2 * U * nka + kLiteSlots - 1) / kLiteSlots + (U * nd + kLiteSlots - 1) / kLiteSlots;
     G = std::max(G, (need + 7) / 8 * 8);
   }
-  for (; G <= 2 * G0; G += 8)
+  for (; G <= kLiteMaxGrid * G0; G += 8)
     if (all_fit(G)) return G;
   return 0;
 }
@@ -2449,9 +2454,9 @@ int lite_forward(const latent_moe_args& a, char* ctrl, char* scratch, int* err, 
   p.weights = a.weights;
   p.w_dtype = a.weights_dtype;
   p.out = static_cast<float*>(a.out);
-  // The partial sums fit the decode layout's partial regions: A's 2 nka
-  // blocks of P <= 16 rows and C's nb blocks are at most one 16-row slot per
-  // block there.
+  // The partial sums sit in the decode layout's partial regions: A's 2 nka
+  // blocks of P rows (lite_grid checks they fit A's slots) and C's nb blocks
+  // of P rows (the size of C's region).
   p.partA = reinterpret_cast<float*>(scratch + L.partA);
   p.partC = reinterpret_cast<float*>(scratch + L.partC);
   p.ybuf = reinterpret_cast<float*>(scratch + L.ybuf);
@@ -2491,7 +2496,7 @@ Layout layout_for(const latent_moe_args& a) {
   const int nka = static_cast<int>(d / kK);
   // Partial blocks of 16 rows: A per workgroup range and segment.  C's
   // partials are rows by grouped pair, nkc per pair (bc_kernel: one per item
-  // and row).  The small-batch chain (at most 16 routed pairs) keeps its
+  // and row).  The small-batch chain (at most 32 routed pairs) keeps its
   // partials in the same regions as [factor block][pair] rows: 2 nka blocks
   // of A (fewer than A's slots here) and nb blocks of P rows of C.
   const int64_t blocksA = part_slots(U, 2 * nka, nka, G);

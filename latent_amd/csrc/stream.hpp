@@ -32,10 +32,11 @@ struct Layout {
   size_t xh, xexp, partA, lath, lexp, partC, dlath, dexp, ybuf, pos_of, total;
 };
 
-// Batches of at most 16 routed pairs: the whole chain in one launch in which
+// Batches of at most 32 routed pairs: the whole chain in one launch in which
 // every workgroup issues all its tile loads first (lite_kernel), grouping and
 // x conversion included, so the prep kernel is not launched.  Taken by default
-// wherever every workgroup's tiles fit its registers; LATENT_STREAM_LAUNCH=phases
+// wherever a grid of at most four resident grids gives every workgroup tiles
+// that fit its registers; LATENT_STREAM_LAUNCH=phases
 // selects the per-phase launches instead.  Its counters live in the
 // workspace control block at kLiteCtrlOffset (zero between calls).
 constexpr size_t kLiteCtrlOffset = 192 * 1024;

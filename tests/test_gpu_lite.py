@@ -1,7 +1,7 @@
-"""Small-batch chain (lite_kernel, at most 16 routed pairs) against the oracle.
+"""Small-batch chain (lite_kernel, at most 32 routed pairs) against the oracle.
 
 With LATENT_STREAM_LAUNCH unset, a layer with a tile layout takes this chain
-for calls of at most 16 routed pairs; the grouping, the x conversion and the
+for calls of at most 32 routed pairs; the grouping, the x conversion and the
 combine all run inside its one launch.  Bar: rel-L2 <= 2e-3 against the
 oracle's fp32 result on the same packed factors, bit-identical results on a
 repeated call, exact zeros where no routed slot contributes, and the
@@ -73,7 +73,7 @@ def _check(gpu, layer, dev, x, ids, w, **kw):
     return got
 
 
-@pytest.mark.parametrize("T,k", [(1, 1), (1, 8), (2, 8), (4, 4), (16, 1)])
+@pytest.mark.parametrize("T,k", [(1, 1), (1, 8), (2, 8), (4, 4), (16, 1), (4, 8), (32, 1)])
 @pytest.mark.parametrize("mode", [0, 1])
 def test_lite_shapes(gpu, layer, dev, T, k, mode):
     rng = np.random.default_rng(100 * T + k)
@@ -111,6 +111,18 @@ def test_lite_dropped_duplicate_invalid(gpu, layer, dev):
             assert not got[1, 2].any() and not got[2, 3].any() and not got[3].any()
         else:
             assert not got[3].any()
+
+
+def test_lite_expert_beyond_16_pairs(gpu, layer, dev):
+    # 18 of 24 single-slot tokens route to expert 5: its pairs fill a 16-row
+    # unit and start a second unit of 2 rows.
+    rng = np.random.default_rng(13)
+    T, k = 24, 1
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    ids, w = routing.softmax_topk(rng.standard_normal((T, E)), k)
+    ids[:18, 0] = 5
+    for mode in (0, 1):
+        _check(gpu, layer, dev, x, ids, w, mode=mode)
 
 
 def test_lite_all_dropped(gpu, dev):
@@ -166,10 +178,10 @@ def test_lite_dsv3_shape(gpu):
     from latent_amd.moe import stream_launch
 
     layer = gsynth.make_layer(seed=9, n_expert=256, d=7168, ff=2048, max_rank=256)
-    # Up to 11 units the chain's 512 workgroups are all resident; two tokens
-    # at top-8 (up to 16 units) take a larger grid whose roles follow the
-    # workgroups' start order.
-    for B, k in [(1, 8), (1, 11), (2, 8), (1, 16)]:
+    # Up to 11 units the chain's 512 workgroups are all resident; two to four
+    # tokens at top-8 (up to 32 units) take a larger grid whose roles follow
+    # the workgroups' start order.
+    for B, k in [(1, 8), (1, 11), (2, 8), (1, 16), (3, 8), (4, 8)]:
         ids_t, w_t = gsynth.route(seed=300 + B, n_tokens=B, n_expert=256, k=k)
         x_t = gsynth.bf16_input(seed=400 + B, n_tokens=B, d=7168)
         assert stream_launch(layer, x_t, k) == "lite"

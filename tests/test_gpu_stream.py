@@ -2,7 +2,7 @@
 
 The path is selected with LATENT_MOE_PATH=stream for every call here, in both
 launch styles (LATENT_STREAM_LAUNCH=auto: the default, which takes the
-small-batch chain for at most 16 routed pairs; =phases: one launch per phase).
+small-batch chain for at most 32 routed pairs; =phases: one launch per phase).
 Bar:
 rel-L2 <= 2e-3 against the oracle's fp32 result on the same packed factors
 (fp16 operands, fp32 accumulation), bit-identical results on a repeated call.
@@ -22,7 +22,7 @@ TOL = 2e-3
 
 @pytest.fixture(params=["auto", "phases"])
 def stream_path(monkeypatch, request):
-    # The default launch style (the small-batch chain up to 16 routed pairs,
+    # The default launch style (the small-batch chain up to 32 routed pairs,
     # per-phase launches above) and per-phase launches throughout.
     monkeypatch.setenv("LATENT_MOE_PATH", "stream")
     monkeypatch.setenv("LATENT_STREAM_LAUNCH", request.param)
