@@ -21,7 +21,7 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
-SOURCES = ["codec.hip", "expert.hip", "moe.hip", "moe_fused.hip", "noalloc.hip", "prefill.hip", "route.hip", "stream.hip"]
+SOURCES = ["codec.hip", "expert.hip", "moe.hip", "moe_fused.hip", "noalloc.hip", "prefill.hip", "route.hip", "rows.hip", "stream.hip"]
 LIB = PKG / "liblatent_hip.so"
 ARCH = os.environ.get("LATENT_OFFLOAD_ARCH", "gfx950")
 

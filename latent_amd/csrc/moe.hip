@@ -22,6 +22,7 @@
 #include "common.hpp"
 #include "fused.hpp"
 #include "prefill.hpp"
+#include "rows.hpp"
 #include "stream.hpp"
 
 #include <cstdlib>
@@ -80,6 +81,7 @@ struct MoeParams {
   int cd, n_d;           // phase D: d columns per item, items per expert
   int64_t zero_floats;   // accumulator floats cleared by prep
   int zero_out;          // reduced mode: prep clears out (the phase kernels accumulate into it)
+  int clear;             // prep clears the accumulators (and out) also where it converts x
 };
 
 __device__ __forceinline__ int ilog2(int v) { return 31 - __builtin_clz(v); }
@@ -476,7 +478,9 @@ __global__ void __launch_bounds__(kRouteThreads) prep_kernel(MoeParams p) {
       }
       if (threadIdx.x == 0) p.xexp[t] = ex;
     }
-    return;  // otherwise the streaming path clears nothing: its kernels write every output
+    // The streaming path clears nothing (its kernels write every output); the
+    // row-layout MFMA phases accumulate like the fp32 ones.
+    if (!p.clear) return;
   }
   // Accumulators gu and dl are contiguous: zero_floats covers both.
   float4* acc4 = reinterpret_cast<float4*>(p.gu);
@@ -870,7 +874,7 @@ constexpr size_t kAlign = 256;
 inline size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Layout {
-  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, hist, units, gu, dl, total;
+  size_t meta, act_expert, act_start, act_count, pair_tok, pair_slot, pair_w, hist, units, gu, dl, xh, xexp, total;
 };
 
 // Pairs per chunk of the multi-workgroup grouping: multiples of the block
@@ -883,7 +887,13 @@ int64_t group_chunk(int64_t P, int64_t E) {
 }
 int64_t group_chunks(int64_t P, int64_t E) { const int64_t c = group_chunk(P, E); return (P + c - 1) / c; }
 
-Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
+// Columns of the fp16 x rows the row-layout MFMA phases read (0: the call's
+// shape never takes them).
+int64_t xh_cols(const latent_moe_args& a) {
+  return a.layout == LATENT_LAYOUT_ROWS && a.max_rank <= 512 ? a.n_embd : 0;
+}
+
+Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R, int64_t d) {
   Layout L{};
   const int64_t P = T * K;
   const int64_t amax = std::max<int64_t>(1, std::min(E, P));
@@ -899,6 +909,9 @@ Layout layout_for(int64_t T, int64_t K, int64_t E, int64_t R) {
   L.units = off;      off = align_up(off + (4 + stream::kMaxM) * stream::max_units(P, E) * sizeof(int));
   L.gu = off;         off += P * 2 * R * sizeof(float);  // gu and dl contiguous (one clear)
   L.dl = off;         off = align_up(off + P * R * sizeof(float));
+  // x as fp16 rows x 2^xexp for the row-layout MFMA phases (d = 0: none).
+  L.xh = off;         off = align_up(off + T * d * 2);
+  L.xexp = off;       off = align_up(off + T * sizeof(int));
   L.total = off;
   return L;
 }
@@ -932,7 +945,7 @@ int pick_pow2_chunk(int64_t per_expert_extent, int64_t experts, int64_t target_i
   return c;
 }
 
-enum { kPathGeneral = 0, kPathFused = 1, kPathPrefill = 2, kPathStream = 3 };
+enum { kPathGeneral = 0, kPathFused = 1, kPathPrefill = 2, kPathStream = 3, kPathRows = 4 };
 
 // The implementation for one call shape.  LATENT_MOE_PATH (general | fused |
 // prefill | stream) selects another path that supports the call, for
@@ -951,8 +964,10 @@ int choose_path(const latent_moe_args& a, fused::Plan& pl) {
   const bool fused_ok = fused::supported(a) && fused::make_plan(a, pl);
   const bool prefill_ok = prefill::supported(a);
   const bool stream_ok = stream::supported(a);
+  const bool rows_ok = rows::supported(a);
   const char* env = std::getenv("LATENT_MOE_PATH");
   if (env && *env) {
+    if (!std::strcmp(env, "rows") && rows_ok) return kPathRows;
     if (!std::strcmp(env, "stream") && stream_ok) return kPathStream;
     if (!std::strcmp(env, "fused") && fused_ok) return kPathFused;
     if (!std::strcmp(env, "prefill") && prefill_ok) return kPathPrefill;
@@ -1058,7 +1073,7 @@ extern "C" int latent_moe_workspace_size(const latent_moe_args* args, size_t* by
   if (!args || !bytes) return LATENT_E_INVALID;
   const int st = validate(*args);
   if (st != LATENT_OK) return st;
-  const Layout L = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank);
+  const Layout L = layout_for(args->n_tokens, args->n_expert_used, args->n_expert, args->max_rank, xh_cols(*args));
   size_t scratch = L.total;
   if (prefill::supported(*args)) scratch = std::max(scratch, L.gu + prefill::layout_for(*args).total);
   fused::Plan pl;
@@ -1159,7 +1174,7 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     if (st != LATENT_OK) return st;
   }
   if (path == kPathFused) return fused::forward(a, s, static_cast<char*>(a.workspace), pl, p.fac);
-  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank);
+  const Layout L = layout_for(a.n_tokens, a.n_expert_used, a.n_expert, a.max_rank, xh_cols(a));
   char* ws = static_cast<char*>(a.workspace) + fused::kReserved;
   p.x = a.x;
   p.ids = a.ids;
@@ -1203,9 +1218,16 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     p.xh = reinterpret_cast<_Float16*>(ws + L.gu + SL.xh);
     p.xexp = reinterpret_cast<int*>(ws + L.gu + SL.xexp);
   }
-  // The MFMA paths write their intermediates whole, and every output row (per-token combine).
+  const bool use_rows = path == kPathRows;
+  if (use_rows) {
+    p.xh = reinterpret_cast<_Float16*>(ws + L.xh);
+    p.xexp = reinterpret_cast<int*>(ws + L.xexp);
+  }
+  // The MFMA paths write their intermediates whole, and every output row
+  // (per-token combine); the row-layout MFMA phases accumulate like the fp32 ones.
   p.zero_floats = use_prefill || use_stream ? 0 : P * 3 * a.max_rank;
   p.zero_out = use_prefill || use_stream ? 0 : 1;
+  p.clear = use_stream ? 0 : 1;
 
   // Work split: enough items to fill 256 CUs even when few experts are routed.
   const int MB = a.n_tokens == 1 ? 1 : 4;
@@ -1221,8 +1243,9 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
       use_stream ? 0
                  : p.zero_floats / 4 + (a.out_mode == LATENT_OUT_REDUCED ? p.zero_out * P / a.n_expert_used * a.n_embd / 4
                                                                          : P * a.n_embd / 4);
-  // The streaming path also converts x, one workgroup per token.
-  const int64_t conv_blocks = use_stream ? a.n_tokens : 1;
+  // The streaming path and the row-layout MFMA phases also convert x, one
+  // workgroup per token.
+  const int64_t conv_blocks = use_stream || use_rows ? a.n_tokens : 1;
   const int zero_blocks = static_cast<int>(
       std::min<int64_t>(512, std::max<int64_t>(conv_blocks, zero_work / (kRouteThreads * 8))));
   if (use_prefill) {
@@ -1245,6 +1268,33 @@ extern "C" int latent_moe_ffn_forward(const latent_moe_args* args, latent_stream
     const stream::Grouping g{p.meta,      p.unit_info, p.unit_tok, p.pair_tok, p.pair_slot, p.pair_w,
                              reinterpret_cast<int*>(static_cast<char*>(a.workspace) + fused::kErrorOffset)};
     return stream::forward(a, g, ws + L.gu, s);
+  }
+  if (use_rows) {
+    rows::Params rp{};
+    for (int i = 0; i < 6; ++i) rp.fac[i] = p.fac[i];
+    rp.ranks = p.ranks;
+    rp.meta = p.meta;
+    rp.act_expert = p.act_expert;
+    rp.act_start = p.act_start;
+    rp.act_count = p.act_count;
+    rp.pair_tok = p.pair_tok;
+    rp.pair_slot = p.pair_slot;
+    rp.pair_w = p.pair_w;
+    rp.xh = p.xh;
+    rp.xexp = p.xexp;
+    rp.gu = p.gu;
+    rp.dl = p.dl;
+    rp.out = p.out;
+    rp.T = p.T;
+    rp.d = p.d;
+    rp.ff = p.ff;
+    rp.K = p.K;
+    rp.R = p.R;
+    rp.wbd = p.wbd;
+    rp.out_mode = p.out_mode;
+    rp.a_max = p.a_max;
+    rows::plan(rp);
+    return rows::launch(rp, any_int8, s);
   }
   if (MB == 1)
     st = any_int8 ? launch_phases<1, true>(p, s) : launch_phases<1, false>(p, s);

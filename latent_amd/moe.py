@@ -343,7 +343,7 @@ def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
     r = lib.latent_moe_path(ctypes.byref(a))
     if r < 0:
         check(r, "latent_moe_path")
-    return {1: "fused", 2: "prefill", 3: "stream"}.get(r, "general")
+    return {1: "fused", 2: "prefill", 3: "stream", 4: "rows"}.get(r, "general")
 
 
 def stream_launch(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> Optional[str]:

@@ -146,7 +146,7 @@ def hetero(gpu):
     return gsynth.make_layer(seed=11, n_expert=E, d=D, ff=FF, max_rank=512, ranks=ranks, int8_fraction=0.1)
 
 
-@pytest.mark.parametrize("T,path", [(16, "default"), (16, "general"), (256, "default")])
+@pytest.mark.parametrize("T,path", [(16, "default"), (16, "general"), (256, "default"), (16, "rows"), (256, "rows")])
 def test_hetero_int8_drop(gpu, hetero, T, path, monkeypatch):
     import torch
 
