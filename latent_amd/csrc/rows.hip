@@ -34,6 +34,7 @@
 #include "rows.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace latent {
 namespace rows {
@@ -72,6 +73,17 @@ __device__ __forceinline__ void lds_st(uint32_t addr, const T& v) {
 }
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Workgroup barrier over LDS only: waits for this wave's LDS accesses, then
+// s_barrier.  (__syncthreads() would also wait for every outstanding global
+// load and drain the chunks loaded ahead.)  Workgroups of these kernels
+// share data through LDS only.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Raw buffer resource over `bytes` bytes (loads beyond them return zero).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
@@ -99,19 +111,37 @@ __device__ __forceinline__ void lut_fill(uint32_t* lut, int tid) {
   lut[tid] = __builtin_bit_cast(uint32_t, lv);
 }
 
-// Chunk shape for ng groups: ngp = ng rounded up to a power of two in
-// [2, 16], rows = 512 / ngp; dwords per decoded column cstr = rows / 2 + 4
-// (16-byte MFMA reads of 8 consecutive columns fall on distinct banks), per
-// group block gstr = 32 cstr + 64 / ngp (the 64 stores of a wave, 64 / ngp
-// row pairs of ngp groups, fall on distinct banks).
+// Chunk shape for ng groups (a compile-time type, so every LDS offset of a
+// chunk is an immediate): ngp = ng rounded up to a power of two in [2, 16],
+// rows = 512 / ngp; dwords per decoded column cstr = rows / 2 + 4 (16-byte
+// MFMA reads of 8 consecutive columns fall on distinct banks), per group
+// block gstr = 32 cstr + 64 / ngp (the 64 stores of a wave, 64 / ngp row
+// pairs of ngp groups, fall on distinct banks).
+template <int NGP>
 struct Shape {
+  static constexpr int ngp = NGP, rows = 512 / NGP, cstr = rows / 2 + 4, gstr = 32 * cstr + 64 / NGP;
+};
+// The same shape as run-time values (one code path for every shape).
+struct DynShape {
   int ngp, rows, cstr, gstr;
 };
-__device__ __forceinline__ Shape shape_for(int ng) {
+__device__ __forceinline__ DynShape dyn_shape(int ng) {
   int ngp = 2;
   while (ngp < ng) ngp <<= 1;
   const int rows = 512 / ngp, cstr = rows / 2 + 4;
-  return Shape{ngp, rows, cstr, 32 * cstr + 64 / ngp};
+  return DynShape{ngp, rows, cstr, 32 * cstr + 64 / ngp};
+}
+// f(Shape<ngp>{}) for the chunk shape of ng groups.
+template <typename F>
+__device__ __forceinline__ void with_shape(int ng, F&& f) {
+  if (ng <= 2)
+    f(Shape<2>{});
+  else if (ng <= 4)
+    f(Shape<4>{});
+  else if (ng <= 8)
+    f(Shape<8>{});
+  else
+    f(Shape<16>{});
 }
 
 // One thread's decode unit of a chunk: rows r, r + 1 of one group.
@@ -125,64 +155,95 @@ struct Q {  // the INT8 bytes of the unit's rows (zero where NF4)
   u32x4 v[2][2];
 };
 
-// Loads of rows r, r + 1 (clamped to row_end - 1, or row 0) of group g of
-// expert rows [ebase, ebase + rows).
+// One thread's view of a decode source: rows below row_end of groups
+// [g0, g0 + ng) of one expert's factor, in chunks of sh.rows rows from row
+// `base`; the thread's unit is group gi and row pair rp of each chunk.  The
+// expert's codes, scales, bitmap words and word offsets through buffer
+// resources (wave-uniform; 32-bit offsets, zeros past the expert's rows or
+// for a factor without INT8 groups), the INT8 bytes through one over the
+// factor's side buffer.
+struct Src {
+  __amdgpu_buffer_rsrc_t rc, rs, rb, ro, rd;
+  int cs, ss, words;
+  int base, row_end, g0, ng, gi, rp;
+};
+__device__ __forceinline__ Src make_src(const Factor& f, int e, int base, int row_end, int g0, int ng, int gi,
+                                        int rp) {
+  const int64_t er = static_cast<int64_t>(e) * f.rows;
+  const int cs = static_cast<int>(f.code_stride()), ss = static_cast<int>(f.scale_stride()), words = f.words();
+  const bool has8 = f.ext.bitmap != nullptr;
+  const uint32_t rows = static_cast<uint32_t>(f.rows);
+  Src s;
+  s.rc = buffer_rsrc(f.codes + er * cs, rows * cs);
+  s.rs = buffer_rsrc(f.scales + er * ss, rows * ss * 2u);
+  s.rb = buffer_rsrc(has8 ? f.ext.bitmap + er * words : nullptr, has8 ? rows * words * 4u : 0u);
+  s.ro = buffer_rsrc(has8 ? f.ext.word_offset + er * words : nullptr, has8 ? rows * words * 4u : 0u);
+  s.rd = buffer_rsrc(f.ext.data, has8 ? 0x7FFFFFF0u : 0u);
+  s.cs = cs;
+  s.ss = ss;
+  s.words = words;
+  s.base = base;
+  s.row_end = row_end;
+  s.g0 = g0;
+  s.ng = ng;
+  s.gi = gi;
+  s.rp = rp;
+  return s;
+}
+
+// Loads of rows r, r + 1 of group g.
 template <bool kInt8>
-__device__ __forceinline__ void unit_load(const Factor& f, int64_t ebase, int r, int row_end, int g, Unit& u) {
-  const int64_t cs = f.code_stride(), ss = f.scale_stride();
-  const int last = max(row_end - 1, 0);
-  const int64_t r0 = ebase + min(r, last), r1 = ebase + min(r + 1, last);
-  u.c[0] = *reinterpret_cast<const u32x4*>(f.codes + r0 * cs + g * kGroupBytes);
-  u.c[1] = *reinterpret_cast<const u32x4*>(f.codes + r1 * cs + g * kGroupBytes);
-  u.s = static_cast<uint32_t>(f.scales[r0 * ss + g]) | (static_cast<uint32_t>(f.scales[r1 * ss + g]) << 16);
+__device__ __forceinline__ void unit_load(const Src& s, int r, int g, Unit& u) {
+  const uint32_t r0 = static_cast<uint32_t>(r), r1 = r0 + 1u;
+  u.c[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.rc, r0 * s.cs + g * kGroupBytes, 0, 0));
+  u.c[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.rc, r1 * s.cs + g * kGroupBytes, 0, 0));
+  const uint32_t s0 = __builtin_amdgcn_raw_buffer_load_b16(s.rs, (r0 * s.ss + g) * 2u, 0, 0);
+  const uint32_t s1 = __builtin_amdgcn_raw_buffer_load_b16(s.rs, (r1 * s.ss + g) * 2u, 0, 0);
+  u.s = s0 | (s1 << 16);
   if (kInt8) {
-    if (f.ext.bitmap) {
-      const int words = f.words(), ws = g >> 5;
-      u.w[0] = f.ext.bitmap[r0 * words + ws];
-      u.w[1] = f.ext.bitmap[r1 * words + ws];
-      u.o[0] = f.ext.word_offset[r0 * words + ws];
-      u.o[1] = f.ext.word_offset[r1 * words + ws];
-    } else {
-      u.w[0] = u.w[1] = 0u;
-      u.o[0] = u.o[1] = 0;
-    }
+    const uint32_t ws = static_cast<uint32_t>(g >> 5);
+    u.w[0] = __builtin_amdgcn_raw_buffer_load_b32(s.rb, (r0 * s.words + ws) * 4u, 0, 0);
+    u.w[1] = __builtin_amdgcn_raw_buffer_load_b32(s.rb, (r1 * s.words + ws) * 4u, 0, 0);
+    u.o[0] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(s.ro, (r0 * s.words + ws) * 4u, 0, 0));
+    u.o[1] = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(s.ro, (r1 * s.words + ws) * 4u, 0, 0));
   }
 }
 
-// The INT8 bytes of a unit's flagged rows, through a buffer resource (an
-// unflagged row reads past its range and gets zeros: no branch).
+// The INT8 bytes of a unit's flagged rows (an unflagged row reads past the
+// range and gets zeros: no branch).
 template <bool kInt8>
-__device__ __forceinline__ void q_load(const Factor& f, const Unit& u, int g, Q& q) {
+__device__ __forceinline__ void q_load(const Src& s, const Unit& u, int g, Q& q) {
   if (!kInt8) return;
-  const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(f.ext.data, 0x7FFFFFF0u);
   const uint32_t bit = 1u << (g & 31);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const bool is8 = (u.w[h] & bit) != 0u;
     const uint32_t off = is8 ? static_cast<uint32_t>(u.o[h] + popc(u.w[h] & (bit - 1u))) * kGroup : 0x80000000u;
-    q.v[h][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, off, 0, 0));
-    q.v[h][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rd, off + 16u, 0, 0));
+    q.v[h][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.rd, off, 0, 0));
+    q.v[h][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(s.rd, off + 16u, 0, 0));
   }
 }
 
 // Row h of a unit as 16 fp16 pairs (columns 2i, 2i + 1): level x scale or
-// q x scale, rounded once; zeros for a dead row.
+// q x scale, rounded once; zeros for a dead row (scale 0: every level and q
+// is finite).  INT8 bytes become fp16 exactly through 0x6400 | (q ^ 0x80) =
+// 1024 + q + 128, less 1152.
 template <bool kInt8>
 __device__ __forceinline__ void unit_row(const Unit& u, const Q& q, int h, int g, bool live, uint32_t lut,
                                          half2v (&v)[16]) {
-  const _Float16 s = __builtin_bit_cast(_Float16, static_cast<uint16_t>(u.s >> (16 * h)));
+  const _Float16 s = live ? __builtin_bit_cast(_Float16, static_cast<uint16_t>(u.s >> (16 * h)))
+                          : static_cast<_Float16>(0.f);
   const half2v s2 = {s, s};
   const bool is8 = kInt8 && ((u.w[h] >> (g & 31)) & 1u);
   if (is8) {
+    const half2v bias = {static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t d = q.v[h][i >> 2][i & 3];
-      const half2v lo = {static_cast<_Float16>(static_cast<int8_t>(d & 0xFFu)),
-                         static_cast<_Float16>(static_cast<int8_t>((d >> 8) & 0xFFu))};
-      const half2v hi = {static_cast<_Float16>(static_cast<int8_t>((d >> 16) & 0xFFu)),
-                         static_cast<_Float16>(static_cast<int8_t>(d >> 24))};
-      v[2 * i] = lo * s2;
-      v[2 * i + 1] = hi * s2;
+      const uint32_t d = q.v[h][i >> 2][i & 3] ^ 0x80808080u;
+      const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, d, 0x04010400u);  // bytes (d0, 0x64, d1, 0x64)
+      const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, d, 0x04030402u);  // bytes (d2, 0x64, d3, 0x64)
+      v[2 * i] = (__builtin_bit_cast(half2v, lo) + bias) * s2;
+      v[2 * i + 1] = (__builtin_bit_cast(half2v, hi) + bias) * s2;
     }
   } else {
 #pragma unroll
@@ -190,10 +251,6 @@ __device__ __forceinline__ void unit_row(const Unit& u, const Q& q, int h, int g
       const uint32_t b = (u.c[h][i >> 2] >> (8 * (i & 3))) & 0xFFu;
       v[i] = __builtin_bit_cast(half2v, lds_ld<uint32_t>(lut + b * 4)) * s2;
     }
-  }
-  if (!live) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = half2v{static_cast<_Float16>(0.f), static_cast<_Float16>(0.f)};
   }
 }
 
@@ -214,45 +271,23 @@ __device__ __forceinline__ void unit_store(const Unit& u, const Q& q, int g, boo
   }
 }
 
-// One thread's view of a decode source: rows below row_end of groups
-// [g0, g0 + ng) of expert e's factor f (wave-uniform), in chunks of sh.rows
-// rows from row `base`; the thread's unit is group gi (its block in the
-// decoded chunk) and row pair rp of each chunk.
-struct Src {
-  const Factor* f;
-  int64_t ebase;  // e * f.rows
-  int base, row_end, g0, ng;
-  int gi, rp;
-};
-// The usual unit of thread tid: group tid % ngp, row pair tid / ngp (a
-// wave's 64 stores then fall on distinct banks).
-__device__ __forceinline__ Src src_of(const Factor* f, int64_t ebase, int base, int row_end, int g0, int ng,
-                                      const Shape& sh, int tid) {
-  return Src{f, ebase, base, row_end, g0, ng, tid & (sh.ngp - 1), tid / sh.ngp};
-}
-
-// The decode ring: units of chunks c, c + 1, c + 2 (slots c % 3) and INT8
-// bytes of chunks c, c + 1 (slots c % 2).  Every chunk issues the same loads
+// The decode ring: units of chunks c .. c + 3 (slots c % 4) and INT8 bytes
+// of chunks c, c + 1 (slots c % 2).  Every chunk issues the same loads
 // (clamped past the last chunk), so the compiler's wait counts hold on every
 // path.
 template <bool kInt8>
 struct Ring {
-  Unit u[3];
+  Unit u[4];
   Q q[2];
 };
 
-template <bool kInt8>
-__device__ __forceinline__ void ring_issue(const Src& s, const Shape& sh, int c, int nc, Unit& u) {
+template <bool kInt8, class SH>
+__device__ __forceinline__ void ring_issue(const Src& s, SH sh, int c, int nc, Unit& u) {
   const int g = s.g0 + min(s.gi, s.ng - 1);
-  const int r = s.base + min(c, nc - 1) * sh.rows + 2 * s.rp;
-  unit_load<kInt8>(*s.f, s.ebase, r, s.row_end, g, u);
+  unit_load<kInt8>(s, s.base + min(c, nc - 1) * sh.rows + 2 * s.rp, g, u);
 }
-template <bool kInt8>
-__device__ __forceinline__ void ring_q(const Src& s, const Unit& u, Q& q) {
-  q_load<kInt8>(*s.f, u, s.g0 + min(s.gi, s.ng - 1), q);
-}
-template <bool kInt8>
-__device__ __forceinline__ void ring_store(const Src& s, const Shape& sh, int c, const Unit& u, const Q& q,
+template <bool kInt8, class SH>
+__device__ __forceinline__ void ring_store(const Src& s, SH sh, int c, const Unit& u, const Q& q,
                                            uint32_t lut, uint32_t bt, int block) {
   if (s.gi >= s.ng) return;
   const int r = s.base + c * sh.rows + 2 * s.rp;
@@ -264,8 +299,8 @@ __device__ __forceinline__ void ring_store(const Src& s, const Shape& sh, int c,
 // cb = cb0 + j * cbs (j < kNcb, cb < ncb), rows / 32 steps of K.  act: LDS
 // byte address of the activation rows (astr dwords apart) at the chunk's
 // first K value.
-template <int kNcb>
-__device__ __forceinline__ void chunk_mfma(uint32_t act, int astr, uint32_t bt, const Shape& sh, int cb0, int cbs,
+template <int kNcb, class SH>
+__device__ __forceinline__ void chunk_mfma(uint32_t act, int astr, uint32_t bt, SH sh, int cb0, int cbs,
                                            int ncb, int n, int kq, float4v (&acc)[kNcb]) {
   const int steps = sh.rows / 32;
   for (int s = 0; s < steps; ++s) {
@@ -282,40 +317,45 @@ __device__ __forceinline__ void chunk_mfma(uint32_t act, int astr, uint32_t bt, 
   }
 }
 
-// The chunk loop of one decode source: for each chunk, stage(c, slot) issues
-// the activation loads of chunk c + 1 into register slot `slot ^ 1` and
-// stores chunk c's (slot) into LDS; mfma(c) runs the chunk's MFMA steps.
-// Two barriers per chunk: the decoded chunk and the activations are complete,
-// then every wave is done with them.
-// block: the thread's group block in the decoded chunk.
-template <bool kInt8, typename Stage, typename Mfma>
-__device__ __forceinline__ void run_chunks(const Src& s, const Shape& sh, int nc, int block, uint32_t lut,
-                                           uint32_t bt, Ring<kInt8>& rg, Stage&& stage, Mfma&& mfma) {
+// The chunk loop of one decode source.  Step c issues the activation loads
+// of chunk c + 1 (issue(c + 1, slot)), the INT8 bytes of chunk c + 1 (whose
+// units were issued two steps earlier) and the units of chunk c + 3, then
+// stores chunk c's activations (store(c, slot)) and decoded units to LDS
+// and runs its MFMA steps (mfma(c)).  Loads complete in issue order, so the
+// decode of chunk c leaves the units of chunks c + 2 and c + 3 in flight.
+// Two barriers per chunk: the decoded chunk and the activations are
+// complete, then every wave is done with them (LDS barriers: the loads
+// issued ahead stay in flight).  block: the thread's group block in the
+// decoded chunk.
+template <bool kInt8, class SH, typename Issue, typename Store, typename Mfma>
+__device__ __forceinline__ void run_chunks(const Src& s, SH sh, int nc, int block, uint32_t lut,
+                                           uint32_t bt, Ring<kInt8>& rg, Issue&& issue, Store&& store,
+                                           Mfma&& mfma) {
+  const int g = s.g0 + min(s.gi, s.ng - 1);
   ring_issue<kInt8>(s, sh, 0, nc, rg.u[0]);
   ring_issue<kInt8>(s, sh, 1, nc, rg.u[1]);
-  ring_q<kInt8>(s, rg.u[0], rg.q[0]);
-  auto step = [&](int c, auto us, auto qs) __attribute__((always_inline)) {
-    constexpr int U = decltype(us)::value, Qs = decltype(qs)::value;
-    ring_q<kInt8>(s, rg.u[(U + 1) % 3], rg.q[Qs ^ 1]);
-    ring_issue<kInt8>(s, sh, c + 2, nc, rg.u[(U + 2) % 3]);
-    stage(c, std::integral_constant<int, Qs>{});
+  ring_issue<kInt8>(s, sh, 2, nc, rg.u[2]);
+  q_load<kInt8>(s, rg.u[0], g, rg.q[0]);
+  issue(0, std::integral_constant<int, 0>{});
+  auto step = [&](int c, auto us) __attribute__((always_inline)) {
+    constexpr int U = decltype(us)::value, Qs = U & 1;
+    issue(c + 1, std::integral_constant<int, Qs ^ 1>{});
+    q_load<kInt8>(s, rg.u[(U + 1) & 3], g, rg.q[Qs ^ 1]);
+    ring_issue<kInt8>(s, sh, c + 3, nc, rg.u[(U + 3) & 3]);
+    store(c, std::integral_constant<int, Qs>{});
     ring_store<kInt8>(s, sh, c, rg.u[U], rg.q[Qs], lut, bt, block);
-    __syncthreads();
+    lds_barrier();
     mfma(c);
-    __syncthreads();
+    lds_barrier();
   };
-  for (int c = 0; c < nc; c += 6) {
-    step(c, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  for (int c = 0; c < nc; c += 4) {
+    step(c, std::integral_constant<int, 0>{});
     if (c + 1 >= nc) break;
-    step(c + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    step(c + 1, std::integral_constant<int, 1>{});
     if (c + 2 >= nc) break;
-    step(c + 2, std::integral_constant<int, 2>{}, std::integral_constant<int, 0>{});
+    step(c + 2, std::integral_constant<int, 2>{});
     if (c + 3 >= nc) break;
-    step(c + 3, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
-    if (c + 4 >= nc) break;
-    step(c + 4, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
-    if (c + 5 >= nc) break;
-    step(c + 5, std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+    step(c + 3, std::integral_constant<int, 3>{});
   }
 }
 
@@ -346,82 +386,83 @@ __global__ void __launch_bounds__(kT, 2) a_kernel(Params p) {
   const int e = p.act_expert[a], s0 = p.act_start[a], mtot = p.act_count[a];
   const int rank = rank_of(p, e, kind), ng = (rank + kGroup - 1) / kGroup;
   if (ng == 0 || mtot == 0) return;
-  const Shape sh = shape_for(ng);
-  // Rows [r_lo, r_hi) of d in chunks of sh.rows.
-  const int r_lo = static_cast<int>(static_cast<int64_t>(split) * p.d / p.na_split) / 32 * 32;
-  const int r_hi = static_cast<int>(static_cast<int64_t>(split + 1) * p.d / p.na_split) / 32 * 32;
-  const int r_end = split + 1 == p.na_split ? p.d : r_hi;
-  const int nc = (r_end - r_lo + sh.rows - 1) / sh.rows;
-  if (nc <= 0) return;
-  lut_fill(sm.lut, tid);
-  const uint32_t L_lut = lds_addr(sm.lut), L_bt = lds_addr(sm.bt);
-  const uint32_t L_act[2] = {lds_addr(sm.act[0]), lds_addr(sm.act[1])};
-  const Src src = src_of(&f, static_cast<int64_t>(e) * f.rows, r_lo, r_end, 0, ng, sh, tid);
-  const int ncb = 2 * ng;  // 16-column blocks of the rank
-  const int astr = sh.cstr;
-  // x staging: 16 rows x sh.rows halves in 16-byte pieces; piece i of this
-  // thread is tid + 256 i (i < 2; sh.rows <= 256).
-  const int pieces = kPass * sh.rows / 8, ppr = sh.rows / 8;
-  for (int tb = 0; tb < mtot; tb += kPass) {
-    const int m = min(kPass, mtot - tb);
-    if (tid < kPass) {
-      const int tok = tid < m ? p.pair_tok[s0 + tb + tid] : -1;
-      sm.rtok[tid] = tok;
-      sm.rexp[tid] = tok >= 0 ? p.xexp[tok] : 0;
-    }
-    __syncthreads();
-    u32x4 xr[2][2];
-    auto load_x = [&](int c, u32x4 (&x)[2]) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int pc = tid + kT * i;
-        const int row = min(pc / ppr, kPass - 1), k8 = pc % ppr;
-        const int tok = sm.rtok[row];
-        const int col = r_lo + min(c, nc - 1) * sh.rows + k8 * 8;
-        const bool ok = pc < pieces && tok >= 0 && col < r_end;
-        const int64_t off = static_cast<int64_t>(max(tok, 0)) * p.d + min(col, p.d - 8);
-        const u32x4 v = *reinterpret_cast<const u32x4*>(p.xh + off);
-        x[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+  with_shape(ng, [&](auto sh) __attribute__((always_inline)) {
+    // The item's share of the expert's chunks of d (chunks of sh.rows rows:
+    // about 8 KB of codes each, so an expert's chunk count grows with its rank).
+    const int nct = (p.d + sh.rows - 1) / sh.rows;
+    const int c_lo = split * nct / p.na_split, c_hi = (split + 1) * nct / p.na_split;
+    const int nc = c_hi - c_lo;
+    if (nc <= 0) return;
+    const int r_lo = c_lo * sh.rows, r_end = min(p.d, c_hi * sh.rows);
+    lut_fill(sm.lut, tid);
+    const uint32_t L_lut = lds_addr(sm.lut), L_bt = lds_addr(sm.bt);
+    const uint32_t L_act[2] = {lds_addr(sm.act[0]), lds_addr(sm.act[1])};
+    const Src src = make_src(f, e, r_lo, r_end, 0, ng, tid & (sh.ngp - 1), tid / sh.ngp);
+    const int ncb = 2 * ng;  // 16-column blocks of the rank
+    const int astr = sh.cstr;
+    // x staging: 16 rows x sh.rows halves in 16-byte pieces; piece i of this
+    // thread is tid + 256 i (i < 2; sh.rows <= 256).
+    const int pieces = kPass * sh.rows / 8, ppr = sh.rows / 8;
+    for (int tb = 0; tb < mtot; tb += kPass) {
+      const int m = min(kPass, mtot - tb);
+      if (tid < kPass) {
+        const int tok = tid < m ? p.pair_tok[s0 + tb + tid] : -1;
+        sm.rtok[tid] = tok;
+        sm.rexp[tid] = tok >= 0 ? p.xexp[tok] : 0;
       }
-    };
-    load_x(0, xr[0]);
-    float4v acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
-    Ring<kInt8> rg;
-    auto stage = [&](int c, auto slot) __attribute__((always_inline)) {
-      constexpr int S = decltype(slot)::value;
-      load_x(c + 1, xr[S ^ 1]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int pc = tid + kT * i;
-        if (pc < pieces)
-          lds_st<u32x4>(L_act[S] + static_cast<uint32_t>((pc / ppr) * astr + (pc % ppr) * 4) * 4u, xr[S][i]);
-      }
-    };
-    auto mfma = [&](int c) __attribute__((always_inline)) {
-      // The stage of chunk c wrote act[c % 2] (the ring's slot order).
-      chunk_mfma<8>(L_act[c & 1], astr, L_bt, sh, wave, 4, ncb, n, kq, acc);
-    };
-    run_chunks<kInt8>(src, sh, nc, src.gi, L_lut, L_bt, rg, stage, mfma);
-    // Partial latents of the pass: scaled back, summed into gu.
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int cb = wave + 4 * j;
-      const int col = cb * 16 + n;
-      if (cb < ncb && col < rank) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = kq * 4 + v;
-          if (row < m) {
-            const float sc = ldexpf(1.0f, -sm.rexp[row]);
-            atomic_add_f32(p.gu + static_cast<int64_t>(s0 + tb + row) * (2 * p.R) + kind * p.R + col, acc[j][v] * sc);
+      lds_barrier();
+      u32x4 xr[2][2];
+      auto load_x = [&](int c, u32x4 (&x)[2]) __attribute__((always_inline)) {
+  #pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int pc = tid + kT * i;
+          const int row = min(pc / ppr, kPass - 1), k8 = pc % ppr;
+          const int tok = sm.rtok[row];
+          const int col = r_lo + min(c, nc - 1) * sh.rows + k8 * 8;
+          const bool ok = pc < pieces && tok >= 0 && col < r_end;
+          const int64_t off = static_cast<int64_t>(max(tok, 0)) * p.d + min(col, p.d - 8);
+          const u32x4 v = *reinterpret_cast<const u32x4*>(p.xh + off);
+          x[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+      };
+      float4v acc[8];
+  #pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
+      Ring<kInt8> rg;
+      auto issue = [&](int c, auto slot) __attribute__((always_inline)) { load_x(c, xr[decltype(slot)::value]); };
+      auto store = [&](int c, auto slot) __attribute__((always_inline)) {
+        constexpr int S = decltype(slot)::value;
+  #pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int pc = tid + kT * i;
+          if (pc < pieces)
+            lds_st<u32x4>(L_act[S] + static_cast<uint32_t>((pc / ppr) * astr + (pc % ppr) * 4) * 4u, xr[S][i]);
+        }
+      };
+      auto mfma = [&](int c) __attribute__((always_inline)) {
+        // The stage of chunk c wrote act[c % 2] (the ring's slot order).
+        chunk_mfma<8>(L_act[c & 1], astr, L_bt, sh, wave, 4, ncb, n, kq, acc);
+      };
+      run_chunks<kInt8>(src, sh, nc, src.gi, L_lut, L_bt, rg, issue, store, mfma);
+      // Partial latents of the pass: scaled back, summed into gu.
+  #pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int cb = wave + 4 * j;
+        const int col = cb * 16 + n;
+        if (cb < ncb && col < rank) {
+  #pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = kq * 4 + v;
+            if (row < m) {
+              const float sc = ldexpf(1.0f, -sm.rexp[row]);
+              atomic_add_f32(p.gu + static_cast<int64_t>(s0 + tb + row) * (2 * p.R) + kind * p.R + col, acc[j][v] * sc);
+            }
           }
         }
       }
+      lds_barrier();  // rtok / rexp of the next pass
     }
-    __syncthreads();  // rtok / rexp of the next pass
-  }
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -455,13 +496,11 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
   const Factor& fbu = p.fac[F_UP_B];
   const Factor& fad = p.fac[F_DOWN_A];
   // Stage 1: 16 groups per chunk (8 of B_g, 8 of B_u), 32 rows of the rank.
-  const Shape sh1 = shape_for(16);
+  constexpr Shape<16> sh1{};
   const int kb = max(rg_, ru);
   const int nc1 = (kb + 31) / 32;
   // Stage 2: the 256 rows of A_d at c0, rd columns.
   const int ngd = (rd + kGroup - 1) / kGroup;
-  const Shape sh2 = shape_for(max(ngd, 1));
-  const int nc2 = (ncol + sh2.rows - 1) / sh2.rows;
   for (int tb = 0; tb < mtot; tb += kPass) {
     const int m = min(kPass, mtot - tb);
     // Latent row exponents: max |g|, then max |u|, over the rank (16 lanes per row).
@@ -477,7 +516,7 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
       mx = op_over(mx, 1, 16, OpMax{});
       if (t == 0) sm.rexp[k][r] = pow2_row_exponent(mx);
     }
-    __syncthreads();
+    lds_barrier();
     float4v accg[4], accu[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) accg[j] = accu[j] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -487,9 +526,7 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
       // (thread: group tid % 8, row pair (tid % 128) / 8).  Rows past a
       // factor's own rank decode as zeros.
       const bool up = uniform(tid >> 7) != 0;
-      const Factor* fb = up ? &fbu : &fbg;
-      const Src mine{fb, static_cast<int64_t>(e) * fb->rows, 0, up ? ru : rg_, c0 / kGroup, ngc, tid & 7,
-                     (tid & 127) >> 3};
+      const Src mine = make_src(up ? fbu : fbg, e, 0, up ? ru : rg_, c0 / kGroup, ngc, tid & 7, (tid & 127) >> 3);
       const int block = (up ? 8 : 0) + (tid & 7);
       // act staging: gate and up latent rows of chunk c (32 rank rows), fp16 x 2^rexp.
       u32x4 lr[2];
@@ -504,10 +541,9 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
         x = ok ? u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)}
                : u32x4{0u, 0u, 0u, 0u};
       };
-      load_l(0, lr[0]);
-      auto stage = [&](int c, auto slot) __attribute__((always_inline)) {
+      auto issue = [&](int c, auto slot) __attribute__((always_inline)) { load_l(c, lr[decltype(slot)::value]); };
+      auto store = [&](int c, auto slot) __attribute__((always_inline)) {
         constexpr int S = decltype(slot)::value;
-        load_l(c + 1, lr[S ^ 1]);
         const int r = tid >> 4, k = (tid >> 3) & 1, q4 = (tid & 7) * 4;
         const int ex = sm.rexp[k][r];
         const half2v h0 = to_h2(__uint_as_float(lr[S][0]), __uint_as_float(lr[S][1]), ex);
@@ -524,7 +560,7 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
         chunk_mfma<4>(lds_addr(sm.act[S][0]), 20, L_bt, sh1, 4 * wave, 1, 2 * ngc, n, kq, accg);
         chunk_mfma<4>(lds_addr(sm.act[S][1]), 20, L_bt, sh1, 16 + 4 * wave, 1, 16 + 2 * ngc, n, kq, accu);
       };
-      run_chunks<kInt8>(mine, sh1, nc1, block, L_lut, L_bt, rg, stage, mfma);
+      run_chunks<kInt8>(mine, sh1, nc1, block, L_lut, L_bt, rg, issue, store, mfma);
     }
     // h = SiLU(g) u (x router weight before down) of the wave's 64 columns,
     // fp16 with one exponent per row (the maximum over the item's columns).
@@ -545,7 +581,7 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
       mx = op_over(mx, 1, 16, OpMax{});
       if (n == 0) sm.hmax[wave][row] = mx;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = kq * 4 + v;
@@ -559,19 +595,22 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
         lds_st<_Float16>(L_h + static_cast<uint32_t>(row * kHDw * 4 + col * 2), hh);
       }
     }
-    __syncthreads();
+    lds_barrier();
     // Stage 2: d latent partial of these 256 rows of A_d.
+    // (One run-time shape: a compile-time one per group count spilled.)
     if (ngd > 0) {
+      const DynShape sh2 = dyn_shape(ngd);
+      const int nc2 = (ncol + sh2.rows - 1) / sh2.rows;
       float4v accd[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) accd[j] = float4v{0.f, 0.f, 0.f, 0.f};
-      const Src sd = src_of(&fad, static_cast<int64_t>(e) * fad.rows, c0, c0 + ncol, 0, ngd, sh2, tid);
-      auto stage = [&](int, auto) __attribute__((always_inline)) {};
+      const Src sd = make_src(fad, e, c0, c0 + ncol, 0, ngd, tid & (sh2.ngp - 1), tid / sh2.ngp);
+      auto none = [&](int, auto) __attribute__((always_inline)) {};
       Ring<kInt8> rg;
       auto mfma = [&](int c) __attribute__((always_inline)) {
         chunk_mfma<8>(L_h + static_cast<uint32_t>(c * sh2.rows) * 2u, kHDw, L_bt, sh2, wave, 4, 2 * ngd, n, kq, accd);
       };
-      run_chunks<kInt8>(sd, sh2, nc2, sd.gi, L_lut, L_bt, rg, stage, mfma);
+      run_chunks<kInt8>(sd, sh2, nc2, sd.gi, L_lut, L_bt, rg, none, none, mfma);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int cb = wave + 4 * j;
@@ -587,7 +626,7 @@ __global__ void __launch_bounds__(kT, 2) bc_kernel(Params p) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -617,9 +656,9 @@ __global__ void __launch_bounds__(kT, 2) d_kernel(Params p) {
   if (mtot == 0) return;
   lut_fill(sm.lut, tid);
   const uint32_t L_lut = lds_addr(sm.lut), L_bt = lds_addr(sm.bt);
-  const Shape sh = shape_for(16);  // 32 rows of the rank per chunk
+  constexpr Shape<16> sh{};  // 32 rows of the rank per chunk
   const int nc = (rd + 31) / 32;
-  const Src src = src_of(&f, static_cast<int64_t>(e) * f.rows, 0, rd, c0 / kGroup, ngc, sh, tid);
+  const Src src = make_src(f, e, 0, rd, c0 / kGroup, ngc, tid & (sh.ngp - 1), tid / sh.ngp);
   for (int tb = 0; tb < mtot; tb += kPass) {
     const int m = min(kPass, mtot - tb);
     {
@@ -637,7 +676,7 @@ __global__ void __launch_bounds__(kT, 2) d_kernel(Params p) {
         sm.rw[r] = p.wbd ? 1.0f : p.pair_w[pair];
       }
     }
-    __syncthreads();
+    lds_barrier();
     float4v acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -652,10 +691,9 @@ __global__ void __launch_bounds__(kT, 2) d_kernel(Params p) {
         const float2 v = *reinterpret_cast<const float2*>(s);
         x = ok ? u32x4{__float_as_uint(v.x), __float_as_uint(v.y), 0u, 0u} : u32x4{0u, 0u, 0u, 0u};
       };
-      load_l(0, lr[0]);
-      auto stage = [&](int c, auto slot) __attribute__((always_inline)) {
+      auto issue = [&](int c, auto slot) __attribute__((always_inline)) { load_l(c, lr[decltype(slot)::value]); };
+      auto store = [&](int c, auto slot) __attribute__((always_inline)) {
         constexpr int S = decltype(slot)::value;
-        load_l(c + 1, lr[S ^ 1]);
         const int r = tid >> 4, q2 = (tid & 15) * 2;
         const half2v h = to_h2(__uint_as_float(lr[S][0]), __uint_as_float(lr[S][1]), sm.rexp[r]);
         lds_st<uint32_t>(lds_addr(sm.act[S]) + static_cast<uint32_t>(r * 20 + q2 / 2) * 4u,
@@ -665,7 +703,7 @@ __global__ void __launch_bounds__(kT, 2) d_kernel(Params p) {
       auto mfma = [&](int c) __attribute__((always_inline)) {
         chunk_mfma<8>(lds_addr(sm.act[c & 1]), 20, L_bt, sh, wave, 4, 2 * ngc, n, kq, acc);
       };
-      run_chunks<kInt8>(src, sh, nc, src.gi, L_lut, L_bt, rg, stage, mfma);
+      run_chunks<kInt8>(src, sh, nc, src.gi, L_lut, L_bt, rg, issue, store, mfma);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -686,7 +724,7 @@ __global__ void __launch_bounds__(kT, 2) d_kernel(Params p) {
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 }
 
@@ -709,6 +747,7 @@ void plan(Params& p) {
   // Enough phase A items to fill the CUs twice over (2 workgroups per CU).
   int s = 1;
   while (s < 16 && 2ll * p.a_max * s < 1024 && p.d / (2 * s) >= 512) s *= 2;
+  if (const char* v = std::getenv("LATENT_ROWS_SPLIT")) s = std::max(1, std::atoi(v));
   p.na_split = s;
   p.n_a = 2 * s;
   p.n_bc = (p.ff + kCB - 1) / kCB;
