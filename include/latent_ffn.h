@@ -224,11 +224,14 @@ int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t st
  *       4096 routed pairs, 16-byte aligned x;
  *   1 = single persistent fp32 decode kernel: row layout, 32 to 512 routed
  *       pairs, 2 * max_rank <= 1024, 16-byte aligned x (INT8 groups allowed);
+ *   4 = multi-kernel fp16-MFMA path on the row layout: at least 16 routed
+ *       pairs, max_rank <= 512, 16-byte aligned x (per-expert ranks and INT8
+ *       groups allowed); factors decoded into LDS chunk by chunk;
  *   0 = multi-kernel fp32 GEMV path: any call on the row layout.
  * A call in the tile layout that neither path 2 nor 3 takes is
  * LATENT_E_UNSUPPORTED.
  * < 0 = LATENT_E_* for bad arguments.  The environment variable
- * LATENT_MOE_PATH (general | fused | prefill | stream) selects another path
+ * LATENT_MOE_PATH (general | fused | prefill | stream | rows) selects another path
  * that supports the call, for comparisons.
  * Diagnostic only; no counterpart in the reference.
  */

@@ -948,7 +948,7 @@ int pick_pow2_chunk(int64_t per_expert_extent, int64_t experts, int64_t target_i
 enum { kPathGeneral = 0, kPathFused = 1, kPathPrefill = 2, kPathStream = 3, kPathRows = 4 };
 
 // The implementation for one call shape.  LATENT_MOE_PATH (general | fused |
-// prefill | stream) selects another path that supports the call, for
+// prefill | stream | rows) selects another path that supports the call, for
 // comparisons; the default is the measured fastest supported path.  A layer
 // in the tile layout has only the two MFMA paths (LATENT_E_UNSUPPORTED when
 // neither takes the call).
@@ -977,10 +977,16 @@ int choose_path(const latent_moe_args& a, fused::Plan& pl) {
   // 256 experts, top-8): below the prefill threshold the streaming MFMA path
   // is the fastest wherever it applies (batch 1: 49 vs 52 us for the
   // multi-kernel path; batch 8: 100 vs 144 us and batch 64: 270 vs 370 us
-  // for the persistent kernel).
+  // for the persistent kernel).  On the row layout (ranks 64..512, 10 %
+  // INT8 groups): the persistent fp32 kernel, bit-reproducible, where it
+  // applies (batch 16: 387 us, level with the row-layout MFMA phases; batch
+  // 64: 817 against 735 us); elsewhere the row-layout MFMA phases from 16
+  // routed pairs (batch 4: 188 against 264 us, batch 256: 871 against
+  // 3,634 us for the multi-kernel fp32 path; batch 1: 160 against 134 us).
   if (prefill_ok) return kPathPrefill;
   if (stream_ok) return kPathStream;
   if (fused_ok) return kPathFused;
+  if (rows_ok && a.n_tokens * a.n_expert_used >= 16) return kPathRows;
   return kPathGeneral;
 }
 

@@ -334,8 +334,9 @@ def workspace_size(layer: StackedLayer, n_tokens: int, n_expert_used: int) -> in
 
 def moe_path(layer: StackedLayer, x: torch.Tensor, n_expert_used: int) -> str:
     """'fused' (one persistent decode kernel), 'prefill' (grouped MFMA), 'stream'
-    (streaming MFMA decode) or 'general' (multi-kernel GEMV) for this call shape
-    (LATENT_MOE_PATH in the environment selects another supported path)."""
+    (streaming MFMA decode), 'rows' (multi-kernel MFMA on the row layout) or
+    'general' (multi-kernel GEMV) for this call shape (LATENT_MOE_PATH in the
+    environment selects another supported path)."""
     a = layer.args()
     a.x = x.data_ptr()
     a.n_tokens, a.n_expert_used = int(x.shape[0]), int(n_expert_used)
