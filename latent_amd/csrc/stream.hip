@@ -872,7 +872,8 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
         } else {
           rowoff = (static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kRows + row) * kN;
         }
-        v[q] = reinterpret_cast<const float4*>(part + rowoff)[lane];
+        // Only the batch's live partials are read (b1 is wave-uniform).
+        v[q] = bb + q <= b1 ? reinterpret_cast<const float4*>(part + rowoff)[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
 #pragma unroll
       for (int q = 0; q < kRedLoads; ++q) {
