@@ -104,6 +104,34 @@ def test_prefill_4096_with_empty_experts(gpu, dsv3):
     assert not torch.isnan(red).any()
 
 
+def _rows_agree(a, b):
+    """rel-L2 of b against a over the whole batch, and the worst token's."""
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    per_token = np.linalg.norm(a - b, axis=1) / np.maximum(np.linalg.norm(a, axis=1), 1e-30)
+    return ref.rel_l2(a, b), float(per_token.max())
+
+
+def test_prefill_4096_engines_agree_on_every_token(gpu, dsv3):
+    # Every one of the 4096 tokens (the oracle checks a subset above): the
+    # streaming-tile engine on the tile layout against the grouped-GEMM engine
+    # on the row layout of the same layer, two independent implementations.
+    import torch
+
+    from latent_amd import synth as gsynth
+
+    T = 4096
+    ids_t, w_t = gsynth.route(seed=30_000, n_tokens=T, n_expert=E, k=K, rank_beta=1.5)
+    x_t = gsynth.bf16_input(seed=30_003, n_tokens=T, d=D)
+    rows = dsv3.to_layout("rows")
+    assert gpu.moe_path(dsv3, x_t, K) == "prefill" and gpu.moe_path(rows, x_t, K) == "prefill"
+    bulk = gpu.moe_forward(x_t, ids_t, w_t, dsv3).cpu().numpy()
+    gemm = gpu.moe_forward(x_t, ids_t, w_t, rows).cpu().numpy()
+    del rows
+    err, worst = _rows_agree(gemm, bulk)
+    print(f"prefill 4096, tile engine vs GEMM engine: rel-L2 {err:.3e}, worst token {worst:.3e}")
+    assert err <= TOL and worst <= 5 * TOL
+
+
 def test_prefill_per_slot_zeroes_dropped_slots(gpu):
     # Per-slot output on the prefill path: dropped (-1) and out-of-range ids
     # give exact zero rows, routed rows match the oracle.
@@ -174,6 +202,33 @@ def test_hetero_int8_drop(gpu, hetero, T, path, monkeypatch):
           f"per-slot {err_slot:.3e}")
     assert err_red <= TOL and err_slot <= TOL
     assert (slot.cpu().numpy()[ids < 0] == 0).all()
+
+
+def test_hetero_256_paths_agree_on_every_token(gpu, hetero, monkeypatch):
+    # All 256 tokens (the oracle checks a subset above): the row-layout MFMA
+    # phases against the fp32 GEMV phases, and each path's reduced output
+    # against the weighted sum of its per-slot rows.
+    import torch
+
+    from latent_amd import synth as gsynth
+
+    T = 256
+    ids_t, w_t = gsynth.route(seed=40_000 + T, n_tokens=T, n_expert=E, k=K, drop_below=0.05)
+    x_t = gsynth.bf16_input(seed=41_000 + T, n_tokens=T, d=D)
+    w = w_t.cpu().numpy().astype(np.float64)
+    outs = {}
+    for path in ("rows", "general"):
+        monkeypatch.setenv("LATENT_MOE_PATH", path)
+        red = gpu.moe_forward(x_t, ids_t, w_t, hetero, out_mode=0, check_timeout=True)
+        slot = gpu.moe_forward(x_t, ids_t, w_t, hetero, out_mode=1, check_timeout=True)
+        torch.cuda.synchronize()
+        red, slot = red.cpu().numpy(), slot.cpu().numpy().astype(np.float64)
+        err, worst = _rows_agree((slot * w[..., None]).sum(1), red)
+        assert err <= 1e-4 and worst <= 1e-3, (path, err, worst)  # fp16 intermediates: ~4e-5 on the MFMA path
+        outs[path] = red
+    err, worst = _rows_agree(outs["general"], outs["rows"])
+    print(f"hetero T=256, row-layout MFMA vs fp32 GEMV: rel-L2 {err:.3e}, worst token {worst:.3e}")
+    assert err <= TOL and worst <= 5 * TOL
 
 
 # --------------------------------------------------------------------------------
