@@ -222,11 +222,13 @@ int latent_moe_check(void* workspace, size_t workspace_bytes, latent_stream_t st
  *       aligned codes) it runs grouped GEMMs;
  *   3 = streaming fp16-MFMA decode: the factors are in the tile layout, 1 to
  *       4096 routed pairs, 16-byte aligned x;
+ *   4 = multi-kernel fp16-MFMA path on the row layout, taken here when a
+ *       factor has INT8 groups: at least 16 routed pairs, max_rank <= 512,
+ *       16-byte aligned x (per-expert ranks allowed); factors decoded into
+ *       LDS chunk by chunk;
  *   1 = single persistent fp32 decode kernel: row layout, 32 to 512 routed
  *       pairs, 2 * max_rank <= 1024, 16-byte aligned x (INT8 groups allowed);
- *   4 = multi-kernel fp16-MFMA path on the row layout: at least 16 routed
- *       pairs, max_rank <= 512, 16-byte aligned x (per-expert ranks and INT8
- *       groups allowed); factors decoded into LDS chunk by chunk;
+ *   4 = as above, for the pure-NF4 calls path 1 does not take;
  *   0 = multi-kernel fp32 GEMV path: any call on the row layout.
  * A call in the tile layout that neither path 2 nor 3 takes is
  * LATENT_E_UNSUPPORTED.

@@ -973,20 +973,27 @@ int choose_path(const latent_moe_args& a, fused::Plan& pl) {
     if (!std::strcmp(env, "prefill") && prefill_ok) return kPathPrefill;
     if (!std::strcmp(env, "general")) return kPathGeneral;
   }
-  // Measured on MI355X at the DeepSeek-V3 shape (d 7168, ff 2048, rank 256,
-  // 256 experts, top-8): below the prefill threshold the streaming MFMA path
-  // is the fastest wherever it applies (batch 1: 49 vs 52 us for the
+  // Measured on MI355X at the DeepSeek-V3 shape (d 7168, ff 2048, 256
+  // experts, top-8): below the prefill threshold the streaming MFMA path is
+  // the fastest wherever it applies (batch 1: 49 vs 52 us for the
   // multi-kernel path; batch 8: 100 vs 144 us and batch 64: 270 vs 370 us
-  // for the persistent kernel).  On the row layout (ranks 64..512, 10 %
-  // INT8 groups): the persistent fp32 kernel, bit-reproducible, where it
-  // applies (batch 16: 387 us, level with the row-layout MFMA phases; batch
-  // 64: 817 against 735 us); elsewhere the row-layout MFMA phases from 16
-  // routed pairs (batch 4: 188 against 264 us, batch 256: 871 against
-  // 3,634 us for the multi-kernel fp32 path; batch 1: 160 against 134 us).
+  // for the persistent kernel).  On the row layout:
+  //   * with INT8 groups (ranks 64..512, 10 % INT8 groups): the row-layout
+  //     MFMA phases from 16 routed pairs (batch 16 / 32 / 64 / 256: 382 /
+  //     567 / 704 / 840 us against 400 / 577 / 830 us for the persistent
+  //     fp32 kernel and 632 / 977 / 1,549 / 3,633 us for the multi-kernel
+  //     path; batch 1: 160 against 134 us, so below 16 pairs the latter);
+  //   * pure NF4 (rank 256): the persistent fp32 kernel where it applies
+  //     (batch 16 / 32 / 64: 189 / 268 / 381 us against 246 / 362 / 495 us
+  //     for the row-layout MFMA phases; batch 8 151 against 154 us).
+  const bool int8 = a.gate_a.int8_bitmap || a.gate_b.int8_bitmap || a.up_a.int8_bitmap || a.up_b.int8_bitmap ||
+                    a.down_a.int8_bitmap || a.down_b.int8_bitmap;
+  const bool rows_pairs = rows_ok && a.n_tokens * a.n_expert_used >= 16;
   if (prefill_ok) return kPathPrefill;
   if (stream_ok) return kPathStream;
+  if (int8 && rows_pairs) return kPathRows;
   if (fused_ok) return kPathFused;
-  if (rows_ok && a.n_tokens * a.n_expert_used >= 16) return kPathRows;
+  if (rows_pairs) return kPathRows;
   return kPathGeneral;
 }
 

@@ -174,7 +174,7 @@ def hetero(gpu):
     return gsynth.make_layer(seed=11, n_expert=E, d=D, ff=FF, max_rank=512, ranks=ranks, int8_fraction=0.1)
 
 
-@pytest.mark.parametrize("T,path", [(16, "default"), (16, "general"), (256, "default"), (16, "rows"), (256, "rows")])
+@pytest.mark.parametrize("T,path", [(16, "default"), (16, "fused"), (16, "general"), (256, "default"), (256, "rows")])
 def test_hetero_int8_drop(gpu, hetero, T, path, monkeypatch):
     import torch
 
@@ -320,15 +320,20 @@ def _fake_int8_args(L, d, E=512, R=256, ff=512, T=8, k=8):
     return a
 
 
-def test_int8_side_buffer_beyond_32_bit_offsets_leaves_the_persistent_kernel(gpu):
-    """The persistent kernel reads INT8 groups with 32-bit byte offsets: a
-    factor whose side buffer could reach 2^31 bytes (every group INT8) goes to
-    the multi-kernel path, one just below stays on the persistent kernel."""
+def test_int8_side_buffer_beyond_32_bit_offsets_leaves_the_persistent_kernel(gpu, monkeypatch):
+    """The persistent kernel and the row-layout MFMA phases read INT8 groups
+    with 32-bit byte offsets: a factor whose side buffer could reach 2^31
+    bytes (every group INT8) goes to the multi-kernel fp32 path, one just
+    below stays on them (the row-layout MFMA phases by default, the
+    persistent kernel when it is asked for)."""
     import ctypes
 
     from latent_amd import _lib as L
 
     below = _fake_int8_args(L, d=8192)  # 512 x 8192 x 256 = 2^30 bytes of INT8 at most
     beyond = _fake_int8_args(L, d=16384)  # 2^31 bytes
+    assert L.lib.latent_moe_path(ctypes.byref(below)) == 4
+    assert L.lib.latent_moe_path(ctypes.byref(beyond)) == 0
+    monkeypatch.setenv("LATENT_MOE_PATH", "fused")
     assert L.lib.latent_moe_path(ctypes.byref(below)) == 1
     assert L.lib.latent_moe_path(ctypes.byref(beyond)) == 0
