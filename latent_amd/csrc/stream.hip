@@ -834,22 +834,37 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   const int total = U * per_unit;
   const int chunk = (total + p.G - 1) / p.G;
   const int maxj = (chunk + per_key - 1) / per_key + 1;
-  const float* part = kPhase == kPhaseA ? p.partA : p.partC;
-  const int nrows = U * keys_per_unit * kRows;
+  float* part = kPhase == kPhaseA ? p.partA : p.partC;
+  const int nkey = U * keys_per_unit;
+  const int J = p.G >> 3;
+  // kByKey, phase C: the rest keys only (fewer than J per XCD).  A whole
+  // key's workgroup left its sum in the key's slot; a rest key's pieces are
+  // summed into that slot here, and phase D finishes both as it stages them.
+  // Phase A: every key, finished here (phase B stages two latent blocks per
+  // unit, and finishing them there measured slower).
+  constexpr bool kRestOnly = kByKey && kPhase == kPhaseC;
+  const int nrows = kRestOnly ? 8 * J * kRows : nkey * kRows;
   for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nrows;
        w += gridDim.x * (kT / kWave)) {
-    const int key = w / kRows, row = w % kRows;
+    const int row = w % kRows;
+    int key = w / kRows;
+    Deal dl{};
+    int xcd = 0;
+    if constexpr (kRestOnly) {
+      xcd = w / (J * kRows);
+      dl = deal_for(nkey, per_key, p.G, xcd);
+      key = dl.rest0 + (w / kRows) % J;
+      if (key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) continue;
+    } else if constexpr (kByKey) {
+      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
+      dl = deal_for(nkey, per_key, p.G, xcd);
+    }
     const int u = key / keys_per_unit, f = key - u * keys_per_unit;
     const int4 info = p.unit_info[u];
     if (row >= info.z) continue;
     int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
     int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
-    Deal dl{};
-    int xcd = 0;
     if constexpr (kByKey) {
-      const int nkey = U * keys_per_unit;
-      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
-      dl = deal_for(nkey, per_key, p.G, xcd);
       // A whole key: b = -1 names its slot; a rest key: workgroups b0..b1 of the XCD.
       const int rk = key - dl.rest0;
       b0 = rk < 0 ? -1 : rk * per_key / dl.c;
@@ -883,7 +898,9 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
       }
     }
     const int64_t pair = info.y + row;
-    if (kPhase == kPhaseA)
+    if constexpr (kRestOnly)
+      reinterpret_cast<float4*>(part + (static_cast<int64_t>(key) * kRows + row) * kN)[lane] = s;
+    else if (kPhase == kPhaseA)
       finish_row(s, p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
     else
       finish_row(s, p.dlat + pair * kK, p.dexp + pair, lane);
@@ -1806,31 +1823,73 @@ __device__ __forceinline__ void bulk_unit_tables(const Params& p, BulkSmem<kPhas
 // Phases B and D: the unit's activation block(s) into LDS (blocking), with
 // their row exponents and, for D's per-slot output, each row's output row and
 // weight.  Runs between barriers.
+//   B: the gate and up latents, finished by A's reduce launch (fp16 rows and
+//      exponents, by grouped pair).
+//   D: the fp32 sum of C's key u, left in the key's partial slot by its
+//      workgroup (or, for a rest key, by the reduce launch), finished here
+//      as finish_row does: fp16 row * 2^e, e from the row's maximum over its
+//      256 columns (a row's 32 chunks are 32 lanes of one wave); four rounds
+//      of rows at a time, two 16-byte loads per chunk of 8 values.
 template <int kPhase>
-__device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>& sm, const TileRef& tr, int tid,
-                                              u32x4 (&st)[kBulkRounds]) {
+__device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>& sm, const TileRef& tr, int u,
+                                              int tid) {
   const int r0 = tid / kActChunks, chunk = tid % kActChunks;
-  constexpr int nblk = BulkShape<kPhase>::kActBlocks;
+  if constexpr (kPhase == kPhaseB) {
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(p.lat, 2u * p.P * kK * 2);
+    u32x4 st[2][kBulkRounds];
 #pragma unroll
-  for (int blk = 0; blk < nblk; ++blk) {
-    const _Float16* src = kPhase == kPhaseB ? p.lat + static_cast<int64_t>(blk) * p.P * kK : p.dlat;
-    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(src, static_cast<uint32_t>(p.P) * kK * 2);
+    for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-    for (int h = 0; h < kBulkRounds; ++h) {
-      const int r = r0 + 8 * h;
-      const uint32_t off = r < tr.m ? static_cast<uint32_t>(tr.start + r) * kK * 2 + chunk * 16 : kNoRow;
-      st[h] = ld128(rl, off, 0);
+      for (int h = 0; h < kBulkRounds; ++h) {
+        const int r = r0 + 8 * h;
+        const uint32_t off =
+            r < tr.m ? (static_cast<uint32_t>(blk) * p.P + tr.start + r) * kK * 2 + chunk * 16 : kNoRow;
+        st[blk][h] = ld128(rl, off, 0);
+      }
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+      for (int h = 0; h < kBulkRounds; ++h) sm.act[blk][bulk_slot(r0 + 8 * h, chunk)] = st[blk][h];
+    if (tid < 2 * kBulkM) {
+      const int blk = tid / kBulkM, r = tid % kBulkM;
+      sm.rexp[blk][r] = p.lexp[blk * p.P + tr.start + min(r, tr.m - 1)];
     }
+  } else {
+    constexpr int kBatch = 4;
+    const float* src = p.partC + static_cast<int64_t>(u) * kBulkM * kN;
+    const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(src, kBulkM * kN * 4);
 #pragma unroll
-    for (int h = 0; h < kBulkRounds; ++h) sm.act[blk][bulk_slot(r0 + 8 * h, chunk)] = st[h];
-  }
-  if (tid < nblk * kBulkM) {
-    const int blk = tid / kBulkM, r = tid % kBulkM;
-    const int pair = tr.start + min(r, tr.m - 1);
-    sm.rexp[blk][r] = kPhase == kPhaseB ? p.lexp[blk * p.P + pair] : p.dexp[pair];
-    if constexpr (kPhase == kPhaseD) {
-      sm.rowoff[0][r] = static_cast<uint32_t>(p.pair_tok[pair] * p.K + p.pair_slot[pair]);
-      sm.pw[r] = p.pair_w[pair];
+    for (int h0 = 0; h0 < kBulkRounds; h0 += kBatch) {
+      u32x4 v[kBatch][2];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int r = r0 + 8 * (h0 + q);
+        const uint32_t off = r < tr.m ? static_cast<uint32_t>(r * kN + chunk * 8) * 4 : kNoRow;
+        v[q][0] = ld128(rl, off, 0);
+        v[q][1] = ld128(rl, off + 16, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int r = r0 + 8 * (h0 + q);
+        float x[8], mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t bits = v[q][i >> 2][i & 3];  // through a scalar: a bit_cast of a vector element reads element 0
+          x[i] = __uint_as_float(bits);
+          mx = fmaxf(mx, fabsf(x[i]));
+        }
+        const int ex = pow2_row_exponent(op_over(mx, 1, 32, OpMax{}));
+        half8 hv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(x[i], ex));
+        sm.act[0][bulk_slot(r, chunk)] = __builtin_bit_cast(u32x4, hv);
+        if (chunk == 0) sm.rexp[0][r] = ex;
+      }
+    }
+    if (tid < kBulkM) {
+      const int pair = tr.start + min(tid, tr.m - 1);
+      sm.rowoff[0][tid] = static_cast<uint32_t>(p.pair_tok[pair] * p.K + p.pair_slot[pair]);
+      sm.pw[tid] = p.pair_w[pair];
     }
   }
 }
@@ -1981,7 +2040,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
     lds_barrier();
     bulk_issue_act<kPhase>(p, sm, ref[0], 0, tid, true, st, tex);
   } else {
-    bulk_unit_act<kPhase>(p, sm, ref[0], tid, st);
+    bulk_unit_act<kPhase>(p, sm, ref[0], vt(0) / per_unit, tid);
   }
 #pragma unroll
   for (int r = 0; r + 1 < kBulkRing; ++r) issue_codes<kPhase>(p, ref[r], tid, lane, wave, r < ntile, sc[r], cb[r]);
@@ -2122,7 +2181,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
       if (i + 2 < ntile && new_seg(i + 2))
         bulk_unit_tables<kPhase>(p, sm, tile_ref<kPhase>(p, vt(i + 2)), kbuf(i + 2), tid);
     } else {
-      if (i + 1 < ntile && new_seg(i + 1)) bulk_unit_act<kPhase>(p, sm, ref[c1], tid, st);
+      if (i + 1 < ntile && new_seg(i + 1)) bulk_unit_act<kPhase>(p, sm, ref[c1], vt(i + 1) / per_unit, tid);
     }
     sm.scales[tid] = sc[c1];
   };
@@ -2401,7 +2460,9 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM, false, true>), dim3(rblocks(U * 2 * kBulkM)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseB>, dim3(p.G), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(p.G), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM, false, true>), dim3(rblocks(U * kBulkM)), dim3(kT), 0, s, p);
+  // C's reduce sums only the rest keys' pieces (a whole key's sum is in its
+  // slot); D finishes the rows as it stages them.
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM, false, true>), dim3(rblocks(p.G * kBulkM)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseD>, dim3(p.G), dim3(kT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
