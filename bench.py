@@ -20,7 +20,7 @@ way the reference's llama.cpp backend launches decode).  The same K steps
 issued eagerly are timed too and reported as `eager_ms_per_step`
 (`--timing eager` makes them the figure).
 
-The headline `value` is tokens/s at batch 64; batches 1, 8 and 32, the
+The headline `value` is tokens/s at batch 64; batches 1, 2, 4, 8, 16 and 32, the
 4096-token prefill, the heterogeneous-rank layer (ranks 64..512, 10% INT8
 groups, drop below 0.05, batches 16 and 256) and the 58-layer graph-captured
 stack are reported under "sweep", "prefill", "hetero" and "stack".  HBM GB/s
@@ -60,7 +60,7 @@ def parse():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--batch", type=int, default=64, help="headline decode batch")
-    p.add_argument("--sweep", type=str, default="1,8,32", help="other decode batches ('' to skip)")
+    p.add_argument("--sweep", type=str, default="1,2,4,8,16,32", help="other decode batches ('' to skip)")
     p.add_argument("--prefill", type=int, default=4096, help="prefill tokens (0 to skip)")
     p.add_argument("--prefill-steps", type=int, default=5)
     p.add_argument("--layers", type=int, default=4, help="distinct layers rotated in the timed loop")
