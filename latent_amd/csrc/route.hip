@@ -21,6 +21,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace latent {
 namespace route {
@@ -132,15 +133,44 @@ __global__ void __launch_bounds__(kThreads) logits_kernel(Params p) {
 }
 
 // Wave arg-max of (v, idx) pairs: larger v wins, equal v -> smaller idx.
+// Each pair is one 64-bit key whose unsigned order is that order (the
+// float's bits made monotonic above, the complemented index below; -0 is
+// +0 first, so equal values tie), reduced over the wave with DPP row
+// permutations and the permlane swaps (no LDS round trips).
 __device__ __forceinline__ void wave_argmax(float& v, int& idx) {
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(v, off, kWave);
-    const int oi = __shfl_xor(idx, off, kWave);
-    if (ov > v || (ov == v && oi < idx)) {
-      v = ov;
-      idx = oi;
-    }
+  const uint32_t u = __float_as_uint(v + 0.0f);
+  uint32_t hi = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  uint32_t lo = ~static_cast<uint32_t>(idx);
+  auto take = [&](uint32_t ohi, uint32_t olo) __attribute__((always_inline)) {
+    const bool gt = ohi > hi || (ohi == hi && olo > lo);
+    hi = gt ? ohi : hi;
+    lo = gt ? olo : lo;
+  };
+  auto dpp = [&](auto ctrl) __attribute__((always_inline)) {
+    constexpr int c = decltype(ctrl)::value;
+    take(static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(hi), c, 0xF, 0xF, false)),
+         static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(lo), c, 0xF, 0xF, false)));
+  };
+  dpp(std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]: lane ^ 1
+  dpp(std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]: lane ^ 2
+  dpp(std::integral_constant<int, 0x124>{});  // row_ror:4
+  dpp(std::integral_constant<int, 0x128>{});  // row_ror:8
+  {  // rows r and r ^ 1
+    const auto h = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const uint32_t h0 = h[0], h1 = h[1], l0 = l[0], l1 = l[1];
+    hi = h0; lo = l0;
+    take(h1, l1);
   }
+  {  // lane halves
+    const auto h = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const auto l = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const uint32_t h0 = h[0], h1 = h[1], l0 = l[0], l1 = l[1];
+    hi = h0; lo = l0;
+    take(h1, l1);
+  }
+  v = __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+  idx = static_cast<int>(~lo);
 }
 
 // One token per 256-thread workgroup.  Thread e sums the slices of expert e

@@ -63,15 +63,19 @@ def test_route_from_logits_drop_rules(gpu, drop, param):
 
 
 def test_route_ties_go_to_lower_expert(gpu):
-    lg = np.zeros((3, 200), np.float32)
+    lg = np.zeros((4, 200), np.float32)
     lg[0, [5, 150, 7]] = 1.0          # equal maxima: 5, 7, 150 then zeros from id 0
     lg[1, :] = -np.inf                 # all -inf: lowest ids first
     lg[2, 199] = np.nan                # NaN never wins
+    lg[3, :] = -1.0
+    lg[3, [64, 3]] = -0.0              # -0 and +0 are equal: lower id first
+    lg[3, [130, 9]] = 0.0
     ids, w = gpu.route(4, logits=_cuda(lg))
     got = ids.cpu().numpy()
     assert got[0].tolist() == [5, 7, 150, 0]
     assert got[1].tolist() == [0, 1, 2, 3]
     assert 199 not in got[2].tolist()
+    assert got[3].tolist() == [3, 9, 64, 130]
 
 
 def test_route_rejects_bad_arguments(gpu):
