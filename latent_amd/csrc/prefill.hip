@@ -694,39 +694,69 @@ __global__ void __launch_bounds__(kThreads) slots_kernel(Grouping g, int* pos_of
 
 // out[t] = sum over slots (in slot order) of w * y[pos_of[t][slot]] * 2^-exp,
 // y rows in fp16 with one exponent per 2^blk_log2 columns (row stride
-// yexp_ld).  One workgroup per token;
-// the slots' rows are loaded together (kCombineSlots at a time) before the
-// sum, so a thread keeps that many 16-byte loads in flight.
+// yexp_ld).  One workgroup per token.  The token's grouped positions and
+// weights are read once into LDS (the output stores could alias them, so
+// they would otherwise be reloaded for every column chunk); then each thread
+// takes 8-column chunks tid, tid + 256, ... two at a time, with the y rows and
+// exponents of both chunks and kCombineSlots slots loaded before any is
+// added (32 loads in flight per thread).  k <= kCombineMaxK.
 constexpr int kCombineSlots = 8;
+constexpr int kCombineMaxK = 64;
+constexpr int kCombineChunks = 2;
 __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, const int* yexp, int yexp_ld, int blk_log2,
                                                            const int* pos_of, const float* pair_w, int k, int d, int wbd,
                                                            float* out) {
-  const int t = blockIdx.x;
-  for (int c = threadIdx.x * 8; c < d; c += kThreads * 8) {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  __shared__ int spos[kCombineMaxK];
+  __shared__ float sw[kCombineMaxK];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  if (tid < k) {
+    // A dropped slot (-1) adds an exact zero; its (unwritten) row is not read.
+    const int pos = pos_of[t * k + tid];
+    spos[tid] = pos;
+    sw[tid] = pos >= 0 ? (wbd ? 1.f : pair_w[pos]) : 0.f;
+  }
+  __syncthreads();
+  const int nc = d / 8;
+  for (int c0 = tid; c0 < nc; c0 += kThreads * kCombineChunks) {
+    float acc[kCombineChunks][8] = {};
     for (int s0 = 0; s0 < k; s0 += kCombineSlots) {
-      half8 h[kCombineSlots];
-      float w[kCombineSlots];
+      half8 h[kCombineChunks][kCombineSlots];
+      int ex[kCombineChunks][kCombineSlots];
 #pragma unroll
       for (int i = 0; i < kCombineSlots; ++i) {
         const int sl = s0 + i;
-        const int pos = sl < k ? pos_of[t * k + sl] : -1;
-        // A dropped slot adds an exact zero; its (unwritten) row is not read.
-        h[i] = half8{};
-        w[i] = 0.f;
-        if (pos >= 0) {
-          h[i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
-          w[i] = __builtin_ldexpf(wbd ? 1.f : pair_w[pos], -yexp[static_cast<int64_t>(pos) * yexp_ld + (c >> blk_log2)]);
+        const int pos = sl < k ? spos[sl] : -1;
+#pragma unroll
+        for (int r = 0; r < kCombineChunks; ++r) {
+          const int c = (c0 + r * kThreads) * 8;
+          h[r][i] = half8{};
+          ex[r][i] = 0;
+          if (pos >= 0 && c < d) {
+            h[r][i] = *reinterpret_cast<const half8*>(y + static_cast<int64_t>(pos) * d + c);
+            ex[r][i] = yexp[static_cast<int64_t>(pos) * yexp_ld + (c >> blk_log2)];
+          }
         }
       }
 #pragma unroll
-      for (int i = 0; i < kCombineSlots; ++i)
+      for (int i = 0; i < kCombineSlots; ++i) {
+        const float wi = s0 + i < k ? sw[s0 + i] : 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = fmaf(w[i], static_cast<float>(h[i][j]), acc[j]);
+        for (int r = 0; r < kCombineChunks; ++r) {
+          const float w = __builtin_ldexpf(wi, -ex[r][i]);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(w, static_cast<float>(h[r][i][j]), acc[r][j]);
+        }
+      }
     }
-    float4* o = reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * d + c);
-    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+#pragma unroll
+    for (int r = 0; r < kCombineChunks; ++r) {
+      const int c = (c0 + r * kThreads) * 8;
+      if (c < d) {
+        float4* o = reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * d + c);
+        o[0] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        o[1] = make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
+      }
+    }
   }
 }
 
@@ -800,6 +830,7 @@ bool supported(const latent_moe_args& a) {
   // any number of pairs per expert (the row-layout paths cannot read tiles).
   const bool beyond_decode = a.layout == LATENT_LAYOUT_TILES && P > stream::kMaxPairs;
   if (P < static_cast<int64_t>(kMinPairsPerExpert) * active && !beyond_decode) return false;
+  if (a.n_expert_used > kCombineMaxK) return false;
   const latent_factor* fs[6] = {&a.gate_a, &a.gate_b, &a.up_a, &a.up_b, &a.down_a, &a.down_b};
   for (const latent_factor* f : fs)
     if (f->int8_bitmap != nullptr) return false;  // per-group INT8 layers take the general path

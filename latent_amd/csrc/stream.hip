@@ -843,6 +843,51 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   // Phase A: every key, finished here (phase B stages two latent blocks per
   // unit, and finishing them there measured slower).
   constexpr bool kRestOnly = kByKey && kPhase == kPhaseC;
+  if constexpr (kByKey && !kRestOnly) {
+    // Phase A by key: a wave takes kRowsPerWave rows of one key, so the key's
+    // dealing and unit are looked up once and those rows' partials are in
+    // flight together (one row per wave left each wave with about ten rows in
+    // turn, two dependent round trips each).  Pieces in workgroup order.
+    constexpr int kRowsPerWave = 8;
+    constexpr int kGroups = kRows / kRowsPerWave;
+    static_assert(kRows % kRowsPerWave == 0, "whole row groups");
+    for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nkey * kGroups;
+         w += gridDim.x * (kT / kWave)) {
+      const int key = uniform(w / kGroups), row0 = (w - key * kGroups) * kRowsPerWave;
+      int xcd = 0;
+      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
+      const Deal dl = deal_for(nkey, per_key, p.G, xcd);
+      const int u = key / keys_per_unit, f = key - u * keys_per_unit;
+      const int4 info = p.unit_info[u];
+      if (row0 >= info.z) continue;
+      const int rk = key - dl.rest0;
+      const int b0 = rk < 0 ? -1 : rk * per_key / dl.c, b1 = rk < 0 ? -1 : ((rk + 1) * per_key - 1) / dl.c;
+      float4 s[kRowsPerWave];
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r) s[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int b = b0; b <= b1; ++b) {
+        const int64_t slot =
+            b < 0 ? key : 2 * U + (xcd + 8 * b) * kRemPieces + key - (dl.rest0 * per_key + b * dl.c) / per_key;
+        float4 v[kRowsPerWave];
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r)
+          v[r] = row0 + r < info.z ? reinterpret_cast<const float4*>(part + (slot * kRows + row0 + r) * kN)[lane]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+          s[r].x += v[r].x; s[r].y += v[r].y; s[r].z += v[r].z; s[r].w += v[r].w;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r) {
+        if (row0 + r < info.z) {
+          const int64_t pair = info.y + row0 + r;
+          finish_row(s[r], p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
+        }
+      }
+    }
+    return;
+  }
   const int nrows = kRestOnly ? 8 * J * kRows : nkey * kRows;
   for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nrows;
        w += gridDim.x * (kT / kWave)) {
@@ -2457,7 +2502,7 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   // Every workgroup is launched (those the dealing leaves without a key
   // return at once), so each XCD's block of keys is covered.
   hipLaunchKernelGGL(bulk_kernel<kPhaseA>, dim3(p.G), dim3(kT), 0, s, p);
-  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM, false, true>), dim3(rblocks(U * 2 * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseA, kBulkM, false, true>), dim3(rblocks(U * 2 * kBulkM / 8)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseB>, dim3(p.G), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(p.G), dim3(kT), 0, s, p);
   // C's reduce sums only the rest keys' pieces (a whole key's sum is in its
