@@ -1777,6 +1777,7 @@ struct alignas(16) BulkSmem {
   uint32_t rowoff[2][kBulkM];  // A: byte offset of each row's x row (by unit parity); D: output row
   int texp[kPhase == kPhaseC ? kK / kBulkHBlock : 1][kBulkM];  // C: the staged tile's h block exponents of each row
   float pw[kBulkM];        // D, per-slot output: router weight of each row
+  int il1[kPhase == kPhaseD ? kBulkM : 1];  // D: floor(log2) of each row's L1 norm (y scale), clamped
 };
 
 // MFMA steps of a tile over the unit's first kRb 16-row blocks: per 32-row
@@ -1835,6 +1836,34 @@ __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32
         acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1, bf[j], acc[rb][j], 0, 0, 0);
     }
   }
+}
+
+// Phase D's y exponents come from a bound instead of each row's maximum over
+// the wave's 64 columns (a 16-lane reduction per row and tile): a staged row's
+// fp16 values a_k times the decoded tile b_kj (|b_kj| <= the largest scale of
+// the wave's two groups, |level| <= 1) give |y_j| <= 2^-e sum_k |a_k| * maxsc
+// < 2^(il1 + 1) * 2^(ilog(maxsc) + 1), so y * 2^(13 - il1 - ilog(maxsc)) stays
+// below 2^15 and fp16 keeps its full relative precision down to 2^-28 of the
+// bound.  il1 = floor(log2(sum |a_k| * 2^-e)), clamped so that the exponent
+// stays within [-122, 120] (a clamp from below only loosens the bound).
+__device__ __forceinline__ int bulk_y_ilog(float l1, int e) {
+  const int il = static_cast<int>((__float_as_uint(l1) >> 23) & 0xFFu) - 127 - e;
+  return min(120, max(-83, il));
+}
+// floor(log2) of the largest |scale| of wave w's two scale groups of a tile's
+// scale block in LDS (group G at dwords 128 G..): fp16 bit patterns of
+// non-negative values order as integers.
+template <class Smem>
+__device__ __forceinline__ int bulk_scale_ilog(const Smem& sm, int wave, int lane) {
+  const u32x4 q = sm.scales[64 * wave + lane];
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = q[i] & 0x7FFF7FFFu;
+    m = max(m, max(v & 0xFFFFu, v >> 16));
+  }
+  const float mx = op_over(static_cast<float>(m), 1, kWave, OpMax{});
+  return static_cast<int>(static_cast<uint32_t>(mx) >> 10) - 15;
 }
 
 // Per-unit tables of the bulk phases (all threads; a barrier must follow).
@@ -1902,6 +1931,10 @@ __device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>&
   } else {
     constexpr int kBatch = 4;
     const float* src = p.partC + static_cast<int64_t>(u) * kBulkM * kN;
+    // The rows' exponent and L1 slots as one opaque lane base plus immediates
+    // (per-row addresses hoisted out of the tile loop spilled).
+    uint32_t rowx = lds_addr(sm.rexp[0][0]) + r0 * 4, rowl = lds_addr(sm.il1[0]) + r0 * 4;
+    asm volatile("" : "+v"(rowx), "+v"(rowl));
     const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(src, kBulkM * kN * 4);
 #pragma unroll
     for (int h0 = 0; h0 < kBulkRounds; h0 += kBatch) {
@@ -1925,10 +1958,18 @@ __device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>&
         }
         const int ex = pow2_row_exponent(op_over(mx, 1, 32, OpMax{}));
         half8 hv;
+        float l1 = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) hv[i] = static_cast<_Float16>(ldexpf(x[i], ex));
+        for (int i = 0; i < 8; ++i) {
+          hv[i] = static_cast<_Float16>(ldexpf(x[i], ex));
+          l1 += fabsf(static_cast<float>(hv[i]));
+        }
+        l1 = op_over(l1, 1, 32, OpAdd{});
         sm.act[0][bulk_slot(r, chunk)] = __builtin_bit_cast(u32x4, hv);
-        if (chunk == 0) sm.rexp[0][r] = ex;
+        if (chunk == 0) {
+          lds_st<int>(rowx + 32 * (h0 + q), ex);
+          lds_st<int>(rowl + 32 * (h0 + q), bulk_y_ilog(l1, ex));
+        }
       }
     }
     if (tid < kBulkM) {
@@ -2182,32 +2223,27 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
       // exponent per row and 64-column block (the wave's own).
       const bool reduced = p.out_mode == LATENT_OUT_REDUCED;
       const int ny = p.d / kBulkYBlock;
+      const int yex0 = reduced ? 13 - bulk_scale_ilog(sm, wave, lane) : 0;
 #pragma unroll
       for (int rb = 0; rb < kBulkBlocks; ++rb) {
         if (rb < nrb) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = rb * 16 + kq * 4 + v;
-            const float s = ldexpf(1.0f, -rx0[rb * 16 + v]);
             const int64_t prow = tr.start + row;
             const int col = tr.r * kN + wave * 64 + n * 4;
             if (reduced) {
-              float y[4], mx = 0.f;
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                y[j] = acc[rb][j][v] * s;
-                mx = fmaxf(mx, fabsf(y[j]));
-              }
-              const int ex = pow2_row_exponent(op_over(mx, 1, 16, OpMax{}));
+              const int ex = yex0 - (&sm.il1[kq * 4])[rb * 16 + v];
+              const int ea = ex - rx0[rb * 16 + v];  // y = acc * 2^-rexp
               if (row < tr.m) {
                 half4v hv;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) hv[j] = static_cast<_Float16>(ldexpf(y[j], ex));
+                for (int j = 0; j < 4; ++j) hv[j] = static_cast<_Float16>(ldexpf(acc[rb][j][v], ea));
                 *reinterpret_cast<half4v*>(p.yh + prow * p.d + col) = hv;
                 if (n == 0) p.yexp[prow * ny + tr.r * 4 + wave] = ex;
               }
             } else if (row < tr.m) {
-              const float w = s * (p.wbd ? (&sm.pw[kq * 4])[rb * 16 + v] : 1.0f);
+              const float w = ldexpf(p.wbd ? (&sm.pw[kq * 4])[rb * 16 + v] : 1.0f, -rx0[rb * 16 + v]);
               *reinterpret_cast<float4*>(p.out + static_cast<int64_t>((&sm.rowoff[0][kq * 4])[rb * 16 + v]) * p.d + col) =
                   make_float4(acc[rb][0][v] * w, acc[rb][1][v] * w, acc[rb][2][v] * w, acc[rb][3][v] * w);
             }
