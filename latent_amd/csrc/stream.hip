@@ -1777,7 +1777,9 @@ struct alignas(16) BulkSmem {
   uint32_t rowoff[2][kBulkM];  // A: byte offset of each row's x row (by unit parity); D: output row
   int texp[kPhase == kPhaseC ? kK / kBulkHBlock : 1][kBulkM];  // C: the staged tile's h block exponents of each row
   float pw[kBulkM];        // D, per-slot output: router weight of each row
-  int il1[kPhase == kPhaseD ? kBulkM : 1];  // D: floor(log2) of each row's L1 norm (y scale), clamped
+  // D: floor(log2) of each row's L1 norm (y scale), clamped; B: the sum of
+  // those of the row's gate and up latents (fp16 scale)
+  int il1[kPhase == kPhaseD || kPhase == kPhaseB ? kBulkM : 1];
 };
 
 // MFMA steps of a tile over the unit's first kRb 16-row blocks: per 32-row
@@ -1850,20 +1852,24 @@ __device__ __forceinline__ int bulk_y_ilog(float l1, int e) {
   const int il = static_cast<int>((__float_as_uint(l1) >> 23) & 0xFFu) - 127 - e;
   return min(120, max(-83, il));
 }
-// floor(log2) of the largest |scale| of wave w's two scale groups of a tile's
-// scale block in LDS (group G at dwords 128 G..): fp16 bit patterns of
-// non-negative values order as integers.
-template <class Smem>
+// floor(log2) of the largest |scale| of the scale groups wave w reads in a
+// tile's scale block in LDS (group G at dwords 128 G..; fp16 bit patterns of
+// non-negative values order as integers).  D: groups 2w and 2w + 1 (its 64
+// columns).  B: the sum over gate group w and up group 4 + w (its 32 h
+// columns' g and u).
+template <bool kB, class Smem>
 __device__ __forceinline__ int bulk_scale_ilog(const Smem& sm, int wave, int lane) {
-  const u32x4 q = sm.scales[64 * wave + lane];
+  const u32x4 q = sm.scales[kB ? 32 * wave + (lane & 31) + (lane >> 5) * 128 : 64 * wave + lane];
   uint32_t m = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t v = q[i] & 0x7FFF7FFFu;
     m = max(m, max(v & 0xFFFFu, v >> 16));
   }
-  const float mx = op_over(static_cast<float>(m), 1, kWave, OpMax{});
-  return static_cast<int>(static_cast<uint32_t>(mx) >> 10) - 15;
+  const float mx = op_over(static_cast<float>(m), 1, kB ? 32 : kWave, OpMax{});
+  const int il = static_cast<int>(static_cast<uint32_t>(mx) >> 10) - 15;
+  if constexpr (kB) return __builtin_amdgcn_readlane(il, 0) + __builtin_amdgcn_readlane(il, 32);
+  return il;
 }
 
 // Per-unit tables of the bulk phases (all threads; a barrier must follow).
@@ -1924,6 +1930,28 @@ __device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>&
     for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
       for (int h = 0; h < kBulkRounds; ++h) sm.act[blk][bulk_slot(r0 + 8 * h, chunk)] = st[blk][h];
+    // floor(log2) of each row's L1 norm, gate plus up (fp16 scale; the row
+    // exponents are applied where they are used).  Row slots through one
+    // opaque lane base plus immediates.
+    uint32_t rowl = lds_addr(sm.il1[0]) + r0 * 4;
+    asm volatile("" : "+v"(rowl));
+#pragma unroll
+    for (int h = 0; h < kBulkRounds; ++h) {
+      int il = 0;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        float l1 = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = st[blk][h][q];  // through a scalar: a bit_cast of a vector element reads element 0
+          const half2v hv = __builtin_bit_cast(half2v, w);
+          l1 += fabsf(static_cast<float>(hv[0])) + fabsf(static_cast<float>(hv[1]));
+        }
+        l1 = op_over(l1, 1, 32, OpAdd{});
+        il += static_cast<int>((__float_as_uint(l1) >> 23) & 0xFFu) - 127;
+      }
+      if (chunk == 0) lds_st<int>(rowl + 32 * h, il);
+    }
     if (tid < 2 * kBulkM) {
       const int blk = tid / kBulkM, r = tid % kBulkM;
       sm.rexp[blk][r] = p.lexp[blk * p.P + tr.start + min(r, tr.m - 1)];
@@ -2194,17 +2222,24 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
     } else if constexpr (kPhase == kPhaseB) {
       // h = SiLU(g) * u of the wave's 32 h columns, fp16 with one exponent
       // per row and 32-column block (the wave's own: no exchange).
+      // The exponent comes from a bound, as D's does: |SiLU(g)| <= |g|, and
+      // |g| < 2^(il_g + 1 - e_g) 2^(ilog(maxsc_g) + 1) with il_g = floor(log2)
+      // of the staged gate latent row's L1 norm (u alike), so h * 2^ex stays
+      // below 2^15 for ex = 11 - il_g - il_u - ilog(maxsc_g) - ilog(maxsc_u)
+      // + e_g + e_u.
       const int nh = p.ff / kBulkHBlock;
+      const int hex0 = 11 - bulk_scale_ilog<true>(sm, wave, lane);
 #pragma unroll
       for (int rb = 0; rb < kBulkBlocks; ++rb) {
         if (rb < nrb) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = rb * 16 + kq * 4 + v;
-            const float sg = ldexpf(1.0f, -rx0[rb * 16 + v]), su = ldexpf(1.0f, -rx1[rb * 16 + v]);
+            const int eg = rx0[rb * 16 + v], eu = rx1[rb * 16 + v];
+            const float sg = ldexpf(1.0f, -eg), su = ldexpf(1.0f, -eu);
             const float h0 = silu(acc[rb][0][v] * sg) * (acc[rb][2][v] * su);
             const float h1 = silu(acc[rb][1][v] * sg) * (acc[rb][3][v] * su);
-            const int ex = pow2_row_exponent(op_over(fmaxf(fabsf(h0), fabsf(h1)), 1, 16, OpMax{}));
+            const int ex = min(120, max(-120, hex0 - (&sm.il1[kq * 4])[rb * 16 + v] + eg + eu));
             if (row < tr.m) {
               half2v hb;
               hb[0] = static_cast<_Float16>(ldexpf(h0, ex));
@@ -2223,7 +2258,7 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
       // exponent per row and 64-column block (the wave's own).
       const bool reduced = p.out_mode == LATENT_OUT_REDUCED;
       const int ny = p.d / kBulkYBlock;
-      const int yex0 = reduced ? 13 - bulk_scale_ilog(sm, wave, lane) : 0;
+      const int yex0 = reduced ? 13 - bulk_scale_ilog<false>(sm, wave, lane) : 0;
 #pragma unroll
       for (int rb = 0; rb < kBulkBlocks; ++rb) {
         if (rb < nrb) {
