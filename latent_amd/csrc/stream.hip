@@ -1768,11 +1768,24 @@ struct BulkShape {
   static constexpr bool kStaged = kPhase == kPhaseA || kPhase == kPhaseC;
 };
 
+// D: 256 table rows of 256 bytes, as the item kernels' (ItemLds): row b's
+// first half holds code byte b's level pair in 32 copies, so a lookup
+// address is one byte permute (lut_addr), and the rows' second halves hold
+// the unit's activation block: activation row r's chunks 8 j .. 8 j + 7 in
+// table row 4 r + j, chunk c at position (c ^ r) & 7 of the 128 bytes (the 8
+// rows an MFMA read takes at once meet 8 distinct bank groups, and every
+// operand address of a K step is one of two lane bases plus an immediate).
+// Measured D 297 -> 284 us; the same layout in A and C (and its address
+// arithmetic next to B's) tipped them into spills: A 428 -> 487 us, C 110 ->
+// 125 us.  A, B and C: a table of 32 (B: 8) copies per byte and the
+// activation block(s) beside it, rows 33 chunks apart.
 template <int kPhase>
 struct alignas(16) BulkSmem {
-  uint32_t lut[256 * BulkShape<kPhase>::kLut];                    // [byte][copy]: half2(level(lo), level(hi))
-  u32x4 scales[kScaleBytes / 16];                                 // the tile's scale block
-  u32x4 act[BulkShape<kPhase>::kActBlocks][kBulkM * kBulkStride];  // [block][row * 33 + chunk]
+  static constexpr bool kTableRows = kPhase == kPhaseD;
+  static_assert(!kTableRows || kBulkM * kActChunks * 16 == 256 * 128, "the block fills the rows' second halves");
+  uint32_t lut[kTableRows ? 256 * 64 : 256 * BulkShape<kPhase>::kLut];  // [byte][copy]: half2(level(lo), level(hi))
+  u32x4 scales[kScaleBytes / 16];                                        // the tile's scale block
+  u32x4 act[kTableRows ? 1 : BulkShape<kPhase>::kActBlocks][kTableRows ? 1 : kBulkM * kBulkStride];
   int rexp[2][kBulkM];     // A: x exponent, C: row exponent c (by unit parity); B: gate / up latent; D: d latent
   uint32_t rowoff[2][kBulkM];  // A: byte offset of each row's x row (by unit parity); D: output row
   int texp[kPhase == kPhaseC ? kK / kBulkHBlock : 1][kBulkM];  // C: the staged tile's h block exponents of each row
@@ -1782,6 +1795,15 @@ struct alignas(16) BulkSmem {
   int il1[kPhase == kPhaseD || kPhase == kPhaseB ? kBulkM : 1];
 };
 
+// LDS byte address of chunk `chunk` of row `row` of activation block blk.
+template <int kPhase>
+__device__ __forceinline__ uint32_t bulk_act(const BulkSmem<kPhase>& sm, int blk, int row, int chunk) {
+  BulkSmem<kPhase>& m = const_cast<BulkSmem<kPhase>&>(sm);
+  if constexpr (BulkSmem<kPhase>::kTableRows)
+    return lds_addr(m.lut[0]) + static_cast<uint32_t>(row * 1024 + (chunk >> 3) * 256 + 128 + (((chunk ^ row) & 7) << 4));
+  else return lds_addr(m.act[blk][0]) + bulk_slot(row, chunk) * 16;
+}
+
 // MFMA steps of a tile over the unit's first kRb 16-row blocks: per 32-row
 // step the four B operands of the wave's columns are decoded once and
 // multiplied into every block.  Rows past the unit's pairs hold zeros.
@@ -1789,6 +1811,8 @@ template <int kPhase, int kRb>
 __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32x4 (&cb)[kSteps], int n, int kq,
                                            int wave, uint32_t lut_lane, float4v (&acc)[kBulkBlocks][4]) {
   const uint32_t sbase = lds_addr(const_cast<BulkSmem<kPhase>&>(sm).scales[0]);
+  // Table rows: the lane's activation bases of even and odd K steps.
+  const uint32_t abase0 = BulkSmem<kPhase>::kTableRows ? bulk_act(sm, 0, n, kq) : 0u, abase1 = abase0 ^ 64u;
   // Phase C: the lane base of the scale rows, of which each step takes an
   // opaque copy, so the compiler neither keeps eight per-step addresses live
   // across the tile loop (they spilled, and every reload waited for the tile
@@ -1821,7 +1845,10 @@ __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32
       uint32_t f[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t pr = lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << BulkShape<kPhase>::kLutShift));
+        const uint32_t pr =
+            BulkSmem<kPhase>::kTableRows
+                ? lds_ld<uint32_t>(lds_addr(const_cast<BulkSmem<kPhase>&>(sm).lut[0]) + lut_addr(x, q, lut_lane))
+                : lds_ld<uint32_t>(lut_lane + (((x >> (8 * q)) & 0xFFu) << BulkShape<kPhase>::kLutShift));
         const uint32_t sq = sc[q];
         f[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, pr) * __builtin_bit_cast(half2v, sq));
       }
@@ -1830,9 +1857,17 @@ __device__ __forceinline__ void bulk_steps(const BulkSmem<kPhase>& sm, const u32
 #pragma unroll
     for (int rb = 0; rb < kRb; ++rb) {
       const int row = rb * 16 + n;
-      const half8 a0 = __builtin_bit_cast(half8, sm.act[0][bulk_slot(row, chunk)]);
-      const half8 a1 =
-          kPhase == kPhaseB ? __builtin_bit_cast(half8, sm.act[BulkShape<kPhase>::kActBlocks - 1][bulk_slot(row, chunk)]) : a0;
+      half8 a0, a1;
+      if constexpr (BulkSmem<kPhase>::kTableRows) {
+        // Row rb * 16 + n, chunk 4 s + kq: table row 4 row + s / 2, position
+        // ((s & 1) * 4 + kq) ^ (n & 7).
+        a0 = lds_ld<half8>((s & 1 ? abase1 : abase0) + rb * 16384 + (s >> 1) * 256);
+        a1 = a0;
+      } else {
+        a0 = __builtin_bit_cast(half8, sm.act[0][bulk_slot(row, chunk)]);
+        a1 = kPhase == kPhaseB ? __builtin_bit_cast(half8, sm.act[BulkShape<kPhase>::kActBlocks - 1][bulk_slot(row, chunk)])
+                               : a0;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(j < 2 ? a0 : a1, bf[j], acc[rb][j], 0, 0, 0);
@@ -1993,7 +2028,7 @@ __device__ __forceinline__ void bulk_unit_act(const Params& p, BulkSmem<kPhase>&
           l1 += fabsf(static_cast<float>(hv[i]));
         }
         l1 = op_over(l1, 1, 32, OpAdd{});
-        sm.act[0][bulk_slot(r, chunk)] = __builtin_bit_cast(u32x4, hv);
+        lds_st<u32x4>(bulk_act(sm, 0, r, chunk), __builtin_bit_cast(u32x4, hv));
         if (chunk == 0) {
           lds_st<int>(rowx + 32 * (h0 + q), ex);
           lds_st<int>(rowl + 32 * (h0 + q), bulk_y_ilog(l1, ex));
@@ -2123,11 +2158,19 @@ __global__ void __launch_bounds__(kT, kGroupsPerCU) bulk_kernel(Params p) {
   {
     const half2v lv = {static_cast<_Float16>(nf4_level(tid & 15)), static_cast<_Float16>(nf4_level(tid >> 4))};
     const uint32_t bits = __builtin_bit_cast(uint32_t, lv);
-    uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * BS::kLut]);
+    if constexpr (BulkSmem<kPhase>::kTableRows) {
 #pragma unroll
-    for (int j = 0; j < BS::kLut / 4; ++j) dstv[(j + tid) & (BS::kLut / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+      for (int j = 0; j < 8; ++j)
+        lds_st<u32x4>(lds_addr(sm.lut[0]) + tid * 256 + ((j + tid) & 7) * 16, u32x4{bits, bits, bits, bits});
+    } else {
+      uint4* dstv = reinterpret_cast<uint4*>(&sm.lut[tid * BS::kLut]);
+#pragma unroll
+      for (int j = 0; j < BS::kLut / 4; ++j) dstv[(j + tid) & (BS::kLut / 4 - 1)] = make_uint4(bits, bits, bits, bits);
+    }
   }
-  const uint32_t lut_lane = lds_addr(sm.lut[0]) + ((lane & (BS::kLut - 1)) << 2);
+  // Table rows: the lane's copy offset (lut_addr); otherwise the lane's copy's address.
+  const uint32_t lut_lane = BulkSmem<kPhase>::kTableRows ? static_cast<uint32_t>(lane & 31) << 2
+                                                         : lds_addr(sm.lut[0]) + ((lane & (BS::kLut - 1)) << 2);
 
   // Code ring of kBulkRing tiles: tile i + kBulkRing - 1's loads are issued
   // while tile i is computed.
