@@ -843,20 +843,31 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
   // Phase A: every key, finished here (phase B stages two latent blocks per
   // unit, and finishing them there measured slower).
   constexpr bool kRestOnly = kByKey && kPhase == kPhaseC;
-  if constexpr (kByKey && !kRestOnly) {
-    // Phase A by key: a wave takes kRowsPerWave rows of one key, so the key's
-    // dealing and unit are looked up once and those rows' partials are in
-    // flight together (one row per wave left each wave with about ten rows in
-    // turn, two dependent round trips each).  Pieces in workgroup order.
+  if constexpr (kByKey) {
+    // A wave takes kRowsPerWave rows of one key, so the key's dealing and
+    // unit are looked up once and those rows' partials are in flight together
+    // (one row per wave left each wave with about ten rows in turn, two
+    // dependent round trips each).  Pieces in workgroup order.
     constexpr int kRowsPerWave = 8;
     constexpr int kGroups = kRows / kRowsPerWave;
     static_assert(kRows % kRowsPerWave == 0, "whole row groups");
-    for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nkey * kGroups;
+    const int nw = (kRestOnly ? 8 * J : nkey) * kGroups;
+    for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nw;
          w += gridDim.x * (kT / kWave)) {
-      const int key = uniform(w / kGroups), row0 = (w - key * kGroups) * kRowsPerWave;
-      int xcd = 0;
-      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
-      const Deal dl = deal_for(nkey, per_key, p.G, xcd);
+      int key, row0, xcd = 0;
+      Deal dl;
+      if constexpr (kRestOnly) {
+        xcd = uniform(w / (J * kGroups));
+        dl = deal_for(nkey, per_key, p.G, xcd);
+        key = dl.rest0 + uniform(w / kGroups) % J;
+        row0 = (w % kGroups) * kRowsPerWave;
+        if (key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) continue;
+      } else {
+        key = uniform(w / kGroups);
+        row0 = (w - key * kGroups) * kRowsPerWave;
+        while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
+        dl = deal_for(nkey, per_key, p.G, xcd);
+      }
       const int u = key / keys_per_unit, f = key - u * keys_per_unit;
       const int4 info = p.unit_info[u];
       if (row0 >= info.z) continue;
@@ -882,39 +893,24 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
       for (int r = 0; r < kRowsPerWave; ++r) {
         if (row0 + r < info.z) {
           const int64_t pair = info.y + row0 + r;
-          finish_row(s[r], p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
+          if constexpr (kRestOnly)
+            reinterpret_cast<float4*>(part + (static_cast<int64_t>(key) * kRows + row0 + r) * kN)[lane] = s[r];
+          else
+            finish_row(s[r], p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
         }
       }
     }
     return;
   }
-  const int nrows = kRestOnly ? 8 * J * kRows : nkey * kRows;
-  for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nrows;
+  for (int w = blockIdx.x * (kT / kWave) + static_cast<int>(threadIdx.x >> 6); w < nkey * kRows;
        w += gridDim.x * (kT / kWave)) {
     const int row = w % kRows;
-    int key = w / kRows;
-    Deal dl{};
-    int xcd = 0;
-    if constexpr (kRestOnly) {
-      xcd = w / (J * kRows);
-      dl = deal_for(nkey, per_key, p.G, xcd);
-      key = dl.rest0 + (w / kRows) % J;
-      if (key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) continue;
-    } else if constexpr (kByKey) {
-      while (xcd < 7 && key >= static_cast<int>(static_cast<int64_t>(nkey) * (xcd + 1) / 8)) ++xcd;
-      dl = deal_for(nkey, per_key, p.G, xcd);
-    }
+    const int key = w / kRows;
     const int u = key / keys_per_unit, f = key - u * keys_per_unit;
     const int4 info = p.unit_info[u];
     if (row >= info.z) continue;
-    int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
-    int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
-    if constexpr (kByKey) {
-      // A whole key: b = -1 names its slot; a rest key: workgroups b0..b1 of the XCD.
-      const int rk = key - dl.rest0;
-      b0 = rk < 0 ? -1 : rk * per_key / dl.c;
-      b1 = rk < 0 ? -1 : ((rk + 1) * per_key - 1) / dl.c;
-    }
+    const int b0 = kPerItem ? key * per_key : (key * per_key) / chunk;
+    const int b1 = kPerItem ? key * per_key + per_key - 1 : (key * per_key + per_key - 1) / chunk;
     // Batches of kRedLoads partials in flight, summed in workgroup (item) order.
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int bb = b0; bb <= b1; bb += kRedLoads) {
@@ -923,15 +919,10 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
       for (int q = 0; q < kRedLoads; ++q) {
         const int b = min(bb + q, b1);
         int64_t rowoff;  // float offset of the partial row
-        if constexpr (kByKey) {
-          const int64_t slot =
-              b < 0 ? key : 2 * U + (xcd + 8 * b) * kRemPieces + key - (dl.rest0 * per_key + b * dl.c) / per_key;
-          rowoff = (slot * kRows + row) * kN;
-        } else if constexpr (kPerItem) {
+        if constexpr (kPerItem)
           rowoff = (static_cast<int64_t>(info.y + row) * per_key + (b - key * per_key)) * kN;  // by grouped pair
-        } else {
+        else
           rowoff = (static_cast<int64_t>(part_slot(b, key, chunk, per_key, maxj)) * kRows + row) * kN;
-        }
         // Only the batch's live partials are read (b1 is wave-uniform).
         v[q] = bb + q <= b1 ? reinterpret_cast<const float4*>(part + rowoff)[lane] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
@@ -943,9 +934,7 @@ __global__ void __launch_bounds__(kT) reduce_kernel(Params p) {
       }
     }
     const int64_t pair = info.y + row;
-    if constexpr (kRestOnly)
-      reinterpret_cast<float4*>(part + (static_cast<int64_t>(key) * kRows + row) * kN)[lane] = s;
-    else if (kPhase == kPhaseA)
+    if (kPhase == kPhaseA)
       finish_row(s, p.lat + (static_cast<int64_t>(f) * p.P + pair) * kK, p.lexp + f * p.P + pair, lane);
     else
       finish_row(s, p.dlat + pair * kK, p.dexp + pair, lane);
@@ -2621,7 +2610,7 @@ int bulk_forward(const latent_moe_args& a, const BulkArgs& bk, int64_t max_units
   hipLaunchKernelGGL(bulk_kernel<kPhaseC>, dim3(p.G), dim3(kT), 0, s, p);
   // C's reduce sums only the rest keys' pieces (a whole key's sum is in its
   // slot); D finishes the rows as it stages them.
-  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM, false, true>), dim3(rblocks(p.G * kBulkM)), dim3(kT), 0, s, p);
+  hipLaunchKernelGGL((reduce_kernel<kPhaseC, kBulkM, false, true>), dim3(rblocks(p.G * kBulkM / 8)), dim3(kT), 0, s, p);
   hipLaunchKernelGGL(bulk_kernel<kPhaseD>, dim3(p.G), dim3(kT), 0, s, p);
   return hipGetLastError() == hipSuccess ? LATENT_OK : LATENT_E_HIP;
 }
