@@ -34,6 +34,7 @@ constexpr int kTok = 32;       // tokens per logits workgroup
 constexpr int kMaxE = 1024;    // experts: 16 per lane in topk_kernel
 constexpr int kPerLane = kMaxE / kWave;
 constexpr int kMaxK = kWave;  // slot s lives in lane s
+constexpr int kSliceBatch = 64;  // logit slices a topk thread loads at once
 
 struct Params {
   const void* x;
@@ -188,13 +189,22 @@ __global__ void __launch_bounds__(kThreads) topk_kernel(Params p) {
     } else {
       const float* src = p.partial + static_cast<int64_t>(t) * p.E + e;
       const int64_t stride = static_cast<int64_t>(p.T) * p.E;
-      float part[16];
+      // Up to kSliceBatch slices in flight (d = 7168: all 56 in one round
+      // trip; batches of 16 took four), added in slice order.
+      float part[kSliceBatch];
       v = 0.f;
-      for (int s0 = 0; s0 < p.nslice; s0 += 16) {
+      for (int s0 = 0; s0 < p.nslice; s0 += kSliceBatch) {
+        // One pointer stepped by the slice stride (64 scalar offsets spilled).
+        typedef const __attribute__((address_space(1))) float* gptr;
+        uintptr_t q = reinterpret_cast<uintptr_t>(src + s0 * stride);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) part[i] = s0 + i < p.nslice ? src[(s0 + i) * stride] : 0.f;
+        for (int i = 0; i < kSliceBatch; ++i) {
+          part[i] = s0 + i < p.nslice ? *reinterpret_cast<gptr>(q) : 0.f;
+          q += static_cast<uintptr_t>(stride) * sizeof(float);
+          asm volatile("" : "+v"(q));
+        }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v += part[i];
+        for (int i = 0; i < kSliceBatch; ++i) v += part[i];
       }
     }
     if (p.logits_out) p.logits_out[static_cast<int64_t>(t) * p.E + e] = v;
@@ -219,6 +229,7 @@ __global__ void __launch_bounds__(kThreads) topk_kernel(Params p) {
     int bi = 0x7FFFFFFF;
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
+      if (j >= nj) break;  // wave-uniform: the layer's experts only
       const int e = j * kWave + lane;
       const bool ok = e < p.E && !((taken >> j) & 1u);
       if (ok && (l[j] > bv || bi == 0x7FFFFFFF)) {
