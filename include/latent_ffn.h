@@ -344,7 +344,7 @@ int latent_expert_forward(const latent_expert_args* args, latent_stream_t stream
 
 /*
  * One router call.  Either logits = x . router (fp32 accumulation, summed over
- * 128-row slices of d in a fixed order) or caller logits (logits_in).  Then
+ * 64-row slices of d in a fixed order) or caller logits (logits_in).  Then
  * softmax over the E experts, top-k by descending probability (ties -> lower
  * expert id), weights renormalised over the k kept slots, then the drop rule.
  * Produces the ids / weights operands of latent_moe_ffn_forward.

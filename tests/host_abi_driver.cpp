@@ -168,7 +168,7 @@ void codec_route_expert_repack() {
   r.x_dtype = LATENT_BF16;
   r.router_dtype = LATENT_F32;
   size_t n = 0;
-  EXPECT(latent_route_workspace_size(&r, &n) == LATENT_OK && n == 56u * 4 * 256 * 4);
+  EXPECT(latent_route_workspace_size(&r, &n) == LATENT_OK && n == 112u * 4 * 256 * 4);
   latent_route_args b = r;
   b.n_expert_used = 257;
   EXPECT(latent_route_workspace_size(&b, &n) == LATENT_E_INVALID);

@@ -135,7 +135,7 @@ def test_route_argument_checks(L):
     a.x_dtype, a.router_dtype = L.LATENT_BF16, L.LATENT_F32
     n = ctypes.c_size_t(0)
     assert L.lib.latent_route_workspace_size(ctypes.byref(a), ctypes.byref(n)) == L.LATENT_OK
-    assert n.value == 56 * 4 * 256 * 4  # one f32 [T][E] slice per 128 rows of d
+    assert n.value == 112 * 4 * 256 * 4  # one f32 [T][E] slice per 64 rows of d
     a.logits_in = 16
     assert L.lib.latent_route_workspace_size(ctypes.byref(a), ctypes.byref(n)) == L.LATENT_OK and n.value == 0
     for field, value, status in [("n_expert_used", 257, L.LATENT_E_INVALID), ("n_expert", 2048, L.LATENT_E_UNSUPPORTED),
