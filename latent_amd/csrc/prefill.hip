@@ -589,34 +589,50 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(Params p) {
 }
 
 // x rows to fp16: xh[t] = fp16(x[t] * 2^e[t]) with 2^e * max|x[t]| in [2^14, 2^15).
-// One workgroup per token; d % 8 == 0 and x 16-byte aligned.
+// One wave per token, four tokens per workgroup: no barrier, and every
+// token of a 4096-token call is resident at once (a workgroup per token,
+// with two barriers around the maximum, ran in two residency rounds).  Lane
+// l holds the 8-element chunks l, l + 64, ... of the row (raw, up to
+// kXPrepChunks of them: rows of up to 8192 elements are read once; longer
+// rows twice); d % 8 == 0 and x 16-byte aligned.
 // Also clears the token's slot entries of pos_of and, when per_slot_out is
 // given (per-slot output mode), writes the zero rows of the token's dropped
 // slots (id outside [0, E)): the GEMMs write routed rows only.
-__global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_dtype, int d, _Float16* xh, int* xexp,
-                                                          int* pos_of, int k, const int32_t* ids, int E,
+constexpr int kXPrepChunks = 16;
+template <bool kF32>
+__global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_dtype, int T, int d, _Float16* xh,
+                                                          int* xexp, int* pos_of, int k, const int32_t* ids, int E,
                                                           float* per_slot_out) {
-  __shared__ float red[kThreads / kWave];
-  __shared__ int ex;
-  const int t = blockIdx.x, tid = threadIdx.x;
-  for (int sl = tid; sl < k; sl += kThreads) pos_of[t * k + sl] = -1;
+  constexpr int kW = kF32 ? 2 : 1;  // 16-byte words per chunk of 8 elements
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * (kThreads / kWave) + static_cast<int>(threadIdx.x >> 6);
+  if (t >= T) return;
+  for (int sl = lane; sl < k; sl += kWave) pos_of[static_cast<int64_t>(t) * k + sl] = -1;
   if (per_slot_out) {
     for (int sl = 0; sl < k; ++sl) {
       const int e = ids[static_cast<int64_t>(t) * k + sl];
       if (e >= 0 && e < E) continue;
       float4* row = reinterpret_cast<float4*>(per_slot_out + (static_cast<int64_t>(t) * k + sl) * d);
-      for (int c = tid; c < d / 4; c += kThreads) row[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int c = lane; c < d / 4; c += kWave) row[c] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   const int64_t base = static_cast<int64_t>(t) * d;
-  auto load8 = [&](int c, float (&v)[8]) {
-    if (x_dtype == LATENT_F32) {
-      const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + c);
-      const float4 a = q[0], b = q[1];
-      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  auto load = [&](int c, uint4 (&r)[kW]) __attribute__((always_inline)) {
+    if constexpr (kF32) {
+      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const float*>(x) + base + c * 8);
+      r[0] = q[0];
+      r[kW - 1] = q[1];
     } else {
-      const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + c);
-      const uint32_t w[4] = {h.x, h.y, h.z, h.w};
+      r[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + c * 8);
+    }
+  };
+  auto vals = [&](const uint4 (&r)[kW], float (&v)[8]) __attribute__((always_inline)) {
+    if constexpr (kF32) {
+      const uint32_t w[8] = {r[0].x, r[0].y, r[0].z, r[0].w, r[kW - 1].x, r[kW - 1].y, r[kW - 1].z, r[kW - 1].w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+    } else {
+      const uint32_t w[4] = {r[0].x, r[0].y, r[0].z, r[0].w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if (x_dtype == LATENT_BF16) {
@@ -629,60 +645,58 @@ __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_d
       }
     }
   };
-  // Rows of up to kXRegs * 8 * kThreads values stay in registers between the
-  // maximum and the conversion; longer rows are read twice.
-  constexpr int kXRegs = 4;
-  float xv[kXRegs][8];
-  const bool cached = d <= kXRegs * 8 * kThreads;
+  const int nc = d / 8;
+  const bool cached = nc <= kXPrepChunks * kWave;
+  uint4 raw[kXPrepChunks][kW];
   float m = 0.f;
   if (cached) {
 #pragma unroll
-    for (int r = 0; r < kXRegs; ++r) {
-      const int c = (tid + r * kThreads) * 8;
-      if (c < d) {
-        load8(c, xv[r]);
+    for (int r = 0; r < kXPrepChunks; ++r)
+      if (lane + r * kWave < nc) load(lane + r * kWave, raw[r]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(xv[r][i]));
+    for (int r = 0; r < kXPrepChunks; ++r) {
+      if (lane + r * kWave < nc) {
+        float v[8];
+        vals(raw[r], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
       }
     }
   } else {
-    for (int c = tid * 8; c < d; c += kThreads * 8) {
+    for (int c = lane; c < nc; c += kWave) {
+      uint4 rr[kW];
       float v[8];
-      load8(c, v);
+      load(c, rr);
+      vals(rr, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     }
   }
-  m = op_over(m, 1, kWave, OpMax{});
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = m;
-  __syncthreads();
-  if (tid == 0) {
-    for (int i = 1; i < kThreads / kWave; ++i) m = fmaxf(m, red[i]);
-    ex = block_exponent(m);
-    xexp[t] = ex;
-  }
-  __syncthreads();
-  const int e = ex;
+  const int e = block_exponent(op_over(m, 1, kWave, OpMax{}));
+  if (lane == 0) xexp[t] = e;
+  auto store = [&](int c, const float (&v)[8]) __attribute__((always_inline)) {
+    half8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(v[i], e));
+    *reinterpret_cast<half8*>(xh + base + c * 8) = h;
+  };
   if (cached) {
 #pragma unroll
-    for (int r = 0; r < kXRegs; ++r) {
-      const int c = (tid + r * kThreads) * 8;
-      if (c < d) {
-        half8 h;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(xv[r][i], e));
-        *reinterpret_cast<half8*>(xh + base + c) = h;
+    for (int r = 0; r < kXPrepChunks; ++r) {
+      if (lane + r * kWave < nc) {
+        float v[8];
+        vals(raw[r], v);
+        store(lane + r * kWave, v);
       }
     }
     return;
   }
-  for (int c = tid * 8; c < d; c += kThreads * 8) {
+  for (int c = lane; c < nc; c += kWave) {
+    uint4 rr[kW];
     float v[8];
-    load8(c, v);
-    half8 h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = static_cast<_Float16>(__builtin_ldexpf(v[i], e));
-    *reinterpret_cast<half8*>(xh + base + c) = h;
+    load(c, rr);
+    vals(rr, v);
+    store(c, v);
   }
 }
 
@@ -894,9 +908,17 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   const int P = static_cast<int>(a.n_tokens * a.n_expert_used);
   const int R = static_cast<int>(a.max_rank), d = static_cast<int>(a.n_embd), ff = static_cast<int>(a.n_ff);
   const int rb = R / kBlk, fb = ff / kBlk, db = d / kBlk;
-  hipLaunchKernelGGL(x_prep_kernel, dim3(static_cast<unsigned>(a.n_tokens)), dim3(kThreads), 0, s, a.x, a.x_dtype, d,
-                     xh, xexp, pos_of, K, a.ids, static_cast<int>(a.n_expert),
-                     a.out_mode == LATENT_OUT_PER_SLOT ? static_cast<float*>(a.out) : nullptr);
+  {
+    const dim3 xg(static_cast<unsigned>((a.n_tokens + kThreads / kWave - 1) / (kThreads / kWave)));
+    float* pso = a.out_mode == LATENT_OUT_PER_SLOT ? static_cast<float*>(a.out) : nullptr;
+    const int T = static_cast<int>(a.n_tokens), E = static_cast<int>(a.n_expert);
+    if (a.x_dtype == LATENT_F32)
+      hipLaunchKernelGGL(x_prep_kernel<true>, xg, dim3(kThreads), 0, s, a.x, a.x_dtype, T, d, xh, xexp, pos_of, K, a.ids,
+                         E, pso);
+    else
+      hipLaunchKernelGGL(x_prep_kernel<false>, xg, dim3(kThreads), 0, s, a.x, a.x_dtype, T, d, xh, xexp, pos_of, K,
+                         a.ids, E, pso);
+  }
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   int4* units = reinterpret_cast<int4*>(scratch + L.units);
   hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, bulk ? stream::kBulkM : kMT, tile_a, tile_r0,
