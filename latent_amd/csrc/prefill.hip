@@ -700,11 +700,6 @@ __global__ void __launch_bounds__(kThreads) x_prep_kernel(const void* x, int x_d
   }
 }
 
-// pos_of[tok * k + slot] = pair for the routed pairs (x_prep_kernel cleared it to -1).
-__global__ void __launch_bounds__(kThreads) slots_kernel(Grouping g, int* pos_of, int P, int k) {
-  const int i = blockIdx.x * kThreads + threadIdx.x;
-  if (i < P && i < g.meta[3]) pos_of[g.pair_tok[i] * k + g.pair_slot[i]] = i;
-}
 
 // out[t] = sum over slots (in slot order) of w * y[pos_of[t][slot]] * 2^-exp,
 // y rows in fp16 with one exponent per 2^blk_log2 columns (row stride
@@ -774,13 +769,20 @@ __global__ void __launch_bounds__(kThreads) combine_kernel(const _Float16* y, co
   }
 }
 
-// M tiles of `rows` pairs (kMT for the GEMMs) for every active expert, in
-// expert order; with `units`, also each tile as {expert, first grouped pair,
-// pairs, 0}.
+// Workgroup 0: M tiles of `rows` pairs (kMT for the GEMMs) for every active
+// expert, in expert order; with `units`, also each tile as {expert, first
+// grouped pair, pairs, 0}.  The other workgroups: pos_of[tok * k + slot] =
+// pair for the routed pairs, kTileThreads pairs each (x_prep_kernel cleared
+// pos_of to -1).  Both read only the grouping, so they share one launch.
 __global__ void __launch_bounds__(kTileThreads) tiles_kernel(Grouping g, int rows, int* tile_a, int* tile_r0,
-                                                             int4* units) {
+                                                             int4* units, int* pos_of, int P, int k) {
   __shared__ int scan[kTileThreads];
   const int tid = threadIdx.x;
+  if (blockIdx.x > 0) {
+    const int i = (blockIdx.x - 1) * kTileThreads + tid;
+    if (i < P && i < g.meta[3]) pos_of[g.pair_tok[i] * k + g.pair_slot[i]] = i;
+    return;
+  }
   const int n_active = g.meta[0];
   const int per = (n_active + kTileThreads - 1) / kTileThreads;
   const int a0 = min(n_active, tid * per), a1 = min(n_active, a0 + per);
@@ -921,10 +923,8 @@ int forward(const latent_moe_args& a, const Factor* fac, const Grouping& g, char
   }
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
   int4* units = reinterpret_cast<int4*>(scratch + L.units);
-  hipLaunchKernelGGL(tiles_kernel, dim3(1), dim3(kTileThreads), 0, s, g, bulk ? stream::kBulkM : kMT, tile_a, tile_r0,
-                     bulk ? units : nullptr);
-  if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
-  hipLaunchKernelGGL(slots_kernel, dim3(static_cast<unsigned>((P + kThreads - 1) / kThreads)), dim3(kThreads), 0, s, g,
+  hipLaunchKernelGGL(tiles_kernel, dim3(static_cast<unsigned>(1 + (P + kTileThreads - 1) / kTileThreads)),
+                     dim3(kTileThreads), 0, s, g, bulk ? stream::kBulkM : kMT, tile_a, tile_r0, bulk ? units : nullptr,
                      pos_of, P, K);
   if (hipGetLastError() != hipSuccess) return LATENT_E_HIP;
 
